@@ -1,0 +1,136 @@
+/*
+ * soc_hip.h - C ABI of the MI355X (gfx950) Qwen3 forward hot path.
+ *
+ * Plain C types only (pointers, sizes, integers); no exceptions cross this boundary. Every call returns a status
+ * code (SOC_OK == 0) and, on failure, leaves a message for soc_last_error() on the calling thread.
+ *
+ * The reference runtime (SongWooYoung/SoC, Mac/gpu) exposes these operations as C++ classes; each declaration below
+ * names the reference interface it replaces. The C++ host layer in include/soc/ keeps those class names and
+ * signatures and calls into this ABI.
+ *
+ * Data contract: weights are fp16 in the Hugging Face [out][in] layout, activations and logits fp32, token ids
+ * int32. Device memory is owned by the library unless an entry point says it takes caller device pointers.
+ * Not thread-safe per context; all work of one context runs in order on that context's HIP stream.
+ */
+#ifndef SOC_HIP_H
+#define SOC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------------------------------------------ */
+enum {
+  SOC_OK = 0,
+  SOC_ERR_INVALID = 1,   /* bad argument, shape, name or dtype (e.g. matmul_op.mm:29-100 validation)          */
+  SOC_ERR_STATE = 2,     /* call out of order (decode before prefill, token mismatch: generation_context.cpp:73-84) */
+  SOC_ERR_CAPACITY = 3,  /* sequence/KV capacity exceeded (generation_context.cpp:85-90, kv_cache.mm:103-108)   */
+  SOC_ERR_HIP = 4,       /* HIP runtime error                                                                  */
+  SOC_ERR_NOMEM = 5      /* device allocation failed (buffer_arena.cpp:59-65 "capacity exceeded" analogue)     */
+};
+
+/* Message of the calling thread's last failed call ("" if none). Replaces the `std::string* error_message`
+ * out-parameter of every reference GPU entry point (e.g. Mac/gpu/include/runtime/generation_context.h:30-50). */
+const char* soc_last_error(void);
+
+/* ---- device context: replaces MetalContext (Mac/gpu/include/metal/metal_context.h; metal_context.mm:78-216) ---- */
+typedef struct soc_ctx soc_ctx;
+int soc_ctx_create(int device, soc_ctx** out);
+int soc_ctx_destroy(soc_ctx* ctx);
+/* Host waits for all work queued on the context stream (MetalContext::FinalizeCommandBuffer's wait). */
+int soc_ctx_synchronize(soc_ctx* ctx);
+/* GPU time between two points of the context stream, from HIP events (metal_context.mm:206-214 GPU ms). */
+int soc_ctx_timer_start(soc_ctx* ctx);
+int soc_ctx_timer_stop(soc_ctx* ctx, float* ms);
+
+/* ---- device buffers: replaces MetalBuffer::CreateShared / Write / Read (Mac/gpu/include/buffer/metal_buffer.h) ---- */
+int soc_buffer_alloc(soc_ctx* ctx, size_t bytes, void** device_ptr);
+int soc_buffer_free(soc_ctx* ctx, void* device_ptr);
+int soc_buffer_write(soc_ctx* ctx, void* device_dst, const void* host_src, size_t bytes);
+int soc_buffer_read(soc_ctx* ctx, void* host_dst, const void* device_src, size_t bytes);
+
+/* ---- model: replaces QwenCausalLM + QwenModelLoader (Mac/gpu/include/model/qwen_causal_lm.h:17-95,
+ *      Mac/gpu/src/model/qwen_model_loader.cpp:57-192; names/shapes of Mac/cpu/src/qwen_model_loader.cpp:35-93) ---- */
+typedef struct soc_qwen_config {
+  int32_t vocab_size;
+  int32_t hidden_size;
+  int32_t num_hidden_layers;
+  int32_t num_attention_heads;
+  int32_t num_key_value_heads;
+  int32_t head_dim;               /* must be 128 */
+  int32_t intermediate_size;
+  int32_t max_position_embeddings;
+  double rope_theta;
+  float rms_norm_eps;
+  int32_t tie_word_embeddings;
+} soc_qwen_config;
+
+typedef struct soc_model soc_model;
+int soc_model_create(soc_ctx* ctx, const soc_qwen_config* cfg, soc_model** out);
+int soc_model_destroy(soc_model* model);
+/* Upload one fp16 tensor by its Hugging Face name ("model.layers.3.self_attn.q_proj.weight", ...). */
+int soc_model_load_tensor(soc_model* model, const char* name, const uint16_t* host_fp16, int64_t numel);
+/* Fill every tensor with the seeded generator (soc_synth_normal_f16 with `sigma`; norm gains = 1.0). */
+int soc_model_synthesize(soc_model* model, uint64_t seed, float sigma);
+/* Validates that every tensor the config needs is present (StartupValidator / loader checks). */
+int soc_model_finalize(soc_model* model);
+/* Bytes of weights held on the device. */
+int soc_model_weight_bytes(const soc_model* model, int64_t* bytes);
+
+/* ---- KV cache: replaces KVCache (Mac/gpu/include/runtime/kv_cache.h:23-79; kv_cache.mm:32-204).
+ *      fp16, `num_slots` independent sequences of `capacity` positions each. ---- */
+typedef struct soc_kv soc_kv;
+int soc_kv_create(soc_model* model, int32_t num_slots, int32_t capacity, soc_kv** out);
+int soc_kv_destroy(soc_kv* kv);
+/* Length (number of cached positions) of one slot; reset sets it to 0 (GenerationContext::Reset). */
+int soc_kv_length(const soc_kv* kv, int32_t slot, int32_t* length);
+int soc_kv_reset(soc_kv* kv, int32_t slot);
+/* Write fp32 key/value rows [nkv][head_dim] of one position (stored as fp16) and extend the length to pos+1
+ * (TensorKVCache::Write, Mac/cpu/src/kv_cache.cpp:50-78). Used to seed long prefixes. */
+int soc_kv_write(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, const float* key, const float* value);
+/* Fill positions [0, length) of a slot in every layer with seeded N(0,1) fp16 keys/values and set the length. */
+int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t seed);
+/* Read back fp16 K and V of one (slot, layer) as [nkv][length][head_dim] (nullable destinations). */
+int soc_kv_read(const soc_kv* kv, int32_t slot, int32_t layer, uint16_t* keys, uint16_t* values);
+
+/* ---- forward: replaces CommandScheduler::RunPrefill / RunDecode (Mac/gpu/include/runtime/command_scheduler.h:14-35)
+ *      -> QwenCausalLM::ForwardLogitsCached (Mac/gpu/src/model/qwen_causal_lm.cpp:250-268) ---- */
+/* Runs `n` tokens of one slot at positions [position_offset, position_offset + n), appending their K/V.
+ * position_offset must equal the slot's current length. Writes the fp32 logits of the last `logit_rows` rows
+ * (nullable) and the greedy next token from the last row (nullable). */
+int soc_prefill(soc_model* model, soc_kv* kv, int32_t slot, const int32_t* token_ids, int32_t n,
+                int32_t position_offset, int32_t logit_rows, float* logits, int32_t* next_token);
+/* One decode step of one slot: feeds `last_token` at position = current length. Logits [V] nullable. */
+int soc_decode(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, float* logits, int32_t* next_token);
+/* `steps` greedy decode steps of one slot with the token fed back on the device (no host round trip per step).
+ * tokens_out[steps] receives the generated ids. */
+int soc_decode_steps(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, int32_t steps,
+                     int32_t* tokens_out);
+
+/* ---- op-level entry points on caller device pointers, queued on the context stream (tests, microbenchmarks).
+ *      These replace the reference's op wrappers (Mac/gpu/include/op/*.h, static Run(...)). ---- */
+/* y[N] = W[N][K] . x[K]; W fp16, x fp16, y fp32 (LinearOp/MatMulOp decode mode, matmul_op.mm:143-163). */
+int soc_gemv_f16(soc_ctx* ctx, const void* w, const void* x, float* y, int32_t n, int32_t k);
+/* Group-quantized matmul: y[M][N] = x[M][K] . dequant(codes, scales)^T; bits 8 or 4; group 64 along K. */
+int soc_qmm(soc_ctx* ctx, const void* x_f16, const void* codes, int32_t bits, const void* scales_f16, float* y,
+            int32_t m, int32_t n, int32_t k);
+/* Dequantize to fp32 [N][K] (bit-exact contract: w = float(code) * float(scale)). */
+int soc_dequant(soc_ctx* ctx, const void* codes, int32_t bits, const void* scales_f16, float* w, int32_t n, int32_t k);
+
+/* ---- seeded synthetic data (this project's generator; the reference has none) ---- */
+int soc_synth_normal_f16(uint64_t seed, const char* name, float sigma, int64_t offset, int64_t n, uint16_t* out);
+int soc_synth_uniform_f16(uint64_t seed, const char* name, float lo, float hi, int64_t offset, int64_t n,
+                          uint16_t* out);
+int soc_synth_tokens(uint64_t seed, const char* name, int32_t vocab, int64_t n, int32_t* out);
+int soc_synth_int_uniform(uint64_t seed, const char* name, int32_t lo, int32_t hi, int64_t n, int32_t* out);
+int soc_synth_codes(uint64_t seed, const char* name, int32_t bits, int64_t n_codes, uint8_t* out);
+uint16_t soc_f64_to_f16_rne(double x);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOC_HIP_H */

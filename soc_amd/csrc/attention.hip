@@ -1,0 +1,331 @@
+// attention.hip - per-head QK-RMSNorm + RoPE + KV-cache append, GQA causal attention over the fp16 KV cache in
+// HBM (split over the key axis with a log-sum-exp combine), and the prefill row helpers (embedding, RMSNorm rows).
+//
+// Reference computation (batch 1, fp32): QwenAttention::ForwardCached (Mac/cpu/src/qwen_attention.cpp:142-205):
+//   q,k,v projections -> q_norm/k_norm over each head's d features (:168-169) -> RoPE at the absolute position
+//   (:170-171; rope.cpp:70-88) -> cache write (:180-193) -> GroupedQueryAttention with prefix = position offset
+//   (grouped_query_attention.cpp:91-139): kv head = h / (nq/nkv), score = (q.k) * (1/sqrt(d)), softmax by
+//   max-subtract and divide-by-sum, output = sum_j w_j v_j over the visible keys j <= position.
+// Here the cache holds fp16 K/V in [slot][layer][kv_head][pos][d]; a new token's key and value are rounded to
+// fp16 before use so that decode and prefill see identical keys.
+#include "kernels.h"
+
+namespace soc {
+
+namespace {
+
+constexpr int HD = 128;  // head_dim handled by these kernels
+
+// Lane l of a wave holds dims (l, l + 64) of one head vector: RMSNorm over the 128 values and rotate-half RoPE at
+// table row `pos` (cos/sin precomputed on the host in double, then rounded to float, like rope.cpp:77-79).
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const f16* gain, float eps, const float* cosr,
+                                               const float* sinr, int lane) {
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(HD) + eps);
+  const float y0 = x0 * scale * static_cast<float>(gain[lane]);
+  const float y1 = x1 * scale * static_cast<float>(gain[lane + 64]);
+  const float c = cosr[lane], s = sinr[lane];
+  x0 = y0 * c - y1 * s;
+  x1 = y0 * s + y1 * c;
+}
+
+}  // namespace
+
+// grid = (max_split, nkv, B), block = 256 (4 waves). Each block: one KV head g, its G query heads, one batch row,
+// one chunk of keys.
+template <int G, bool FUSED>
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
+  __shared__ float qs[G][HD];
+  __shared__ float kn[HD], vn[HD];
+  __shared__ float sc[G][256];
+  __shared__ float red[4][G][HD];
+  __shared__ float mstat[G], lstat[G];
+  __shared__ int last;
+
+  const int b = blockIdx.z, g = blockIdx.y, s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int qpos = (a.pos != nullptr ? a.pos[b] : b) + a.pos_base;
+  const int S = qpos + 1;
+  const int nact = (S + a.chunk - 1) / a.chunk;
+  if (s >= nact) return;
+  const int slot = a.slot != nullptr ? a.slot[b] : a.slot_base;
+  const size_t head_base = static_cast<size_t>(slot) * a.slot_stride + static_cast<size_t>(a.layer) * a.layer_stride +
+                           static_cast<size_t>(g) * a.cap * HD;
+  f16* kb = a.kcache + head_base;
+  f16* vb = a.vcache + head_base;
+  const float* row = a.qkv + static_cast<size_t>(b) * a.ld_qkv;
+
+  if constexpr (FUSED) {
+    const float* cr = a.rope_cos + static_cast<size_t>(qpos) * (HD / 2);
+    const float* sr = a.rope_sin + static_cast<size_t>(qpos) * (HD / 2);
+    for (int vi = wid; vi < G + 2; vi += 4) {
+      if (vi < G) {
+        const float* src = row + (g * G + vi) * HD;
+        float x0 = src[lane], x1 = src[lane + 64];
+        norm_rope_pair(x0, x1, a.q_gain, a.eps, cr, sr, lane);
+        qs[vi][lane] = x0;
+        qs[vi][lane + 64] = x1;
+      } else if (vi == G) {
+        const float* src = row + a.nq * HD + g * HD;
+        float x0 = src[lane], x1 = src[lane + 64];
+        norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
+        const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
+        kn[lane] = static_cast<float>(h0);
+        kn[lane + 64] = static_cast<float>(h1);
+        if (s == nact - 1) {
+          kb[static_cast<size_t>(qpos) * HD + lane] = h0;
+          kb[static_cast<size_t>(qpos) * HD + lane + 64] = h1;
+        }
+      } else {
+        const float* src = row + (a.nq + a.nkv) * HD + g * HD;
+        const f16 h0 = static_cast<f16>(src[lane]), h1 = static_cast<f16>(src[lane + 64]);
+        vn[lane] = static_cast<float>(h0);
+        vn[lane + 64] = static_cast<float>(h1);
+        if (s == nact - 1) {
+          vb[static_cast<size_t>(qpos) * HD + lane] = h0;
+          vb[static_cast<size_t>(qpos) * HD + lane + 64] = h1;
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = row[(g * G) * HD + i];
+  }
+  __syncthreads();
+
+  const int c0 = s * a.chunk;
+  const int n = min(a.chunk, S - c0);
+  const int sub = lane & 15, r = lane >> 4;
+  float qreg[G][8];
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qreg[j][i] = qs[j][sub * 8 + i];
+
+  // scores: 16 lanes per key (8 dims each), 4 keys per wave step, 16 keys per block step
+  for (int base = 0; base < n; base += 64) {
+    u32x4 kraw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = base + u * 16 + wid * 4 + r;
+      kraw[u] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = base + u * 16 + wid * 4 + r;
+      float kf[8];
+      if (FUSED && c0 + p == qpos) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
+      } else {
+        f16x8_to_f32(kraw[u], kf);
+      }
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
+        d = group_sum<16>(d);
+        if (sub == 0 && p < n) sc[j][p] = d * a.scale;
+      }
+    }
+  }
+  __syncthreads();
+
+  // softmax statistics per query head
+  for (int j = wid; j < G; j += 4) {
+    float m = -INFINITY;
+    for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[j][p]);
+    m = wave_max(m);
+    float l = 0.0f;
+    for (int p = lane; p < n; p += 64) {
+      const float w = expf(sc[j][p] - m);
+      sc[j][p] = w;
+      l += w;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      mstat[j] = m;
+      lstat[j] = l;
+    }
+  }
+  __syncthreads();
+
+  // weighted sum of values
+  float acc[G][8];
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
+  for (int base = 0; base < n; base += 64) {
+    u32x4 vraw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = base + u * 16 + wid * 4 + r;
+      vraw[u] = (p < n) ? load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = base + u * 16 + wid * 4 + r;
+      if (p < n) {
+        float vf[8];
+        if (FUSED && c0 + p == qpos) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+        } else {
+          f16x8_to_f32(vraw[u], vf);
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const float w = sc[j][p];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = acc[j][i];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      acc[j][i] = v;
+    }
+  if (r == 0) {
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red[wid][j][sub * 8 + i] = acc[j][i];
+  }
+  __syncthreads();
+
+  if (nact == 1) {
+    for (int idx = tid; idx < G * HD; idx += 256) {
+      const int j = idx / HD, i = idx % HD;
+      const float o = red[0][j][i] + red[1][j][i] + red[2][j][i] + red[3][j][i];
+      a.out[static_cast<size_t>(b) * a.ld_out + (g * G + j) * HD + i] = o / lstat[j];
+    }
+    return;
+  }
+  // several chunks: write (o, m, l) partials; the last chunk block to arrive combines them
+  const int stride = HD + 2;
+  for (int idx = tid; idx < G * HD; idx += 256) {
+    const int j = idx / HD, i = idx % HD;
+    const float o = red[0][j][i] + red[1][j][i] + red[2][j][i] + red[3][j][i];
+    float* p = a.part + ((static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split + s) * stride;
+    p[i] = o;
+    if (i == 0) {
+      p[HD] = mstat[j];
+      p[HD + 1] = lstat[j];
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int done = atomicAdd(a.counters + b * a.nkv + g, 1);
+    last = (done == nact - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int idx = tid; idx < G * HD; idx += 256) {
+    const int j = idx / HD, i = idx % HD;
+    const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split * stride;
+    float M = -INFINITY;
+    for (int t = 0; t < nact; ++t) M = fmaxf(M, ld_dev(p0 + t * stride + HD));
+    float L = 0.0f, O = 0.0f;
+    for (int t = 0; t < nact; ++t) {
+      const float e = expf(ld_dev(p0 + t * stride + HD) - M);
+      L += ld_dev(p0 + t * stride + HD + 1) * e;
+      O += ld_dev(p0 + t * stride + i) * e;
+    }
+    a.out[static_cast<size_t>(b) * a.ld_out + (g * G + j) * HD + i] = O / L;
+  }
+  if (tid == 0) a.counters[b * a.nkv + g] = 0;
+}
+
+// grid = (T, nq + nkv), block = 64: one wave per (row, head). q heads -> q_out; k heads -> cache (and v copy).
+__global__ __launch_bounds__(64) void k_qk_norm_rope_append(QkNormRopeArgs a) {
+  const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int pos = a.pos_base + t;
+  const float* row = a.qkv + static_cast<size_t>(t) * a.ld_qkv;
+  const float* cr = a.rope_cos + static_cast<size_t>(pos) * (HD / 2);
+  const float* sr = a.rope_sin + static_cast<size_t>(pos) * (HD / 2);
+  if (h < a.nq) {
+    float x0 = row[h * HD + lane], x1 = row[h * HD + lane + 64];
+    norm_rope_pair(x0, x1, a.q_gain, a.eps, cr, sr, lane);
+    float* dst = a.q_out + static_cast<size_t>(t) * a.nq * HD + h * HD;
+    dst[lane] = x0;
+    dst[lane + 64] = x1;
+  } else {
+    const int g = h - a.nq;
+    const float* ks = row + a.nq * HD + g * HD;
+    const float* vs = row + (a.nq + a.nkv) * HD + g * HD;
+    float x0 = ks[lane], x1 = ks[lane + 64];
+    norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
+    const size_t base = static_cast<size_t>(a.slot) * a.slot_stride + static_cast<size_t>(a.layer) * a.layer_stride +
+                        static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(pos) * HD;
+    a.kcache[base + lane] = static_cast<f16>(x0);
+    a.kcache[base + lane + 64] = static_cast<f16>(x1);
+    a.vcache[base + lane] = static_cast<f16>(vs[lane]);
+    a.vcache[base + lane + 64] = static_cast<f16>(vs[lane + 64]);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_embed(const int32_t* ids, const f16* table, int H, float* x) {
+  const int t = blockIdx.x;
+  const f16* src = table + static_cast<size_t>(ids[t]) * H;
+  for (int i = threadIdx.x; i < H; i += 256) x[static_cast<size_t>(t) * H + i] = static_cast<float>(src[i]);
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, int H, const f16* gain, float eps, float* yf,
+                                                      f16* yh) {
+  __shared__ float red[4];
+  const float* xr = x + static_cast<size_t>(blockIdx.x) * H;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) ss += xr[i] * xr[i];
+  ss = block_sum<256>(ss, red);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float y = xr[i] * scale * static_cast<float>(gain[i]);
+    if (yf) yf[static_cast<size_t>(blockIdx.x) * H + i] = y;
+    if (yh) yh[static_cast<size_t>(blockIdx.x) * H + i] = static_cast<f16>(y);
+  }
+}
+
+hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s) {
+  const int G = a.nq / a.nkv;
+  if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;
+  const dim3 grid(a.max_split, a.nkv, a.B), block(256);
+#define SOC_ATTN_CASE(GG)                                                                  \
+  if (G == GG) {                                                                          \
+    if (fused) hipLaunchKernelGGL((k_attention<GG, true>), grid, block, 0, s, a);          \
+    else hipLaunchKernelGGL((k_attention<GG, false>), grid, block, 0, s, a);               \
+    return hipGetLastError();                                                             \
+  }
+  SOC_ATTN_CASE(1)
+  SOC_ATTN_CASE(2)
+  SOC_ATTN_CASE(4)
+  SOC_ATTN_CASE(8)
+#undef SOC_ATTN_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_qk_norm_rope_append, dim3(a.T, a.nq + a.nkv), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, float* x, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(T), dim3(256), 0, s, ids, table, H, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const f16* gain, float eps, float* yf, f16* yh,
+                               hipStream_t s) {
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, H, gain, eps, yf, yh);
+  return hipGetLastError();
+}
+
+}  // namespace soc

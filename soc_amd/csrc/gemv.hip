@@ -1,0 +1,365 @@
+// gemv.hip - decode-time weight GEMVs (batch 1) with fused RMSNorm prologue and epilogues, the LM head with a
+// fused greedy argmax, and the group-quantized (int8 / int4, fp16 scale per 64 inputs) GEMV.
+//
+// Reference computation: Linear::Forward (Mac/cpu/src/linear.cpp:51-84): y[o] = sum_i x[i] * float(W[o][i]),
+// accumulated in fp32. Weights stay fp16 in HBM (row-major [out][in], the Hugging Face layout) and are streamed
+// with 16-byte nontemporal loads; each wave owns R output rows and reduces its 64 partial sums with shuffles.
+#include "kernels.h"
+
+namespace soc {
+
+namespace {
+
+// Loads x (fp32 [K]) into LDS, optionally applying RMSNorm with an fp16 gain exactly in the reference's order:
+// ms = sum(x^2) / K; scale = 1 / sqrt(ms + eps); y = x * scale * gain (Mac/cpu/src/rms_norm_module.cpp:56-64).
+template <int NT>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, const f16* __restrict__ xh,
+                                        const f16* __restrict__ gain, float eps, int K, float* xs, float* red) {
+  float ss = 0.0f;
+  for (int i = threadIdx.x * 4; i < K; i += NT * 4) {
+    f32x4 v;
+    if (xh != nullptr) {
+      const f16x4 h = *reinterpret_cast<const f16x4*>(xh + i);
+      v = f32x4{static_cast<float>(h.x), static_cast<float>(h.y), static_cast<float>(h.z), static_cast<float>(h.w)};
+    } else {
+      v = *reinterpret_cast<const f32x4*>(x + i);
+    }
+    *reinterpret_cast<f32x4*>(xs + i) = v;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  if (gain != nullptr) {
+    ss = block_sum<NT>(ss, red);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(K) + eps);
+    for (int i = threadIdx.x; i < K; i += NT) xs[i] = xs[i] * scale * static_cast<float>(gain[i]);
+  }
+  __syncthreads();
+}
+
+// Dot products of R consecutive rows (starting at row0) with xs; U 512-wide chunks of K are loaded per iteration.
+template <int R, int U>
+__device__ __forceinline__ void rows_dot(const f16* __restrict__ W, int row0, int N, int K, const float* xs, float* acc) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int k0 = lane * 8; k0 < K; k0 += 512 * U) {
+    u32x4 w[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, N - 1);
+        const int k = k0 + u * 512;
+        w[u][r] = k < K ? load_stream16(W + static_cast<size_t>(row) * K + k) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + u * 512;
+      if (k < K) {
+        float xv[8];
+        *reinterpret_cast<f32x4*>(xv) = *reinterpret_cast<const f32x4*>(xs + k);
+        *reinterpret_cast<f32x4*>(xv + 4) = *reinterpret_cast<const f32x4*>(xs + k + 4);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float wf[8];
+          f16x8_to_f32(w[u][r], wf);
+          float a = acc[r];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a += xv[i] * wf[i];
+          acc[r] = a;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+}
+
+}  // namespace
+
+// y = epilogue(W . norm(x)). EPI_STORE: y[n] = acc. EPI_RESIDUAL: y[n] = y[n] + acc (in place on the residual
+// stream, Mac/cpu/src/qwen_block.cpp:70-72). EPI_SWIGLU: y[n] = silu(W.x) * (W2.x) (qwen_mlp.cpp:69-72).
+template <int R, int U, int EPI>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[4];
+  stage_x<256>(a.x, a.xh, a.gain, a.eps, a.K, xs, red);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nwaves = gridDim.x * 4;
+  for (int row0 = wave * R; row0 < a.N; row0 += nwaves * R) {
+    float acc[R];
+    rows_dot<R, U>(a.w, row0, a.N, a.K, xs, acc);
+    if constexpr (EPI == EPI_SWIGLU) {
+      float acc2[R];
+      rows_dot<R, U>(a.w2, row0, a.N, a.K, xs, acc2);
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = silu_ref(acc[r]) * acc2[r];
+    }
+    if (lane < R && row0 + lane < a.N) {
+      float v = acc[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r)
+        if (lane == r) v = acc[r];
+      float* dst = a.y + row0 + lane;
+      if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+      *dst = v;
+    }
+  }
+}
+
+// Tied / untied LM head for one row with the final RMSNorm as prologue, optional fp32 logits, and a greedy argmax
+// with the reference sampler's tie rule (lowest index among equal maxima, Mac/cpu/src/sampler.cpp:42-55).
+// The last block to finish reduces the per-block winners, writes the token and advances the decode state.
+template <int R, int U>
+__global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float red[4];
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  __shared__ int last;
+  stage_x<256>(a.x, nullptr, a.gain, a.eps, a.K, xs, red);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x >> 6;
+  const int wave = blockIdx.x * 4 + wid;
+  const int nwaves = gridDim.x * 4;
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  for (int row0 = wave * R; row0 < a.N; row0 += nwaves * R) {
+    float acc[R];
+    rows_dot<R, U>(a.w, row0, a.N, a.K, xs, acc);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = row0 + r;
+      if (row < a.N) {
+        if (acc[r] > best) {  // rows are visited in increasing order within a wave: strict > keeps the lowest index
+          best = acc[r];
+          best_i = row;
+        }
+      }
+    }
+    if (a.logits != nullptr && lane < R && row0 + lane < a.N) {
+      float v = acc[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r)
+        if (lane == r) v = acc[r];
+      a.logits[row0 + lane] = v;
+    }
+  }
+  // wave winners are uniform across lanes; reduce over the 4 waves, then over blocks
+  if (lane == 0) {
+    bv[wid] = best;
+    bi[wid] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = bv[0];
+    int i = bi[0];
+    for (int w = 1; w < 4; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < i)) {
+        v = bv[w];
+        i = bi[w];
+      }
+    a.part_val[blockIdx.x] = v;
+    a.part_idx[blockIdx.x] = i;
+    __threadfence();
+    const int done = atomicAdd(a.counter, 1);
+    last = (done == static_cast<int>(gridDim.x) - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) {
+    const float pv = __hip_atomic_load(a.part_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int pi = __hip_atomic_load(a.part_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (pv > v || (pv == v && pi < i)) {
+      v = pv;
+      i = pi;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(i, off, kWave);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  if (lane == 0) {
+    bv[wid] = v;
+    bi[wid] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
+        bv[0] = bv[w];
+        bi[0] = bi[w];
+      }
+    const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
+    if (a.token_out != nullptr) a.token_out[0] = tok;
+    if (a.state != nullptr) {
+      a.state[0] = tok;      // next input token
+      a.state[1] += 1;       // next position
+    }
+    if (a.ring != nullptr) a.ring[a.ring_pos != nullptr ? a.ring_pos[0] : 0] = tok;
+    if (a.ring_pos != nullptr) a.ring_pos[0] += 1;
+    *a.counter = 0;
+  }
+}
+
+// Group-quantized GEMV/skinny GEMM: y[m][n] = sum_k x[m][k] * (float(code[n][k]) * float(scale[n][k/64])).
+// BITS = 8: codes int8 [N][K]; BITS = 4: two's complement nibbles, even k in the low nibble, [N][K/2].
+// Each lane covers 16 consecutive k (one fp16 scale group spans 4 lanes); M <= 8 activation rows are staged in LDS.
+template <int BITS, int M>
+__global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
+  extern __shared__ float xs[];  // [M][K]
+  for (int m = 0; m < M; ++m)
+    for (int i = threadIdx.x; i < a.K; i += 256) xs[m * a.K + i] = static_cast<float>(a.x[static_cast<size_t>(m) * a.K + i]);
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nwaves = gridDim.x * 4;
+  constexpr int R = 2;
+  const int G = a.K / 64;
+  for (int row0 = wave * R; row0 < a.N; row0 += nwaves * R) {
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+    for (int k0 = lane * 16; k0 < a.K; k0 += 1024) {
+      float wf[R][16];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, a.N - 1);
+        const float sc = static_cast<float>(a.scales[static_cast<size_t>(row) * G + k0 / 64]);
+        if constexpr (BITS == 8) {
+          const u32x4 c = load_stream16(static_cast<const int8_t*>(a.codes) + static_cast<size_t>(row) * a.K + k0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              wf[r][j * 4 + b] = static_cast<float>(static_cast<int8_t>((c[j] >> (8 * b)) & 0xff)) * sc;
+        } else {
+          const uint2 c = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.codes) +
+                                                           static_cast<size_t>(row) * (a.K / 2) + k0 / 2);
+          const uint32_t words[2] = {c.x, c.y};
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+              const int32_t nib = static_cast<int32_t>((words[j] >> (4 * b)) & 0xf);
+              wf[r][j * 8 + b] = static_cast<float>(nib >= 8 ? nib - 16 : nib) * sc;
+            }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float xv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+          *reinterpret_cast<f32x4*>(xv + i) = *reinterpret_cast<const f32x4*>(xs + m * a.K + k0 + i);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float s = acc[r][m];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s += xv[i] * wf[r][i];
+          acc[r][m] = s;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = wave_sum(acc[r][m]);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < a.N)
+#pragma unroll
+          for (int m = 0; m < M; ++m) a.y[static_cast<size_t>(m) * a.N + row0 + r] = acc[r][m];
+    }
+  }
+}
+
+// Dequantize codes to fp32 [N][K] (the bit-exact dequant contract, checked element for element).
+template <int BITS>
+__global__ void k_dequant(const void* codes, const f16* scales, int N, int K, float* w) {
+  const size_t total = static_cast<size_t>(N) * K;
+  for (size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int n = static_cast<int>(idx / K), k = static_cast<int>(idx % K);
+    int32_t c;
+    if constexpr (BITS == 8) {
+      c = static_cast<const int8_t*>(codes)[idx];
+    } else {
+      const uint8_t byte = static_cast<const uint8_t*>(codes)[static_cast<size_t>(n) * (K / 2) + k / 2];
+      const int32_t nib = (k & 1) ? (byte >> 4) : (byte & 0xf);
+      c = nib >= 8 ? nib - 16 : nib;
+    }
+    w[idx] = static_cast<float>(c) * static_cast<float>(scales[static_cast<size_t>(n) * (K / 64) + k / 64]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Launchers
+// ------------------------------------------------------------------------------------------------------------
+static int gemv_grid(int N, int R) {
+  const int groups = (N + R - 1) / R;
+  int blocks = (groups + 3) / 4;
+  return blocks < 1024 ? (blocks < 1 ? 1 : blocks) : 1024;
+}
+
+hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s) {
+  constexpr int R = 4, U = 2;
+  const size_t lds = static_cast<size_t>(a.K) * sizeof(float);
+  const dim3 grid(gemv_grid(a.N, R)), block(256);
+  switch (epi) {
+    case EPI_STORE: hipLaunchKernelGGL((k_gemv<R, U, EPI_STORE>), grid, block, lds, s, a); break;
+    case EPI_RESIDUAL: hipLaunchKernelGGL((k_gemv<R, U, EPI_RESIDUAL>), grid, block, lds, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemv<2, U, EPI_SWIGLU>), dim3(gemv_grid(a.N, 2)), block, lds, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int lm_head_blocks(int N) { return gemv_grid(N, 4) < 512 ? gemv_grid(N, 4) : 512; }
+
+hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(a.K) * sizeof(float);
+  hipLaunchKernelGGL((k_lm_head_argmax<4, 2>), dim3(lm_head_blocks(a.N)), dim3(256), lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
+  const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(float);
+  const dim3 grid(gemv_grid(a.N, 2)), block(256);
+#define SOC_QMM_CASE(B, MM)                                                        \
+  if (bits == B && a.M == MM) {                                                   \
+    hipLaunchKernelGGL((k_qmm<B, MM>), grid, block, lds, s, a);                    \
+    return hipGetLastError();                                                     \
+  }
+  SOC_QMM_CASE(8, 1)
+  SOC_QMM_CASE(8, 2)
+  SOC_QMM_CASE(8, 4)
+  SOC_QMM_CASE(8, 8)
+  SOC_QMM_CASE(4, 1)
+  SOC_QMM_CASE(4, 2)
+  SOC_QMM_CASE(4, 4)
+  SOC_QMM_CASE(4, 8)
+#undef SOC_QMM_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dequant(const void* codes, int bits, const f16* scales, int N, int K, float* w, hipStream_t s) {
+  const dim3 grid(1024), block(256);
+  if (bits == 8) hipLaunchKernelGGL((k_dequant<8>), grid, block, 0, s, codes, scales, N, K, w);
+  else if (bits == 4) hipLaunchKernelGGL((k_dequant<4>), grid, block, 0, s, codes, scales, N, K, w);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace soc

@@ -1,0 +1,118 @@
+// kernels.h - argument blocks and launchers of the HIP kernels (all launched on the caller's stream).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device_common.h"
+
+namespace soc {
+
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+
+// ---- decode GEMV (batch 1) ----
+struct GemvArgs {
+  const float* x;    // [K] fp32 activations (or nullptr when xh is given)
+  const f16* xh;     // [K] fp16 activations (op-level entry point)
+  const f16* gain;   // RMSNorm gain [K] or nullptr (no normalisation)
+  float eps;
+  const f16* w;      // [N][K]
+  const f16* w2;     // EPI_SWIGLU: up-projection rows [N][K]
+  float* y;          // [N]
+  int N, K;
+};
+hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s);
+
+struct LmHeadArgs {
+  const float* x;     // [K] residual stream (pre final norm)
+  const f16* gain;    // final norm gain [K]
+  float eps;
+  const f16* w;       // [N][K] embedding table (tied) or lm_head
+  float* logits;      // [N] or nullptr
+  float* part_val;    // [blocks]
+  int* part_idx;      // [blocks]
+  int* counter;       // zero-initialised; the last block resets it
+  int* token_out;     // nullable: argmax token
+  int* state;         // nullable: {token, pos} decode state; token <- argmax, pos += 1
+  int* ring;          // nullable: ring[ring_pos[0]] = token
+  int* ring_pos;      // nullable
+  int N, K;
+};
+int lm_head_blocks(int N);
+hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t s);
+
+struct QmmArgs {
+  const f16* x;        // [M][K] fp16 activations
+  const void* codes;   // int8 [N][K] or packed int4 [N][K/2]
+  const f16* scales;   // [N][K/64]
+  float* y;            // [M][N]
+  int M, N, K;
+};
+hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s);
+hipError_t launch_dequant(const void* codes, int bits, const f16* scales, int N, int K, float* w, hipStream_t s);
+
+// ---- attention ----
+struct AttnArgs {
+  const float* qkv;      // fused mode: raw projections [B][ld_qkv] (q | k | v); else normed+roped q [B][ld_qkv]
+  int ld_qkv;
+  const f16* q_gain;     // [d] (fused mode)
+  const f16* k_gain;     // [d] (fused mode)
+  float eps;
+  const float* rope_cos; // [max_pos][d/2]
+  const float* rope_sin;
+  f16* kcache;           // layer-0 base of slot 0; element (slot, layer, head, pos, i) at
+  f16* vcache;           //   slot*slot_stride + layer*layer_stride + head*cap*d + pos*d + i
+  long long slot_stride, layer_stride;
+  int layer, cap;
+  const int32_t* pos;    // [B] query position (== number of earlier keys)
+  const int32_t* slot;   // [B] KV slot of each row, nullptr = slot_base for every row
+  int slot_base;
+  int pos_base;          // added to pos[] (prefill rows use pos = nullptr and pos_base + row)
+  float* out;            // [B][nq*d]
+  int ld_out;
+  float* part;           // split partials [B][nq][max_split][d + 2]
+  int* counters;         // [B][nkv] zero-initialised
+  int B, nq, nkv, max_split, chunk;
+  float scale;
+};
+// fused = 1: q/k norm + RoPE + KV append of the new token are done inside (decode).
+hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s);
+
+// q/k RMSNorm over each head + RoPE + KV-cache append for T new rows at positions pos_base + t (prefill).
+struct QkNormRopeArgs {
+  const float* qkv;      // [T][ld_qkv] raw projections
+  int ld_qkv;
+  const f16* q_gain;
+  const f16* k_gain;
+  float eps;
+  const float* rope_cos;
+  const float* rope_sin;
+  float* q_out;          // [T][nq*d]
+  f16* kcache;
+  f16* vcache;
+  long long slot_stride, layer_stride;
+  int slot, layer, cap, pos_base;
+  int T, nq, nkv;
+};
+hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s);
+
+// ---- prefill helpers ----
+// x[t][:] = float(table[ids[t]][:]) for t < T (Mac/cpu/src/embedding.cpp:51-77).
+hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, float* x, hipStream_t s);
+// y[t] = RMSNorm(x[t]) with an fp16 gain; y may be fp32 (yf) or fp16 (yh), whichever is non-null.
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const f16* gain, float eps, float* yf, f16* yh,
+                               hipStream_t s);
+
+// C[M][N] (epilogue) = A[M][K] . W[N][K]^T, fp32 activations, fp16 weights, fp32 accumulation.
+struct GemmArgs {
+  const float* a;   // [M][lda]
+  int lda;
+  const f16* w;     // [N][K]
+  const f16* w2;    // EPI_SWIGLU up rows
+  float* c;         // [M][ldc]
+  int ldc;
+  int M, N, K;
+};
+hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
+
+}  // namespace soc

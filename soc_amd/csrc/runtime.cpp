@@ -1,0 +1,1021 @@
+// runtime.cpp - host side of the C ABI: device context, weight placement and upload, fp16 KV cache, prefill and
+// decode orchestration (decode steps replay one captured HIP graph; the sampled token and the position live in
+// device memory so that consecutive steps need no host round trip).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "soc_hip.h"
+#include "status.h"
+
+using soc::f16;
+
+// ------------------------------------------------------------------------------------------------------------
+// errors
+// ------------------------------------------------------------------------------------------------------------
+namespace soc {
+static thread_local std::string g_last_error;
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+void clear_error() { g_last_error.clear(); }
+}  // namespace soc
+
+#define SOC_API_BEGIN try {
+#define SOC_API_END                                                         \
+  }                                                                         \
+  catch (const std::bad_alloc&) {                                           \
+    return soc::fail(SOC_ERR_NOMEM, "host allocation failed");              \
+  }                                                                         \
+  catch (const std::exception& e) {                                         \
+    return soc::fail(SOC_ERR_INVALID, e.what());                            \
+  }
+
+// ------------------------------------------------------------------------------------------------------------
+// objects
+// ------------------------------------------------------------------------------------------------------------
+struct soc_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  bool timing = false;
+};
+
+namespace {
+
+struct DevLayer {
+  f16 *in_norm, *post_norm, *q_norm, *k_norm, *wqkv, *wo, *wgate, *wup, *wdown;
+};
+
+struct TensorSlot {
+  f16* ptr;
+  int64_t numel;
+  bool loaded;
+};
+
+// Device scratch of one forward kind; pointers stay fixed once allocated (captured graphs refer to them).
+struct DecodeWs {
+  bool ready = false;
+  float *x = nullptr, *qkv = nullptr, *attn = nullptr, *h = nullptr, *logits = nullptr, *part = nullptr,
+        *lm_val = nullptr;
+  int *lm_idx = nullptr, *lm_counter = nullptr, *attn_counters = nullptr, *state = nullptr, *ring = nullptr,
+      *ring_pos = nullptr;
+  int max_split = 0, ring_cap = 0;
+  std::vector<void*> allocs;
+};
+
+struct PrefillWs {
+  int cap_rows = 0, cap_split = 0;
+  float *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr,
+        *logits = nullptr, *part = nullptr, *lm_val = nullptr;
+  int *ids = nullptr, *attn_counters = nullptr, *lm_idx = nullptr, *lm_counter = nullptr, *token = nullptr;
+  int cap_logit_rows = 0;
+  std::vector<void*> allocs;
+};
+
+constexpr int kAttnChunk = 256;
+
+}  // namespace
+
+struct soc_model {
+  soc_ctx* ctx = nullptr;
+  soc_qwen_config cfg{};
+  int qd = 0, kvd = 0, qkv_rows = 0;
+  char* wbuf = nullptr;
+  size_t wbytes = 0;
+  f16 *embed = nullptr, *final_norm = nullptr, *lm_head = nullptr;
+  std::vector<DevLayer> layers;
+  std::map<std::string, TensorSlot> tensors;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  int rope_len = 0;
+  DecodeWs dws;
+  int dws_gen = 0;  // bumped whenever the decode scratch is reallocated (captured graphs refer to it)
+  PrefillWs pws;
+  bool finalized = false;
+};
+
+struct soc_kv {
+  soc_model* model = nullptr;
+  int slots = 0, cap = 0;
+  f16 *k = nullptr, *v = nullptr;
+  long long slot_stride = 0, layer_stride = 0;
+  std::vector<int32_t> len;
+  std::map<int, std::pair<int, hipGraphExec_t>> graphs;  // decode graph per slot, tagged with the scratch generation
+};
+
+namespace {
+
+int hip_fail(hipError_t e, const char* what) {
+  return soc::fail(SOC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int dev_alloc(std::vector<void*>& owner, size_t bytes, void** p) {
+  hipError_t e = hipMalloc(p, bytes == 0 ? 256 : bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return soc::fail(SOC_ERR_NOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  }
+  owner.push_back(*p);
+  return SOC_OK;
+}
+
+template <typename T>
+int dev_alloc_t(std::vector<void*>& owner, size_t count, T** p) {
+  return dev_alloc(owner, count * sizeof(T), reinterpret_cast<void**>(p));
+}
+
+void free_all(std::vector<void*>& v) {
+  for (void* p : v) (void)hipFree(p);
+  v.clear();
+}
+
+bool env_flag(const char* name) {
+  const char* v = std::getenv(name);
+  return v != nullptr && v[0] != '\0' && v[0] != '0';
+}
+
+int check_config(const soc_qwen_config& c) {
+  if (c.vocab_size <= 0 || c.hidden_size <= 0 || c.num_hidden_layers <= 0 || c.num_attention_heads <= 0 ||
+      c.num_key_value_heads <= 0 || c.intermediate_size <= 0 || c.max_position_embeddings <= 0)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: sizes must be positive");
+  if (c.head_dim != 128) return soc::fail(SOC_ERR_INVALID, "qwen config: head_dim must be 128");
+  if (c.num_attention_heads % c.num_key_value_heads != 0)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: num_attention_heads must be divisible by num_key_value_heads");
+  const int G = c.num_attention_heads / c.num_key_value_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: query heads per KV head must be 1, 2, 4 or 8");
+  if (c.hidden_size % 8 != 0 || c.intermediate_size % 8 != 0)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: hidden and intermediate sizes must be multiples of 8");
+  if (!(c.rms_norm_eps > 0.0f) || !(c.rope_theta > 0.0))
+    return soc::fail(SOC_ERR_INVALID, "qwen config: eps and rope_theta must be positive");
+  if (static_cast<size_t>(c.hidden_size) * 4 > 64 * 1024 || static_cast<size_t>(c.intermediate_size) * 4 > 64 * 1024)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: hidden/intermediate size too large for the decode kernels");
+  return SOC_OK;
+}
+
+int ensure_decode_ws(soc_model* m, int cap) {
+  DecodeWs& w = m->dws;
+  const int need_split = (cap + kAttnChunk - 1) / kAttnChunk;
+  if (w.ready && w.max_split >= need_split && w.ring_cap >= cap) return SOC_OK;
+  hipError_t se = hipStreamSynchronize(m->ctx->stream);
+  if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
+  free_all(w.allocs);
+  w = DecodeWs();
+  ++m->dws_gen;
+  const soc_qwen_config& c = m->cfg;
+  w.max_split = need_split;
+  w.ring_cap = cap;
+  SOC_TRY(dev_alloc_t(w.allocs, c.hidden_size, &w.x));
+  SOC_TRY(dev_alloc_t(w.allocs, m->qkv_rows, &w.qkv));
+  SOC_TRY(dev_alloc_t(w.allocs, m->qd, &w.attn));
+  SOC_TRY(dev_alloc_t(w.allocs, c.intermediate_size, &w.h));
+  SOC_TRY(dev_alloc_t(w.allocs, c.vocab_size, &w.logits));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(c.num_attention_heads) * w.max_split * (128 + 2), &w.part));
+  SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_val));
+  SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_idx));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.lm_counter));
+  SOC_TRY(dev_alloc_t(w.allocs, c.num_key_value_heads, &w.attn_counters));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.state));
+  SOC_TRY(dev_alloc_t(w.allocs, cap, &w.ring));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.ring_pos));
+  hipError_t e;
+  if ((e = hipMemset(w.lm_counter, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.attn_counters, 0, c.num_key_value_heads * sizeof(int))) != hipSuccess)
+    return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.state, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.ring_pos, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  w.ready = true;
+  return SOC_OK;
+}
+
+int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
+  PrefillWs& w = m->pws;
+  const int need_split = (total_len + kAttnChunk - 1) / kAttnChunk;
+  if (w.cap_rows >= rows && w.cap_split >= need_split && w.cap_logit_rows >= logit_rows) return SOC_OK;
+  hipError_t e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  free_all(w.allocs);
+  const int R = std::max(rows, w.cap_rows), SP = std::max(need_split, w.cap_split),
+            LR = std::max(std::max(logit_rows, 1), w.cap_logit_rows);
+  w = PrefillWs();
+  const soc_qwen_config& c = m->cfg;
+  const size_t H = c.hidden_size;
+  SOC_TRY(dev_alloc_t(w.allocs, R * H, &w.x));
+  SOC_TRY(dev_alloc_t(w.allocs, R * H, &w.xn));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * m->qkv_rows, &w.qkv));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * m->qd, &w.q));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * m->qd, &w.attn));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.intermediate_size, &w.h));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(LR) * c.vocab_size, &w.logits));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.num_attention_heads * SP * (128 + 2), &w.part));
+  SOC_TRY(dev_alloc_t(w.allocs, R, &w.ids));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.num_key_value_heads, &w.attn_counters));
+  SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_val));
+  SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_idx));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.lm_counter));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.token));
+  if ((e = hipMemset(w.attn_counters, 0, static_cast<size_t>(R) * c.num_key_value_heads * sizeof(int))) != hipSuccess)
+    return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.lm_counter, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  w.cap_rows = R;
+  w.cap_split = SP;
+  w.cap_logit_rows = LR;
+  return SOC_OK;
+}
+
+// RoPE table: angle = pos / theta^(2i/d) in double, cos/sin rounded to float (Mac/cpu/src/rope.cpp:72-79).
+int build_rope_table(soc_model* m, int len) {
+  const int half = m->cfg.head_dim / 2;
+  std::vector<float> c(static_cast<size_t>(len) * half), s(c.size());
+  for (int p = 0; p < len; ++p) {
+    const double abs_pos = static_cast<double>(p);
+    for (int i = 0; i < half; ++i) {
+      const double exponent = static_cast<double>(i * 2) / static_cast<double>(m->cfg.head_dim);
+      const double angle = abs_pos / std::pow(m->cfg.rope_theta, exponent);
+      c[static_cast<size_t>(p) * half + i] = static_cast<float>(std::cos(angle));
+      s[static_cast<size_t>(p) * half + i] = static_cast<float>(std::sin(angle));
+    }
+  }
+  hipError_t e;
+  if ((e = hipMalloc(&m->rope_cos, c.size() * 4)) != hipSuccess) return hip_fail(e, "hipMalloc rope");
+  if ((e = hipMalloc(&m->rope_sin, s.size() * 4)) != hipSuccess) return hip_fail(e, "hipMalloc rope");
+  if ((e = hipMemcpy(m->rope_cos, c.data(), c.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy rope");
+  if ((e = hipMemcpy(m->rope_sin, s.data(), s.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy rope");
+  m->rope_len = len;
+  return SOC_OK;
+}
+
+soc::AttnArgs attn_args(soc_model* m, soc_kv* kv, int layer) {
+  soc::AttnArgs a{};
+  a.q_gain = m->layers[layer].q_norm;
+  a.k_gain = m->layers[layer].k_norm;
+  a.eps = m->cfg.rms_norm_eps;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.kcache = kv->k;
+  a.vcache = kv->v;
+  a.slot_stride = kv->slot_stride;
+  a.layer_stride = kv->layer_stride;
+  a.layer = layer;
+  a.cap = kv->cap;
+  a.nq = m->cfg.num_attention_heads;
+  a.nkv = m->cfg.num_key_value_heads;
+  a.chunk = kAttnChunk;
+  a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));  // grouped_query_attention.cpp:81
+  return a;
+}
+
+// Queues one decode step for `slot` reading {token, pos} from dws.state. Used eagerly and under graph capture.
+int enqueue_decode(soc_model* m, soc_kv* kv, int slot, const int32_t* d_slot) {
+  const soc_qwen_config& c = m->cfg;
+  DecodeWs& w = m->dws;
+  hipStream_t s = m->ctx->stream;
+  hipError_t e;
+  if ((e = soc::launch_embed(w.state, 1, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const DevLayer& L = m->layers[l];
+    soc::GemvArgs g{};
+    g.x = w.x;
+    g.gain = L.in_norm;
+    g.eps = c.rms_norm_eps;
+    g.w = L.wqkv;
+    g.y = w.qkv;
+    g.N = m->qkv_rows;
+    g.K = c.hidden_size;
+    if ((e = soc::launch_gemv(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemv qkv");
+    soc::AttnArgs a = attn_args(m, kv, l);
+    a.qkv = w.qkv;
+    a.ld_qkv = m->qkv_rows;
+    a.pos = w.state + 1;
+    a.slot = d_slot;
+    a.slot_base = slot;
+    a.pos_base = 0;
+    a.out = w.attn;
+    a.ld_out = m->qd;
+    a.part = w.part;
+    a.counters = w.attn_counters;
+    a.B = 1;
+    a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+    if ((e = soc::launch_attention(a, 1, s)) != hipSuccess) return hip_fail(e, "attention decode");
+    g = soc::GemvArgs{};
+    g.x = w.attn;
+    g.w = L.wo;
+    g.y = w.x;
+    g.N = c.hidden_size;
+    g.K = m->qd;
+    if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv o");
+    g = soc::GemvArgs{};
+    g.x = w.x;
+    g.gain = L.post_norm;
+    g.eps = c.rms_norm_eps;
+    g.w = L.wgate;
+    g.w2 = L.wup;
+    g.y = w.h;
+    g.N = c.intermediate_size;
+    g.K = c.hidden_size;
+    if ((e = soc::launch_gemv(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemv gate/up");
+    g = soc::GemvArgs{};
+    g.x = w.h;
+    g.w = L.wdown;
+    g.y = w.x;
+    g.N = c.hidden_size;
+    g.K = c.intermediate_size;
+    if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv down");
+  }
+  soc::LmHeadArgs h{};
+  h.x = w.x;
+  h.gain = m->final_norm;
+  h.eps = c.rms_norm_eps;
+  h.w = m->lm_head;
+  h.logits = w.logits;
+  h.part_val = w.lm_val;
+  h.part_idx = w.lm_idx;
+  h.counter = w.lm_counter;
+  h.state = w.state;
+  h.ring = w.ring;
+  h.ring_pos = w.ring_pos;
+  h.N = c.vocab_size;
+  h.K = c.hidden_size;
+  if ((e = soc::launch_lm_head_argmax(h, s)) != hipSuccess) return hip_fail(e, "lm head");
+  return SOC_OK;
+}
+
+int get_decode_graph(soc_model* m, soc_kv* kv, int slot, hipGraphExec_t* out) {
+  auto it = kv->graphs.find(slot);
+  if (it != kv->graphs.end()) {
+    if (it->second.first == m->dws_gen) {
+      *out = it->second.second;
+      return SOC_OK;
+    }
+    (void)hipGraphExecDestroy(it->second.second);
+    kv->graphs.erase(it);
+  }
+  hipStream_t s = m->ctx->stream;
+  hipGraph_t graph;
+  hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+  int rc = enqueue_decode(m, kv, slot, nullptr);
+  e = hipStreamEndCapture(s, &graph);
+  if (rc != SOC_OK) return rc;
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  hipGraphExec_t exec;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  kv->graphs[slot] = std::make_pair(m->dws_gen, exec);
+  *out = exec;
+  return SOC_OK;
+}
+
+int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps) {
+  DecodeWs& w = m->dws;
+  hipStream_t s = m->ctx->stream;
+  const int32_t st[2] = {last, kv->len[slot]};
+  hipError_t e = hipMemcpyAsync(w.state, st, sizeof(st), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync state");
+  const int32_t zero = 0;
+  if ((e = hipMemcpyAsync(w.ring_pos, &zero, sizeof(zero), hipMemcpyHostToDevice, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync ring");
+  if (env_flag("SOC_EAGER")) {
+    for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_decode(m, kv, slot, nullptr));
+  } else {
+    hipGraphExec_t g;
+    SOC_TRY(get_decode_graph(m, kv, slot, &g));
+    for (int i = 0; i < steps; ++i)
+      if ((e = hipGraphLaunch(g, s)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+  }
+  return SOC_OK;
+}
+
+int validate_ids(const soc_model* m, const int32_t* ids, int n) {
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= m->cfg.vocab_size)
+      return soc::fail(SOC_ERR_INVALID, "token id out of range");  // embedding.cpp:66-68
+  return SOC_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------------------
+// C ABI
+// ------------------------------------------------------------------------------------------------------------
+extern "C" {
+
+const char* soc_last_error(void) { return soc::g_last_error.c_str(); }
+
+int soc_ctx_create(int device, soc_ctx** out) {
+  SOC_API_BEGIN
+  if (out == nullptr) return soc::fail(SOC_ERR_INVALID, "soc_ctx_create: null output");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device < 0 || device >= count) return soc::fail(SOC_ERR_INVALID, "soc_ctx_create: no such device");
+  if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+  std::unique_ptr<soc_ctx> c(new soc_ctx());
+  c->device = device;
+  if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
+    return hip_fail(e, "hipStreamCreate");
+  if ((e = hipEventCreate(&c->ev0)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+  if ((e = hipEventCreate(&c->ev1)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+  *out = c.release();
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_ctx_destroy(soc_ctx* ctx) {
+  if (ctx == nullptr) return SOC_OK;
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipEventDestroy(ctx->ev0);
+  (void)hipEventDestroy(ctx->ev1);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return SOC_OK;
+}
+
+int soc_ctx_synchronize(soc_ctx* ctx) {
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int soc_ctx_timer_start(soc_ctx* ctx) {
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  hipError_t e = hipEventRecord(ctx->ev0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+  ctx->timing = true;
+  return SOC_OK;
+}
+
+int soc_ctx_timer_stop(soc_ctx* ctx, float* ms) {
+  if (ctx == nullptr || ms == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (!ctx->timing) return soc::fail(SOC_ERR_STATE, "soc_ctx_timer_stop without soc_ctx_timer_start");
+  hipError_t e = hipEventRecord(ctx->ev1, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+  if ((e = hipEventSynchronize(ctx->ev1)) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+  if ((e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1)) != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+  ctx->timing = false;
+  return SOC_OK;
+}
+
+int soc_buffer_alloc(soc_ctx* ctx, size_t bytes, void** p) {
+  if (ctx == nullptr || p == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  hipError_t e = hipMalloc(p, bytes == 0 ? 256 : bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return soc::fail(SOC_ERR_NOMEM, "hipMalloc failed");
+  }
+  return SOC_OK;
+}
+
+int soc_buffer_free(soc_ctx* ctx, void* p) {
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if ((e = hipFree(p)) != hipSuccess) return hip_fail(e, "hipFree");
+  return SOC_OK;
+}
+
+int soc_buffer_write(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (ctx == nullptr || (bytes && (dst == nullptr || src == nullptr))) return soc::fail(SOC_ERR_INVALID, "null argument");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "soc_buffer_write");
+}
+
+int soc_buffer_read(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (ctx == nullptr || (bytes && (dst == nullptr || src == nullptr))) return soc::fail(SOC_ERR_INVALID, "null argument");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "soc_buffer_read");
+}
+
+int soc_model_create(soc_ctx* ctx, const soc_qwen_config* cfg, soc_model** out) {
+  SOC_API_BEGIN
+  if (ctx == nullptr || cfg == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  *out = nullptr;
+  SOC_TRY(check_config(*cfg));
+  std::unique_ptr<soc_model> m(new soc_model());
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  const soc_qwen_config& c = m->cfg;
+  m->qd = c.num_attention_heads * c.head_dim;
+  m->kvd = c.num_key_value_heads * c.head_dim;
+  m->qkv_rows = m->qd + 2 * m->kvd;
+  const int64_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+  // placement: every tensor 256-byte aligned inside one allocation
+  struct Item {
+    std::string name;
+    int64_t numel;
+    f16** dst;
+    int64_t row_offset;  // for q/k/v inside the fused qkv matrix
+  };
+  std::vector<std::pair<std::string, int64_t>> order;
+  size_t off = 0;
+  std::map<std::string, size_t> offsets;
+  auto place = [&](const std::string& name, int64_t numel) {
+    offsets[name] = off;
+    off += (static_cast<size_t>(numel) * 2 + 255) / 256 * 256;
+  };
+  place("model.embed_tokens.weight", V * H);
+  place("model.norm.weight", H);
+  if (!c.tie_word_embeddings) place("lm_head.weight", V * H);
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    place(p + "input_layernorm.weight", H);
+    place(p + "post_attention_layernorm.weight", H);
+    place(p + "self_attn.q_norm.weight", c.head_dim);
+    place(p + "self_attn.k_norm.weight", c.head_dim);
+    place(p + "@qkv", static_cast<int64_t>(m->qkv_rows) * H);
+    place(p + "self_attn.o_proj.weight", H * m->qd);
+    place(p + "mlp.gate_proj.weight", I * H);
+    place(p + "mlp.up_proj.weight", I * H);
+    place(p + "mlp.down_proj.weight", H * I);
+  }
+  m->wbytes = off;
+  hipError_t e = hipMalloc(&m->wbuf, m->wbytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return soc::fail(SOC_ERR_NOMEM, "weight allocation of " + std::to_string(m->wbytes) + " bytes failed");
+  }
+  auto at = [&](const std::string& name) { return reinterpret_cast<f16*>(m->wbuf + offsets.at(name)); };
+  m->embed = at("model.embed_tokens.weight");
+  m->final_norm = at("model.norm.weight");
+  m->lm_head = c.tie_word_embeddings ? m->embed : at("lm_head.weight");
+  m->tensors["model.embed_tokens.weight"] = {m->embed, V * H, false};
+  m->tensors["model.norm.weight"] = {m->final_norm, H, false};
+  if (!c.tie_word_embeddings) m->tensors["lm_head.weight"] = {m->lm_head, V * H, false};
+  m->layers.resize(c.num_hidden_layers);
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    DevLayer& L = m->layers[l];
+    L.in_norm = at(p + "input_layernorm.weight");
+    L.post_norm = at(p + "post_attention_layernorm.weight");
+    L.q_norm = at(p + "self_attn.q_norm.weight");
+    L.k_norm = at(p + "self_attn.k_norm.weight");
+    L.wqkv = at(p + "@qkv");
+    L.wo = at(p + "self_attn.o_proj.weight");
+    L.wgate = at(p + "mlp.gate_proj.weight");
+    L.wup = at(p + "mlp.up_proj.weight");
+    L.wdown = at(p + "mlp.down_proj.weight");
+    m->tensors[p + "input_layernorm.weight"] = {L.in_norm, H, false};
+    m->tensors[p + "post_attention_layernorm.weight"] = {L.post_norm, H, false};
+    m->tensors[p + "self_attn.q_norm.weight"] = {L.q_norm, c.head_dim, false};
+    m->tensors[p + "self_attn.k_norm.weight"] = {L.k_norm, c.head_dim, false};
+    m->tensors[p + "self_attn.q_proj.weight"] = {L.wqkv, static_cast<int64_t>(m->qd) * H, false};
+    m->tensors[p + "self_attn.k_proj.weight"] = {L.wqkv + static_cast<size_t>(m->qd) * H,
+                                                  static_cast<int64_t>(m->kvd) * H, false};
+    m->tensors[p + "self_attn.v_proj.weight"] = {L.wqkv + static_cast<size_t>(m->qd + m->kvd) * H,
+                                                  static_cast<int64_t>(m->kvd) * H, false};
+    m->tensors[p + "self_attn.o_proj.weight"] = {L.wo, H * m->qd, false};
+    m->tensors[p + "mlp.gate_proj.weight"] = {L.wgate, I * H, false};
+    m->tensors[p + "mlp.up_proj.weight"] = {L.wup, I * H, false};
+    m->tensors[p + "mlp.down_proj.weight"] = {L.wdown, H * I, false};
+  }
+  SOC_TRY(build_rope_table(m.get(), c.max_position_embeddings));
+  *out = m.release();
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_model_destroy(soc_model* m) {
+  if (m == nullptr) return SOC_OK;
+  (void)hipStreamSynchronize(m->ctx->stream);
+  free_all(m->dws.allocs);
+  free_all(m->pws.allocs);
+  (void)hipFree(m->wbuf);
+  (void)hipFree(m->rope_cos);
+  (void)hipFree(m->rope_sin);
+  delete m;
+  return SOC_OK;
+}
+
+int soc_model_load_tensor(soc_model* m, const char* name, const uint16_t* host, int64_t numel) {
+  SOC_API_BEGIN
+  if (m == nullptr || name == nullptr || host == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  auto it = m->tensors.find(name);
+  if (it == m->tensors.end()) return soc::fail(SOC_ERR_INVALID, std::string("unknown tensor name: ") + name);
+  if (it->second.numel != numel)
+    return soc::fail(SOC_ERR_INVALID, std::string("tensor ") + name + " has " + std::to_string(numel) +
+                                          " elements, expected " + std::to_string(it->second.numel));
+  hipError_t e = hipMemcpy(it->second.ptr, host, static_cast<size_t>(numel) * 2, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy weight");
+  it->second.loaded = true;
+  m->finalized = false;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_model_synthesize(soc_model* m, uint64_t seed, float sigma) {
+  SOC_API_BEGIN
+  if (m == nullptr) return soc::fail(SOC_ERR_INVALID, "null model");
+  std::vector<uint16_t> buf;
+  for (auto& kv : m->tensors) {
+    const std::string& name = kv.first;
+    buf.resize(static_cast<size_t>(kv.second.numel));
+    const bool gain = name.find("norm.weight") != std::string::npos;
+    if (gain) {
+      std::fill(buf.begin(), buf.end(), static_cast<uint16_t>(0x3c00));  // 1.0
+    } else {
+      SOC_TRY(soc_synth_normal_f16(seed, name.c_str(), sigma, 0, kv.second.numel, buf.data()));
+    }
+    hipError_t e = hipMemcpy(kv.second.ptr, buf.data(), buf.size() * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy weight");
+    kv.second.loaded = true;
+  }
+  m->finalized = false;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_model_finalize(soc_model* m) {
+  if (m == nullptr) return soc::fail(SOC_ERR_INVALID, "null model");
+  for (auto& kv : m->tensors)
+    if (!kv.second.loaded) return soc::fail(SOC_ERR_INVALID, "missing tensor: " + kv.first);
+  m->finalized = true;
+  return SOC_OK;
+}
+
+int soc_model_weight_bytes(const soc_model* m, int64_t* bytes) {
+  if (m == nullptr || bytes == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  int64_t total = 0;
+  for (const auto& kv : m->tensors) total += kv.second.numel * 2;
+  *bytes = total;
+  return SOC_OK;
+}
+
+int soc_kv_create(soc_model* m, int32_t slots, int32_t cap, soc_kv** out) {
+  SOC_API_BEGIN
+  if (m == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (slots <= 0 || cap <= 0) return soc::fail(SOC_ERR_INVALID, "soc_kv_create: slots and capacity must be positive");
+  if (cap > m->rope_len)
+    return soc::fail(SOC_ERR_CAPACITY, "soc_kv_create: capacity exceeds max_position_embeddings");
+  std::unique_ptr<soc_kv> kv(new soc_kv());
+  kv->model = m;
+  kv->slots = slots;
+  kv->cap = cap;
+  const soc_qwen_config& c = m->cfg;
+  kv->layer_stride = static_cast<long long>(c.num_key_value_heads) * cap * c.head_dim;
+  kv->slot_stride = kv->layer_stride * c.num_hidden_layers;
+  const size_t bytes = static_cast<size_t>(kv->slot_stride) * slots * 2;
+  hipError_t e = hipMalloc(&kv->k, bytes);
+  if (e == hipSuccess) e = hipMalloc(&kv->v, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(kv->k);
+    return soc::fail(SOC_ERR_NOMEM, "KV cache allocation of " + std::to_string(2 * bytes) + " bytes failed");
+  }
+  kv->len.assign(slots, 0);
+  *out = kv.release();
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_kv_destroy(soc_kv* kv) {
+  if (kv == nullptr) return SOC_OK;
+  (void)hipStreamSynchronize(kv->model->ctx->stream);
+  for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second.second);
+  (void)hipFree(kv->k);
+  (void)hipFree(kv->v);
+  delete kv;
+  return SOC_OK;
+}
+
+int soc_kv_length(const soc_kv* kv, int32_t slot, int32_t* length) {
+  if (kv == nullptr || length == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  *length = kv->len[slot];
+  return SOC_OK;
+}
+
+int soc_kv_reset(soc_kv* kv, int32_t slot) {
+  if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  kv->len[slot] = 0;
+  return SOC_OK;
+}
+
+int soc_kv_write(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, const float* key, const float* value) {
+  SOC_API_BEGIN
+  if (kv == nullptr || key == nullptr || value == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  const soc_qwen_config& c = kv->model->cfg;
+  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= c.num_hidden_layers || pos < 0 || pos >= kv->cap)
+    return soc::fail(SOC_ERR_INVALID, "soc_kv_write: index out of range");  // kv_cache.cpp:51-53
+  const int d = c.head_dim;
+  std::vector<_Float16> kh(d), vh(d);
+  for (int h = 0; h < c.num_key_value_heads; ++h) {
+    for (int i = 0; i < d; ++i) {
+      kh[i] = static_cast<_Float16>(key[h * d + i]);
+      vh[i] = static_cast<_Float16>(value[h * d + i]);
+    }
+    const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(layer) * kv->layer_stride +
+                       (static_cast<size_t>(h) * kv->cap + pos) * d;
+    hipError_t e = hipMemcpy(kv->k + off, kh.data(), d * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(kv->v + off, vh.data(), d * 2, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy kv");
+  }
+  if (pos + 1 > kv->len[slot]) kv->len[slot] = pos + 1;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t seed) {
+  SOC_API_BEGIN
+  if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
+  if (slot < 0 || slot >= kv->slots || length < 0 || length > kv->cap)
+    return soc::fail(SOC_ERR_INVALID, "soc_kv_fill_synthetic: bad slot or length");
+  const soc_qwen_config& c = kv->model->cfg;
+  const int d = c.head_dim;
+  std::vector<uint16_t> buf(static_cast<size_t>(length) * d);
+  for (int l = 0; l < c.num_hidden_layers; ++l)
+    for (int h = 0; h < c.num_key_value_heads; ++h)
+      for (int which = 0; which < 2; ++which) {
+        const std::string name = "kv." + std::to_string(slot) + "." + std::to_string(l) + "." + std::to_string(h) +
+                                 (which ? ".v" : ".k");
+        SOC_TRY(soc_synth_normal_f16(seed, name.c_str(), 1.0f, 0, static_cast<int64_t>(buf.size()), buf.data()));
+        const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(l) * kv->layer_stride +
+                           static_cast<size_t>(h) * kv->cap * d;
+        hipError_t e = hipMemcpy((which ? kv->v : kv->k) + off, buf.data(), buf.size() * 2, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy kv");
+      }
+  kv->len[slot] = length;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_kv_read(const soc_kv* kv, int32_t slot, int32_t layer, uint16_t* keys, uint16_t* values) {
+  SOC_API_BEGIN
+  if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
+  const soc_qwen_config& c = kv->model->cfg;
+  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= c.num_hidden_layers)
+    return soc::fail(SOC_ERR_INVALID, "soc_kv_read: index out of range");
+  hipError_t e = hipStreamSynchronize(kv->model->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  const int d = c.head_dim, n = kv->len[slot];
+  for (int h = 0; h < c.num_key_value_heads; ++h) {
+    const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(layer) * kv->layer_stride +
+                       static_cast<size_t>(h) * kv->cap * d;
+    if (keys && (e = hipMemcpy(keys + static_cast<size_t>(h) * n * d, kv->k + off, static_cast<size_t>(n) * d * 2,
+                               hipMemcpyDeviceToHost)) != hipSuccess)
+      return hip_fail(e, "hipMemcpy kv");
+    if (values && (e = hipMemcpy(values + static_cast<size_t>(h) * n * d, kv->v + off,
+                                 static_cast<size_t>(n) * d * 2, hipMemcpyDeviceToHost)) != hipSuccess)
+      return hip_fail(e, "hipMemcpy kv");
+  }
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off,
+                int32_t logit_rows, float* logits, int32_t* next_token) {
+  SOC_API_BEGIN
+  if (m == nullptr || kv == nullptr || ids == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (n <= 0) return soc::fail(SOC_ERR_INVALID, "prefill requires at least one token");  // generation_context.cpp:22-27
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (pos_off != kv->len[slot])
+    return soc::fail(SOC_ERR_STATE, "position_offset must equal the cached length of the slot");
+  if (pos_off + n > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "prefill exceeds KV capacity");
+  if (logit_rows < 0 || logit_rows > n) return soc::fail(SOC_ERR_INVALID, "logit_rows out of range");
+  SOC_TRY(validate_ids(m, ids, n));
+  SOC_TRY(ensure_prefill_ws(m, n, pos_off + n, logit_rows));
+  const soc_qwen_config& c = m->cfg;
+  PrefillWs& w = m->pws;
+  hipStream_t s = m->ctx->stream;
+  hipError_t e = hipMemcpyAsync(w.ids, ids, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync ids");
+  if ((e = soc::launch_embed(w.ids, n, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
+  const int H = c.hidden_size;
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const DevLayer& L = m->layers[l];
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    soc::GemmArgs g{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = L.wqkv;
+    g.c = w.qkv;
+    g.ldc = m->qkv_rows;
+    g.M = n;
+    g.N = m->qkv_rows;
+    g.K = H;
+    if ((e = soc::launch_gemm_f32a(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    soc::QkNormRopeArgs q{};
+    q.qkv = w.qkv;
+    q.ld_qkv = m->qkv_rows;
+    q.q_gain = L.q_norm;
+    q.k_gain = L.k_norm;
+    q.eps = c.rms_norm_eps;
+    q.rope_cos = m->rope_cos;
+    q.rope_sin = m->rope_sin;
+    q.q_out = w.q;
+    q.kcache = kv->k;
+    q.vcache = kv->v;
+    q.slot_stride = kv->slot_stride;
+    q.layer_stride = kv->layer_stride;
+    q.slot = slot;
+    q.layer = l;
+    q.cap = kv->cap;
+    q.pos_base = pos_off;
+    q.T = n;
+    q.nq = c.num_attention_heads;
+    q.nkv = c.num_key_value_heads;
+    if ((e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
+    soc::AttnArgs a = attn_args(m, kv, l);
+    a.qkv = w.q;
+    a.ld_qkv = m->qd;
+    a.pos = nullptr;
+    a.slot = nullptr;
+    a.slot_base = slot;
+    a.pos_base = pos_off;
+    a.out = w.attn;
+    a.ld_out = m->qd;
+    a.part = w.part;
+    a.counters = w.attn_counters;
+    a.B = n;
+    a.max_split = (pos_off + n + kAttnChunk - 1) / kAttnChunk;
+    if ((e = soc::launch_attention(a, 0, s)) != hipSuccess) return hip_fail(e, "attention prefill");
+    g = soc::GemmArgs{};
+    g.a = w.attn;
+    g.lda = m->qd;
+    g.w = L.wo;
+    g.c = w.x;
+    g.ldc = H;
+    g.M = n;
+    g.N = H;
+    g.K = m->qd;
+    if ((e = soc::launch_gemm_f32a(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    g = soc::GemmArgs{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = L.wgate;
+    g.w2 = L.wup;
+    g.c = w.h;
+    g.ldc = c.intermediate_size;
+    g.M = n;
+    g.N = c.intermediate_size;
+    g.K = H;
+    if ((e = soc::launch_gemm_f32a(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    g = soc::GemmArgs{};
+    g.a = w.h;
+    g.lda = c.intermediate_size;
+    g.w = L.wdown;
+    g.c = w.x;
+    g.ldc = H;
+    g.M = n;
+    g.N = H;
+    g.K = c.intermediate_size;
+    if ((e = soc::launch_gemm_f32a(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+  }
+  // logits of the last row (with the greedy token), then of the other requested rows
+  soc::LmHeadArgs h{};
+  h.x = w.x + static_cast<size_t>(n - 1) * H;
+  h.gain = m->final_norm;
+  h.eps = c.rms_norm_eps;
+  h.w = m->lm_head;
+  h.logits = w.logits + static_cast<size_t>(std::max(logit_rows, 1) - 1) * c.vocab_size;
+  h.part_val = w.lm_val;
+  h.part_idx = w.lm_idx;
+  h.counter = w.lm_counter;
+  h.token_out = w.token;
+  h.N = c.vocab_size;
+  h.K = H;
+  if ((e = soc::launch_lm_head_argmax(h, s)) != hipSuccess) return hip_fail(e, "lm head");
+  if (logit_rows > 1) {
+    const int rows = logit_rows - 1;
+    const float* xr = w.x + static_cast<size_t>(n - logit_rows) * H;
+    if ((e = soc::launch_rmsnorm_rows(xr, rows, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    soc::GemmArgs g{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = m->lm_head;
+    g.c = w.logits;
+    g.ldc = c.vocab_size;
+    g.M = rows;
+    g.N = c.vocab_size;
+    g.K = H;
+    if ((e = soc::launch_gemm_f32a(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+  }
+  if (logits != nullptr && logit_rows > 0) {
+    if ((e = hipMemcpyAsync(logits, w.logits, static_cast<size_t>(logit_rows) * c.vocab_size * 4,
+                            hipMemcpyDeviceToHost, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync logits");
+  }
+  int32_t tok = 0;
+  if ((e = hipMemcpyAsync(&tok, w.token, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync token");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "prefill");
+  kv->len[slot] = pos_off + n;
+  if (next_token) *next_token = tok;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_decode(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, float* logits, int32_t* next_token) {
+  SOC_API_BEGIN
+  if (m == nullptr || kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (kv->len[slot] + 1 > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
+  SOC_TRY(validate_ids(m, &last, 1));
+  SOC_TRY(ensure_decode_ws(m, kv->cap));
+  SOC_TRY(run_decode_steps(m, kv, slot, last, 1));
+  hipStream_t s = m->ctx->stream;
+  hipError_t e;
+  if (logits != nullptr &&
+      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDeviceToHost,
+                          s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync logits");
+  int32_t tok = 0;
+  if ((e = hipMemcpyAsync(&tok, m->dws.state, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync token");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode");
+  kv->len[slot] += 1;
+  if (next_token) *next_token = tok;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_decode_steps(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, int32_t steps, int32_t* tokens_out) {
+  SOC_API_BEGIN
+  if (m == nullptr || kv == nullptr || (steps > 0 && tokens_out == nullptr))
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
+  if (kv->len[slot] + steps > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
+  if (steps == 0) return SOC_OK;
+  SOC_TRY(validate_ids(m, &last, 1));
+  SOC_TRY(ensure_decode_ws(m, kv->cap));
+  SOC_TRY(run_decode_steps(m, kv, slot, last, steps));
+  hipStream_t s = m->ctx->stream;
+  hipError_t e = hipMemcpyAsync(tokens_out, m->dws.ring, static_cast<size_t>(steps) * 4, hipMemcpyDeviceToHost, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync tokens");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode steps");
+  kv->len[slot] += steps;
+  return SOC_OK;
+  SOC_API_END
+}
+
+// ---- op-level ----
+int soc_gemv_f16(soc_ctx* ctx, const void* w, const void* x, float* y, int32_t n, int32_t k) {
+  if (ctx == nullptr || w == nullptr || x == nullptr || y == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (n <= 0 || k <= 0 || k % 8 != 0 || k > 16384) return soc::fail(SOC_ERR_INVALID, "soc_gemv_f16: need n > 0, 0 < k <= 16384, k % 8 == 0");
+  soc::GemvArgs g{};
+  g.xh = static_cast<const f16*>(x);
+  g.w = static_cast<const f16*>(w);
+  g.y = y;
+  g.N = n;
+  g.K = k;
+  hipError_t e = soc::launch_gemv(g, soc::EPI_STORE, ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "gemv");
+}
+
+int soc_qmm(soc_ctx* ctx, const void* x, const void* codes, int32_t bits, const void* scales, float* y, int32_t mm,
+            int32_t n, int32_t k) {
+  if (ctx == nullptr || x == nullptr || codes == nullptr || scales == nullptr || y == nullptr)
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (bits != 8 && bits != 4) return soc::fail(SOC_ERR_INVALID, "soc_qmm: bits must be 8 or 4");
+  if (!(mm == 1 || mm == 2 || mm == 4 || mm == 8)) return soc::fail(SOC_ERR_INVALID, "soc_qmm: m must be 1, 2, 4 or 8");
+  if (n <= 0 || k <= 0 || k % 64 != 0) return soc::fail(SOC_ERR_INVALID, "soc_qmm: k must be a positive multiple of 64");
+  if (static_cast<size_t>(mm) * k * 4 > 160 * 1024) return soc::fail(SOC_ERR_INVALID, "soc_qmm: m*k too large");
+  soc::QmmArgs a{};
+  a.x = static_cast<const f16*>(x);
+  a.codes = codes;
+  a.scales = static_cast<const f16*>(scales);
+  a.y = y;
+  a.M = mm;
+  a.N = n;
+  a.K = k;
+  hipError_t e = soc::launch_qmm(a, bits, ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "qmm");
+}
+
+int soc_dequant(soc_ctx* ctx, const void* codes, int32_t bits, const void* scales, float* w, int32_t n, int32_t k) {
+  if (ctx == nullptr || codes == nullptr || scales == nullptr || w == nullptr)
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if ((bits != 8 && bits != 4) || n <= 0 || k <= 0 || k % 64 != 0)
+    return soc::fail(SOC_ERR_INVALID, "soc_dequant: bad shape or bits");
+  hipError_t e = soc::launch_dequant(codes, bits, static_cast<const f16*>(scales), n, k, w, ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,206 @@
+"""End-to-end parity of the HIP Qwen3 forward (prefill + decode through the fp16 KV cache) on an MI355X.
+
+Checks against (1) golden fixtures written by the reference's own compiled CPU sources (tests/golden), and
+(2) the CPU oracle run live on the same seeded inputs. Tolerance (logits, fp32 compute with fp16 weights and an fp16
+KV cache): max |gpu - ref| <= 2e-2 and max |gpu - ref| / max |ref| <= 1e-2; greedy tokens must be identical.
+"""
+import numpy as np
+import pytest
+
+import soc_amd as S
+from tests.golden.make_golden import SMALL_MODELS
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def assert_logits_close(got, ref, what=""):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    err = float(np.max(np.abs(got - ref)))
+    scale = float(np.max(np.abs(ref)))
+    assert err <= ATOL and err <= RTOL * scale, f"{what}: max abs err {err:.3e}, ref scale {scale:.3e}"
+
+
+def _gpu_model(ctx, cfg, weights):
+    return S.Model(ctx, cfg).load(weights)
+
+
+@pytest.mark.parametrize("name", list(SMALL_MODELS))
+def test_small_model_generation_matches_reference(gpu_ctx, golden, name):
+    cfg, seed, plen, new = SMALL_MODELS[name]
+    g = golden(f"model_{name}.npz")
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
+    kv = S.KVCache(m, 1, 64)
+    try:
+        prompt = g["prompt"]
+        logits, tok = S.prefill(m, kv, 0, prompt, 0, logit_rows=plen)
+        assert_logits_close(logits, g["prompt_logits"], f"{name} prompt rows")
+        toks = [tok]
+        assert_logits_close(logits[-1], g["step_logits"][0], f"{name} step 0")
+        for i in range(1, new):
+            lg, tok = S.decode(m, kv, 0, toks[-1])
+            assert_logits_close(lg, g["step_logits"][i], f"{name} step {i}")
+            toks.append(tok)
+        assert toks == g["tokens"].tolist()
+        assert kv.length(0) == plen + new - 1
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_chunked_prefill_equals_single_prefill(gpu_ctx):
+    cfg, seed, _, _ = SMALL_MODELS["tiny_untied"]
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
+    ids = S.synth_tokens(5, "chunk", cfg.vocab_size, 40)
+    a = S.KVCache(m, 1, 64)
+    b = S.KVCache(m, 1, 64)
+    try:
+        la, ta = S.prefill(m, a, 0, ids, 0, logit_rows=12)
+        S.prefill(m, b, 0, ids[:17], 0, logit_rows=0)
+        S.prefill(m, b, 0, ids[17:29], 17, logit_rows=0)
+        lb, tb = S.prefill(m, b, 0, ids[29:], 29, logit_rows=11)
+        # rows are computed independently by the same kernels: bit-identical
+        assert np.array_equal(la[1:], lb) and ta == tb
+        ka, va = a.read(0, 1)
+        kb, vb = b.read(0, 1)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    finally:
+        a.close()
+        b.close()
+        m.close()
+
+
+def test_decode_matches_prefill_rows(gpu_ctx):
+    """Token-by-token decode (GEMV path) reproduces the prefill (GEMM path) logits of the same rows."""
+    cfg, seed, _, _ = SMALL_MODELS["tiny_g4"]
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
+    ids = S.synth_tokens(6, "dec", cfg.vocab_size, 24)
+    a = S.KVCache(m, 1, 32)
+    b = S.KVCache(m, 1, 32)
+    try:
+        full, _ = S.prefill(m, a, 0, ids, 0, logit_rows=24)
+        S.prefill(m, b, 0, ids[:10], 0, logit_rows=0)
+        for t in range(10, 24):
+            lg, _ = S.decode(m, b, 0, int(ids[t]))
+            assert_logits_close(lg, full[t], f"row {t}")
+    finally:
+        a.close()
+        b.close()
+        m.close()
+
+
+def test_decode_steps_equal_decode_loop(gpu_ctx):
+    cfg, seed, _, _ = SMALL_MODELS["tiny_untied"]
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
+    ids = S.synth_tokens(8, "steps", cfg.vocab_size, 7)
+    a = S.KVCache(m, 1, 48)
+    b = S.KVCache(m, 2, 48)
+    try:
+        _, t0 = S.prefill(m, a, 0, ids)
+        _, u0 = S.prefill(m, b, 1, ids)
+        assert t0 == u0
+        loop = [t0]
+        for _ in range(20):
+            loop.append(S.decode(m, a, 0, loop[-1], want_logits=False)[1])
+        steps = S.decode_steps(m, b, 1, u0, 20)
+        assert steps.tolist() == loop[1:]
+        assert a.length(0) == b.length(1) == 27
+    finally:
+        a.close()
+        b.close()
+        m.close()
+
+
+def test_prefill_against_live_oracle_long_prompt(gpu_ctx, oracle_mod):
+    """Qwen3-0.6B layer shapes (4 of its 28 layers), 512-token prompt, last-row logits vs the oracle."""
+    cfg = S.QwenConfig(vocab_size=151936, hidden_size=1024, num_hidden_layers=4, num_attention_heads=16,
+                       num_key_value_heads=8, intermediate_size=3072)
+    w = S.synth_weights(cfg, 3)
+    ids = S.synth_tokens(3, "prompt", cfg.vocab_size, 512)
+    m = _gpu_model(gpu_ctx, cfg, w)
+    kv = S.KVCache(m, 1, 520)
+    try:
+        logits, tok = S.prefill(m, kv, 0, ids, 0, logit_rows=1)
+        om = oracle_mod.OracleModel(cfg, w)
+        cache = oracle_mod.OracleCache(om, 520)
+        ref = cache.forward(ids, 0, logit_rows=1)
+        assert_logits_close(logits[0], ref[0], "last row")
+        assert tok == oracle_mod.sample(ref[0])
+        # three decode steps after the long prompt
+        t = tok
+        for i in range(3):
+            lg, nt = S.decode(m, kv, 0, t)
+            r = cache.forward(np.array([t], np.int32), 512 + i)
+            assert_logits_close(lg, r[0], f"decode {i}")
+            assert nt == oracle_mod.sample(r[0])
+            t = nt
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_qwen3_0p6b_greedy_matches_reference(gpu_ctx, golden):
+    """Qwen3-0.6B, random-init fp16 N(0,0.02) seed 1, 32-token prompt, 16 greedy tokens at batch 1."""
+    g = golden("qwen3_0p6b.npz")
+    cfg = S.QWEN3_0_6B
+    m = S.Model(gpu_ctx, cfg).synthesize(int(g["weight_seed"]), 0.02)
+    kv = S.KVCache(m, 1, 64)
+    try:
+        prompt = g["prompt"]
+        logits, tok = S.prefill(m, kv, 0, prompt)
+        rows = [logits[0]]
+        toks = [tok]
+        for _ in range(15):
+            lg, tok = S.decode(m, kv, 0, toks[-1])
+            rows.append(lg)
+            toks.append(tok)
+        assert toks == g["tokens"].tolist()
+        for i, lg in enumerate(rows):
+            assert_logits_close(lg[g["sample_idx"]], g["sample_vals"][i], f"step {i} sampled")
+            assert_logits_close(lg[g["top_ids"][i]], g["top_vals"][i], f"step {i} top-64")
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_error_paths_leave_state_unchanged(gpu_ctx):
+    """Host-forced failures (Mac/gpu/src/runtime/generation_context.cpp:22-27,67-90; kv_cache.mm:103-108)."""
+    cfg, seed, _, _ = SMALL_MODELS["tiny_tied"]
+    m = S.Model(gpu_ctx, cfg)
+    kv = S.KVCache(m, 1, 16)
+    try:
+        with pytest.raises(S.SocError) as e:
+            S.prefill(m, kv, 0, [1, 2, 3])
+        assert e.value.code == S.capi.SOC_ERR_STATE  # not finalized
+        m.load(S.synth_weights(cfg, seed))
+        with pytest.raises(S.SocError) as e:
+            S.prefill(m, kv, 0, np.zeros(0, np.int32))
+        assert e.value.code == S.capi.SOC_ERR_INVALID
+        with pytest.raises(S.SocError) as e:
+            S.prefill(m, kv, 0, [1, cfg.vocab_size])
+        assert e.value.code == S.capi.SOC_ERR_INVALID
+        with pytest.raises(S.SocError) as e:
+            S.prefill(m, kv, 0, np.arange(17, dtype=np.int32))
+        assert e.value.code == S.capi.SOC_ERR_CAPACITY
+        assert kv.length(0) == 0
+        S.prefill(m, kv, 0, np.arange(15, dtype=np.int32))
+        with pytest.raises(S.SocError) as e:
+            S.prefill(m, kv, 0, [1], position_offset=3)
+        assert e.value.code == S.capi.SOC_ERR_STATE
+        _, t = S.decode(m, kv, 0, 1)
+        with pytest.raises(S.SocError) as e:
+            S.decode(m, kv, 0, t)
+        assert e.value.code == S.capi.SOC_ERR_CAPACITY
+        assert kv.length(0) == 16
+        with pytest.raises(S.SocError) as e:
+            S.decode(m, kv, 5, 1)
+        assert e.value.code == S.capi.SOC_ERR_INVALID
+        kv.reset(0)
+        assert kv.length(0) == 0
+        _, t2 = S.prefill(m, kv, 0, [3])
+        assert kv.length(0) == 1
+    finally:
+        kv.close()
+        m.close()
