@@ -70,5 +70,25 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+CPP_TESTS = ROOT / "tests" / "cpp"
+
+
+def build_cpp_tests(verbose: bool = False) -> list[Path]:
+    """Host-only C++ programs that drive the C++ host interface (include/soc/gpu/runtime.h) through the library."""
+    outs = []
+    for src in sorted(CPP_TESTS.glob("*.cpp")):
+        exe = src.with_suffix("")
+        cmd = ["g++", "-O2", "-std=c++17", f"-I{ROOT / 'include'}", str(src), f"-L{PKG}", "-lsoc_hip",
+               f"-Wl,-rpath,{PKG}", "-o", str(exe)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"g++ failed for {src.name}:\n{r.stderr}")
+        outs.append(exe)
+    return outs
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_cpp_tests(verbose="-v" in sys.argv))

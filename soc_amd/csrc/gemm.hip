@@ -84,6 +84,176 @@ __global__ __launch_bounds__(256) void k_gemm_f32a(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// MFMA GEMM: 128x128 output tile per 256-thread block, K slices of 32 staged in LDS (double buffered), each wave
+// owns a 64x64 quadrant as 2x2 tiles of v_mfma_f32_32x32x16_f16. Activations arrive in fp32 and are split on the
+// way into LDS into hi = f16(a) and lo = f16((a - hi) * 2^11); with SPLIT the product is hi.W + 2^-11 lo.W, which
+// keeps about 22 bits of each activation (weights are exact fp16), so the result tracks the fp32 reference.
+// EPI_SWIGLU stages 64 gate rows and the matching 64 up rows per tile; a wave holds gate and up accumulators of the
+// same outputs in the same registers and writes silu(g) * u.
+// ------------------------------------------------------------------------------------------------------------
+namespace {
+constexpr int MBM = 128, MBN = 128, MBK = 32, MPAD = 8;  // LDS rows padded to 40 halves (80 B)
+constexpr int MLD = MBK + MPAD;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+}  // namespace
+
+template <int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
+  constexpr int NA = SPLIT ? 2 : 1;
+  __shared__ _Float16 As[2][NA][MBM * MLD];
+  __shared__ _Float16 Bs[2][MBN * MLD];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int m0 = blockIdx.y * MBM;
+  // output columns covered by this block: plain GEMM 128, SwiGLU 64 (gate/up pairs)
+  const int n0 = blockIdx.x * (EPI == EPI_SWIGLU ? MBN / 2 : MBN);
+
+  // global -> register staging: A 128 x 32 fp32 = 1024 float4 (4 per thread); W 128 x 32 fp16 = 512 x 16 B (2 per thread)
+  f32x4 ra[4];
+  u32x4 rb[2];
+  auto load_tiles = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + e * 256;
+      const int r = idx >> 3, c = (idx & 7) * 4;
+      const int m = m0 + r;
+      ra[e] = (m < g.M) ? *reinterpret_cast<const f32x4*>(g.a + static_cast<size_t>(m) * g.lda + k0 + c)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int idx = tid + e * 256;
+      const int r = idx >> 2, c = (idx & 3) * 8;
+      const f16* src;
+      int n;
+      if constexpr (EPI == EPI_SWIGLU) {
+        n = n0 + (r & 63);
+        src = r < 64 ? g.w : g.w2;
+      } else {
+        n = n0 + r;
+        src = g.w;
+      }
+      rb[e] = (n < g.N) ? load16(src + static_cast<size_t>(n) * g.K + k0 + c) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + e * 256;
+      const int r = idx >> 3, c = (idx & 7) * 4;
+      f16x4 hi, lo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ra[e][i];
+        const _Float16 h = static_cast<_Float16>(v);
+        hi[i] = h;
+        lo[i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
+      }
+      *reinterpret_cast<f16x4*>(&As[buf][0][r * MLD + c]) = hi;
+      if constexpr (SPLIT) *reinterpret_cast<f16x4*>(&As[buf][NA - 1][r * MLD + c]) = lo;
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int idx = tid + e * 256;
+      const int r = idx >> 2, c = (idx & 3) * 8;
+      *reinterpret_cast<u32x4*>(&Bs[buf][r * MLD + c]) = rb[e];
+    }
+  };
+
+  f32x16 acc[2][2], acc_lo[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+        acc_lo[i][j][r] = 0.0f;
+      }
+
+  // B sub-tile rows of this wave: plain = wn*64 + t*32; SwiGLU: t = 0 gate rows wn*32, t = 1 up rows 64 + wn*32
+  const int brow[2] = {EPI == EPI_SWIGLU ? wn * 32 : wn * 64, EPI == EPI_SWIGLU ? 64 + wn * 32 : wn * 64 + 32};
+  const int KT = g.K / MBK;
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load_tiles((kt + 1) * MBK);
+#pragma unroll
+    for (int ks = 0; ks < MBK / 16; ++ks) {
+      const int kc = ks * 16 + (lane >> 5) * 8;
+      h8 bf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        bf[t] = *reinterpret_cast<const h8*>(&Bs[buf][(brow[t] + (lane & 31)) * MLD + kc]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int arow = wm * 64 + i * 32 + (lane & 31);
+        const h8 ah = *reinterpret_cast<const h8*>(&As[buf][0][arow * MLD + kc]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bf[t], acc[i][t], 0, 0, 0);
+        if constexpr (SPLIT) {
+          const h8 al = *reinterpret_cast<const h8*>(&As[buf][NA - 1][arow * MLD + kc]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bf[t], acc_lo[i][t], 0, 0, 0);
+        }
+      }
+    }
+    if (kt + 1 < KT) store_tiles(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds D[m][n] for n = lane % 32, m = (r / 4) * 8 + (lane / 32) * 4 + r % 4
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (m >= g.M) continue;
+      float v[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) v[t] = acc[i][t][r] + (SPLIT ? acc_lo[i][t][r] * (1.0f / 2048.0f) : 0.0f);
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int n = n0 + wn * 32 + (lane & 31);
+        if (n < g.N) g.c[static_cast<size_t>(m) * g.ldc + n] = silu_ref(v[0]) * v[1];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int n = n0 + wn * 64 + t * 32 + (lane & 31);
+          if (n < g.N) {
+            float* dst = g.c + static_cast<size_t>(m) * g.ldc + n;
+            *dst = EPI == EPI_RESIDUAL ? *dst + v[t] : v[t];
+          }
+        }
+      }
+    }
+}
+
+bool gemm_mfma_supported(const GemmArgs& g) { return g.K % MBK == 0 && g.lda % 4 == 0; }
+
+hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s) {
+  if (!gemm_mfma_supported(g)) return hipErrorInvalidValue;
+  const int bn = epi == EPI_SWIGLU ? MBN / 2 : MBN;
+  const dim3 grid((g.N + bn - 1) / bn, (g.M + MBM - 1) / MBM), block(256);
+#define SOC_MFMA_CASE(E, SP) hipLaunchKernelGGL((k_gemm_mfma<E, SP>), grid, block, 0, s, g)
+  if (split) {
+    if (epi == EPI_STORE) SOC_MFMA_CASE(EPI_STORE, true);
+    else if (epi == EPI_RESIDUAL) SOC_MFMA_CASE(EPI_RESIDUAL, true);
+    else if (epi == EPI_SWIGLU) SOC_MFMA_CASE(EPI_SWIGLU, true);
+    else return hipErrorInvalidValue;
+  } else {
+    if (epi == EPI_STORE) SOC_MFMA_CASE(EPI_STORE, false);
+    else if (epi == EPI_RESIDUAL) SOC_MFMA_CASE(EPI_RESIDUAL, false);
+    else if (epi == EPI_SWIGLU) SOC_MFMA_CASE(EPI_SWIGLU, false);
+    else return hipErrorInvalidValue;
+  }
+#undef SOC_MFMA_CASE
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s) {
   const dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM), block(256);
   switch (epi) {

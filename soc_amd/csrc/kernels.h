@@ -96,6 +96,40 @@ struct QkNormRopeArgs {
 };
 hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s);
 
+// ---- persistent batch-1 decode step (one launch per token) ----
+struct PersistArgs {
+  const f16* const* layer_w;  // device array [L][9]: in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+  const f16* embed;
+  const f16* final_norm;
+  const f16* lm_head;
+  const float* rope_cos;
+  const float* rope_sin;
+  f16* kcache;                // base of this slot's layer 0
+  f16* vcache;
+  long long layer_stride;
+  int cap;
+  int L, H, I, V, nq, nkv, qkv_rows, qd, xs_cap;
+  float eps, scale;
+  uint64_t* xa;               // exchange vectors: {value, tag} per element
+  uint64_t* xb;
+  uint64_t* qkv;
+  uint64_t* attn;
+  uint64_t* h;
+  float* logits;              // [V] or nullptr
+  float* part_val;            // [nblocks]
+  int* part_idx;              // [nblocks]
+  int* counter;               // zero; reset by the last block
+  int* state;                 // {token, pos, step}; step starts at 1
+  int* ring;                  // nullable
+  int* ring_pos;
+  int* err;                   // raised when a wait times out
+  uint64_t* trace;            // nullable: phase timestamps [2][3 + 5 L] (diagnostics)
+};
+bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks);
+size_t persistent_lds_bytes(const PersistArgs& a, int G);
+hipError_t persistent_blocks_per_cu(int G, int* blocks);
+hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream_t s);
+
 // ---- prefill helpers ----
 // x[t][:] = float(table[ids[t]][:]) for t < T (Mac/cpu/src/embedding.cpp:51-77).
 hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, float* x, hipStream_t s);
@@ -114,5 +148,8 @@ struct GemmArgs {
   int M, N, K;
 };
 hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
+// Same contract on MFMA (fp16 inputs, fp32 accumulation); split = hi/lo fp16 parts of the fp32 activations.
+bool gemm_mfma_supported(const GemmArgs& g);
+hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s);
 
 }  // namespace soc

@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -45,6 +46,7 @@ void clear_error() { g_last_error.clear(); }
 // ------------------------------------------------------------------------------------------------------------
 struct soc_ctx {
   int device = 0;
+  int num_cus = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool timing = false;
@@ -70,6 +72,11 @@ struct DecodeWs {
   int *lm_idx = nullptr, *lm_counter = nullptr, *attn_counters = nullptr, *state = nullptr, *ring = nullptr,
       *ring_pos = nullptr;
   int max_split = 0, ring_cap = 0;
+  // persistent decode kernel: exchange vectors ({value, tag} per element), argmax partials, error flag
+  uint64_t *xa = nullptr, *xb = nullptr, *qkv_x = nullptr, *attn_x = nullptr, *h_x = nullptr;
+  float* pv = nullptr;
+  int *pi = nullptr, *err = nullptr;
+  int nblocks = 0;
   std::vector<void*> allocs;
 };
 
@@ -97,6 +104,7 @@ struct soc_model {
   std::map<std::string, TensorSlot> tensors;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int rope_len = 0;
+  const f16** d_layer_w = nullptr;  // device copy of the per-layer weight pointers [L][9]
   DecodeWs dws;
   int dws_gen = 0;  // bumped whenever the decode scratch is reallocated (captured graphs refer to it)
   PrefillWs pws;
@@ -193,6 +201,23 @@ int ensure_decode_ws(soc_model* m, int cap) {
     return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.state, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.ring_pos, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  // persistent-kernel state: zeroed exchange vectors (tag 0 is never expected), step counter starts at 1
+  w.nblocks = m->ctx->num_cus;
+  SOC_TRY(dev_alloc_t(w.allocs, c.hidden_size, &w.xa));
+  SOC_TRY(dev_alloc_t(w.allocs, c.hidden_size, &w.xb));
+  SOC_TRY(dev_alloc_t(w.allocs, m->qkv_rows, &w.qkv_x));
+  SOC_TRY(dev_alloc_t(w.allocs, m->qd, &w.attn_x));
+  SOC_TRY(dev_alloc_t(w.allocs, c.intermediate_size, &w.h_x));
+  SOC_TRY(dev_alloc_t(w.allocs, w.nblocks, &w.pv));
+  SOC_TRY(dev_alloc_t(w.allocs, w.nblocks, &w.pi));
+  SOC_TRY(dev_alloc_t(w.allocs, 64, &w.err));
+  for (auto pr : {std::make_pair((void*)w.xa, (size_t)c.hidden_size), std::make_pair((void*)w.xb, (size_t)c.hidden_size),
+                  std::make_pair((void*)w.qkv_x, (size_t)m->qkv_rows), std::make_pair((void*)w.attn_x, (size_t)m->qd),
+                  std::make_pair((void*)w.h_x, (size_t)c.intermediate_size)})
+    if ((e = hipMemset(pr.first, 0, pr.second * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.err, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  const int32_t step1 = 1;
+  if ((e = hipMemcpy(w.state + 2, &step1, 4, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy");
   w.ready = true;
   return SOC_OK;
 }
@@ -378,6 +403,63 @@ int get_decode_graph(soc_model* m, soc_kv* kv, int slot, hipGraphExec_t* out) {
   return SOC_OK;
 }
 
+// The persistent one-launch decode step is used when the shapes fit its register tiling and every block can be
+// resident at once; SOC_DECODE=graph selects the per-op kernels replayed from a HIP graph instead.
+bool use_persistent(soc_model* m) {
+  const char* mode = std::getenv("SOC_DECODE");
+  if (mode != nullptr && std::strcmp(mode, "persistent") != 0) return false;
+  if (env_flag("SOC_EAGER")) return false;
+  const soc_qwen_config& c = m->cfg;
+  const int nb = m->ctx->num_cus;
+  if (!soc::persistent_supported(c.hidden_size, m->qd, c.intermediate_size, m->qkv_rows, c.num_attention_heads,
+                                 c.num_key_value_heads, nb))
+    return false;
+  int per_cu = 0;
+  if (soc::persistent_blocks_per_cu(c.num_attention_heads / c.num_key_value_heads, &per_cu) != hipSuccess) return false;
+  return per_cu * m->ctx->num_cus >= nb;
+}
+
+soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
+  const soc_qwen_config& c = m->cfg;
+  DecodeWs& w = m->dws;
+  soc::PersistArgs p{};
+  p.layer_w = m->d_layer_w;
+  p.embed = m->embed;
+  p.final_norm = m->final_norm;
+  p.lm_head = m->lm_head;
+  p.rope_cos = m->rope_cos;
+  p.rope_sin = m->rope_sin;
+  p.kcache = kv->k + static_cast<size_t>(slot) * kv->slot_stride;
+  p.vcache = kv->v + static_cast<size_t>(slot) * kv->slot_stride;
+  p.layer_stride = kv->layer_stride;
+  p.cap = kv->cap;
+  p.L = c.num_hidden_layers;
+  p.H = c.hidden_size;
+  p.I = c.intermediate_size;
+  p.V = c.vocab_size;
+  p.nq = c.num_attention_heads;
+  p.nkv = c.num_key_value_heads;
+  p.qkv_rows = m->qkv_rows;
+  p.qd = m->qd;
+  p.xs_cap = std::max(std::max(c.hidden_size, m->qd), c.intermediate_size);
+  p.eps = c.rms_norm_eps;
+  p.scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+  p.xa = w.xa;
+  p.xb = w.xb;
+  p.qkv = w.qkv_x;
+  p.attn = w.attn_x;
+  p.h = w.h_x;
+  p.logits = w.logits;
+  p.part_val = w.pv;
+  p.part_idx = w.pi;
+  p.counter = w.lm_counter;
+  p.state = w.state;
+  p.ring = w.ring;
+  p.ring_pos = w.ring_pos;
+  p.err = w.err;
+  return p;
+}
+
 int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps) {
   DecodeWs& w = m->dws;
   hipStream_t s = m->ctx->stream;
@@ -387,7 +469,46 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
   const int32_t zero = 0;
   if ((e = hipMemcpyAsync(w.ring_pos, &zero, sizeof(zero), hipMemcpyHostToDevice, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync ring");
-  if (env_flag("SOC_EAGER")) {
+  if (use_persistent(m)) {
+    soc::PersistArgs p = persist_args(m, kv, slot);
+    // SOC_TRACE_FILE=<path>: append the last step's per-phase timestamps (diagnostics)
+    const char* trace_path = std::getenv("SOC_TRACE_FILE");
+    const size_t trace_n = 2 * (3 + 5 * static_cast<size_t>(m->cfg.num_hidden_layers));
+    if (trace_path != nullptr) {
+      if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
+    }
+    for (int i = 0; i < steps; ++i)
+      if ((e = soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
+        return hip_fail(e, "persistent decode launch");
+    int32_t err = 0;
+    if ((e = hipMemcpyAsync(&err, w.err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync err");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "persistent decode");
+    if (p.trace != nullptr) {
+      std::vector<uint64_t> t(trace_n);
+      e = hipMemcpy(t.data(), p.trace, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost);
+      (void)hipFree(p.trace);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy trace");
+      if (FILE* f = std::fopen(trace_path, "a")) {
+        const size_t per = trace_n / 2;
+        for (int which = 0; which < 2; ++which) {
+          std::fprintf(f, "%s:", which == 0 ? "block0" : "blockN");
+          for (size_t i = 1; i < per; ++i) {
+            const uint64_t x = t[which * per + i], y = t[which * per + i - 1];
+            if (x == 0 || y == 0) std::fprintf(f, " -");
+            else std::fprintf(f, " %.2f", (static_cast<double>(x) - static_cast<double>(y)) * 0.01);  // us (100 MHz)
+          }
+          std::fprintf(f, " | total %.2f us\n", (t[which * per + per - 1] - t[which * per]) * 0.01);
+        }
+        std::fclose(f);
+      }
+    }
+    if (err != 0) {
+      // a bounded wait expired: drop the exchange state so the next call starts clean
+      m->dws.ready = false;
+      return soc::fail(SOC_ERR_HIP, "persistent decode: a cross-block wait timed out (grid not co-resident?)");
+    }
+  } else if (env_flag("SOC_EAGER")) {
     for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_decode(m, kv, slot, nullptr));
   } else {
     hipGraphExec_t g;
@@ -396,6 +517,19 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       if ((e = hipGraphLaunch(g, s)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
   }
   return SOC_OK;
+}
+
+// Prefill projections run on MFMA with hi/lo-split activations when K allows (SOC_PREFILL_GEMM=fma selects the
+// FMA kernel; SOC_PREFILL_SPLIT=0 feeds single fp16 activations to the MFMA).
+hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
+  const char* mode = std::getenv("SOC_PREFILL_GEMM");
+  const bool fma = mode != nullptr && std::strcmp(mode, "fma") == 0;
+  if (!fma && soc::gemm_mfma_supported(g)) {
+    const char* sp = std::getenv("SOC_PREFILL_SPLIT");
+    const bool split = !(sp != nullptr && sp[0] == '0');
+    return soc::launch_gemm_mfma(g, epi, split, s);
+  }
+  return soc::launch_gemm_f32a(g, epi, s);
 }
 
 int validate_ids(const soc_model* m, const int32_t* ids, int n) {
@@ -425,6 +559,8 @@ int soc_ctx_create(int device, soc_ctx** out) {
   if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   std::unique_ptr<soc_ctx> c(new soc_ctx());
   c->device = device;
+  if ((e = hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
+    return hip_fail(e, "hipDeviceGetAttribute");
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
     return hip_fail(e, "hipStreamCreate");
   if ((e = hipEventCreate(&c->ev0)) != hipSuccess) return hip_fail(e, "hipEventCreate");
@@ -584,6 +720,15 @@ int soc_model_create(soc_ctx* ctx, const soc_qwen_config* cfg, soc_model** out) 
     m->tensors[p + "mlp.down_proj.weight"] = {L.wdown, H * I, false};
   }
   SOC_TRY(build_rope_table(m.get(), c.max_position_embeddings));
+  {
+    std::vector<const f16*> ptrs;
+    for (const DevLayer& L : m->layers)
+      for (const f16* p : {L.in_norm, L.post_norm, L.q_norm, L.k_norm, L.wqkv, L.wo, L.wgate, L.wup, L.wdown})
+        ptrs.push_back(p);
+    if ((e = hipMalloc(&m->d_layer_w, ptrs.size() * sizeof(f16*))) != hipSuccess) return hip_fail(e, "hipMalloc");
+    if ((e = hipMemcpy(m->d_layer_w, ptrs.data(), ptrs.size() * sizeof(f16*), hipMemcpyHostToDevice)) != hipSuccess)
+      return hip_fail(e, "hipMemcpy");
+  }
   *out = m.release();
   return SOC_OK;
   SOC_API_END
@@ -597,6 +742,7 @@ int soc_model_destroy(soc_model* m) {
   (void)hipFree(m->wbuf);
   (void)hipFree(m->rope_cos);
   (void)hipFree(m->rope_sin);
+  (void)hipFree(m->d_layer_w);
   delete m;
   return SOC_OK;
 }
@@ -812,7 +958,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = m->qkv_rows;
     g.K = H;
-    if ((e = soc::launch_gemm_f32a(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    if ((e = prefill_gemm(g,soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
     soc::QkNormRopeArgs q{};
     q.qkv = w.qkv;
     q.ld_qkv = m->qkv_rows;
@@ -857,7 +1003,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = H;
     g.K = m->qd;
-    if ((e = soc::launch_gemm_f32a(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = prefill_gemm(g,soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
     if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
@@ -870,7 +1016,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = c.intermediate_size;
     g.K = H;
-    if ((e = soc::launch_gemm_f32a(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    if ((e = prefill_gemm(g,soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
     g = soc::GemmArgs{};
     g.a = w.h;
     g.lda = c.intermediate_size;
@@ -880,7 +1026,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = H;
     g.K = c.intermediate_size;
-    if ((e = soc::launch_gemm_f32a(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+    if ((e = prefill_gemm(g,soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
   }
   // logits of the last row (with the greedy token), then of the other requested rows
   soc::LmHeadArgs h{};
@@ -910,7 +1056,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = rows;
     g.N = c.vocab_size;
     g.K = H;
-    if ((e = soc::launch_gemm_f32a(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+    if ((e = prefill_gemm(g,soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
   }
   if (logits != nullptr && logit_rows > 0) {
     if ((e = hipMemcpyAsync(logits, w.logits, static_cast<size_t>(logit_rows) * c.vocab_size * 4,

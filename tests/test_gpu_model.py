@@ -113,6 +113,34 @@ def test_decode_steps_equal_decode_loop(gpu_ctx):
         m.close()
 
 
+@pytest.mark.parametrize("name", ["tiny_untied", "tiny_g4"])
+def test_persistent_decode_matches_graph_decode(gpu_ctx, name, monkeypatch):
+    """The one-launch persistent decode step and the per-op kernels (graph replay) agree on every step."""
+    cfg, seed, _, _ = SMALL_MODELS[name]
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
+    ids = S.synth_tokens(9, "paths", cfg.vocab_size, 13)
+    runs = {}
+    try:
+        for mode in ("graph", "persistent"):
+            monkeypatch.setenv("SOC_DECODE", mode)
+            kv = S.KVCache(m, 1, 300)
+            _, t = S.prefill(m, kv, 0, ids)
+            rows, toks = [], [t]
+            for _ in range(12):
+                lg, t = S.decode(m, kv, 0, toks[-1])
+                rows.append(lg)
+                toks.append(t)
+            # long run on the device-resident token loop crosses the 256-key attention chunk boundary
+            more = S.decode_steps(m, kv, 0, toks[-1], 270)
+            kv.close()
+            runs[mode] = (np.stack(rows), toks, more)
+        assert runs["graph"][1] == runs["persistent"][1]
+        assert_logits_close(runs["persistent"][0], runs["graph"][0], f"{name} persistent vs graph")
+        assert np.array_equal(runs["graph"][2], runs["persistent"][2])
+    finally:
+        m.close()
+
+
 def test_prefill_against_live_oracle_long_prompt(gpu_ctx, oracle_mod):
     """Qwen3-0.6B layer shapes (4 of its 28 layers), 512-token prompt, last-row logits vs the oracle."""
     cfg = S.QwenConfig(vocab_size=151936, hidden_size=1024, num_hidden_layers=4, num_attention_heads=16,
