@@ -5,10 +5,13 @@ Workload (headline): Qwen3-0.6B architecture, random-init fp16 weights N(0, 0.02
 prompt is prefilled (untimed), then W warmup and K timed greedy decode steps run with the sampled token fed back on
 the device. A "step" is one decode token. Also measured in the same run:
   * prefill of a 2048-token prompt (tok/s),
-  * the dominant decode kernel (the fused RMSNorm + QKV projection GEMV, 4096 x 1024 fp16) on a rotating set of
-    weight copies larger than the 256 MB Infinity Cache, timed with HIP events on the stream it runs on,
+  * the dominant decode kernel: k_decode_persistent (one launch = one whole token) when the device runs the
+    persistent decode, timed with HIP events on the stream it is launched on; the fused RMSNorm + QKV GEMV
+    (4096 x 1024 fp16, over weight copies larger than the 256 MB Infinity Cache) is reported beside it,
   * the reference CPU runtime (compiled reference sources when available, else the oracle restatement), on the
     host, one core, on a bounded sample.
+HBM traffic per launch of the dominant kernel comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
+profiles/ (scaled by the same counters over a plain copy of known size), when that summary exists.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -136,20 +139,56 @@ def cpu_baseline(cfg: S.QwenConfig, budget_s: float = 20.0):
                       f"(one decode step each; median {sec:.3f} s), 1 host thread of {os.cpu_count()}"}
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "k_decode_persistent_qwen3_0p6b_traffic.md"
+
+
+def measured_traffic(path: Path = TRAFFIC_SUMMARY):
+    """HBM bytes per launch of the persistent decode kernel from the committed rocprofv3 counter summary
+    (line `traffic_bytes_per_launch: <int>`), or None when no summary exists."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibrate(mib: int = 1024) -> None:
+    """A plain device copy of known size (`mib` MiB read + `mib` MiB written, one elementwise kernel), run under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE to scale those counters to bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibrate_bytes_read": n * 4, "copy_calibrate_bytes_written": n * 4, "launches": 3}),
+          flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--copy-calibrate", action="store_true",
+                    help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)")
+    if args.copy_calibrate:
+        copy_calibrate()
+        return
 
     cfg = S.QWEN3_0_6B
     ctx = S.Context(0)
     m = S.Model(ctx, cfg).synthesize(1, 0.02)
+    path = m.decode_path()
     ms, mean_kv, toks = bench_decode(ctx, m, cfg, args.steps, args.warmup)
     ms_per_step = ms / args.steps
     tok_s = 1000.0 / ms_per_step
@@ -158,9 +197,22 @@ def main() -> None:
 
     prefill_ms = None if args.no_prefill else bench_prefill(ctx, m, cfg, 2048)
     us, alg = bench_gemv_kernel(ctx)
-    achieved = alg / (us * 1e-6) / 1e9
+    gemv_gbs = alg / (us * 1e-6) / 1e9
     m.close()
     ctx.close()
+
+    if path == "persistent":
+        # one launch per token: the events around the K launches give the average launch duration (the short
+        # gaps between back-to-back launches included)
+        roofline = {"kernel": "k_decode_persistent (whole decode token: 28 layers + LM head + argmax)",
+                    "bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                    "avg_launch_us": round(ms_per_step * 1e3, 3), "alg_bytes_per_launch": int(bpt)}
+    else:
+        roofline = {"kernel": "k_gemv<4,2,EPI_STORE> (decode QKV projection 4096x1024 fp16)", "bound": "hbm",
+                    "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "avg_launch_us": round(us, 3), "alg_bytes_per_launch": alg}
 
     cpu = None if args.no_cpu else cpu_baseline(cfg)
     out = {
@@ -179,15 +231,15 @@ def main() -> None:
         "config": {"workload": "Qwen3-0.6B (28 layers, hidden 1024, 16 q / 8 kv heads, head_dim 128, "
                                "intermediate 3072, vocab 151936, tied) greedy decode at batch 1 after a 32-token "
                                "prompt", "global_batch": 1, "seq_len": int(mean_kv), "parallelism": "none (1 GPU)"},
+        "decode_path": path,
         "decode_bytes_per_token": int(bpt),
         "decode_hbm_gbs": round(step_gbs, 1),
         "decode_hbm_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "prefill_tok_s": None if prefill_ms is None else round(2048 / (prefill_ms * 1e-3), 1),
         "prefill_ms_2048": None if prefill_ms is None else round(prefill_ms, 3),
-        "roofline": {"kernel": "k_gemv<4,2,EPI_STORE> (decode QKV projection 4096x1024 fp16)", "bound": "hbm",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(us, 3), "alg_bytes_per_launch": alg},
+        "roofline": roofline,
+        "gemv_qkv_4096x1024": {"avg_launch_us": round(us, 3), "gbs": round(gemv_gbs, 1),
+                               "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
         "generated_tokens_head": [int(t) for t in toks[:8]],
     }

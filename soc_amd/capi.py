@@ -121,6 +121,7 @@ def lib() -> C.CDLL:
         "soc_model_synthesize": (C.c_int, [P, U64, F32]),
         "soc_model_finalize": (C.c_int, [P]),
         "soc_model_weight_bytes": (C.c_int, [P, C.POINTER(I64)]),
+        "soc_model_decode_path": (C.c_int, [P, C.POINTER(I32)]),
         "soc_kv_create": (C.c_int, [P, I32, I32, C.POINTER(P)]),
         "soc_kv_destroy": (C.c_int, [P]),
         "soc_kv_length": (C.c_int, [P, I32, C.POINTER(I32)]),
@@ -284,6 +285,12 @@ class Model:
         v = C.c_int64()
         check(lib().soc_model_weight_bytes(self.h, C.byref(v)))
         return v.value
+
+    def decode_path(self) -> str:
+        """"persistent" (one k_decode_persistent launch per token) or "graph" (per-operator kernels)."""
+        v = C.c_int32()
+        check(lib().soc_model_decode_path(self.h, C.byref(v)))
+        return "persistent" if v.value == 1 else "graph"
 
     def close(self) -> None:
         if self.h:

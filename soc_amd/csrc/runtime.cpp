@@ -801,6 +801,15 @@ int soc_model_weight_bytes(const soc_model* m, int64_t* bytes) {
   return SOC_OK;
 }
 
+int soc_model_decode_path(soc_model* m, int32_t* path) {
+  SOC_API_BEGIN
+  if (m == nullptr || path == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  *path = use_persistent(m) ? 1 : 0;
+  return SOC_OK;
+  SOC_API_END
+}
+
 int soc_kv_create(soc_model* m, int32_t slots, int32_t cap, soc_kv** out) {
   SOC_API_BEGIN
   if (m == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
