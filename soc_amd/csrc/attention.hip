@@ -294,6 +294,206 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, int H, con
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Causal GQA attention for a prefill chunk on MFMA (v_mfma_f32_32x32x16_f16), flash-style: one pass over the
+// visible keys in tiles of 32 with an online softmax, K/V tiles staged through LDS (double buffered) and shared by
+// the G query heads of a KV head.
+//
+// Each wave owns 32 query rows of one head. Scores are computed transposed, S^T[key][query] = K . Q^T, so that in
+// the MFMA result layout (lane l holds rows (r/4)*8 + (l/32)*4 + r%4, r = 0..15, of column l%32) a lane owns one
+// query's scores: the running max and sum stay in the lane, and only the lane pair (l, l^32) that splits a query's
+// 32 keys exchanges its max. The same register file then feeds P^T as the B operand of O^T = V^T . P^T: the k index
+// 8*(l/32)+i of that MFMA meets key (i/4)*8 + (l/32)*4 + i%4 of the 16-key step, so V^T is stored in LDS with key
+// bits 2 and 3 swapped, which makes each lane's 8 keys one contiguous 16-byte LDS read.
+//
+// Precision: K and V are exact fp16 (the cache format). q (fp32) is split as hi = f16(q), lo = f16((q - hi) 2^11)
+// into two accumulators; p = exp(s - m) in [0, 1] is split as hi + f16(p - hi) into the same accumulator. Both keep
+// about 22 bits of the fp32 operand, so scores and weighted sums track the fp32 reference
+// (grouped_query_attention.cpp:96-137) to fp32 rounding, with the order of the sums changed.
+// grid = (ceil(B / (32 * 4 / G)), nkv), block = 256 (4 waves: head g*G + w%G, rows 32*(w/G) of the block's tile).
+// ------------------------------------------------------------------------------------------------------------
+namespace {
+constexpr int FA_KT = 32;           // keys per tile
+constexpr int FA_KLD = HD + 8;      // K tile row stride in halves (272 B: 8 consecutive rows hit disjoint banks)
+constexpr int FA_VLD = FA_KT + 8;   // V^T tile row stride in halves (80 B)
+typedef _Float16 fa_h8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ int fa_swizzle(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+}  // namespace
+
+template <int G>
+__global__ __launch_bounds__(256) void k_attention_prefill_mfma(AttnArgs a) {
+  constexpr int SUB = 4 / G;     // 32-row sub-tiles per block
+  constexpr int BP = 32 * SUB;   // query rows per block
+  __shared__ _Float16 Ks[2][FA_KT * FA_KLD];
+  __shared__ _Float16 Vt[2][HD * FA_VLD];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int g = blockIdx.y;
+  const int qt = gridDim.x - 1 - blockIdx.x;  // the longest (last) query tiles start first
+  const int head = g * G + wid % G;
+  const int t0 = qt * BP + (wid / G) * 32;    // first query row of this wave
+  const int ql = lane & 31, hb = lane >> 5;
+  const int t = t0 + ql;
+  const int tq = min(t, a.B - 1);             // rows past the chunk compute a copy of the last row, never stored
+  const int qpos = a.pos_base + tq;           // keys 0..qpos are visible to this row
+  const int blk_last = a.pos_base + min(qt * BP + BP, a.B) - 1;
+  const int ntiles = blk_last / FA_KT + 1;
+  const int wtiles = t0 < a.B ? (a.pos_base + min(t0 + 31, a.B - 1)) / FA_KT + 1 : 0;
+  const int nkeys = blk_last + 1;             // keys written to the cache so far that this block reads
+  const size_t head_base = static_cast<size_t>(a.slot_base) * a.slot_stride +
+                           static_cast<size_t>(a.layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+  const f16* kb = a.kcache + head_base;
+  const f16* vb = a.vcache + head_base;
+
+  // Q^T operand: lane holds q[t][16 ks + 8 hb + i]
+  fa_h8 qh[8], qlo[8];
+  {
+    const float* qrow = a.qkv + static_cast<size_t>(tq) * a.ld_qkv + head * HD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8 + 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = t < a.B ? (i < 4 ? v0[i] : v1[i - 4]) : 0.0f;
+        const _Float16 h = static_cast<_Float16>(v);
+        qh[ks][i] = h;
+        qlo[ks][i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
+      }
+    }
+  }
+
+  // tile staging: 2 x (32 keys x 16 chunks of 8 dims) per thread pair; chunk c: key c % 32, dims 8 (c / 32)
+  u32x4 rk[2], rv[2];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * 256;
+      const int key = kt * FA_KT + (c & 31);
+      const size_t off = static_cast<size_t>(key) * HD + (c >> 5) * 8;
+      rk[u] = key < nkeys ? load16(kb + off) : u32x4{0, 0, 0, 0};
+      rv[u] = key < nkeys ? load16(vb + off) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = tid + u * 256;
+      const int key = c & 31, d0 = (c >> 5) * 8;
+      *reinterpret_cast<u32x4*>(&Ks[buf][key * FA_KLD + d0]) = rk[u];
+      const fa_h8 v = __builtin_bit_cast(fa_h8, rv[u]);
+      const int col = fa_swizzle(key);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Vt[buf][(d0 + i) * FA_VLD + col] = v[i];
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ntiles) load_tile(kt + 1);
+    if (kt < wtiles) {
+      f32x16 sh, sl;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sh[r] = 0.0f;
+        sl[r] = 0.0f;
+      }
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const fa_h8 ka = *reinterpret_cast<const fa_h8*>(&Ks[buf][ql * FA_KLD + ks * 16 + hb * 8]);
+        sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sl, 0, 0, 0);
+      }
+      // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
+      float s[16];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
+        const float v = (sh[r] + sl[r] * (1.0f / 2048.0f)) * a.scale;
+        s[r] = key <= qpos ? v : -INFINITY;
+        mt = fmaxf(mt, s[r]);
+      }
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mn = fmaxf(m, mt);  // finite: key 0 is visible to every row and tile 0 comes first
+      const float corr = expf(m - mn);
+      m = mn;
+      l *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = expf(s[r] - mn);
+        l += s[r];
+      }
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        fa_h8 ph, pl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = s[k2 * 8 + i];
+          ph[i] = static_cast<_Float16>(p);
+          pl[i] = static_cast<_Float16>(p - static_cast<float>(ph[i]));
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const fa_h8 va = *reinterpret_cast<const fa_h8*>(&Vt[buf][(db * 32 + ql) * FA_VLD + k2 * 16 + hb * 8]);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[db], 0, 0, 0);
+        }
+      }
+    }
+    if (kt + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float lt = l + __shfl_xor(l, 32);
+  if (t < a.B) {
+    float* dst = a.out + static_cast<size_t>(t) * a.ld_out + head * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = o[db][r4 * 4 + i] / lt;
+        *reinterpret_cast<f32x4*>(dst + db * 32 + r4 * 8 + hb * 4) = v;
+      }
+  }
+}
+
+hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s) {
+  const int G = a.nq / a.nkv;
+  if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;
+  if (a.ld_qkv % 4 != 0 || a.ld_out % 4 != 0) return hipErrorInvalidValue;
+#define SOC_FA_CASE(GG)                                                                        \
+  if (G == GG) {                                                                               \
+    const dim3 grid((a.B + 32 * (4 / GG) - 1) / (32 * (4 / GG)), a.nkv);                       \
+    hipLaunchKernelGGL((k_attention_prefill_mfma<GG>), grid, dim3(256), 0, s, a);              \
+    return hipGetLastError();                                                                  \
+  }
+  SOC_FA_CASE(1)
+  SOC_FA_CASE(2)
+  SOC_FA_CASE(4)
+#undef SOC_FA_CASE
+  return hipErrorInvalidValue;
+}
+
+bool attention_prefill_mfma_supported(int nq, int nkv) {
+  return nkv > 0 && nq % nkv == 0 && (nq / nkv == 1 || nq / nkv == 2 || nq / nkv == 4);
+}
+
 hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;

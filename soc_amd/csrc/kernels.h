@@ -77,6 +77,10 @@ struct AttnArgs {
 };
 // fused = 1: q/k norm + RoPE + KV append of the new token are done inside (decode).
 hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s);
+// Prefill chunk (pos == slot == nullptr) on MFMA: causal over keys 0..pos_base+row of the slot's cache, which must
+// already hold the chunk's own keys. Supports nq/nkv in {1, 2, 4}; `part`, `counters`, `max_split`, `chunk` unused.
+hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s);
+bool attention_prefill_mfma_supported(int nq, int nkv);
 
 // q/k RMSNorm over each head + RoPE + KV-cache append for T new rows at positions pos_base + t (prefill).
 struct QkNormRopeArgs {

@@ -532,6 +532,15 @@ hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
   return soc::launch_gemm_f32a(g, epi, s);
 }
 
+// Prefill attention runs the MFMA flash kernel where the head grouping allows (SOC_PREFILL_ATTN=rows selects the
+// per-row split-key kernel that decode also uses).
+hipError_t prefill_attention(const soc::AttnArgs& a, hipStream_t s) {
+  const char* mode = std::getenv("SOC_PREFILL_ATTN");
+  const bool rows = mode != nullptr && std::strcmp(mode, "rows") == 0;
+  if (!rows && soc::attention_prefill_mfma_supported(a.nq, a.nkv)) return soc::launch_attention_prefill_mfma(a, s);
+  return soc::launch_attention(a, 0, s);
+}
+
 int validate_ids(const soc_model* m, const int32_t* ids, int n) {
   for (int i = 0; i < n; ++i)
     if (ids[i] < 0 || ids[i] >= m->cfg.vocab_size)
@@ -1002,7 +1011,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     a.counters = w.attn_counters;
     a.B = n;
     a.max_split = (pos_off + n + kAttnChunk - 1) / kAttnChunk;
-    if ((e = soc::launch_attention(a, 0, s)) != hipSuccess) return hip_fail(e, "attention prefill");
+    if ((e = prefill_attention(a, s)) != hipSuccess) return hip_fail(e, "attention prefill");
     g = soc::GemmArgs{};
     g.a = w.attn;
     g.lda = m->qd;

@@ -91,6 +91,40 @@ def test_decode_matches_prefill_rows(gpu_ctx):
         m.close()
 
 
+@pytest.mark.parametrize("nq,nkv", [(2, 2), (4, 2), (8, 2)])
+def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv):
+    """The MFMA flash prefill attention (q and p carried as fp16 hi/lo pairs) agrees with the per-row fp32 kernel to
+    well inside fp32 noise x depth: max |diff| <= 1e-3 * max |logit| over every row, for a single prefill and for a
+    chunked one whose chunk starts off the 32-key tile grid (positions 70.., rows 0..79 of the chunk)."""
+    cfg = S.QwenConfig(vocab_size=384, hidden_size=256, num_hidden_layers=2, num_attention_heads=nq,
+                       num_key_value_heads=nkv, intermediate_size=512, tie_word_embeddings=False)
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, 11))
+    ids = S.synth_tokens(12, "fa", cfg.vocab_size, 150)
+    runs = {}
+    try:
+        for mode in ("rows", "mfma"):
+            if mode == "rows":
+                monkeypatch.setenv("SOC_PREFILL_ATTN", "rows")
+            else:
+                monkeypatch.delenv("SOC_PREFILL_ATTN", raising=False)
+            kv = S.KVCache(m, 1, 160)
+            try:
+                full, tok = S.prefill(m, kv, 0, ids, 0, logit_rows=150)
+                kv.reset(0)
+                S.prefill(m, kv, 0, ids[:70], 0, logit_rows=0)
+                part, tok2 = S.prefill(m, kv, 0, ids[70:], 70, logit_rows=80)
+            finally:
+                kv.close()
+            runs[mode] = (full, tok, part, tok2)
+        for i, what in ((0, "single prefill"), (2, "chunked prefill")):
+            got, ref = runs["mfma"][i], runs["rows"][i]
+            err = float(np.max(np.abs(got - ref)))
+            assert err <= 1e-3 * float(np.max(np.abs(ref))), f"{what}: max abs diff {err:.3e}"
+        assert runs["mfma"][1] == runs["rows"][1] and runs["mfma"][3] == runs["rows"][3]
+    finally:
+        m.close()
+
+
 def test_decode_steps_equal_decode_loop(gpu_ctx):
     cfg, seed, _, _ = SMALL_MODELS["tiny_untied"]
     m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
