@@ -114,6 +114,18 @@ int soc_decode(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, f
 int soc_decode_steps(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, int32_t steps,
                      int32_t* tokens_out);
 
+/* ---- Ragged multi-sequence decode. The reference decodes one sequence per call (GenerationContext::
+ *      DecodeNextToken, Mac/gpu/src/runtime/generation_context.cpp:68-172, one token at pos = len - 1); a batch of n
+ *      rows gives each row exactly that semantics for its own slot, in one pass over the weights: row i feeds
+ *      tokens[i] to slot slots[i] at position = that slot's current length (per-sequence KV length, any mix of
+ *      lengths) and appends its K/V. Slots must be distinct; 1 <= n <= 1024. ---- */
+/* One step. logits: nullable [n][vocab]; next_tokens [n]: greedy ids (lowest index on ties, sampler.cpp:42-48). */
+int soc_decode_batch(soc_model* model, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens,
+                     float* logits, int32_t* next_tokens);
+/* `steps` greedy steps with each row's token fed back on the device; tokens_out [steps][n]. */
+int soc_decode_batch_steps(soc_model* model, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens,
+                           int32_t steps, int32_t* tokens_out);
+
 /* ---- op-level entry points on caller device pointers, queued on the context stream (tests, microbenchmarks).
  *      These replace the reference's op wrappers (Mac/gpu/include/op/*.h, static Run(...)). ---- */
 /* y[N] = W[N][K] . x[K]; W fp16, x fp16, y fp32 (LinearOp/MatMulOp decode mode, matmul_op.mm:143-163). */

@@ -132,6 +132,8 @@ def lib() -> C.CDLL:
         "soc_prefill": (C.c_int, [P, P, I32, P, I32, I32, I32, P, C.POINTER(I32)]),
         "soc_decode": (C.c_int, [P, P, I32, I32, P, C.POINTER(I32)]),
         "soc_decode_steps": (C.c_int, [P, P, I32, I32, I32, P]),
+        "soc_decode_batch": (C.c_int, [P, P, I32, P, P, P, P]),
+        "soc_decode_batch_steps": (C.c_int, [P, P, I32, P, P, I32, P]),
         "soc_gemv_f16": (C.c_int, [P, P, P, P, I32, I32]),
         "soc_qmm": (C.c_int, [P, P, P, I32, P, P, I32, I32, I32]),
         "soc_dequant": (C.c_int, [P, P, I32, P, P, I32, I32]),
@@ -360,6 +362,29 @@ def decode(model: Model, kv: KVCache, slot: int, last_token: int, want_logits: b
 def decode_steps(model: Model, kv: KVCache, slot: int, last_token: int, steps: int) -> np.ndarray:
     out = np.empty(steps, dtype=np.int32)
     check(lib().soc_decode_steps(model.h, kv.h, slot, int(last_token), steps, _ptr(out)))
+    return out
+
+
+def decode_batch(model: Model, kv: KVCache, slots, tokens, want_logits: bool = True):
+    """One ragged decode step: row i feeds tokens[i] to slot slots[i] at that slot's current length.
+    Returns (logits [n][V] or None, next tokens [n])."""
+    slots = np.ascontiguousarray(slots, dtype=np.int32)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    n = int(slots.size)
+    logits = np.empty((n, model.cfg.vocab_size), dtype=np.float32) if want_logits else None
+    nxt = np.empty(n, dtype=np.int32)
+    check(lib().soc_decode_batch(model.h, kv.h, n, _ptr(slots), _ptr(tokens),
+                                 _ptr(logits) if logits is not None else None, _ptr(nxt)))
+    return logits, nxt
+
+
+def decode_batch_steps(model: Model, kv: KVCache, slots, tokens, steps: int) -> np.ndarray:
+    """`steps` greedy ragged decode steps, tokens fed back on the device. Returns [steps][n] token ids."""
+    slots = np.ascontiguousarray(slots, dtype=np.int32)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    n = int(slots.size)
+    out = np.empty((steps, n), dtype=np.int32)
+    check(lib().soc_decode_batch_steps(model.h, kv.h, n, _ptr(slots), _ptr(tokens), steps, _ptr(out)))
     return out
 
 

@@ -248,7 +248,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 // grid = (T, nq + nkv), block = 64: one wave per (row, head). q heads -> q_out; k heads -> cache (and v copy).
 __global__ __launch_bounds__(64) void k_qk_norm_rope_append(QkNormRopeArgs a) {
   const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const int pos = a.pos_base + t;
+  const int pos = a.pos != nullptr ? a.pos[t] : a.pos_base + t;
+  const int slot = a.slots != nullptr ? a.slots[t] : a.slot;
   const float* row = a.qkv + static_cast<size_t>(t) * a.ld_qkv;
   const float* cr = a.rope_cos + static_cast<size_t>(pos) * (HD / 2);
   const float* sr = a.rope_sin + static_cast<size_t>(pos) * (HD / 2);
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_append(QkNormRopeArgs a) {
     const float* vs = row + (a.nq + a.nkv) * HD + g * HD;
     float x0 = ks[lane], x1 = ks[lane + 64];
     norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
-    const size_t base = static_cast<size_t>(a.slot) * a.slot_stride + static_cast<size_t>(a.layer) * a.layer_stride +
+    const size_t base = static_cast<size_t>(slot) * a.slot_stride + static_cast<size_t>(a.layer) * a.layer_stride +
                         static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(pos) * HD;
     a.kcache[base + lane] = static_cast<f16>(x0);
     a.kcache[base + lane + 64] = static_cast<f16>(x1);

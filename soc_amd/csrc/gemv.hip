@@ -334,6 +334,59 @@ hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// One block per logit row: the greedy token (the first index holding the maximum, like the strict `>` scan of
+// Sampler::SampleFromLogits, sampler.cpp:42-48), fed back as the row's next input id at the next position.
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float* logits, int V, int32_t* ids, int32_t* pos,
+                                                      const int32_t* start, int32_t* ring, int ring_stride) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const float* x = logits + static_cast<size_t>(row) * V;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < V; i += 1024) {
+    const float v = x[i];
+    if (v > bv) {  // strided scan: the first (lowest) index of this thread's maxima
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sv[wid] = bv;
+    si[wid] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    if (bi == 0x7fffffff) bi = 0;  // every logit NaN: token 0
+    const int p = pos[row];
+    const int k = p - start[row];
+    if (k >= 0 && k < ring_stride) ring[static_cast<size_t>(row) * ring_stride + k] = bi;
+    ids[row] = bi;
+    pos[row] = p + 1;
+  }
+}
+
+hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, int32_t* pos, const int32_t* start,
+                              int32_t* ring, int ring_stride, hipStream_t s) {
+  if (n <= 0 || V <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_argmax_rows, dim3(n), dim3(1024), 0, s, logits, V, ids, pos, start, ring, ring_stride);
+  return hipGetLastError();
+}
+
 hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
   const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(float);
   const dim3 grid(gemv_grid(a.N, 2)), block(256);

@@ -97,8 +97,15 @@ struct QkNormRopeArgs {
   long long slot_stride, layer_stride;
   int slot, layer, cap, pos_base;
   int T, nq, nkv;
+  const int32_t* pos;    // nullable [T]: row t sits at position pos[t] of slot slots[t] (ragged decode batch);
+  const int32_t* slots;  //   nullptr: row t at position pos_base + t of `slot` (prefill chunk)
 };
 hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s);
+
+// Greedy token of each of n logit rows (lowest index among equal maxima) for a ragged decode batch: writes it as
+// the row's next input id, records it at ring[row * ring_stride + (pos[row] - start[row])] and advances pos[row].
+hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, int32_t* pos, const int32_t* start,
+                              int32_t* ring, int ring_stride, hipStream_t s);
 
 // ---- persistent batch-1 decode step (one launch per token) ----
 struct PersistArgs {

@@ -3,6 +3,7 @@
 // device memory so that consecutive steps need no host round trip).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstdio>
@@ -89,7 +90,15 @@ struct PrefillWs {
   std::vector<void*> allocs;
 };
 
+// Per-row state of a ragged decode batch (device arrays of `cap` rows).
+struct BatchWs {
+  int cap = 0;
+  int32_t *ids = nullptr, *pos = nullptr, *start = nullptr, *slots = nullptr, *ring1 = nullptr;
+  std::vector<void*> allocs;
+};
+
 constexpr int kAttnChunk = 256;
+constexpr int kMaxBatchRows = 1024;
 
 }  // namespace
 
@@ -108,6 +117,7 @@ struct soc_model {
   DecodeWs dws;
   int dws_gen = 0;  // bumped whenever the decode scratch is reallocated (captured graphs refer to it)
   PrefillWs pws;
+  BatchWs bws;
   bool finalized = false;
 };
 
@@ -532,6 +542,9 @@ hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
   return soc::launch_gemm_f32a(g, epi, s);
 }
 
+// Projections of a ragged decode batch (M = rows of the batch).
+hipError_t batch_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) { return prefill_gemm(g, epi, s); }
+
 // Prefill attention runs the MFMA flash kernel where the head grouping allows (SOC_PREFILL_ATTN=rows selects the
 // per-row split-key kernel that decode also uses).
 hipError_t prefill_attention(const soc::AttnArgs& a, hipStream_t s) {
@@ -545,6 +558,175 @@ int validate_ids(const soc_model* m, const int32_t* ids, int n) {
   for (int i = 0; i < n; ++i)
     if (ids[i] < 0 || ids[i] >= m->cfg.vocab_size)
       return soc::fail(SOC_ERR_INVALID, "token id out of range");  // embedding.cpp:66-68
+  return SOC_OK;
+}
+
+
+int ensure_batch_ws(soc_model* m, int n) {
+  BatchWs& b = m->bws;
+  if (b.cap >= n) return SOC_OK;
+  hipError_t e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  free_all(b.allocs);
+  b = BatchWs();
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.ids));
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.pos));
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.start));
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.slots));
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.ring1));
+  b.cap = n;
+  return SOC_OK;
+}
+
+// Checks a ragged batch: 1 <= n <= kMaxBatchRows, distinct slots in range, valid token ids, room for `steps` more
+// positions in every slot. Returns the largest final length in *max_len.
+int validate_batch(soc_model* m, soc_kv* kv, int n, const int32_t* slots, const int32_t* tokens, int steps,
+                   int* max_len) {
+  if (m == nullptr || kv == nullptr || slots == nullptr || tokens == nullptr)
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (n <= 0 || n > kMaxBatchRows) return soc::fail(SOC_ERR_INVALID, "batch size must be in [1, 1024]");
+  std::vector<char> seen(kv->slots, 0);
+  int ml = 0;
+  for (int i = 0; i < n; ++i) {
+    const int sl = slots[i];
+    if (sl < 0 || sl >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+    if (seen[sl]) return soc::fail(SOC_ERR_INVALID, "a slot appears twice in the batch");
+    seen[sl] = 1;
+    if (kv->len[sl] + steps > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
+    ml = std::max(ml, kv->len[sl] + steps);
+  }
+  SOC_TRY(validate_ids(m, tokens, n));
+  *max_len = ml;
+  return SOC_OK;
+}
+
+// Queues one decode step of the n rows in m->bws: row i runs token ids[i] at position pos[i] of KV slot slots[i].
+// Its greedy token is written back to ids[i], recorded in ring[i * ring_stride + pos[i] - start[i]], and pos[i]
+// advances. Used eagerly and under graph capture (every per-step quantity lives in device memory).
+int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* ring, int ring_stride) {
+  const soc_qwen_config& c = m->cfg;
+  PrefillWs& w = m->pws;
+  BatchWs& b = m->bws;
+  hipStream_t s = m->ctx->stream;
+  const int H = c.hidden_size;
+  hipError_t e;
+  if ((e = soc::launch_embed(b.ids, n, m->embed, H, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const DevLayer& L = m->layers[l];
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    soc::GemmArgs g{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = L.wqkv;
+    g.c = w.qkv;
+    g.ldc = m->qkv_rows;
+    g.M = n;
+    g.N = m->qkv_rows;
+    g.K = H;
+    if ((e = batch_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    soc::QkNormRopeArgs q{};
+    q.qkv = w.qkv;
+    q.ld_qkv = m->qkv_rows;
+    q.q_gain = L.q_norm;
+    q.k_gain = L.k_norm;
+    q.eps = c.rms_norm_eps;
+    q.rope_cos = m->rope_cos;
+    q.rope_sin = m->rope_sin;
+    q.q_out = w.q;
+    q.kcache = kv->k;
+    q.vcache = kv->v;
+    q.slot_stride = kv->slot_stride;
+    q.layer_stride = kv->layer_stride;
+    q.layer = l;
+    q.cap = kv->cap;
+    q.T = n;
+    q.nq = c.num_attention_heads;
+    q.nkv = c.num_key_value_heads;
+    q.pos = b.pos;
+    q.slots = b.slots;
+    if ((e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
+    soc::AttnArgs a = attn_args(m, kv, l);
+    a.qkv = w.q;
+    a.ld_qkv = m->qd;
+    a.pos = b.pos;
+    a.slot = b.slots;
+    a.out = w.attn;
+    a.ld_out = m->qd;
+    a.part = w.part;
+    a.counters = w.attn_counters;
+    a.B = n;
+    a.max_split = max_split;
+    if ((e = soc::launch_attention(a, 0, s)) != hipSuccess) return hip_fail(e, "attention");
+    g = soc::GemmArgs{};
+    g.a = w.attn;
+    g.lda = m->qd;
+    g.w = L.wo;
+    g.c = w.x;
+    g.ldc = H;
+    g.M = n;
+    g.N = H;
+    g.K = m->qd;
+    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    g = soc::GemmArgs{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = L.wgate;
+    g.w2 = L.wup;
+    g.c = w.h;
+    g.ldc = c.intermediate_size;
+    g.M = n;
+    g.N = c.intermediate_size;
+    g.K = H;
+    if ((e = batch_gemm(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    g = soc::GemmArgs{};
+    g.a = w.h;
+    g.lda = c.intermediate_size;
+    g.w = L.wdown;
+    g.c = w.x;
+    g.ldc = H;
+    g.M = n;
+    g.N = H;
+    g.K = c.intermediate_size;
+    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+  }
+  if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+    return hip_fail(e, "rmsnorm");
+  soc::GemmArgs g{};
+  g.a = w.xn;
+  g.lda = H;
+  g.w = m->lm_head;
+  g.c = w.logits;
+  g.ldc = c.vocab_size;
+  g.M = n;
+  g.N = c.vocab_size;
+  g.K = H;
+  if ((e = batch_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+  if ((e = soc::launch_argmax_rows(w.logits, c.vocab_size, n, b.ids, b.pos, b.start, ring, ring_stride, s)) !=
+      hipSuccess)
+    return hip_fail(e, "argmax");
+  return SOC_OK;
+}
+
+// Uploads the batch's rows (ids, positions = current lengths, slots) into m->bws.
+int upload_batch(soc_model* m, soc_kv* kv, int n, const int32_t* slots, const int32_t* tokens,
+                 std::vector<int32_t>* pos_host) {
+  hipStream_t s = m->ctx->stream;
+  BatchWs& b = m->bws;
+  pos_host->resize(n);
+  for (int i = 0; i < n; ++i) (*pos_host)[i] = kv->len[slots[i]];
+  hipError_t e;
+  if ((e = hipMemcpyAsync(b.ids, tokens, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s)) != hipSuccess ||
+      (e = hipMemcpyAsync(b.slots, slots, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s)) != hipSuccess ||
+      (e = hipMemcpyAsync(b.pos, pos_host->data(), static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s)) !=
+          hipSuccess ||
+      (e = hipMemcpyAsync(b.start, pos_host->data(), static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s)) !=
+          hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync batch");
   return SOC_OK;
 }
 
@@ -748,6 +930,7 @@ int soc_model_destroy(soc_model* m) {
   (void)hipStreamSynchronize(m->ctx->stream);
   free_all(m->dws.allocs);
   free_all(m->pws.allocs);
+  free_all(m->bws.allocs);
   (void)hipFree(m->wbuf);
   (void)hipFree(m->rope_cos);
   (void)hipFree(m->rope_sin);
@@ -1135,6 +1318,82 @@ int soc_decode_steps(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, int32
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync tokens");
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode steps");
   kv->len[slot] += steps;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_decode_batch(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens, float* logits,
+                     int32_t* next_tokens) {
+  SOC_API_BEGIN
+  if (next_tokens == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  int max_len = 0;
+  SOC_TRY(validate_batch(m, kv, n, slots, tokens, 1, &max_len));
+  SOC_TRY(ensure_prefill_ws(m, n, max_len, n));
+  SOC_TRY(ensure_batch_ws(m, n));
+  std::vector<int32_t> pos;
+  SOC_TRY(upload_batch(m, kv, n, slots, tokens, &pos));
+  SOC_TRY(enqueue_batch_step(m, kv, n, (max_len + kAttnChunk - 1) / kAttnChunk, m->bws.ring1, 1));
+  hipStream_t s = m->ctx->stream;
+  hipError_t e;
+  if (logits != nullptr &&
+      (e = hipMemcpyAsync(logits, m->pws.logits, static_cast<size_t>(n) * m->cfg.vocab_size * 4,
+                          hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync logits");
+  if ((e = hipMemcpyAsync(next_tokens, m->bws.ids, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, s)) !=
+      hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync tokens");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode batch");
+  for (int i = 0; i < n; ++i) kv->len[slots[i]] += 1;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_decode_batch_steps(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens,
+                           int32_t steps, int32_t* tokens_out) {
+  SOC_API_BEGIN
+  if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
+  if (steps > 0 && tokens_out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  int max_len = 0;
+  SOC_TRY(validate_batch(m, kv, n, slots, tokens, steps, &max_len));
+  if (steps == 0) return SOC_OK;
+  SOC_TRY(ensure_prefill_ws(m, n, max_len, n));
+  SOC_TRY(ensure_batch_ws(m, n));
+  std::vector<int32_t> pos;
+  SOC_TRY(upload_batch(m, kv, n, slots, tokens, &pos));
+  hipStream_t s = m->ctx->stream;
+  int32_t* ring = nullptr;
+  hipError_t e = hipMalloc(&ring, static_cast<size_t>(n) * steps * 4);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc ring");
+  std::unique_ptr<int32_t, void (*)(int32_t*)> ring_guard(ring, [](int32_t* p) { (void)hipFree(p); });
+  const int max_split = (max_len + kAttnChunk - 1) / kAttnChunk;
+  if (env_flag("SOC_EAGER")) {
+    for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_batch_step(m, kv, n, max_split, ring, steps));
+  } else {
+    // one step captured once and replayed: per-step state (ids, positions) advances in device memory
+    hipGraph_t graph;
+    if ((e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+      return hip_fail(e, "hipStreamBeginCapture");
+    const int rc = enqueue_batch_step(m, kv, n, max_split, ring, steps);
+    e = hipStreamEndCapture(s, &graph);
+    if (rc != SOC_OK) return rc;
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t exec;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(exec, s);
+    const hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipGraphExecDestroy(exec);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+    if (e2 != hipSuccess) return hip_fail(e2, "decode batch steps");
+  }
+  std::vector<int32_t> host(static_cast<size_t>(n) * steps);
+  if ((e = hipMemcpyAsync(host.data(), ring, host.size() * 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync tokens");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode batch steps");
+  for (int t = 0; t < steps; ++t)
+    for (int i = 0; i < n; ++i) tokens_out[static_cast<size_t>(t) * n + i] = host[static_cast<size_t>(i) * steps + t];
+  for (int i = 0; i < n; ++i) kv->len[slots[i]] += steps;
   return SOC_OK;
   SOC_API_END
 }
