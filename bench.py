@@ -80,6 +80,50 @@ def bench_prefill(ctx, m, cfg, n: int = 2048):
     return ms
 
 
+RAGGED_SEQS, RAGGED_STEPS, RAGGED_MIN, RAGGED_MAX = 16, 64, 64, 4096
+
+
+def ragged_bytes_per_step(cfg: S.QwenConfig, kv_lens) -> float:
+    """Algorithmic HBM bytes of one ragged step: every weight once (tied head once), gains, one embedding row per
+    sequence, and each sequence's fp16 KV read of S_i positions plus the write of one."""
+    H, I, L = cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers
+    per_layer = (cfg.q_dim + 2 * cfg.kv_dim) * H + H * cfg.q_dim + 3 * I * H
+    weights = 2 * (L * per_layer + cfg.vocab_size * H)
+    gains = 2 * (L * (2 * H + 2 * cfg.head_dim) + H)
+    kv_pos = L * 2 * cfg.num_key_value_heads * cfg.head_dim * 2
+    return weights + gains + len(kv_lens) * 2 * H + kv_pos * float(sum(s + 1 for s in kv_lens))
+
+
+def bench_ragged(ctx):
+    """Qwen3-4B ragged continuous-batch decode: 16 sequences with seeded KV lengths U[64, 4096] (seeded N(0,1) fp16
+    cache contents), 64 greedy steps of one token per sequence, each step one replay of the captured batch step."""
+    cfg = S.QWEN3_4B
+    m = S.Model(ctx, cfg).synthesize(1, 0.02)
+    lens = S.synth_int_uniform(5, "ragged.kv_len", RAGGED_MIN, RAGGED_MAX, RAGGED_SEQS).astype(np.int64)
+    kv = S.KVCache(m, RAGGED_SEQS, RAGGED_MAX + 2 * RAGGED_STEPS + 8)
+    try:
+        for slot, n in enumerate(lens):
+            kv.fill_synthetic(slot, int(n), 7)
+        slots = np.arange(RAGGED_SEQS, dtype=np.int32)
+        toks = S.synth_tokens(6, "ragged.tokens", cfg.vocab_size, RAGGED_SEQS)
+        warm = S.decode_batch_steps(m, kv, slots, toks, RAGGED_STEPS)  # builds and replays the step graph
+        start = [kv.length(int(i)) for i in slots]
+        ctx.synchronize()
+        ctx.timer_start()
+        out = S.decode_batch_steps(m, kv, slots, warm[-1], RAGGED_STEPS)
+        ms = ctx.timer_stop()
+    finally:
+        kv.close()
+        m.close()
+    per_step = ms / RAGGED_STEPS
+    mean_bytes = np.mean([ragged_bytes_per_step(cfg, [s + t for s in start]) for t in range(RAGGED_STEPS)])
+    gbs = mean_bytes / (per_step * 1e-3) / 1e9
+    return {"workload": "Qwen3-4B ragged decode, 16 sequences, KV lengths U[64,4096] (seed 5), 64 steps",
+            "kv_lengths": [int(x) for x in lens], "tok_s": round(RAGGED_SEQS * RAGGED_STEPS / (ms * 1e-3), 1),
+            "ms_per_step": round(per_step, 4), "bytes_per_step": int(mean_bytes), "hbm_gbs": round(gbs, 1),
+            "hbm_roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_head": [int(t) for t in out[0][:4]]}
+
+
 def bench_gemv_kernel(ctx, n=4096, k=1024, iters=200):
     """Average duration of the decode GEMV kernel over weight copies that defeat the Infinity Cache."""
     wbytes = n * k * 2
@@ -176,6 +220,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the Qwen3-4B ragged decode measurement")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -199,6 +244,7 @@ def main() -> None:
     us, alg = bench_gemv_kernel(ctx)
     gemv_gbs = alg / (us * 1e-6) / 1e9
     m.close()
+    ragged = None if args.no_ragged else bench_ragged(ctx)
     ctx.close()
 
     if path == "persistent":
@@ -240,6 +286,7 @@ def main() -> None:
         "roofline": roofline,
         "gemv_qkv_4096x1024": {"avg_launch_us": round(us, 3), "gbs": round(gemv_gbs, 1),
                                "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+        "ragged_4b": ragged,
         "cpu_baseline": cpu,
         "generated_tokens_head": [int(t) for t in toks[:8]],
     }

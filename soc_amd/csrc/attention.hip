@@ -15,6 +15,7 @@ namespace soc {
 namespace {
 
 constexpr int HD = 128;  // head_dim handled by these kernels
+constexpr int kMaxCombine = 160;  // key chunks one attention row may be split into (160 x 256 = 40960 keys)
 
 // Lane l of a wave holds dims (l, l + 64) of one head vector: RMSNorm over the 128 values and rotate-half RoPE at
 // table row `pos` (cos/sin precomputed on the host in double, then rounded to float, like rope.cpp:77-79).
@@ -40,6 +41,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   __shared__ float sc[G][256];
   __shared__ float red[4][G][HD];
   __shared__ float mstat[G], lstat[G];
+  __shared__ float cm[G][kMaxCombine], cl[G][kMaxCombine];  // split combine: chunk maxima / weights, sums
   __shared__ int last;
 
   const int b = blockIdx.z, g = blockIdx.y, s = blockIdx.x;
@@ -214,35 +216,58 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int j = idx / HD, i = idx % HD;
     const float o = red[0][j][i] + red[1][j][i] + red[2][j][i] + red[3][j][i];
     float* p = a.part + ((static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split + s) * stride;
-    p[i] = o;
+    st_dev(p + i, o);
     if (i == 0) {
-      p[HD] = mstat[j];
-      p[HD + 1] = lstat[j];
+      st_dev(p + HD, mstat[j]);
+      st_dev(p + HD + 1, lstat[j]);
     }
   }
-  __threadfence();
+  wait_mem();  // partials (device-scope stores) complete before this block is counted
   __syncthreads();
   if (tid == 0) {
     const int done = atomicAdd(a.counters + b * a.nkv + g, 1);
     last = (done == nact - 1);
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
+  if (!last) return;  // the last block reads every partial with device-scope loads
+  // combine: every chunk's (m, l) first, all loads in flight at once, then the weighted sums over chunks with the
+  // partial outputs fetched eight chunks at a time (the loads are independent; only their sum is ordered)
+  for (int idx = tid; idx < G * nact; idx += 256) {
+    const int j = idx / nact, t = idx % nact;
+    const float* pj = a.part + ((static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split + t) * stride;
+    cm[j][t] = ld_dev(pj + HD);
+    cl[j][t] = ld_dev(pj + HD + 1);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int t = 0; t < nact; ++t) M = fmaxf(M, cm[tid][t]);
+    float L = 0.0f;
+    for (int t = 0; t < nact; ++t) {
+      const float e = expf(cm[tid][t] - M);
+      cm[tid][t] = e;
+      L += cl[tid][t] * e;
+    }
+    lstat[tid] = L;
+  }
+  __syncthreads();
   for (int idx = tid; idx < G * HD; idx += 256) {
     const int j = idx / HD, i = idx % HD;
-    const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split * stride;
-    float M = -INFINITY;
-    for (int t = 0; t < nact; ++t) M = fmaxf(M, ld_dev(p0 + t * stride + HD));
-    float L = 0.0f, O = 0.0f;
-    for (int t = 0; t < nact; ++t) {
-      const float e = expf(ld_dev(p0 + t * stride + HD) - M);
-      L += ld_dev(p0 + t * stride + HD + 1) * e;
-      O += ld_dev(p0 + t * stride + i) * e;
+    const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split * stride + i;
+    const float* ej = cm[j];
+    float O = 0.0f;
+    int t = 0;
+    for (; t + 8 <= nact; t += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = ld_dev(p0 + (t + u) * stride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) O += v[u] * ej[t + u];
     }
-    a.out[static_cast<size_t>(b) * a.ld_out + (g * G + j) * HD + i] = O / L;
+    for (; t < nact; ++t) O += ld_dev(p0 + t * stride) * ej[t];
+    a.out[static_cast<size_t>(b) * a.ld_out + (g * G + j) * HD + i] = O / lstat[j];
   }
-  if (tid == 0) a.counters[b * a.nkv + g] = 0;
+  if (tid == 0) st_dev(a.counters + b * a.nkv + g, 0);
 }
 
 // grid = (T, nq + nkv), block = 64: one wave per (row, head). q heads -> q_out; k heads -> cache (and v copy).
@@ -498,6 +523,7 @@ bool attention_prefill_mfma_supported(int nq, int nkv) {
 hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;
+  if (a.max_split > kMaxCombine) return hipErrorInvalidValue;
   const dim3 grid(a.max_split, a.nkv, a.B), block(256);
 #define SOC_ATTN_CASE(GG)                                                                  \
   if (G == GG) {                                                                          \

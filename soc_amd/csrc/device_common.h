@@ -86,4 +86,13 @@ __device__ __forceinline__ int32_t ld_dev(const int32_t* p) {
   return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Waits until this wave's earlier memory accesses have completed. After device-scope (write-through) stores this
+// makes them visible to any agent-scope reader, so a following relaxed counter update publishes them without a
+// full release fence (which on gfx950 writes back and invalidates the whole L2 of the XCD).
+__device__ __forceinline__ void wait_mem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace soc

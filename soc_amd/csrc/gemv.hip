@@ -159,15 +159,14 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
         v = bv[w];
         i = bi[w];
       }
-    a.part_val[blockIdx.x] = v;
-    a.part_idx[blockIdx.x] = i;
-    __threadfence();
+    st_dev(a.part_val + blockIdx.x, v);
+    st_dev(a.part_idx + blockIdx.x, i);
+    wait_mem();  // the block's candidate is visible device-wide before it is counted
     const int done = atomicAdd(a.counter, 1);
     last = (done == static_cast<int>(gridDim.x) - 1);
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
+  if (!last) return;  // the last block reads every candidate with device-scope loads
   float v = -INFINITY;
   int i = 0x7fffffff;
   for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) {
@@ -206,7 +205,7 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
     }
     if (a.ring != nullptr) a.ring[a.ring_pos != nullptr ? a.ring_pos[0] : 0] = tok;
     if (a.ring_pos != nullptr) a.ring_pos[0] += 1;
-    *a.counter = 0;
+    st_dev(a.counter, 0);
   }
 }
 

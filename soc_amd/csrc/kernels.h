@@ -163,4 +163,24 @@ hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
 bool gemm_mfma_supported(const GemmArgs& g);
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s);
 
+// Skinny projection of a ragged decode batch: c[M][.] (epi) x[M][K] . [w | w2]^T for 1 <= M <= 16, K % 256 == 0.
+// Rows 0..N0-1 come from w, rows N0..Ntot-1 from w2 (SwiGLU: Ntot = 2 N0, c = silu(gate) * up over N0 outputs;
+// store/residual: Ntot = N0). part: split-K scratch of skinny_part_floats(Ntot, K) floats.
+struct SkinnyArgs {
+  const float* x;
+  int ldx;
+  const f16* w;
+  const f16* w2;
+  int N0, Ntot, K, M;
+  float* part;
+  float* c;
+  int ldc;
+  int KS, Kb;  // set by the launcher
+};
+bool skinny_supported(int M, int K);
+int skinny_splits(int rows, int K);
+size_t skinny_part_floats(int rows, int K);
+hipError_t skinny_configure();
+hipError_t launch_skinny(const SkinnyArgs& a, int epi, hipStream_t s);
+
 }  // namespace soc

@@ -12,6 +12,7 @@
 #include <memory>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "kernels.h"
@@ -88,6 +89,7 @@ struct PrefillWs {
   int *ids = nullptr, *attn_counters = nullptr, *lm_idx = nullptr, *lm_counter = nullptr, *token = nullptr;
   int cap_logit_rows = 0;
   std::vector<void*> allocs;
+  float* skpart = nullptr;  // split-K partials of the skinny batch projections
 };
 
 // Per-row state of a ragged decode batch (device arrays of `cap` rows).
@@ -95,6 +97,8 @@ struct BatchWs {
   int cap = 0;
   int32_t *ids = nullptr, *pos = nullptr, *start = nullptr, *slots = nullptr, *ring1 = nullptr;
   std::vector<void*> allocs;
+  int32_t* ring = nullptr;  // [rows][steps] tokens of soc_decode_batch_steps
+  size_t ring_cap = 0;
 };
 
 constexpr int kAttnChunk = 256;
@@ -116,6 +120,7 @@ struct soc_model {
   const f16** d_layer_w = nullptr;  // device copy of the per-layer weight pointers [L][9]
   DecodeWs dws;
   int dws_gen = 0;  // bumped whenever the decode scratch is reallocated (captured graphs refer to it)
+  int bws_gen = 0;  // bumped whenever the prefill/batch scratch is reallocated (captured batch graphs refer to it)
   PrefillWs pws;
   BatchWs bws;
   bool finalized = false;
@@ -128,6 +133,8 @@ struct soc_kv {
   long long slot_stride = 0, layer_stride = 0;
   std::vector<int32_t> len;
   std::map<int, std::pair<int, hipGraphExec_t>> graphs;  // decode graph per slot, tagged with the scratch generation
+  // batch-step graphs keyed by (rows, steps), tagged with the scratch generation
+  std::map<std::pair<int, int>, std::pair<int, hipGraphExec_t>> batch_graphs;
 };
 
 namespace {
@@ -232,6 +239,8 @@ int ensure_decode_ws(soc_model* m, int cap) {
   return SOC_OK;
 }
 
+size_t skinny_scratch_floats(const soc_model* m);
+
 int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
   PrefillWs& w = m->pws;
   const int need_split = (total_len + kAttnChunk - 1) / kAttnChunk;
@@ -239,6 +248,7 @@ int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
   hipError_t e = hipStreamSynchronize(m->ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   free_all(w.allocs);
+  ++m->bws_gen;
   const int R = std::max(rows, w.cap_rows), SP = std::max(need_split, w.cap_split),
             LR = std::max(std::max(logit_rows, 1), w.cap_logit_rows);
   w = PrefillWs();
@@ -258,6 +268,10 @@ int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
   SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_idx));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.lm_counter));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.token));
+  if (const size_t sk = skinny_scratch_floats(m)) {
+    SOC_TRY(dev_alloc_t(w.allocs, sk, &w.skpart));
+    if ((e = soc::skinny_configure()) != hipSuccess) return hip_fail(e, "skinny kernel attributes");
+  }
   if ((e = hipMemset(w.attn_counters, 0, static_cast<size_t>(R) * c.num_key_value_heads * sizeof(int))) != hipSuccess)
     return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.lm_counter, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
@@ -542,8 +556,44 @@ hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
   return soc::launch_gemm_f32a(g, epi, s);
 }
 
-// Projections of a ragged decode batch (M = rows of the batch).
-hipError_t batch_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) { return prefill_gemm(g, epi, s); }
+// Projections of a ragged decode batch (M = rows of the batch): the skinny MFMA kernel in slabs of 16 rows up to
+// 64 rows (SOC_BATCH_GEMM=tile selects the 128x128-tile GEMM of the prefill path).
+hipError_t batch_gemm(const soc::GemmArgs& g, int epi, float* part, hipStream_t s) {
+  const char* mode = std::getenv("SOC_BATCH_GEMM");
+  const bool tile = mode != nullptr && std::strcmp(mode, "tile") == 0;
+  if (tile || part == nullptr || g.M > 64 || !soc::skinny_supported(1, g.K)) return prefill_gemm(g, epi, s);
+  for (int m0 = 0; m0 < g.M; m0 += 16) {
+    soc::SkinnyArgs a{};
+    a.x = g.a + static_cast<size_t>(m0) * g.lda;
+    a.ldx = g.lda;
+    a.w = g.w;
+    a.w2 = epi == soc::EPI_SWIGLU ? g.w2 : nullptr;
+    a.N0 = g.N;
+    a.Ntot = epi == soc::EPI_SWIGLU ? 2 * g.N : g.N;
+    a.K = g.K;
+    a.M = std::min(16, g.M - m0);
+    a.part = part;
+    a.c = g.c + static_cast<size_t>(m0) * g.ldc;
+    a.ldc = g.ldc;
+    const hipError_t e = soc::launch_skinny(a, epi, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// Largest split-K scratch any projection of the model needs in the skinny kernel (floats).
+size_t skinny_scratch_floats(const soc_model* m) {
+  const soc_qwen_config& c = m->cfg;
+  const int H = c.hidden_size, I = c.intermediate_size;
+  if (H % 256 != 0 || I % 256 != 0 || m->qd % 256 != 0) return 0;
+  size_t need = 0;
+  need = std::max(need, soc::skinny_part_floats(m->qkv_rows, H));
+  need = std::max(need, soc::skinny_part_floats(H, m->qd));
+  need = std::max(need, soc::skinny_part_floats(2 * I, H));
+  need = std::max(need, soc::skinny_part_floats(H, I));
+  need = std::max(need, soc::skinny_part_floats(c.vocab_size, H));
+  return need;
+}
 
 // Prefill attention runs the MFMA flash kernel where the head grouping allows (SOC_PREFILL_ATTN=rows selects the
 // per-row split-key kernel that decode also uses).
@@ -568,6 +618,8 @@ int ensure_batch_ws(soc_model* m, int n) {
   hipError_t e = hipStreamSynchronize(m->ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   free_all(b.allocs);
+  (void)hipFree(b.ring);
+  ++m->bws_gen;
   b = BatchWs();
   SOC_TRY(dev_alloc_t(b.allocs, n, &b.ids));
   SOC_TRY(dev_alloc_t(b.allocs, n, &b.pos));
@@ -626,7 +678,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.M = n;
     g.N = m->qkv_rows;
     g.K = H;
-    if ((e = batch_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    if ((e = batch_gemm(g, soc::EPI_STORE, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
     soc::QkNormRopeArgs q{};
     q.qkv = w.qkv;
     q.ld_qkv = m->qkv_rows;
@@ -669,7 +721,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.M = n;
     g.N = H;
     g.K = m->qd;
-    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm o");
     if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
@@ -682,7 +734,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.M = n;
     g.N = c.intermediate_size;
     g.K = H;
-    if ((e = batch_gemm(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    if ((e = batch_gemm(g, soc::EPI_SWIGLU, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
     g = soc::GemmArgs{};
     g.a = w.h;
     g.lda = c.intermediate_size;
@@ -692,7 +744,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.M = n;
     g.N = H;
     g.K = c.intermediate_size;
-    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm down");
   }
   if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
     return hip_fail(e, "rmsnorm");
@@ -705,7 +757,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
   g.M = n;
   g.N = c.vocab_size;
   g.K = H;
-  if ((e = batch_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+  if ((e = batch_gemm(g, soc::EPI_STORE, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
   if ((e = soc::launch_argmax_rows(w.logits, c.vocab_size, n, b.ids, b.pos, b.start, ring, ring_stride, s)) !=
       hipSuccess)
     return hip_fail(e, "argmax");
@@ -931,6 +983,7 @@ int soc_model_destroy(soc_model* m) {
   free_all(m->dws.allocs);
   free_all(m->pws.allocs);
   free_all(m->bws.allocs);
+  (void)hipFree(m->bws.ring);
   (void)hipFree(m->wbuf);
   (void)hipFree(m->rope_cos);
   (void)hipFree(m->rope_sin);
@@ -1034,6 +1087,7 @@ int soc_kv_destroy(soc_kv* kv) {
   if (kv == nullptr) return SOC_OK;
   (void)hipStreamSynchronize(kv->model->ctx->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second.second);
+  for (auto& g : kv->batch_graphs) (void)hipGraphExecDestroy(g.second.second);
   (void)hipFree(kv->k);
   (void)hipFree(kv->v);
   delete kv;
@@ -1084,19 +1138,38 @@ int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t see
   if (slot < 0 || slot >= kv->slots || length < 0 || length > kv->cap)
     return soc::fail(SOC_ERR_INVALID, "soc_kv_fill_synthetic: bad slot or length");
   const soc_qwen_config& c = kv->model->cfg;
-  const int d = c.head_dim;
-  std::vector<uint16_t> buf(static_cast<size_t>(length) * d);
-  for (int l = 0; l < c.num_hidden_layers; ++l)
-    for (int h = 0; h < c.num_key_value_heads; ++h)
+  const int d = c.head_dim, L = c.num_hidden_layers, nkv = c.num_key_value_heads;
+  const size_t per_head = static_cast<size_t>(length) * d;
+  // host image [layer][k|v][head][length][d], generated per (layer, k|v, head) stream on up to 16 threads
+  std::vector<uint16_t> buf(static_cast<size_t>(L) * 2 * nkv * per_head);
+  const int jobs = L * 2 * nkv;
+  std::vector<int> rcs(jobs, SOC_OK);
+  auto work = [&](int t, int nt) {
+    for (int j = t; j < jobs; j += nt) {
+      const int l = j / (2 * nkv), which = (j / nkv) % 2, h = j % nkv;
+      const std::string name = "kv." + std::to_string(slot) + "." + std::to_string(l) + "." + std::to_string(h) +
+                               (which ? ".v" : ".k");
+      rcs[j] = soc_synth_normal_f16(seed, name.c_str(), 1.0f, 0, static_cast<int64_t>(per_head),
+                                    buf.data() + static_cast<size_t>(j) * per_head);
+    }
+  };
+  const unsigned hw = std::thread::hardware_concurrency();
+  const int nt = std::max(1, std::min<int>(16, hw == 0 ? 1 : static_cast<int>(hw)));
+  std::vector<std::thread> th;
+  for (int t = 0; t < nt; ++t) th.emplace_back(work, t, nt);
+  for (auto& t : th) t.join();
+  for (int rc : rcs)
+    if (rc != SOC_OK) return rc;
+  if (length > 0) {
+    for (int l = 0; l < L; ++l)
       for (int which = 0; which < 2; ++which) {
-        const std::string name = "kv." + std::to_string(slot) + "." + std::to_string(l) + "." + std::to_string(h) +
-                                 (which ? ".v" : ".k");
-        SOC_TRY(soc_synth_normal_f16(seed, name.c_str(), 1.0f, 0, static_cast<int64_t>(buf.size()), buf.data()));
-        const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(l) * kv->layer_stride +
-                           static_cast<size_t>(h) * kv->cap * d;
-        hipError_t e = hipMemcpy((which ? kv->v : kv->k) + off, buf.data(), buf.size() * 2, hipMemcpyHostToDevice);
-        if (e != hipSuccess) return hip_fail(e, "hipMemcpy kv");
+        const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(l) * kv->layer_stride;
+        const uint16_t* src = buf.data() + static_cast<size_t>((l * 2 + which) * nkv) * per_head;
+        hipError_t e = hipMemcpy2D((which ? kv->v : kv->k) + off, static_cast<size_t>(kv->cap) * d * 2, src,
+                                   per_head * 2, per_head * 2, nkv, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy2D kv");
       }
+  }
   kv->len[slot] = length;
   return SOC_OK;
   SOC_API_END
@@ -1356,37 +1429,55 @@ int soc_decode_batch_steps(soc_model* m, soc_kv* kv, int32_t n, const int32_t* s
   int max_len = 0;
   SOC_TRY(validate_batch(m, kv, n, slots, tokens, steps, &max_len));
   if (steps == 0) return SOC_OK;
-  SOC_TRY(ensure_prefill_ws(m, n, max_len, n));
+  SOC_TRY(ensure_prefill_ws(m, n, kv->cap, n));
   SOC_TRY(ensure_batch_ws(m, n));
   std::vector<int32_t> pos;
   SOC_TRY(upload_batch(m, kv, n, slots, tokens, &pos));
   hipStream_t s = m->ctx->stream;
-  int32_t* ring = nullptr;
-  hipError_t e = hipMalloc(&ring, static_cast<size_t>(n) * steps * 4);
-  if (e != hipSuccess) return hip_fail(e, "hipMalloc ring");
-  std::unique_ptr<int32_t, void (*)(int32_t*)> ring_guard(ring, [](int32_t* p) { (void)hipFree(p); });
-  const int max_split = (max_len + kAttnChunk - 1) / kAttnChunk;
-  if (env_flag("SOC_EAGER")) {
-    for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_batch_step(m, kv, n, max_split, ring, steps));
-  } else {
-    // one step captured once and replayed: per-step state (ids, positions) advances in device memory
-    hipGraph_t graph;
-    if ((e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal)) != hipSuccess)
-      return hip_fail(e, "hipStreamBeginCapture");
-    const int rc = enqueue_batch_step(m, kv, n, max_split, ring, steps);
-    e = hipStreamEndCapture(s, &graph);
-    if (rc != SOC_OK) return rc;
-    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-    hipGraphExec_t exec;
-    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-    for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(exec, s);
-    const hipError_t e2 = hipStreamSynchronize(s);
-    (void)hipGraphExecDestroy(exec);
-    if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
-    if (e2 != hipSuccess) return hip_fail(e2, "decode batch steps");
+  BatchWs& b = m->bws;
+  hipError_t e;
+  const size_t ring_need = static_cast<size_t>(n) * steps;
+  if (b.ring_cap < ring_need) {
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    (void)hipFree(b.ring);
+    b.ring = nullptr;
+    b.ring_cap = 0;
+    ++m->bws_gen;
+    if ((e = hipMalloc(&b.ring, ring_need * 4)) != hipSuccess) return hip_fail(e, "hipMalloc ring");
+    b.ring_cap = ring_need;
   }
+  // the attention grid covers the whole capacity (rows past their own length exit at once), so one captured step
+  // serves every call with the same (rows, steps)
+  const int max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+  if (env_flag("SOC_EAGER")) {
+    for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_batch_step(m, kv, n, max_split, b.ring, steps));
+  } else {
+    const std::pair<int, int> key(n, steps);
+    hipGraphExec_t exec = nullptr;
+    auto it = kv->batch_graphs.find(key);
+    if (it != kv->batch_graphs.end() && it->second.first == m->bws_gen) {
+      exec = it->second.second;
+    } else {
+      if (it != kv->batch_graphs.end()) {
+        (void)hipGraphExecDestroy(it->second.second);
+        kv->batch_graphs.erase(it);
+      }
+      hipGraph_t graph;
+      if ((e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+        return hip_fail(e, "hipStreamBeginCapture");
+      const int rc = enqueue_batch_step(m, kv, n, max_split, b.ring, steps);
+      e = hipStreamEndCapture(s, &graph);
+      if (rc != SOC_OK) return rc;
+      if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+      e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+      kv->batch_graphs[key] = std::make_pair(m->bws_gen, exec);
+    }
+    for (int i = 0; i < steps; ++i)
+      if ((e = hipGraphLaunch(exec, s)) != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+  }
+  int32_t* ring = b.ring;
   std::vector<int32_t> host(static_cast<size_t>(n) * steps);
   if ((e = hipMemcpyAsync(host.data(), ring, host.size() * 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync tokens");
