@@ -3,29 +3,36 @@
 //
 // Per layer the step has five dependent phases (reference: QwenBlock::ForwardCached, Mac/cpu/src/qwen_block.cpp:
 // 63-73, with QwenAttention::ForwardCached and QwenMLP::Forward):
-//   P1 RMSNorm(x) . Wqkv^T                                   every block, 1/NB of the rows
+//   P1 RMSNorm(x) . Wqkv^T                                   every projection block, 1/NB of the rows
 //   P2 q/k RMSNorm + RoPE + KV append + GQA attention        one block per KV head
-//   P3 x' = x + Wo . attn                                    every block
-//   P4 h = silu(RMSNorm(x') . Wg^T) * (RMSNorm(x') . Wu^T)   every block
-//   P5 x'' = x' + Wd . h                                     every block
+//   P3 x' = x + Wo . attn                                    every projection block
+//   P4 h = silu(RMSNorm(x') . Wg^T) * (RMSNorm(x') . Wu^T)   every projection block
+//   P5 x'' = x' + Wd . h                                     every projection block
 // Activations move between phases through small exchange vectors written with 8-byte stores that carry the value
 // and a tag unique to (step, layer): a reader spins until every element carries the expected tag. An aligned 8-byte
 // store is single-copy atomic, so a value is never seen without its tag, and no barrier or cache flush is needed.
-// Loads and stores of the exchange vectors are relaxed device-scope atomics (coherent across XCDs). Before waiting
-// for a phase's input, a block issues the loads of everything that phase needs and that does not depend on the
-// input (its weight rows, norm gains, RoPE factors, cached keys/values), so HBM streaming overlaps the hand-off.
-// A block's rows are spread over all 512 threads (TPR threads per row). Every wait is bounded: on timeout the block
-// raises an error flag and the whole grid drains.
+// Loads and stores of the exchange vectors are relaxed device-scope atomics (coherent across XCDs).
+//
+// Each block splits into seven compute waves and one receiver wave (wave 7). The receiver alone waits for a phase's
+// input and writes it into one of two LDS buffers, applying the RMSNorm (projection blocks) or the per-head
+// QK-RMSNorm + RoPE and the KV-cache append (attention blocks) in its registers; one block barrier per phase then
+// hands the buffer to the compute waves. The receiver issues no other loads, so its polls never queue behind the
+// weight stream, and the compute waves issue a layer's weight loads in the order the phases consume them, so each
+// phase waits only for its own rows. Every wait is bounded: on timeout the block raises an error flag and the whole
+// grid drains.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace soc {
 
 namespace {
 
-constexpr int NT = 512;  // threads per block
+constexpr int NT = 512;          // threads per block
+constexpr int NC = 448;          // compute threads: waves 0..6
+constexpr int RECV = 7;          // receiver wave
 constexpr int HD = 128;
 constexpr uint64_t kSpinTicks = 20000000ull;  // 200 ms of the 100 MHz real-time counter per wait
-constexpr int MAXG = 2;                       // norm-gain values held per thread (H <= 1024)
 
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
@@ -42,86 +49,136 @@ __device__ __forceinline__ bool err_raised(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Up to three tagged ranges read into LDS in one polling loop: range r copies src[r][0..n[r]) to dst[r].
-// Returns false (block-uniform) when the wait timed out or an error was raised somewhere in the grid.
-struct LLRanges {
-  const uint64_t* src[3];
-  float* dst[3];
-  int n[3];
-  int count;
-};
+__device__ __forceinline__ uint32_t tag_of(uint64_t v) { return static_cast<uint32_t>(v >> 32); }
+__device__ __forceinline__ float val_of(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 
-__device__ bool ll_read(const LLRanges& rg, uint32_t tag, int* err, int* flag) {
-  constexpr int MAXE = 8;  // elements per thread per round
-  int total = 0;
-  for (int r = 0; r < rg.count; ++r) total += rg.n[r];
-  bool ok = true;
-  for (int base = 0; base < total && ok; base += NT * MAXE) {
-    uint64_t v[MAXE];
-    const uint64_t* sp[MAXE];
-    float* dp[MAXE];
-    bool done[MAXE];
-    const int n0 = rg.n[0], n01 = rg.n[0] + (rg.count > 1 ? rg.n[1] : 0);
+// Receiver wave: elements i = lane + 64 e (e < MAXE) of a tagged vector, re-read until every one carries `tag`.
+// `addr(i)` gives the source of element i < n. Returns false (wave-uniform) on timeout or a raised error flag.
+template <int MAXE, typename Addr>
+__device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int i = lane + 64 * e;
+    v[e] = i < n ? ll_peek(addr(i)) : (static_cast<uint64_t>(tag) << 32);
+  }
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
+  while (true) {
+    bool all = true;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) all = all && tag_of(v[e]) == tag;
+    if (__all(all)) return true;
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
-      const int i = base + e * NT + static_cast<int>(threadIdx.x);
-      done[e] = i >= total;
-      if (i < n0) {
-        sp[e] = rg.src[0] + i;
-        dp[e] = rg.dst[0] + i;
-      } else if (i < n01) {
-        sp[e] = rg.src[1] + (i - n0);
-        dp[e] = rg.dst[1] + (i - n0);
-      } else {
-        sp[e] = rg.src[2] + (i - n01);
-        dp[e] = rg.dst[2] + (i - n01);
-      }
-      v[e] = done[e] ? 0 : ll_peek(sp[e]);
-    }
-    const uint64_t t0 = now_ticks();
-    uint32_t spins = 0;
-    while (true) {
-      bool all = true;
-#pragma unroll
-      for (int e = 0; e < MAXE; ++e) {
-        if (!done[e]) {
-          if (static_cast<uint32_t>(v[e] >> 32) == tag) {
-            *dp[e] = __uint_as_float(static_cast<uint32_t>(v[e]));
-            done[e] = true;
-          } else {
-            all = false;
-          }
-        }
-      }
-      if (all) break;
-      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = false;
-        break;
-      }
-#pragma unroll
-      for (int e = 0; e < MAXE; ++e)
-        if (!done[e]) v[e] = ll_peek(sp[e]);
+      const int i = lane + 64 * e;
+      if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek(addr(i));
     }
   }
-  if (threadIdx.x == 0) *flag = 0;
-  __syncthreads();
-  if (!ok) *flag = 1;
-  __syncthreads();
-  return *flag == 0;
 }
 
-__device__ __forceinline__ bool ll_read1(const uint64_t* src, int n, float* dst, uint32_t tag, int* err, int* flag) {
-  LLRanges rg{};
-  rg.src[0] = src;
-  rg.dst[0] = dst;
-  rg.n[0] = n;
-  rg.count = 1;
-  return ll_read(rg, tag, err, flag);
+// Relaxed device-scope read of one tagged word through a buffer resource (sc1: coherent across XCDs). The lane's
+// byte offset stays in one register and the per-element part folds into the instruction's offset fields, so a
+// receiver polling thousands of elements needs no per-element address registers. An aligned 8-byte load is
+// single-copy atomic.
+__device__ __forceinline__ uint64_t ll_peek_buf(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 16);
+  return (static_cast<uint64_t>(v.y) << 32) | v.x;
 }
 
-// A block's share of one weight matrix held in registers: slot s = threadIdx.x / TPR owns row r0 + s; thread t of the
-// slot holds the 8-half chunks at k = 8 (t + TPR c), c < CPT.
+// Receiver: the tagged vector src[0..n) into dst; with NORM, RMSNorm-ed with `gain`
+// (Mac/cpu/src/rms_norm_module.cpp:56-64: ms = sum x^2 / n; y = x * (1 / sqrt(ms + eps)) * g).
+template <int MAXE, bool NORM>
+__device__ __forceinline__ bool recv_vec(const uint64_t* src, int n, uint32_t tag, float* dst, const f16* gain,
+                                         float eps, int* err) {
+  const int lane = threadIdx.x & 63;
+  float g[NORM ? MAXE : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int i = lane + 64 * e;
+      g[e] = i < n ? static_cast<float>(gain[i]) : 0.0f;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(src), 0, n * 8, 0x00020000);
+  uint64_t v[MAXE];
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int i = lane + 64 * e;
+    v[e] = i < n ? ll_peek_buf(rsrc, lane * 8 + 512 * e) : (static_cast<uint64_t>(tag) << 32);
+  }
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
+  bool ok = true;
+  while (true) {
+    bool all = true;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) all = all && tag_of(v[e]) == tag;
+    if (__all(all)) break;
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = false;
+      break;
+    }
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int i = lane + 64 * e;
+      if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek_buf(rsrc, lane * 8 + 512 * e);
+    }
+  }
+  if (!ok) return false;
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int i = lane + 64 * e;
+      if (i < n) dst[i] = val_of(v[e]);
+    }
+  } else {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const float x = lane + 64 * e < n ? val_of(v[e]) : 0.0f;
+      ss += x * x;
+    }
+    ss = wave_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int i = lane + 64 * e;
+      if (i < n) dst[i] = val_of(v[e]) * scale * g[e];
+    }
+  }
+  return true;
+}
+
+// Receiver, layer 0: the embedding row (embedding.cpp:51-77) RMSNorm-ed with the layer-0 input gain.
+template <int MAXE>
+__device__ __forceinline__ void recv_embed(const f16* row, int n, float* dst, const f16* gain, float eps) {
+  const int lane = threadIdx.x & 63;
+  float x[MAXE];
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int i = lane + 64 * e;
+    x[e] = i < n ? static_cast<float>(row[i]) : 0.0f;
+    ss += x[e] * x[e];
+  }
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int i = lane + 64 * e;
+    if (i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
+  }
+}
+
+// A block's share of one weight matrix held in registers: slot s = threadIdx.x / TPR (threads < NC) owns row
+// r0 + s; thread t of the slot holds the 8-half chunks at k = 8 (t + TPR c), c < CPT.
 template <int TPR, int CPT>
 struct Slice {
   u32x4 w[CPT];
@@ -137,10 +194,10 @@ __device__ __forceinline__ void slice_load(Slice<TPR, CPT>& s, const f16* __rest
   }
 }
 
-// Row sum of the slot's row with xs[0..K); every thread of the slot gets it. TPR > 64 reduces through LDS
-// (`part` holds NT / 64 floats) and synchronises the block.
+// Row sum of the slot's row with xs[0..K) (TPR <= 64: the slot lives in one wave); every thread of the slot gets it.
 template <int TPR, int CPT>
-__device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float* xs, int K, float* part) {
+__device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float* xs, int K) {
+  static_assert(TPR <= 64, "a slot must not span waves");
   const int t = threadIdx.x % TPR;
   float acc = 0.0f;
 #pragma unroll
@@ -155,389 +212,460 @@ __device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float
       for (int i = 0; i < 8; ++i) acc += xv[i] * wf[i];
     }
   }
-  if constexpr (TPR <= 64) {
-    return group_sum<TPR>(acc);
-  } else {
-    acc = wave_sum(acc);
-    const int w = threadIdx.x >> 6, slot = threadIdx.x / TPR;
-    if ((threadIdx.x & 63) == 0) part[w] = acc;
-    __syncthreads();
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < TPR / 64; ++i) sum += part[slot * (TPR / 64) + i];
-    __syncthreads();
-    return sum;
-  }
+  return group_sum<TPR>(acc);
 }
-
-// Norm gain values used by this thread (elements threadIdx.x + NT j).
-struct Gains {
-  float g[MAXG];
-};
-
-__device__ __forceinline__ void gains_load(Gains& gs, const f16* gain, int n) {
-#pragma unroll
-  for (int j = 0; j < MAXG; ++j) {
-    const int i = threadIdx.x + NT * j;
-    gs.g[j] = i < n ? static_cast<float>(gain[i]) : 0.0f;
-  }
-}
-
-// RMSNorm of xs[0..n) in place (Mac/cpu/src/rms_norm_module.cpp:56-64): ms = sum x^2 / n; y = x * (1/sqrt(ms+eps)) * g.
-__device__ __forceinline__ void rmsnorm_lds(float* xs, int n, const Gains& gs, float eps, float* red) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int j = 0; j < MAXG; ++j) {
-    const int i = threadIdx.x + NT * j;
-    if (i < n) ss += xs[i] * xs[i];
-  }
-  ss = block_sum<NT>(ss, red);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
-#pragma unroll
-  for (int j = 0; j < MAXG; ++j) {
-    const int i = threadIdx.x + NT * j;
-    if (i < n) xs[i] = xs[i] * scale * gs.g[j];
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ int rows_per_block(int n) { return (n + static_cast<int>(gridDim.x) - 1) / gridDim.x; }
 
 // Thread-per-row widths and chunk counts of each projection, sized for Qwen3-0.6B (H 1024, q_dim 2048, I 3072)
-// over 248 GEMV blocks: up to 32 QKV rows, 8 hidden rows and 16 gate/up pairs per block.
+// over 248 projection blocks of 448 compute threads: up to 28 QKV rows, 7 hidden rows and 14 gate/up pairs per block.
 constexpr int TPR_QKV = 16, CPT_QKV = 8;   // K = H
 constexpr int TPR_O = 64, CPT_O = 4;       // K = q_dim
 constexpr int TPR_GU = 32, CPT_GU = 4;     // K = H
 constexpr int TPR_D = 64, CPT_D = 6;       // K = I
-constexpr int TPR_LM = 32, CPT_LM = 4;     // LM head, 16 rows per fragment
+constexpr int TPR_LM = 32, CPT_LM = 4;     // LM head, NC / 32 = 14 rows per fragment
+constexpr int MAXE_H = 16, MAXE_Q = 32, MAXE_I = 48;  // receiver elements per lane: H, q_dim, I <= 64 x MAXE
+constexpr int KCH = 224;                   // attention keys per chunk: 28 groups of 16 lanes x 8 keys
 
 }  // namespace
 
-// Optional phase timestamps (diagnostics): thread 0 of the first GEMV block and of the first attention block write
-// the real-time counter at each phase boundary into trace[which][idx], idx < 3 + 5 L.
+// Optional phase timestamps (diagnostics): thread 0 of the first projection block and of the first attention block
+// write the real-time counter at each phase boundary into trace[which][idx], idx < 4 + 8 L.
 #define SOC_TRACE(idx)                                                                                   \
   do {                                                                                                   \
-    if (a.trace != nullptr && threadIdx.x == 0 && (b == 0 || b == ng))                                   \
-      a.trace[(b == 0 ? 0 : 1) * (3 + 5 * a.L) + (idx)] = now_ticks();                                   \
+    if (c.a.trace != nullptr && threadIdx.x == 0) {                                                      \
+      const uint64_t t_ = now_ticks();                                                                   \
+      if (c.b == 0 || c.b == c.ng) c.a.trace[(c.b == 0 ? 0 : 1) * (4 + 8 * c.a.L) + (idx)] = t_;         \
+      /* every block: the 8 points of the middle layer, after the two per-role rows */                   \
+      if ((idx) >= 1 && ((idx) - 1) / 8 == c.a.L / 2)                                                    \
+        c.a.trace[2 * (4 + 8 * c.a.L) + c.b * 8 + ((idx) - 1) % 8] = t_;                                 \
+    }                                                                                                    \
   } while (0)
 
-// Block roles: blocks [0, ng) hold weight rows and run the projections (P1, P3, P4, P5); the last nkv blocks hold no
-// weights and run attention for one KV head each (P2), prefetching the next layer's cached keys/values while the
-// projections run. All blocks share the LM head.
+// Block barrier; afterwards every wave leaves if the receiver reported a failed wait (flag[0] != 0).
+#define SOC_SYNC()                      \
+  do {                                  \
+    __syncthreads();                    \
+    if (c.flag[0] != 0) return false;   \
+  } while (0)
+
+namespace {
+
+// What every role of a block shares: the arguments, the step state and the LDS carve-up.
+struct Ctx {
+  const PersistArgs& a;
+  int b, ng, token, pos;
+  uint32_t step;
+  float* xs0;   // [xs_cap] phase inputs, double buffered
+  float* xs1;
+  int* flag;    // [2] block-uniform status
+  float* bv;    // [16] argmax values per slot
+  int* bi;      // [16] argmax indices
+  float* att;   // attention scratch
+};
+
+// Receiver wave reports a failed wait; the barrier that follows publishes it.
+__device__ __forceinline__ void report(const Ctx& c, bool ok) {
+  if (!ok && (threadIdx.x & 63) == 0) c.flag[0] = 1;
+}
+
+// ---------------- attention block (one KV head g): receiver wave ----------------
 template <int G>
-__global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
-  extern __shared__ float lds[];
-  float* xs = lds;                                   // [max(H, qd, I)] staged input vector
-  float* red = lds + a.xs_cap;                       // [16] block reductions
-  int* flag = reinterpret_cast<int*>(red + 16);      // [1]  block-uniform status
-  float* bv = red + 32;                              // [16] argmax values per slot
-  int* bi = reinterpret_cast<int*>(red + 48);        // [16] argmax indices
-  float* part = red + 64;                            // [16] cross-wave row sums
-  float* att = red + 96;                             // attention scratch
+__device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, float* kn, float* vn) {
+  const PersistArgs& a = c.a;
+  const int lane = threadIdx.x & 63;
+  const int S = c.pos + 1;
+  for (int layer = 0; layer < a.L; ++layer) {
+    const f16* const* W = a.layer_w + layer * 9;
+    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    f16* kb = a.kcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+    f16* vb = a.vcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+    // q heads, key and value of KV head g: (G + 2) x 128 tagged elements, two per lane per head
+    constexpr int E = 2 * (G + 2);
+    uint64_t v[E];
+    const uint64_t* q_src = a.qkv + g * G * HD;
+    const uint64_t* k_src = a.qkv + a.qd + g * HD;
+    const uint64_t* v_src = a.qkv + a.qd + a.nkv * HD + g * HD;
+    const float qg0 = static_cast<float>(W[2][lane]), qg1 = static_cast<float>(W[2][lane + 64]);
+    const float kg0 = static_cast<float>(W[3][lane]), kg1 = static_cast<float>(W[3][lane + 64]);
+    const float rc = a.rope_cos[static_cast<size_t>(c.pos) * (HD / 2) + lane];
+    const float rs = a.rope_sin[static_cast<size_t>(c.pos) * (HD / 2) + lane];
+    const bool ok = recv_wait<E>(v, E * 64, tag,
+                                 [&](int i) {
+                                   const int hidx = i / HD, d = i % HD;
+                                   return hidx < G ? q_src + hidx * HD + d : (hidx == G ? k_src + d : v_src + d);
+                                 },
+                                 a.err);
+    if (ok) {
+      // per-head RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171; rope.cpp:81-84): lane holds dims
+      // (lane, lane + 64) of each head; the key and value are rounded to fp16 and appended at `pos`
+#pragma unroll
+      for (int hh = 0; hh <= G; ++hh) {
+        const float x0 = val_of(v[2 * hh]), x1 = val_of(v[2 * hh + 1]);
+        const float ssum = wave_sum(x0 * x0 + x1 * x1);
+        const float sc = 1.0f / sqrtf(ssum / static_cast<float>(HD) + a.eps);
+        const float y0 = x0 * sc * (hh < G ? qg0 : kg0);
+        const float y1 = x1 * sc * (hh < G ? qg1 : kg1);
+        const float r0 = y0 * rc - y1 * rs;
+        const float r1 = y0 * rs + y1 * rc;
+        if (hh < G) {
+          qs[hh * HD + lane] = r0;
+          qs[hh * HD + lane + 64] = r1;
+        } else {
+          const f16 h0v = static_cast<f16>(r0), h1v = static_cast<f16>(r1);
+          kb[static_cast<size_t>(c.pos) * HD + lane] = h0v;
+          kb[static_cast<size_t>(c.pos) * HD + lane + 64] = h1v;
+          kn[lane] = static_cast<float>(h0v);
+          kn[lane + 64] = static_cast<float>(h1v);
+        }
+      }
+      const f16 v0h = static_cast<f16>(val_of(v[2 * G + 2])), v1h = static_cast<f16>(val_of(v[2 * G + 3]));
+      vb[static_cast<size_t>(c.pos) * HD + lane] = v0h;
+      vb[static_cast<size_t>(c.pos) * HD + lane + 64] = v1h;
+      vn[lane] = static_cast<float>(v0h);
+      vn[lane + 64] = static_cast<float>(v1h);
+    }
+    report(c, ok);
+    SOC_SYNC();                                    // inputs ready
+    for (int c0 = 0; c0 < S; c0 += KCH) {
+      SOC_SYNC();                                  // scores written
+      SOC_SYNC();                                  // softmax statistics
+      SOC_SYNC();                                  // weighted values
+    }
+    SOC_SYNC();                                    // group partials
+    SOC_SYNC();                                    // outputs stored; LDS free for the next layer
+  }
+  return true;
+}
 
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int token = a.state[0], pos = a.state[1];
-  const uint32_t step = static_cast<uint32_t>(a.state[2]);
-  const int H = a.H, I = a.I, qd = a.qd, qkv_rows = a.qkv_rows;
-  const int ng = static_cast<int>(gridDim.x) - a.nkv;
+// ---------------- attention block: compute waves (28 groups of 16 lanes, 8 dims per lane) ----------------
+template <int G>
+__device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* qs, const float* kn, const float* vn) {
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int sub = tid & 15, grp = tid >> 4;
+  float* sc = c.att + G * HD + 2 * HD;     // [G][KCH] scores, then weights
+  float* pred = sc + G * KCH;              // [28][G][HD] key-group partials
+  float* stat = pred + (NC / 16) * G * HD;  // [G] running max, [G] running sum, [G] correction
+  const int pos = c.pos, S = pos + 1;
+  u32x4 kreg[8], vreg[8];
+  for (int layer = 0; layer < a.L; ++layer) {
+    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    const f16* kb = a.kcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+    const f16* vb = a.vcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+    auto kv_fetch = [&](int c0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int ap = c0 + grp + 28 * u;
+        const bool ok = ap < pos;
+        kreg[u] = ok ? load16(kb + static_cast<size_t>(ap) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+        vreg[u] = ok ? load16(vb + static_cast<size_t>(ap) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+      }
+    };
+    // cached keys/values of the first chunk do not depend on this layer's q/k/v: in flight before the wait
+    kv_fetch(0);
+    if (tid < G) {
+      stat[tid] = -INFINITY;
+      stat[G + tid] = 0.0f;
+    }
+    SOC_TRACE(1 + 8 * layer);
+    SOC_SYNC();                                    // inputs ready
+    SOC_TRACE(2 + 8 * layer);
+    float qreg[G][8], acc[G][8];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qreg[j][i] = qs[j * HD + sub * 8 + i];
+        acc[j][i] = 0.0f;
+      }
+    for (int c0 = 0; c0 < S; c0 += KCH) {
+      const int n = min(KCH, S - c0);
+      // scores (grouped_query_attention.cpp:105-116); key p of the chunk lives in group p % 28, slot p / 28
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = grp + 28 * u;
+        if (p < n) {
+          float kf[8];
+          if (c0 + p == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
+          } else {
+            f16x8_to_f32(kreg[u], kf);
+          }
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
+            d = group_sum<16>(d);
+            if (sub == 0) sc[j * KCH + p] = d * a.scale;
+          }
+        }
+      }
+      SOC_SYNC();                                  // scores written
+      // running max / sum (online form of :113-122), one wave per query head
+      if (wid < G) {
+        const int j = wid;
+        float m = -INFINITY;
+        for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[j * KCH + p]);
+        m = wave_max(m);
+        const float m_old = stat[j];
+        const float m_new = fmaxf(m_old, m);
+        float ssum = 0.0f;
+        for (int p = lane; p < n; p += 64) {
+          const float w = expf(sc[j * KCH + p] - m_new);
+          sc[j * KCH + p] = w;
+          ssum += w;
+        }
+        ssum = wave_sum(ssum);
+        if (lane == 0) {
+          const float corr = expf(m_old - m_new);
+          stat[2 * G + j] = corr;
+          stat[G + j] = stat[G + j] * corr + ssum;
+          stat[j] = m_new;
+        }
+      }
+      SOC_SYNC();                                  // softmax statistics
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const float corr = stat[2 * G + j];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[j][i] *= corr;
+      }
+      // weighted values (:130-136)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = grp + 28 * u;
+        if (p < n) {
+          float vf[8];
+          if (c0 + p == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+          } else {
+            f16x8_to_f32(vreg[u], vf);
+          }
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            const float w = sc[j * KCH + p];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
+          }
+        }
+      }
+      if (c0 + KCH < S) kv_fetch(c0 + KCH);
+      SOC_SYNC();                                  // weighted values
+    }
+    // the 28 key groups' partial sums, reduced through LDS
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pred[(grp * G + j) * HD + sub * 8 + i] = acc[j][i];
+    SOC_SYNC();                                    // group partials
+    for (int idx = tid; idx < G * HD; idx += NC) {
+      const int j = idx / HD, i = idx % HD;
+      float o = 0.0f;
+#pragma unroll 4
+      for (int q = 0; q < NC / 16; ++q) o += pred[(q * G + j) * HD + i];
+      ll_store(a.attn + (g * G + j) * HD + i, o / stat[G + j], tag);
+    }
+    SOC_TRACE(3 + 8 * layer);
+    SOC_SYNC();                                    // outputs stored; LDS free for the next layer
+  }
+  return true;
+}
 
-  if (b >= ng) {
-    // ================================ attention block ================================
-    const int g = b - ng;
-    float* qs = att;                       // [G][HD]
-    float* kn = qs + G * HD;               // [HD]
-    float* vn = kn + HD;                   // [HD]
-    float* sc = vn + HD;                   // [G][256]
-    float* pred = sc + G * 256;            // [8][G][HD] wave partials
-    float* stat = pred + 8 * G * HD;       // [G] running max, [G] running sum, [G] correction
-    const int wid = tid >> 6, lane = tid & 63;
-    const int sub = tid & 15, grp = tid >> 4;  // 32 groups of 16 lanes, 8 dims per lane
-    const bool normer = wid <= G;              // waves 0..G-1 normalise q heads, wave G the key
-    const int S = pos + 1;
-    u32x4 kreg[8], vreg[8];
-    for (int layer = 0; layer < a.L; ++layer) {
-      const f16* const* W = a.layer_w + layer * 9;
-      const uint32_t tag = step * 64u + static_cast<uint32_t>(layer) + 1u;
-      f16* kb = a.kcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
-      f16* vb = a.vcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
-      // everything that does not depend on this layer's q/k/v is loaded before waiting for them: the first 256-key
-      // chunk of cached keys/values, the q/k norm gains and the RoPE factors of this position
-      auto kv_fetch = [&](int c0) {
+// ---------------- whole-block receive (all 8 waves; used where no weight loads are in flight) ----------------
+// Entries i = tid + 512 e of the tagged vector src[0..n) go to dst; with NORM, the block then applies the RMSNorm
+// with `gain` (a block-wide sum of squares through LDS). Two barriers with NORM, one without.
+template <bool NORM>
+__device__ __forceinline__ bool block_recv(const Ctx& c, const uint64_t* src, const f16* embed_row, int n,
+                                           uint32_t tag, float* dst, const f16* gain, float eps) {
+  constexpr int MB = 6;  // n <= 3072
+  const int tid = threadIdx.x, wid = tid >> 6;
+  float x[MB];
+  bool ok = true;
+  if (embed_row != nullptr) {
+    // layer 0: the embedding row itself (embedding.cpp:51-77)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int ap = c0 + grp + 32 * u;
-          const bool ok = ap < pos;
-          kreg[u] = ok ? load16(kb + static_cast<size_t>(ap) * HD + sub * 8) : u32x4{0, 0, 0, 0};
-          vreg[u] = ok ? load16(vb + static_cast<size_t>(ap) * HD + sub * 8) : u32x4{0, 0, 0, 0};
-        }
-      };
-      kv_fetch(0);
-      const f16* ngain = wid < G ? W[2] : W[3];
-      float gn0 = 0.f, gn1 = 0.f, rc = 0.f, rs = 0.f;
-      if (normer) {
-        gn0 = static_cast<float>(ngain[lane]);
-        gn1 = static_cast<float>(ngain[lane + 64]);
-        rc = a.rope_cos[static_cast<size_t>(pos) * (HD / 2) + lane];
-        rs = a.rope_sin[static_cast<size_t>(pos) * (HD / 2) + lane];
-      }
-      LLRanges rg{};
-      rg.src[0] = a.qkv + g * G * HD;
-      rg.dst[0] = qs;
-      rg.n[0] = G * HD;
-      rg.src[1] = a.qkv + qd + g * HD;
-      rg.dst[1] = kn;
-      rg.n[1] = HD;
-      rg.src[2] = a.qkv + qd + a.nkv * HD + g * HD;
-      rg.dst[2] = vn;
-      rg.n[2] = HD;
-      rg.count = 3;
-      SOC_TRACE(1 + 5 * layer);
-      if (!ll_read(rg, tag, a.err, flag)) return;
-      SOC_TRACE(2 + 5 * layer);
-      // per-head RMSNorm + RoPE (lane l holds dims l and l+64); the new key/value are rounded to fp16 and appended
-      if (normer) {
-        float* v = wid < G ? qs + wid * HD : kn;
-        float x0 = v[lane], x1 = v[lane + 64];
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float s = 1.0f / sqrtf(ss / static_cast<float>(HD) + a.eps);
-        const float y0 = x0 * s * gn0;
-        const float y1 = x1 * s * gn1;
-        x0 = y0 * rc - y1 * rs;
-        x1 = y0 * rs + y1 * rc;
-        if (wid == G) {
-          const f16 h0v = static_cast<f16>(x0), h1v = static_cast<f16>(x1);
-          kb[static_cast<size_t>(pos) * HD + lane] = h0v;
-          kb[static_cast<size_t>(pos) * HD + lane + 64] = h1v;
-          x0 = static_cast<float>(h0v);
-          x1 = static_cast<float>(h1v);
-        }
-        v[lane] = x0;
-        v[lane + 64] = x1;
-      } else if (wid == G + 1) {
-        const f16 h0v = static_cast<f16>(vn[lane]), h1v = static_cast<f16>(vn[lane + 64]);
-        vb[static_cast<size_t>(pos) * HD + lane] = h0v;
-        vb[static_cast<size_t>(pos) * HD + lane + 64] = h1v;
-        vn[lane] = static_cast<float>(h0v);
-        vn[lane + 64] = static_cast<float>(h1v);
-      }
-      if (tid < G) {
-        stat[tid] = -INFINITY;
-        stat[G + tid] = 0.0f;
-      }
-      __syncthreads();
-      float qreg[G][8];
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qreg[j][i] = qs[j * HD + sub * 8 + i];
-      float acc[G][8];
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
-      for (int c0 = 0; c0 < S; c0 += 256) {
-        const int n = min(256, S - c0);
-        // scores (grouped_query_attention.cpp:105-116); key p of the chunk lives in group p % 32, slot p / 32
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int p = grp + 32 * u;
-          if (p < n) {
-            float kf[8];
-            if (c0 + p == pos) {
-#pragma unroll
-              for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-            } else {
-              f16x8_to_f32(kreg[u], kf);
-            }
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-              float d = 0.0f;
-#pragma unroll
-              for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
-              d = group_sum<16>(d);
-              if (sub == 0) sc[j * 256 + p] = d * a.scale;
-            }
-          }
-        }
-        __syncthreads();
-        // running max / sum (online form of :113-122)
-        if (wid < G) {
-          const int j = wid;
-          float m = -INFINITY;
-          for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[j * 256 + p]);
-          m = wave_max(m);
-          const float m_old = stat[j];
-          const float m_new = fmaxf(m_old, m);
-          float ssum = 0.0f;
-          for (int p = lane; p < n; p += 64) {
-            const float w = expf(sc[j * 256 + p] - m_new);
-            sc[j * 256 + p] = w;
-            ssum += w;
-          }
-          ssum = wave_sum(ssum);
-          if (lane == 0) {
-            const float corr = expf(m_old - m_new);
-            stat[2 * G + j] = corr;
-            stat[G + j] = stat[G + j] * corr + ssum;
-            stat[j] = m_new;
-          }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-          const float corr = stat[2 * G + j];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[j][i] *= corr;
-        }
-        // weighted values (:130-136)
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int p = grp + 32 * u;
-          if (p < n) {
-            float vf[8];
-            if (c0 + p == pos) {
-#pragma unroll
-              for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
-            } else {
-              f16x8_to_f32(vreg[u], vf);
-            }
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-              const float w = sc[j * 256 + p];
-#pragma unroll
-              for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
-            }
-          }
-        }
-        if (c0 + 256 < S) kv_fetch(c0 + 256);
-        __syncthreads();
-      }
-      // reduce the 4 key groups of a wave, then the 8 waves
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float v = acc[j][i];
-          v += __shfl_xor(v, 16, kWave);
-          v += __shfl_xor(v, 32, kWave);
-          acc[j][i] = v;
-        }
-      if ((lane >> 4) == 0) {
-#pragma unroll
-        for (int j = 0; j < G; ++j)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) pred[(wid * G + j) * HD + sub * 8 + i] = acc[j][i];
-      }
-      __syncthreads();
-      for (int idx = tid; idx < G * HD; idx += NT) {
-        const int j = idx / HD, i = idx % HD;
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NT / 64; ++w) o += pred[(w * G + j) * HD + i];
-        ll_store(a.attn + (g * G + j) * HD + i, o / stat[G + j], tag);
-      }
-      SOC_TRACE(3 + 5 * layer);
-      __syncthreads();
+    for (int e = 0; e < MB; ++e) {
+      const int i = tid + NT * e;
+      x[e] = i < n ? static_cast<float>(embed_row[i]) : 0.0f;
     }
   } else {
-    // ================================ projection block ================================
-    const int rq = (qkv_rows + ng - 1) / ng, q0 = b * rq, q1 = min(qkv_rows, q0 + rq);
-    const int rh = (H + ng - 1) / ng, h0 = b * rh, h1 = min(H, h0 + rh);
-    const int ri = (I + ng - 1) / ng, i0 = b * ri, i1 = min(I, i0 + ri);
-    const int slot_q = tid / TPR_QKV, slot_h = tid / TPR_O, slot_i = tid / TPR_GU;
-    const bool lead_q = (tid % TPR_QKV) == 0, lead_h = (tid % TPR_O) == 0, lead_i = (tid % TPR_GU) == 0;
-    Slice<TPR_QKV, CPT_QKV> sq;
-    Slice<TPR_O, CPT_O> so;
-    Slice<TPR_GU, CPT_GU> sg, su;
-    Slice<TPR_D, CPT_D> sd;
-    Gains gin, gpost;
-    // residual stream value of this slot's H-row; layer 0 starts from the embedding row (embedding.cpp:51-77)
-    const int hrow = h0 + slot_h;
-    float xres = hrow < h1 ? static_cast<float>(a.embed[static_cast<size_t>(token) * H + hrow]) : 0.0f;
-    slice_load(sq, a.layer_w[4], H, q0, q1);
-    gains_load(gin, a.layer_w[0], H);
-    SOC_TRACE(0);
-
-    for (int layer = 0; layer < a.L; ++layer) {
-      const f16* const* W = a.layer_w + layer * 9;  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
-      const uint32_t tag = step * 64u + static_cast<uint32_t>(layer) + 1u;
-
-      // ---- P1: RMSNorm + QKV projection ----
-      if (layer == 0) {
-        for (int i = tid; i < H; i += NT) xs[i] = static_cast<float>(a.embed[static_cast<size_t>(token) * H + i]);
-        __syncthreads();
-      } else if (!ll_read1(a.xb, H, xs, tag - 1, a.err, flag)) {
-        return;
-      }
-      rmsnorm_lds(xs, H, gin, a.eps, red);
-      {
-        const float out = slice_dot(sq, xs, H, part);
-        const int row = q0 + slot_q;
-        if (lead_q && row < q1) ll_store(a.qkv + row, out, tag);
-      }
-      // every remaining weight row of this layer and the next layer's QKV rows: the stream drains while the
-      // attention blocks work, so the later polls of this layer wait behind nothing
-      slice_load(so, W[5], qd, h0, h1);
-      slice_load(sg, W[6], H, i0, i1);
-      slice_load(su, W[7], H, i0, i1);
-      slice_load(sd, W[8], I, h0, h1);
-      gains_load(gpost, W[1], H);
-      if (layer + 1 < a.L) {
-        slice_load(sq, a.layer_w[(layer + 1) * 9 + 4], H, q0, q1);
-        gains_load(gin, a.layer_w[(layer + 1) * 9 + 0], H);
-      }
-      SOC_TRACE(1 + 5 * layer);
-
-      // ---- P3: o_proj + residual ----
-      if (!ll_read1(a.attn, qd, xs, tag, a.err, flag)) return;
-      SOC_TRACE(2 + 5 * layer);
-      {
-        const float out = slice_dot(so, xs, qd, part);
-        xres = xres + out;
-        if (lead_h && hrow < h1) ll_store(a.xa + hrow, xres, tag);
-      }
-      SOC_TRACE(3 + 5 * layer);
-
-      // ---- P4: RMSNorm + gate/up + SwiGLU ----
-      if (!ll_read1(a.xa, H, xs, tag, a.err, flag)) return;
-      rmsnorm_lds(xs, H, gpost, a.eps, red);
-      {
-        const float og = slice_dot(sg, xs, H, part);
-        const float ou = slice_dot(su, xs, H, part);
-        const int row = i0 + slot_i;
-        if (lead_i && row < i1) ll_store(a.h + row, silu_ref(og) * ou, tag);
-      }
-      SOC_TRACE(4 + 5 * layer);
-
-      // ---- P5: down + residual ----
-      if (!ll_read1(a.h, I, xs, tag, a.err, flag)) return;
-      {
-        const float out = slice_dot(sd, xs, I, part);
-        xres = xres + out;
-        if (lead_h && hrow < h1) ll_store(a.xb + hrow, xres, tag);
-      }
-      SOC_TRACE(5 + 5 * layer);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(src), 0, n * 8, 0x00020000);
+    uint64_t v[MB];
+#pragma unroll
+    for (int e = 0; e < MB; ++e) {
+      const int i = tid + NT * e;
+      v[e] = i < n ? ll_peek_buf(rsrc, tid * 8 + NT * 8 * e) : (static_cast<uint64_t>(tag) << 32);
     }
+    const uint64_t t0 = now_ticks();
+    uint32_t spins = 0;
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int e = 0; e < MB; ++e) all = all && tag_of(v[e]) == tag;
+      if (__all(all)) break;
+      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+        __hip_atomic_store(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = false;
+        break;
+      }
+#pragma unroll
+      for (int e = 0; e < MB; ++e) {
+        const int i = tid + NT * e;
+        if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek_buf(rsrc, tid * 8 + NT * 8 * e);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < MB; ++e) x[e] = val_of(v[e]);
   }
+  if (!ok && (tid & 63) == 0) c.flag[0] = 1;
+  float* red = reinterpret_cast<float*>(c.bv);  // [8] wave partial sums (argmax scratch is idle until the LM head)
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int e = 0; e < MB; ++e) {
+      const int i = tid + NT * e;
+      if (i < n) dst[i] = x[e];
+    }
+    SOC_SYNC();
+  } else {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < MB; ++e) ss += tid + NT * e < n ? x[e] * x[e] : 0.0f;
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[wid] = ss;
+    SOC_SYNC();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) tot += red[w];
+    const float scale = 1.0f / sqrtf(tot / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int e = 0; e < MB; ++e) {
+      const int i = tid + NT * e;
+      if (i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
+    }
+    SOC_SYNC();
+  }
+  return true;
+}
 
-  // ---- final RMSNorm + LM head + greedy argmax (sampler.cpp:26-61 with top_k = 1), all blocks ----
+// ---------------- projection block: receiver wave ----------------
+__device__ __forceinline__ bool proj_receiver(const Ctx& c) {
+  const PersistArgs& a = c.a;
+  const int H = a.H;
+  for (int layer = 0; layer < a.L; ++layer) {
+    const f16* const* W = a.layer_w + layer * 9;
+    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    if (!block_recv<true>(c, a.xb, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, H, tag - 1,
+                          c.xs0, W[0], a.eps))
+      return false;                                // P1 input
+    report(c, recv_vec<MAXE_Q, false>(a.attn, a.qd, tag, c.xs1, nullptr, a.eps, a.err));
+    SOC_SYNC();                                    // P3 input (receiver alone: the weight stream is in flight)
+    if (!block_recv<true>(c, a.xa, nullptr, H, tag, c.xs0, W[1], a.eps)) return false;      // P4 input
+    if (!block_recv<false>(c, a.h, nullptr, a.I, tag, c.xs1, nullptr, a.eps)) return false;  // P5 input
+  }
+  return true;
+}
+
+// ---------------- projection block: compute waves ----------------
+__device__ __forceinline__ bool proj_compute(const Ctx& c) {
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x;
+  const int H = a.H, I = a.I, qd = a.qd, ng = c.ng, b = c.b;
+  const int rq = (a.qkv_rows + ng - 1) / ng, q0 = b * rq, q1 = min(a.qkv_rows, q0 + rq);
+  const int rh = (H + ng - 1) / ng, h0 = b * rh, h1 = min(H, h0 + rh);
+  const int ri = (I + ng - 1) / ng, i0 = b * ri, i1 = min(I, i0 + ri);
+  const int slot_q = tid / TPR_QKV, slot_h = tid / TPR_O, slot_i = tid / TPR_GU;
+  const bool lead_q = (tid % TPR_QKV) == 0, lead_h = (tid % TPR_O) == 0, lead_i = (tid % TPR_GU) == 0;
+  Slice<TPR_QKV, CPT_QKV> sq;
+  Slice<TPR_O, CPT_O> so;
+  Slice<TPR_GU, CPT_GU> sg, su;
+  Slice<TPR_D, CPT_D> sd;
+  // residual stream value of this slot's H-row; layer 0 starts from the embedding row (embedding.cpp:51-77)
+  const int hrow = h0 + slot_h;
+  float xres = hrow < h1 ? static_cast<float>(a.embed[static_cast<size_t>(c.token) * H + hrow]) : 0.0f;
+  slice_load(sq, a.layer_w[4], H, q0, q1);
+  SOC_TRACE(0);
+  for (int layer = 0; layer < a.L; ++layer) {
+    const f16* const* W = a.layer_w + layer * 9;  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    // ---- P1: RMSNorm + QKV projection ----
+    if (!block_recv<true>(c, a.xb, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, H, tag - 1,
+                          c.xs0, W[0], a.eps))
+      return false;
+    SOC_TRACE(1 + 8 * layer);
+    {
+      const float out = slice_dot(sq, c.xs0, H);
+      const int row = q0 + slot_q;
+      if (lead_q && row < q1) ll_store(a.qkv + row, out, tag);
+    }
+    // the layer's other weight rows, in the order the phases use them, then the next layer's QKV rows: they stream
+    // while the attention blocks work
+    slice_load(so, W[5], qd, h0, h1);
+    slice_load(sg, W[6], H, i0, i1);
+    slice_load(su, W[7], H, i0, i1);
+    slice_load(sd, W[8], I, h0, h1);
+    if (layer + 1 < a.L) slice_load(sq, a.layer_w[(layer + 1) * 9 + 4], H, q0, q1);
+    SOC_TRACE(2 + 8 * layer);
+    // ---- P3: o_proj + residual ----
+    SOC_SYNC();
+    SOC_TRACE(3 + 8 * layer);
+    {
+      const float out = slice_dot(so, c.xs1, qd);
+      xres = xres + out;
+      if (lead_h && hrow < h1) ll_store(a.xa + hrow, xres, tag);
+    }
+    SOC_TRACE(4 + 8 * layer);
+    // ---- P4: RMSNorm + gate/up + SwiGLU ----
+    if (!block_recv<true>(c, a.xa, nullptr, H, tag, c.xs0, W[1], a.eps)) return false;
+    SOC_TRACE(5 + 8 * layer);
+    {
+      const float og = slice_dot(sg, c.xs0, H);
+      const float ou = slice_dot(su, c.xs0, H);
+      const int row = i0 + slot_i;
+      if (lead_i && row < i1) ll_store(a.h + row, silu_ref(og) * ou, tag);
+    }
+    SOC_TRACE(6 + 8 * layer);
+    // ---- P5: down + residual ----
+    if (!block_recv<false>(c, a.h, nullptr, I, tag, c.xs1, nullptr, a.eps)) return false;
+    SOC_TRACE(7 + 8 * layer);
+    {
+      const float out = slice_dot(sd, c.xs1, I);
+      xres = xres + out;
+      if (lead_h && hrow < h1) ll_store(a.xb + hrow, xres, tag);
+    }
+    SOC_TRACE(8 + 8 * layer);
+  }
+  return true;
+}
+
+// ---------------- LM head: receiver wave gets the final hidden state ----------------
+__device__ __forceinline__ bool lm_receiver(const Ctx& c) {
+  const PersistArgs& a = c.a;
+  const uint32_t last_tag = c.step * 64u + static_cast<uint32_t>(a.L);
+  report(c, recv_vec<MAXE_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err));
+  SOC_SYNC();
+  return true;
+}
+
+// ---------------- LM head: compute waves, this block's rows, best (value, index) per 32-lane slot ----------------
+__device__ __forceinline__ bool lm_compute(const Ctx& c) {
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x;
   const int slot32 = tid / 32;
   const bool lead32 = (tid % 32) == 0;
-  const uint32_t last_tag = step * 64u + static_cast<uint32_t>(a.L);
-  const int rv = rows_per_block(a.V), v0 = b * rv, v1 = min(a.V, v0 + rv);
-  constexpr int STEP = NT / TPR_LM;  // rows per fragment
+  const int rv = (a.V + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int v0 = c.b * rv, v1 = min(a.V, v0 + rv);
+  constexpr int STEP = NC / TPR_LM;  // rows per fragment
   Slice<TPR_LM, CPT_LM> f0, f1;
-  Gains gfin;
-  slice_load(f0, a.lm_head, H, v0, v1);  // does not depend on the hidden state: issue before waiting for it
-  gains_load(gfin, a.final_norm, H);
-  if (!ll_read1(a.xb, H, xs, last_tag, a.err, flag)) return;
-  SOC_TRACE(1 + 5 * a.L);
-  rmsnorm_lds(xs, H, gfin, a.eps, red);
+  slice_load(f0, a.lm_head, a.H, v0, v1);  // does not depend on the hidden state: in flight before the wait
+  SOC_SYNC();
+  SOC_TRACE(1 + 8 * a.L);
   float best = -INFINITY;
   int best_i = 0x7fffffff;
   auto consume = [&](const Slice<TPR_LM, CPT_LM>& f, int r0) {
-    const float out = slice_dot(f, xs, H, part);
+    const float out = slice_dot(f, c.xs0, a.H);
     const int row = r0 + slot32;
     if (row < v1) {
       if (lead32 && a.logits != nullptr) a.logits[row] = out;
@@ -548,34 +676,68 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
     }
   };
   for (int r0 = v0; r0 < v1; r0 += 2 * STEP) {
-    slice_load(f1, a.lm_head, H, r0 + STEP, v1);
+    slice_load(f1, a.lm_head, a.H, r0 + STEP, v1);
     consume(f0, r0);
-    slice_load(f0, a.lm_head, H, r0 + 2 * STEP, v1);
+    slice_load(f0, a.lm_head, a.H, r0 + 2 * STEP, v1);
     consume(f1, r0 + STEP);
   }
-  SOC_TRACE(2 + 5 * a.L);
-  __syncthreads();
   if (lead32) {
-    bv[slot32] = best;
-    bi[slot32] = best_i;
+    c.bv[slot32] = best;
+    c.bi[slot32] = best_i;
   }
+  SOC_TRACE(2 + 8 * a.L);
+  return true;
+}
+
+}  // namespace
+
+// Block roles: blocks [0, ng) hold weight rows and run the projections (P1, P3, P4, P5); the last nkv blocks hold no
+// weights and run attention for one KV head each (P2), prefetching the next layer's cached keys/values while the
+// projections run. All blocks share the LM head. In every block wave 7 is the receiver, waves 0..6 compute; the two
+// run separate loops with the same sequence of block barriers.
+template <int G>
+__global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
+  extern __shared__ float lds[];
+  float* red = lds + 2 * a.xs_cap;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int ng = static_cast<int>(gridDim.x) - a.nkv;
+  Ctx c{a, static_cast<int>(blockIdx.x), ng, a.state[0], a.state[1], static_cast<uint32_t>(a.state[2]),
+        lds, lds + a.xs_cap, reinterpret_cast<int*>(red + 16), red + 32, reinterpret_cast<int*>(red + 48), red + 96};
+  if (tid == 0) c.flag[0] = 0;
+  __syncthreads();
+  const bool recv = wid == RECV;
+  bool ok;
+  if (c.b >= ng) {
+    const int g = c.b - ng;
+    float* qs = c.att;
+    float* kn = qs + G * HD;
+    float* vn = kn + HD;
+    ok = recv ? attn_receiver<G>(c, g, qs, kn, vn) : attn_compute<G>(c, g, qs, kn, vn);
+  } else {
+    ok = recv ? proj_receiver(c) : proj_compute(c);
+  }
+  if (!ok) return;
+  ok = recv ? lm_receiver(c) : lm_compute(c);
+  if (!ok) return;
+
+  // ---- greedy argmax over the blocks' candidates (sampler.cpp:26-61 with top_k = 1) ----
   __syncthreads();
   if (tid == 0) {
-    float v = bv[0];
-    int i = bi[0];
-    for (int w = 1; w < NT / 32; ++w)
-      if (bv[w] > v || (bv[w] == v && bi[w] < i)) {
-        v = bv[w];
-        i = bi[w];
+    float v = c.bv[0];
+    int i = c.bi[0];
+    for (int w = 1; w < NC / 32; ++w)
+      if (c.bv[w] > v || (c.bv[w] == v && c.bi[w] < i)) {
+        v = c.bv[w];
+        i = c.bi[w];
       }
-    st_dev(a.part_val + b, v);
-    st_dev(a.part_idx + b, i);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial is in memory before the arrival is counted
+    st_dev(a.part_val + c.b, v);
+    st_dev(a.part_idx + c.b, i);
+    wait_mem();  // the block's candidate is visible device-wide before it is counted
     const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = (done == static_cast<int>(gridDim.x) - 1);
+    c.flag[1] = (done == static_cast<int>(gridDim.x) - 1);
   }
   __syncthreads();
-  if (*flag == 0) return;
+  if (c.flag[1] == 0) return;
   float v = -INFINITY;
   int i = 0x7fffffff;
   for (int q = tid; q < static_cast<int>(gridDim.x); q += NT) {
@@ -596,21 +758,21 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
     }
   }
   __syncthreads();
-  if ((tid & 63) == 0) {
-    bv[tid >> 6] = v;
-    bi[tid >> 6] = i;
+  if (lane == 0) {
+    c.bv[wid] = v;
+    c.bi[wid] = i;
   }
   __syncthreads();
   if (tid == 0) {
     for (int w = 1; w < NT / 64; ++w)
-      if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
-        bv[0] = bv[w];
-        bi[0] = bi[w];
+      if (c.bv[w] > c.bv[0] || (c.bv[w] == c.bv[0] && c.bi[w] < c.bi[0])) {
+        c.bv[0] = c.bv[w];
+        c.bi[0] = c.bi[w];
       }
-    const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
+    const int tok = c.bi[0] == 0x7fffffff ? 0 : c.bi[0];
     a.state[0] = tok;
-    a.state[1] = pos + 1;
-    a.state[2] = static_cast<int>(step + 1);
+    a.state[1] = c.pos + 1;
+    a.state[2] = static_cast<int>(c.step + 1);
     if (a.ring != nullptr) {
       a.ring[*a.ring_pos] = tok;
       *a.ring_pos += 1;
@@ -618,10 +780,12 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
     __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+#undef SOC_SYNC
+#undef SOC_TRACE
 
 size_t persistent_lds_bytes(const PersistArgs& a, int G) {
-  const size_t att = static_cast<size_t>(G) * HD + 2 * HD + static_cast<size_t>(G) * 256 + 8 * G * HD + 3 * G;
-  return (static_cast<size_t>(a.xs_cap) + 96 + att) * sizeof(float);
+  const size_t att = static_cast<size_t>(G) * HD + 2 * HD + static_cast<size_t>(G) * KCH + (NC / 16) * G * HD + 3 * G;
+  return (2 * static_cast<size_t>(a.xs_cap) + 96 + att) * sizeof(float);
 }
 
 namespace {
@@ -658,18 +822,18 @@ hipError_t persistent_blocks_per_cu(int G, int* blocks) {
 }
 
 // Shapes the register tiling covers: K = hidden <= 1024, q_dim <= 2048, intermediate <= 3072; over the projection
-// blocks (all but nkv) at most 32 QKV rows, 8 hidden rows and 16 gate/up pairs per block.
+// blocks (all but nkv) at most 28 QKV rows, 7 hidden rows and 14 gate/up pairs per block.
 bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks) {
   const int G = nq / nkv;
   if (G != 1 && G != 2 && G != 4) return false;
   if (H > CPT_QKV * TPR_QKV * 8 || H > CPT_GU * TPR_GU * 8 || qd > CPT_O * TPR_O * 8 || I > CPT_D * TPR_D * 8)
     return false;
-  if (H > MAXG * NT) return false;
+  if (H > 64 * MAXE_H || qd > 64 * MAXE_Q || I > 64 * MAXE_I || I > 6 * NT || H > 6 * NT) return false;
   if (H % 8 || qd % 8 || I % 8) return false;
   const int ng = nblocks - nkv;
   if (ng < 1) return false;
   auto rpb = [ng](int n) { return (n + ng - 1) / ng; };
-  if (rpb(qkv_rows) > NT / TPR_QKV || rpb(I) > NT / TPR_GU || rpb(H) > NT / TPR_O) return false;
+  if (rpb(qkv_rows) > NC / TPR_QKV || rpb(I) > NC / TPR_GU || rpb(H) > NC / TPR_O) return false;
   return true;
 }
 

@@ -15,6 +15,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
@@ -34,24 +35,52 @@ __device__ __forceinline__ void f16x8_to_f32(u32x4 v, float* out) {
   for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(h[i]);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+// Cross-lane moves inside a row of 16 lanes (DPP, no LDS round trip). CTRL: 0xB1 = quad_perm [1,0,3,2] (lane ^ 1),
+// 0x4E = quad_perm [2,3,0,1] (lane ^ 2), 0x141 = row_half_mirror (lane ^ 7 within 8), 0x140 = row_mirror
+// (lane ^ 15 within 16).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
-
-// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+// Sum over aligned groups of `width` lanes (width a power of two <= 64); every lane gets its group's sum.
+// Within a 16-lane row: DPP steps (xor 1, xor 2, half mirror, mirror); across rows: lane reads of the row sums.
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  static_assert(width == 1 || width == 2 || width == 4 || width == 8 || width == 16 || width == 32 || width == 64,
+                "width must be a power of two <= 64");
+  if constexpr (width >= 2) v += dpp_mov<0xB1>(v);
+  if constexpr (width >= 4) v += dpp_mov<0x4E>(v);
+  if constexpr (width >= 8) v += dpp_mov<0x141>(v);
+  if constexpr (width >= 16) v += dpp_mov<0x140>(v);
+  if constexpr (width == 32) {
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    v = (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+  } else if constexpr (width == 64) {
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    v = (r0 + r1) + (r2 + r3);
+  }
   return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // Block-wide sum for blockDim.x == NT threads; `red` must hold NT/64 floats. All threads get the result.

@@ -497,9 +497,11 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     soc::PersistArgs p = persist_args(m, kv, slot);
     // SOC_TRACE_FILE=<path>: append the last step's per-phase timestamps (diagnostics)
     const char* trace_path = std::getenv("SOC_TRACE_FILE");
-    const size_t trace_n = 2 * (3 + 5 * static_cast<size_t>(m->cfg.num_hidden_layers));
+    const size_t trace_roles = 2 * (4 + 8 * static_cast<size_t>(m->cfg.num_hidden_layers));
+    const size_t trace_n = trace_roles + static_cast<size_t>(w.nblocks) * 8;
     if (trace_path != nullptr) {
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
+      if ((e = hipMemset(p.trace, 0, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
     }
     for (int i = 0; i < steps; ++i)
       if ((e = soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
@@ -514,7 +516,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       (void)hipFree(p.trace);
       if (e != hipSuccess) return hip_fail(e, "hipMemcpy trace");
       if (FILE* f = std::fopen(trace_path, "a")) {
-        const size_t per = trace_n / 2;
+        const size_t per = trace_roles / 2;
         for (int which = 0; which < 2; ++which) {
           std::fprintf(f, "%s:", which == 0 ? "block0" : "blockN");
           for (size_t i = 1; i < per; ++i) {
@@ -522,8 +524,22 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
             if (x == 0 || y == 0) std::fprintf(f, " -");
             else std::fprintf(f, " %.2f", (static_cast<double>(x) - static_cast<double>(y)) * 0.01);  // us (100 MHz)
           }
-          std::fprintf(f, " | total %.2f us\n", (t[which * per + per - 1] - t[which * per]) * 0.01);
+          std::fprintf(f, "\n");
         }
+        // middle layer, every projection block: per point, min / median / max relative to the earliest point-0
+        const int ng = w.nblocks - m->cfg.num_key_value_heads;
+        uint64_t t0 = ~0ull;
+        for (int b = 0; b < ng; ++b)
+          if (t[trace_roles + b * 8] != 0) t0 = std::min(t0, t[trace_roles + b * 8]);
+        std::fprintf(f, "middle layer (us from earliest P1-input):");
+        for (int pnt = 0; pnt < 8; ++pnt) {
+          std::vector<double> v;
+          for (int b = 0; b < ng; ++b)
+            if (t[trace_roles + b * 8 + pnt] != 0) v.push_back((static_cast<double>(t[trace_roles + b * 8 + pnt]) - t0) * 0.01);
+          std::sort(v.begin(), v.end());
+          if (!v.empty()) std::fprintf(f, " p%d[%.2f %.2f %.2f]", pnt, v.front(), v[v.size() / 2], v.back());
+        }
+        std::fprintf(f, "\n");
         std::fclose(f);
       }
     }
