@@ -50,12 +50,17 @@ __device__ __forceinline__ bool err_raised(int* err) {
 }
 
 __device__ __forceinline__ uint32_t tag_of(uint64_t v) { return static_cast<uint32_t>(v >> 32); }
+
+// Back-off between polling rounds: fewer re-reads of lines that producers are about to write.
+__device__ __forceinline__ void poll_pause(int n) {
+  for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(1);
+}
 __device__ __forceinline__ float val_of(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 
 // Receiver wave: elements i = lane + 64 e (e < MAXE) of a tagged vector, re-read until every one carries `tag`.
 // `addr(i)` gives the source of element i < n. Returns false (wave-uniform) on timeout or a raised error flag.
 template <int MAXE, typename Addr>
-__device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err) {
+__device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err, int pause) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int e = 0; e < MAXE; ++e) {
@@ -73,6 +78,7 @@ __device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t t
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
+    poll_pause(pause);
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
       const int i = lane + 64 * e;
@@ -94,7 +100,7 @@ __device__ __forceinline__ uint64_t ll_peek_buf(__amdgpu_buffer_rsrc_t r, int by
 // (Mac/cpu/src/rms_norm_module.cpp:56-64: ms = sum x^2 / n; y = x * (1 / sqrt(ms + eps)) * g).
 template <int MAXE, bool NORM>
 __device__ __forceinline__ bool recv_vec(const uint64_t* src, int n, uint32_t tag, float* dst, const f16* gain,
-                                         float eps, int* err) {
+                                         float eps, int* err, int pause) {
   const int lane = threadIdx.x & 63;
   float g[NORM ? MAXE : 1];
   if constexpr (NORM) {
@@ -125,6 +131,7 @@ __device__ __forceinline__ bool recv_vec(const uint64_t* src, int n, uint32_t ta
       ok = false;
       break;
     }
+    poll_pause(pause);
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
       const int i = lane + 64 * e;
@@ -272,7 +279,6 @@ template <int G>
 __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, float* kn, float* vn) {
   const PersistArgs& a = c.a;
   const int lane = threadIdx.x & 63;
-  const int S = c.pos + 1;
   for (int layer = 0; layer < a.L; ++layer) {
     const f16* const* W = a.layer_w + layer * 9;
     const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
@@ -293,7 +299,7 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
                                    const int hidx = i / HD, d = i % HD;
                                    return hidx < G ? q_src + hidx * HD + d : (hidx == G ? k_src + d : v_src + d);
                                  },
-                                 a.err);
+                                 a.err, a.spin_sleep);
     if (ok) {
       // per-head RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171; rope.cpp:81-84): lane holds dims
       // (lane, lane + 64) of each head; the key and value are rounded to fp16 and appended at `pos`
@@ -325,26 +331,23 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
     }
     report(c, ok);
     SOC_SYNC();                                    // inputs ready
-    for (int c0 = 0; c0 < S; c0 += KCH) {
-      SOC_SYNC();                                  // scores written
-      SOC_SYNC();                                  // softmax statistics
-      SOC_SYNC();                                  // weighted values
-    }
-    SOC_SYNC();                                    // group partials
+    SOC_SYNC();                                    // partials
     SOC_SYNC();                                    // outputs stored; LDS free for the next layer
   }
   return true;
 }
 
 // ---------------- attention block: compute waves (28 groups of 16 lanes, 8 dims per lane) ----------------
+// Flash-decoding inside the block (the online form of grouped_query_attention.cpp:105-136): every wave keeps its
+// own running max, sum and weighted values over the keys its 4 groups own (key p of a chunk: group p % 28), in
+// registers across all chunks; one barrier then merges the 7 waves: out = sum_w o_w e^(m_w - M) / sum_w l_w e^(m_w - M).
 template <int G>
 __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* qs, const float* kn, const float* vn) {
   const PersistArgs& a = c.a;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
   const int sub = tid & 15, grp = tid >> 4;
-  float* sc = c.att + G * HD + 2 * HD;     // [G][KCH] scores, then weights
-  float* pred = sc + G * KCH;              // [28][G][HD] key-group partials
-  float* stat = pred + (NC / 16) * G * HD;  // [G] running max, [G] running sum, [G] correction
+  float* pred = c.att + G * HD + 2 * HD;   // [28][G][HD] group partial sums (scaled by the wave's max)
+  float* wst = pred + (NC / 16) * G * HD;  // [7][G][2] wave max, wave sum
   const int pos = c.pos, S = pos + 1;
   u32x4 kreg[8], vreg[8];
   for (int layer = 0; layer < a.L; ++layer) {
@@ -362,24 +365,23 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
     };
     // cached keys/values of the first chunk do not depend on this layer's q/k/v: in flight before the wait
     kv_fetch(0);
-    if (tid < G) {
-      stat[tid] = -INFINITY;
-      stat[G + tid] = 0.0f;
-    }
     SOC_TRACE(1 + 8 * layer);
     SOC_SYNC();                                    // inputs ready
     SOC_TRACE(2 + 8 * layer);
-    float qreg[G][8], acc[G][8];
+    float qreg[G][8], acc[G][8], mw[G], lw[G];
 #pragma unroll
-    for (int j = 0; j < G; ++j)
+    for (int j = 0; j < G; ++j) {
+      mw[j] = -INFINITY;
+      lw[j] = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         qreg[j][i] = qs[j * HD + sub * 8 + i];
         acc[j][i] = 0.0f;
       }
+    }
     for (int c0 = 0; c0 < S; c0 += KCH) {
       const int n = min(KCH, S - c0);
-      // scores (grouped_query_attention.cpp:105-116); key p of the chunk lives in group p % 28, slot p / 28
+      float sc[8][G];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int p = grp + 28 * u;
@@ -396,42 +398,34 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
             float d = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
-            d = group_sum<16>(d);
-            if (sub == 0) sc[j * KCH + p] = d * a.scale;
+            sc[u][j] = group_sum<16>(d) * a.scale;   // every lane of the group holds the key's score
           }
+        } else {
+#pragma unroll
+          for (int j = 0; j < G; ++j) sc[u][j] = -INFINITY;
         }
       }
-      SOC_SYNC();                                  // scores written
-      // running max / sum (online form of :113-122), one wave per query head
-      if (wid < G) {
-        const int j = wid;
-        float m = -INFINITY;
-        for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[j * KCH + p]);
-        m = wave_max(m);
-        const float m_old = stat[j];
-        const float m_new = fmaxf(m_old, m);
-        float ssum = 0.0f;
-        for (int p = lane; p < n; p += 64) {
-          const float w = expf(sc[j * KCH + p] - m_new);
-          sc[j * KCH + p] = w;
-          ssum += w;
-        }
-        ssum = wave_sum(ssum);
-        if (lane == 0) {
-          const float corr = expf(m_old - m_new);
-          stat[2 * G + j] = corr;
-          stat[G + j] = stat[G + j] * corr + ssum;
-          stat[j] = m_new;
-        }
-      }
-      SOC_SYNC();                                  // softmax statistics
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        const float corr = stat[2 * G + j];
+        float mx = sc[0][j];
+#pragma unroll
+        for (int u = 1; u < 8; ++u) mx = fmaxf(mx, sc[u][j]);
+        mx = wave_max(mx);
+        const float mn = fmaxf(mw[j], mx);
+        const float corr = mn == -INFINITY ? 1.0f : expf(mw[j] - mn);
+        float ls = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float pw = sc[u][j] == -INFINITY ? 0.0f : expf(sc[u][j] - mn);
+          sc[u][j] = pw;
+          ls += pw;
+        }
+        // the 16 lanes of a group hold the same keys: the wave sum over 64 lanes counts each group 16 times
+        lw[j] = lw[j] * corr + wave_sum(ls) * (1.0f / 16.0f);
+        mw[j] = mn;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[j][i] *= corr;
       }
-      // weighted values (:130-136)
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int p = grp + 28 * u;
@@ -444,28 +438,44 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
             f16x8_to_f32(vreg[u], vf);
           }
 #pragma unroll
-          for (int j = 0; j < G; ++j) {
-            const float w = sc[j * KCH + p];
+          for (int j = 0; j < G; ++j)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
-          }
+            for (int i = 0; i < 8; ++i) acc[j][i] += sc[u][j] * vf[i];
         }
       }
       if (c0 + KCH < S) kv_fetch(c0 + KCH);
-      SOC_SYNC();                                  // weighted values
     }
-    // the 28 key groups' partial sums, reduced through LDS
+    // group partials and the wave statistics, then one merge
 #pragma unroll
     for (int j = 0; j < G; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) pred[(grp * G + j) * HD + sub * 8 + i] = acc[j][i];
-    SOC_SYNC();                                    // group partials
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        wst[(wid * G + j) * 2] = mw[j];
+        wst[(wid * G + j) * 2 + 1] = lw[j];
+      }
+    }
+    SOC_SYNC();                                    // partials
     for (int idx = tid; idx < G * HD; idx += NC) {
-      const int j = idx / HD, i = idx % HD;
-      float o = 0.0f;
-#pragma unroll 4
-      for (int q = 0; q < NC / 16; ++q) o += pred[(q * G + j) * HD + i];
-      ll_store(a.attn + (g * G + j) * HD + i, o / stat[G + j], tag);
+      const int j = idx / HD, d = idx % HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NC / 64; ++w) M = fmaxf(M, wst[(w * G + j) * 2]);
+      float L = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NC / 64; ++w) {
+        const float m_w = wst[(w * G + j) * 2];
+        if (m_w == -INFINITY) continue;          // a wave that owned no visible key
+        const float e = expf(m_w - M);
+        L += wst[(w * G + j) * 2 + 1] * e;
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o += pred[((w * 4 + q) * G + j) * HD + d];
+        O += o * e;
+      }
+      ll_store(a.attn + (g * G + j) * HD + d, O / L, tag);
     }
     SOC_TRACE(3 + 8 * layer);
     SOC_SYNC();                                    // outputs stored; LDS free for the next layer
@@ -473,66 +483,86 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
   return true;
 }
 
-// ---------------- whole-block receive (all 8 waves; used where no weight loads are in flight) ----------------
-// Entries i = tid + 512 e of the tagged vector src[0..n) go to dst; with NORM, the block then applies the RMSNorm
-// with `gain` (a block-wide sum of squares through LDS). Two barriers with NORM, one without.
+// ---------------- multi-wave receive (waves w0..7; used where those waves have no loads or stores in flight) -----
+// Element pairs of the tagged vector src[0..n) are spread over the polling threads and go to dst; with NORM, the
+// block then applies the RMSNorm with `gain` (a block-wide sum of squares through LDS). Every wave takes part in
+// the barriers: two with NORM, one without. (A single polling wave sees the first data sooner, but more polling
+// threads see the last element sooner when the vector is long; which wins is a per-phase measurement.)
 template <bool NORM>
 __device__ __forceinline__ bool block_recv(const Ctx& c, const uint64_t* src, const f16* embed_row, int n,
-                                           uint32_t tag, float* dst, const f16* gain, float eps) {
-  constexpr int MB = 6;  // n <= 3072
+                                           uint32_t tag, float* dst, const f16* gain, float eps, int w0) {
+  constexpr int MP = 3;  // pairs of elements per polling thread
+  constexpr int MB = 2 * MP;
   const int tid = threadIdx.x, wid = tid >> 6;
+  const bool polls = wid >= w0;
+  const int tp = tid - 64 * w0, np = NT - 64 * w0;  // polling thread index and count
+  // polling thread tp owns the element pairs (2 tp + 2 np e, + 1): one 16-byte load reads both tagged words
+  auto elem = [&](int e) { return 2 * tp + (e & 1) + 2 * np * (e >> 1); };
   float x[MB];
   bool ok = true;
-  if (embed_row != nullptr) {
+  if (!polls) {
+#pragma unroll
+    for (int e = 0; e < MB; ++e) x[e] = 0.0f;
+  } else if (embed_row != nullptr) {
     // layer 0: the embedding row itself (embedding.cpp:51-77)
 #pragma unroll
     for (int e = 0; e < MB; ++e) {
-      const int i = tid + NT * e;
+      const int i = elem(e);
       x[e] = i < n ? static_cast<float>(embed_row[i]) : 0.0f;
     }
   } else {
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(src), 0, n * 8, 0x00020000);
-    uint64_t v[MB];
+    u32x4 v[MP];
+    auto done = [&](const u32x4& w, int e) {  // both words of pair e carry the tag (or lie past n)
+      const int i = 2 * tp + 2 * np * e;
+      return (i >= n || w.y == tag) && (i + 1 >= n || w.w == tag);
+    };
 #pragma unroll
-    for (int e = 0; e < MB; ++e) {
-      const int i = tid + NT * e;
-      v[e] = i < n ? ll_peek_buf(rsrc, tid * 8 + NT * 8 * e) : (static_cast<uint64_t>(tag) << 32);
+    for (int e = 0; e < MP; ++e) {
+      const int i = 2 * tp + 2 * np * e;
+      v[e] = i < n ? __builtin_amdgcn_raw_buffer_load_b128(rsrc, tp * 16 + np * 16 * e, 0, 16)
+                   : u32x4{0, tag, 0, tag};
     }
     const uint64_t t0 = now_ticks();
     uint32_t spins = 0;
     while (true) {
       bool all = true;
 #pragma unroll
-      for (int e = 0; e < MB; ++e) all = all && tag_of(v[e]) == tag;
+      for (int e = 0; e < MP; ++e) all = all && done(v[e], e);
       if (__all(all)) break;
       if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
         __hip_atomic_store(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ok = false;
         break;
       }
+      poll_pause(c.a.spin_sleep);
 #pragma unroll
-      for (int e = 0; e < MB; ++e) {
-        const int i = tid + NT * e;
-        if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek_buf(rsrc, tid * 8 + NT * 8 * e);
-      }
+      for (int e = 0; e < MP; ++e)
+        if (!done(v[e], e)) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tp * 16 + np * 16 * e, 0, 16);
     }
 #pragma unroll
-    for (int e = 0; e < MB; ++e) x[e] = val_of(v[e]);
+    for (int e = 0; e < MP; ++e) {
+      x[2 * e] = __uint_as_float(v[e].x);
+      x[2 * e + 1] = __uint_as_float(v[e].z);
+    }
   }
   if (!ok && (tid & 63) == 0) c.flag[0] = 1;
   float* red = reinterpret_cast<float*>(c.bv);  // [8] wave partial sums (argmax scratch is idle until the LM head)
   if constexpr (!NORM) {
 #pragma unroll
     for (int e = 0; e < MB; ++e) {
-      const int i = tid + NT * e;
-      if (i < n) dst[i] = x[e];
+      const int i = elem(e);
+      if (polls && i < n) dst[i] = x[e];
     }
     SOC_SYNC();
   } else {
     float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < MB; ++e) ss += tid + NT * e < n ? x[e] * x[e] : 0.0f;
+    for (int e = 0; e < MB; ++e) {
+      const int i = elem(e);
+      ss += polls && i < n ? x[e] * x[e] : 0.0f;
+    }
     ss = wave_sum(ss);
     if ((tid & 63) == 0) red[wid] = ss;
     SOC_SYNC();
@@ -542,8 +572,8 @@ __device__ __forceinline__ bool block_recv(const Ctx& c, const uint64_t* src, co
     const float scale = 1.0f / sqrtf(tot / static_cast<float>(n) + eps);
 #pragma unroll
     for (int e = 0; e < MB; ++e) {
-      const int i = tid + NT * e;
-      if (i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
+      const int i = elem(e);
+      if (polls && i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
     }
     SOC_SYNC();
   }
@@ -558,12 +588,13 @@ __device__ __forceinline__ bool proj_receiver(const Ctx& c) {
     const f16* const* W = a.layer_w + layer * 9;
     const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
     if (!block_recv<true>(c, a.xb, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, H, tag - 1,
-                          c.xs0, W[0], a.eps))
+                          c.xs0, W[0], a.eps, 0))
       return false;                                // P1 input
-    report(c, recv_vec<MAXE_Q, false>(a.attn, a.qd, tag, c.xs1, nullptr, a.eps, a.err));
+    report(c, recv_vec<MAXE_Q, false>(a.attn, a.qd, tag, c.xs1, nullptr, a.eps, a.err, a.spin_sleep));
     SOC_SYNC();                                    // P3 input (receiver alone: the weight stream is in flight)
-    if (!block_recv<true>(c, a.xa, nullptr, H, tag, c.xs0, W[1], a.eps)) return false;      // P4 input
-    if (!block_recv<false>(c, a.h, nullptr, a.I, tag, c.xs1, nullptr, a.eps)) return false;  // P5 input
+    report(c, recv_vec<MAXE_H, true>(a.xa, H, tag, c.xs0, W[1], a.eps, a.err, a.spin_sleep));
+    SOC_SYNC();                                    // P4 input (receiver alone: its first sight of the data is earliest)
+    if (!block_recv<false>(c, a.h, nullptr, a.I, tag, c.xs1, nullptr, a.eps, 0)) return false;      // P5 input
   }
   return true;
 }
@@ -592,7 +623,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
     // ---- P1: RMSNorm + QKV projection ----
     if (!block_recv<true>(c, a.xb, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, H, tag - 1,
-                          c.xs0, W[0], a.eps))
+                          c.xs0, W[0], a.eps, 0))
       return false;
     SOC_TRACE(1 + 8 * layer);
     {
@@ -607,6 +638,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     slice_load(su, W[7], H, i0, i1);
     slice_load(sd, W[8], I, h0, h1);
     if (layer + 1 < a.L) slice_load(sq, a.layer_w[(layer + 1) * 9 + 4], H, q0, q1);
+    if (a.trace != nullptr) __builtin_amdgcn_s_waitcnt(0);  // diagnostics: point 2 = the weight stream has landed
     SOC_TRACE(2 + 8 * layer);
     // ---- P3: o_proj + residual ----
     SOC_SYNC();
@@ -618,7 +650,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     }
     SOC_TRACE(4 + 8 * layer);
     // ---- P4: RMSNorm + gate/up + SwiGLU ----
-    if (!block_recv<true>(c, a.xa, nullptr, H, tag, c.xs0, W[1], a.eps)) return false;
+    SOC_SYNC();
     SOC_TRACE(5 + 8 * layer);
     {
       const float og = slice_dot(sg, c.xs0, H);
@@ -628,7 +660,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     }
     SOC_TRACE(6 + 8 * layer);
     // ---- P5: down + residual ----
-    if (!block_recv<false>(c, a.h, nullptr, I, tag, c.xs1, nullptr, a.eps)) return false;
+    if (!block_recv<false>(c, a.h, nullptr, I, tag, c.xs1, nullptr, a.eps, 0)) return false;
     SOC_TRACE(7 + 8 * layer);
     {
       const float out = slice_dot(sd, c.xs1, I);
@@ -644,7 +676,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
 __device__ __forceinline__ bool lm_receiver(const Ctx& c) {
   const PersistArgs& a = c.a;
   const uint32_t last_tag = c.step * 64u + static_cast<uint32_t>(a.L);
-  report(c, recv_vec<MAXE_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err));
+  report(c, recv_vec<MAXE_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err, a.spin_sleep));
   SOC_SYNC();
   return true;
 }
@@ -784,7 +816,7 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
 #undef SOC_TRACE
 
 size_t persistent_lds_bytes(const PersistArgs& a, int G) {
-  const size_t att = static_cast<size_t>(G) * HD + 2 * HD + static_cast<size_t>(G) * KCH + (NC / 16) * G * HD + 3 * G;
+  const size_t att = static_cast<size_t>(G) * HD + 2 * HD + (NC / 16) * G * HD + (NC / 64) * G * 2;
   return (2 * static_cast<size_t>(a.xs_cap) + 96 + att) * sizeof(float);
 }
 

@@ -134,7 +134,8 @@ struct PersistArgs {
   int* ring;                  // nullable
   int* ring_pos;
   int* err;                   // raised when a wait times out
-  uint64_t* trace;            // nullable: phase timestamps [2][3 + 5 L] (diagnostics)
+  uint64_t* trace;            // nullable: phase timestamps (diagnostics)
+  int spin_sleep;             // back-off between polling rounds, in units of s_sleep 1 (about 64 clocks)
 };
 bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks);
 size_t persistent_lds_bytes(const PersistArgs& a, int G);

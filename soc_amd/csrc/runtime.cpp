@@ -481,6 +481,7 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
   p.ring = w.ring;
   p.ring_pos = w.ring_pos;
   p.err = w.err;
+  if (const char* sl = std::getenv("SOC_SPIN_SLEEP")) p.spin_sleep = std::max(0, std::atoi(sl));
   return p;
 }
 
