@@ -8,6 +8,9 @@ the device. A "step" is one decode token. Also measured in the same run:
   * the dominant decode kernel: k_decode_persistent (one launch = one whole token) when the device runs the
     persistent decode, timed with HIP events on the stream it is launched on; the fused RMSNorm + QKV GEMV
     (4096 x 1024 fp16, over weight copies larger than the 256 MB Infinity Cache) is reported beside it,
+  * every decode projection shape (q, k/v, o, gate/up, down, LM head) as an fp16 GEMV at batch 1 and as the
+    int8 / int4 group-quantized matmul (group 64, fp16 scales) at batch 1 and 8, in GB/s against 8 TB/s,
+  * the Qwen3-4B ragged decode batch (16 sequences, seeded KV lengths in [64, 4096]),
   * the reference CPU runtime (compiled reference sources when available, else the oracle restatement), on the
     host, one core, on a bounded sample.
 HBM traffic per launch of the dominant kernel comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
@@ -147,6 +150,72 @@ def bench_gemv_kernel(ctx, n=4096, k=1024, iters=200):
     return us, alg_bytes
 
 
+# Decode projection shapes of Qwen3-0.6B (out x in): the GEMV and group-quantized matmul microbenchmarks
+OP_SHAPES = [("q_proj", 2048, 1024), ("k_proj/v_proj", 1024, 1024), ("o_proj", 1024, 2048),
+             ("gate/up_proj", 3072, 1024), ("down_proj", 1024, 3072), ("lm_head", 151936, 1024)]
+
+
+def _timed_op(ctx, launch, copies: int, iters: int) -> float:
+    """Average microseconds of `launch(i)` (i selects the weight copy) over `iters` back-to-back launches."""
+    for i in range(3):
+        launch(i % copies)
+    ctx.synchronize()
+    ctx.timer_start()
+    for i in range(iters):
+        launch(i % copies)
+    return ctx.timer_stop() * 1e3 / iters
+
+
+def bench_ops(ctx, min_bytes: int = 640 << 20):
+    """fp16 decode GEMV (batch 1) and int8/int4 group-quantized matmul (batch 1 and 8) on every projection shape.
+
+    Weights cycle through enough copies (>= 640 MB) that no launch finds its weights in the 256 MB Infinity Cache;
+    algorithmic bytes: GEMV 2NK + 2K + 4N, QMM NK bits/8 + 2NK/64 (scales) + 2MK + 4MN."""
+    gemv, qmm = [], []
+    for name, n, k in OP_SHAPES:
+        wbytes = 2 * n * k
+        copies = max(2, -(-min_bytes // wbytes))
+        iters = 50 if n > 100000 else 200
+        w_host = S.synth_normal_f16(7, f"ops.{name}.w", 0.02, n * k)
+        dw = ctx.alloc(wbytes * copies)
+        for c in range(copies):
+            ctx.write(dw + c * wbytes, w_host)
+        dx = ctx.upload(S.synth_normal_f16(7, f"ops.{name}.x", 1.0, 8 * k))
+        dy = ctx.alloc(8 * n * 4)
+        try:
+            us = _timed_op(ctx, lambda i: S.gemv_f16(ctx, dw + i * wbytes, dx, dy, n, k), copies, iters)
+            alg = 2 * n * k + 2 * k + 4 * n
+            gemv.append({"shape": f"{name} {n}x{k}", "us": round(us, 3), "gbs": round(alg / us * 1e-3, 1),
+                         "frac": round(alg / us * 1e-3 / HBM_PEAK_GBS, 4)})
+        finally:
+            ctx.free(dw)
+        del w_host
+        for bits in (8, 4):
+            cbytes = n * k * bits // 8
+            sbytes = 2 * n * (k // 64)
+            copies = max(2, -(-min_bytes // (cbytes + sbytes)))
+            dc = ctx.alloc(cbytes * copies)
+            ds = ctx.alloc(sbytes * copies)
+            c_host = S.synth_codes(7, f"ops.{name}.codes{bits}", bits, n * k)
+            s_host = S.synth_uniform_f16(7, f"ops.{name}.scales{bits}", 0.005, 0.02, n * (k // 64))
+            for c in range(copies):
+                ctx.write(dc + c * cbytes, c_host)
+                ctx.write(ds + c * sbytes, s_host)
+            try:
+                for m in (1, 8):
+                    us = _timed_op(ctx, lambda i: S.qmm(ctx, dx, dc + i * cbytes, bits, ds + i * sbytes, dy, m, n, k),
+                                   copies, iters)
+                    alg = cbytes + sbytes + 2 * m * k + 4 * m * n
+                    qmm.append({"shape": f"{name} {n}x{k}", "bits": bits, "m": m, "us": round(us, 3),
+                                "gbs": round(alg / us * 1e-3, 1), "frac": round(alg / us * 1e-3 / HBM_PEAK_GBS, 4)})
+            finally:
+                ctx.free(dc)
+                ctx.free(ds)
+        ctx.free(dx)
+        ctx.free(dy)
+    return gemv, qmm
+
+
 def cpu_baseline(cfg: S.QwenConfig, budget_s: float = 20.0):
     """The reference CPU runtime on a bounded sample: single-token cached forwards of the full model."""
     try:
@@ -221,6 +290,7 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-ragged", action="store_true", help="skip the Qwen3-4B ragged decode measurement")
+    ap.add_argument("--no-ops", action="store_true", help="skip the GEMV / group-quantized matmul microbenchmarks")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -244,6 +314,7 @@ def main() -> None:
     us, alg = bench_gemv_kernel(ctx)
     gemv_gbs = alg / (us * 1e-6) / 1e9
     m.close()
+    ops_gemv, ops_qmm = (None, None) if args.no_ops else bench_ops(ctx)
     ragged = None if args.no_ragged else bench_ragged(ctx)
     ctx.close()
 
@@ -286,6 +357,8 @@ def main() -> None:
         "roofline": roofline,
         "gemv_qkv_4096x1024": {"avg_launch_us": round(us, 3), "gbs": round(gemv_gbs, 1),
                                "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+        "gemv_f16_bs1": ops_gemv,
+        "qmm_g64": ops_qmm,
         "ragged_4b": ragged,
         "cpu_baseline": cpu,
         "generated_tokens_head": [int(t) for t in toks[:8]],
