@@ -6,6 +6,8 @@
 // with 16-byte nontemporal loads; each wave owns R output rows and reduces its 64 partial sums with shuffles.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace soc {
 
 namespace {
@@ -209,11 +211,121 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
   }
 }
 
-// Group-quantized GEMV/skinny GEMM: y[m][n] = sum_k x[m][k] * (float(code[n][k]) * float(scale[n][k/64])).
+// Group-quantized GEMV/skinny GEMM: y[m][n] = sum_g scale[n][g] * sum_{k in group g} x[m][k] * code[n][k], with
+// groups of 64 along K (the product per element is w = float(code) * float(scale), dequant_group's contract).
 // BITS = 8: codes int8 [N][K]; BITS = 4: two's complement nibbles, even k in the low nibble, [N][K/2].
-// Each lane covers 16 consecutive k (one fp16 scale group spans 4 lanes); M <= 8 activation rows are staged in LDS.
-template <int BITS, int M>
+//
+// Each lane streams 16-byte chunks of a row's codes (16 int8 or 32 int4 codes; a chunk never crosses a scale
+// group). The codes become exact fp16 pairs without per-code conversions: the biased code (code + 128, or the
+// nibble + 8) is placed in the low mantissa bits of 1024.0 (fp16 0x64xx) by one byte permute (int8) or one
+// mask-or (int4), and one packed fp16 subtract of 1152 (or 1032) leaves the code itself. v_dot2_f32_f16 then
+// accumulates code pairs times fp16 activation pairs in fp32 (products exact), and one fma per chunk applies the
+// group scale. The activations are staged once per block in LDS as fp16 pairs in the order the codes unpack
+// (int4: k and k + 4 of each group of 8). L lanes share a row (64, or 32 / 16 for short rows) and each lane
+// keeps RR rows in flight: 4 rows per wave for tall matrices, one row per lane group when fewer than 4096 rows
+// would leave most SIMDs idle.
+namespace {
+typedef _Float16 qh2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ qh2 as_qh2(uint32_t v) { return __builtin_bit_cast(qh2, v); }
+
+template <int BITS>
+__device__ __forceinline__ void unpack_codes(const u32x4& w, qh2 (&p)[BITS == 8 ? 8 : 16]) {
+  if constexpr (BITS == 8) {
+    const qh2 bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[j] ^ 0x80808080u;  // code + 128 per byte
+      p[2 * j] = as_qh2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + bias;      // k = 4j, 4j + 1
+      p[2 * j + 1] = as_qh2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias;  // k = 4j + 2, 4j + 3
+    }
+  } else {
+    const qh2 bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[j] ^ 0x88888888u;  // nibble + 8 per nibble
+#pragma unroll
+      for (int i = 0; i < 4; ++i)  // k = 8j + i and 8j + i + 4
+        p[4 * j + i] = as_qh2(((u >> (4 * i)) & 0x000F000Fu) | 0x64006400u) + bias;
+    }
+  }
+}
+}  // namespace
+
+template <int BITS, int M, int L, int RR>
 __global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
+  extern __shared__ uint32_t xq[];  // [M][K / 2] fp16 pairs
+  const int K = a.K, KP = K / 2;
+  for (int i = threadIdx.x; i < M * KP; i += 256) {
+    const int m = i / KP, p = i - m * KP;
+    const int k0 = BITS == 8 ? 2 * p : 8 * (p >> 2) + (p & 3);
+    const int k1 = BITS == 8 ? k0 + 1 : k0 + 4;
+    const f16* xr = a.x + static_cast<size_t>(m) * K;
+    xq[i] = __builtin_bit_cast(uint32_t, qh2{xr[k0], xr[k1]});
+  }
+  __syncthreads();
+  constexpr int CH = BITS == 8 ? 16 : 32;  // codes per 16-byte chunk
+  constexpr int NP = CH / 2;               // fp16 pairs per chunk
+  constexpr int RP = 64 / L;               // rows side by side in a wave
+  constexpr int QR = RR * RP;              // rows per wave per step
+  const int lane = threadIdx.x & 63, sub = lane / L, ln = lane % L;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
+  const int nch = K / CH, G = K / 64;
+  const size_t rowbytes = BITS == 8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
+  const uint8_t* codes = static_cast<const uint8_t*>(a.codes);
+  for (int base = wave * QR; base < a.N; base += nwaves * QR) {
+    int rows[RR];
+#pragma unroll
+    for (int r = 0; r < RR; ++r) rows[r] = min(base + r * RP + sub, a.N - 1);
+    float acc[RR][M];
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+    for (int c = ln; c < nch; c += L) {
+      u32x4 cw[RR];
+      float sc[RR];
+#pragma unroll
+      for (int r = 0; r < RR; ++r) {
+        cw[r] = load_stream16(codes + static_cast<size_t>(rows[r]) * rowbytes + static_cast<size_t>(c) * 16);
+        sc[r] = static_cast<float>(a.scales[static_cast<size_t>(rows[r]) * G + (c * CH) / 64]);
+      }
+      qh2 cp[RR][NP];
+#pragma unroll
+      for (int r = 0; r < RR; ++r) unpack_codes<BITS>(cw[r], cp[r]);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        qh2 xp[NP];
+        const u32x4* xs = reinterpret_cast<const u32x4*>(xq + m * KP + c * NP);
+#pragma unroll
+        for (int q = 0; q < NP / 4; ++q) {
+          const u32x4 v = xs[q];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) xp[4 * q + t] = as_qh2(v[t]);
+        }
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+          float part = 0.0f;
+#pragma unroll
+          for (int q = 0; q < NP; ++q) part = __builtin_amdgcn_fdot2(cp[r][q], xp[q], part, false);
+          acc[r][m] = fmaf(sc[r], part, acc[r][m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float v = group_sum<L>(acc[r][m]);
+        const int row = base + r * RP + sub;
+        if (ln == 0 && row < a.N) a.y[static_cast<size_t>(m) * a.N + row] = v;
+      }
+  }
+}
+
+// Rows too short for 16 lanes of 16-byte chunks (K < 256 int8 / 512 int4): one lane per 16 k, two rows per wave.
+template <int BITS, int M>
+__global__ __launch_bounds__(256) void k_qmm_short(QmmArgs a) {
   extern __shared__ float xs[];  // [M][K]
   for (int m = 0; m < M; ++m)
     for (int i = threadIdx.x; i < a.K; i += 256) xs[m * a.K + i] = static_cast<float>(a.x[static_cast<size_t>(m) * a.K + i]);
@@ -387,21 +499,37 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
 }
 
 hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
-  const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(float);
-  const dim3 grid(gemv_grid(a.N, 2)), block(256);
-#define SOC_QMM_CASE(B, MM)                                                        \
-  if (bits == B && a.M == MM) {                                                   \
-    hipLaunchKernelGGL((k_qmm<B, MM>), grid, block, lds, s, a);                    \
-    return hipGetLastError();                                                     \
+  const int nch = a.K / (bits == 8 ? 16 : 32);  // 16-byte chunks per row
+  if (nch < 16) {
+    const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(float);
+    const dim3 grid(gemv_grid(a.N, 2)), block(256);
+#define SOC_QMM_SHORT(B, MM)                                                       \
+    if (bits == B && a.M == MM) {                                                 \
+      hipLaunchKernelGGL((k_qmm_short<B, MM>), grid, block, lds, s, a);            \
+      return hipGetLastError();                                                   \
+    }
+    SOC_QMM_SHORT(8, 1) SOC_QMM_SHORT(8, 2) SOC_QMM_SHORT(8, 4) SOC_QMM_SHORT(8, 8)
+    SOC_QMM_SHORT(4, 1) SOC_QMM_SHORT(4, 2) SOC_QMM_SHORT(4, 4) SOC_QMM_SHORT(4, 8)
+#undef SOC_QMM_SHORT
+    return hipErrorInvalidValue;
   }
-  SOC_QMM_CASE(8, 1)
-  SOC_QMM_CASE(8, 2)
-  SOC_QMM_CASE(8, 4)
-  SOC_QMM_CASE(8, 8)
-  SOC_QMM_CASE(4, 1)
-  SOC_QMM_CASE(4, 2)
-  SOC_QMM_CASE(4, 4)
-  SOC_QMM_CASE(4, 8)
+  const int L = nch >= 64 ? 64 : nch >= 32 ? 32 : 16;
+  const bool tall = a.N >= 4096;
+  const int rows_per_wave = tall ? 4 : 64 / L;  // RR = 4 / RP, or 1
+  const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(f16);
+  const int waves = (a.N + rows_per_wave - 1) / rows_per_wave;
+  const int blocks = std::min((waves + 3) / 4, 2048);
+  const dim3 grid(std::max(blocks, 1)), block(256);
+#define SOC_QMM_CASE(B, MM, LL)                                                                    \
+  if (bits == B && a.M == MM && L == LL) {                                                        \
+    if (tall) hipLaunchKernelGGL((k_qmm<B, MM, LL, 4 * LL / 64>), grid, block, lds, s, a);         \
+    else hipLaunchKernelGGL((k_qmm<B, MM, LL, 1>), grid, block, lds, s, a);                        \
+    return hipGetLastError();                                                                     \
+  }
+#define SOC_QMM_M(B, LL) SOC_QMM_CASE(B, 1, LL) SOC_QMM_CASE(B, 2, LL) SOC_QMM_CASE(B, 4, LL) SOC_QMM_CASE(B, 8, LL)
+  SOC_QMM_M(8, 64) SOC_QMM_M(8, 32) SOC_QMM_M(8, 16)
+  SOC_QMM_M(4, 64) SOC_QMM_M(4, 32) SOC_QMM_M(4, 16)
+#undef SOC_QMM_M
 #undef SOC_QMM_CASE
   return hipErrorInvalidValue;
 }

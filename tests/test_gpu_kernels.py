@@ -64,7 +64,9 @@ def test_device_f16_decode_exhaustive(gpu_ctx):
     assert np.array_equal(y[np.isinf(want)], want[np.isinf(want)])
 
 
-QMM_SHAPES = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072), (151936, 1024)]
+QMM_SHAPES = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072), (151936, 1024),
+              # short rows: 16 lanes per row (int8 K 256, int4 K 512) and the one-lane-per-16-k kernel (K 128)
+              (96, 256), (80, 512), (40, 128)]
 
 
 def _qmm_inputs(n, k, bits, m):
