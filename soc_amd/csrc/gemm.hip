@@ -85,41 +85,59 @@ __global__ __launch_bounds__(256) void k_gemm_f32a(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// MFMA GEMM: 128x128 output tile per 256-thread block, K slices of 32 staged in LDS (double buffered), each wave
-// owns a 64x64 quadrant as 2x2 tiles of v_mfma_f32_32x32x16_f16. Activations arrive in fp32 and are split on the
-// way into LDS into hi = f16(a) and lo = f16((a - hi) * 2^11); with SPLIT the product is hi.W + 2^-11 lo.W, which
-// keeps about 22 bits of each activation (weights are exact fp16), so the result tracks the fp32 reference.
+// MFMA GEMM: BM x 128 output tile per 256-thread block (BM = 128, or 64 when 128-row tiles would leave CUs idle),
+// K slices of 32 staged in LDS (double buffered), each wave owns a (BM / 2) x 64 quadrant as tiles of
+// v_mfma_f32_32x32x16_f16. Activations arrive in fp32 and are split on the way into LDS into hi = f16(a) and
+// lo = f16((a - hi) * 2^11); with SPLIT the product is hi.W + 2^-11 lo.W, which keeps about 22 bits of each
+// activation (weights are exact fp16), so the result tracks the fp32 reference.
+// Global loads run two K slices ahead of the MFMAs (two register stages), so a slice's loads have two slices of
+// MFMA work to arrive in.
 // EPI_SWIGLU stages 64 gate rows and the matching 64 up rows per tile; a wave holds gate and up accumulators of the
 // same outputs in the same registers and writes silu(g) * u.
 // ------------------------------------------------------------------------------------------------------------
 namespace {
-constexpr int MBM = 128, MBN = 128, MBK = 32, MPAD = 8;  // LDS rows padded to 40 halves (80 B)
+constexpr int MBN = 128, MBK = 32, MPAD = 8;  // LDS rows padded to 40 halves (80 B)
 constexpr int MLD = MBK + MPAD;
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 }  // namespace
 
-template <int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
+template <int EPI, bool SPLIT, int BM>
+__global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
   constexpr int NA = SPLIT ? 2 : 1;
-  __shared__ _Float16 As[2][NA][MBM * MLD];
+  constexpr int MI = BM / 64;         // 32-row MFMA tiles per wave
+  constexpr int AV = BM * MBK / 1024;  // float4 of A per thread per slice
+  __shared__ _Float16 As[2][NA][BM * MLD];
   __shared__ _Float16 Bs[2][MBN * MLD];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
-  const int m0 = blockIdx.y * MBM;
+  // XCD-aware tile order: blocks are dispatched round-robin over the 8 XCDs, so block b runs on XCD b % 8. Each
+  // XCD takes a contiguous eighth of the column tiles (its weight rows stay in its L2) and walks them fastest, so
+  // its co-resident blocks share activation row tiles too.
+  const int mt = (g.M + BM - 1) / BM, nt = gridDim.x / mt;
+  int mtile, ntile;
+  if (nt % 8 == 0) {
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, per = nt >> 3;
+    ntile = xcd * per + j % per;
+    mtile = j / per;
+  } else {
+    ntile = blockIdx.x % nt;
+    mtile = blockIdx.x / nt;
+  }
+  const int m0 = mtile * BM;
   // output columns covered by this block: plain GEMM 128, SwiGLU 64 (gate/up pairs)
-  const int n0 = blockIdx.x * (EPI == EPI_SWIGLU ? MBN / 2 : MBN);
+  const int n0 = ntile * (EPI == EPI_SWIGLU ? MBN / 2 : MBN);
 
-  // global -> register staging: A 128 x 32 fp32 = 1024 float4 (4 per thread); W 128 x 32 fp16 = 512 x 16 B (2 per thread)
-  f32x4 ra[4];
-  u32x4 rb[2];
-  auto load_tiles = [&](int k0) {
+  // global -> register staging (two stages): A BM x 32 fp32, W 128 x 32 fp16 = 512 x 16 B (2 per thread)
+  f32x4 ra[2][AV];
+  u32x4 rb[2][2];
+  auto load_tiles = [&](int st, int k0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < AV; ++e) {
       const int idx = tid + e * 256;
       const int r = idx >> 3, c = (idx & 7) * 4;
       const int m = m0 + r;
-      ra[e] = (m < g.M) ? *reinterpret_cast<const f32x4*>(g.a + static_cast<size_t>(m) * g.lda + k0 + c)
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      ra[st][e] = (m < g.M) ? *reinterpret_cast<const f32x4*>(g.a + static_cast<size_t>(m) * g.lda + k0 + c)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -134,18 +152,18 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
         n = n0 + r;
         src = g.w;
       }
-      rb[e] = (n < g.N) ? load16(src + static_cast<size_t>(n) * g.K + k0 + c) : u32x4{0, 0, 0, 0};
+      rb[st][e] = (n < g.N) ? load16(src + static_cast<size_t>(n) * g.K + k0 + c) : u32x4{0, 0, 0, 0};
     }
   };
-  auto store_tiles = [&](int buf) {
+  auto store_tiles = [&](int st, int buf) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < AV; ++e) {
       const int idx = tid + e * 256;
       const int r = idx >> 3, c = (idx & 7) * 4;
       f16x4 hi, lo;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = ra[e][i];
+        const float v = ra[st][e][i];
         const _Float16 h = static_cast<_Float16>(v);
         hi[i] = h;
         lo[i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
@@ -157,13 +175,13 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
     for (int e = 0; e < 2; ++e) {
       const int idx = tid + e * 256;
       const int r = idx >> 2, c = (idx & 3) * 8;
-      *reinterpret_cast<u32x4*>(&Bs[buf][r * MLD + c]) = rb[e];
+      *reinterpret_cast<u32x4*>(&Bs[buf][r * MLD + c]) = rb[st][e];
     }
   };
 
-  f32x16 acc[2][2], acc_lo[2][2];
+  f32x16 acc[MI][2], acc_lo[MI][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -175,12 +193,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
   // B sub-tile rows of this wave: plain = wn*64 + t*32; SwiGLU: t = 0 gate rows wn*32, t = 1 up rows 64 + wn*32
   const int brow[2] = {EPI == EPI_SWIGLU ? wn * 32 : wn * 64, EPI == EPI_SWIGLU ? 64 + wn * 32 : wn * 64 + 32};
   const int KT = g.K / MBK;
-  load_tiles(0);
-  store_tiles(0);
+  // slice kt is loaded into register stage kt & 1 and stored into LDS buffer kt & 1
+  load_tiles(0, 0);
+  if (KT > 1) load_tiles(1, MBK);
+  store_tiles(0, 0);
   __syncthreads();
   for (int kt = 0; kt < KT; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) load_tiles((kt + 1) * MBK);
+    if (kt + 2 < KT) load_tiles(buf, (kt + 2) * MBK);  // stage buf held slice kt, already in LDS
 #pragma unroll
     for (int ks = 0; ks < MBK / 16; ++ks) {
       const int kc = ks * 16 + (lane >> 5) * 8;
@@ -189,8 +209,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
       for (int t = 0; t < 2; ++t)
         bf[t] = *reinterpret_cast<const h8*>(&Bs[buf][(brow[t] + (lane & 31)) * MLD + kc]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int arow = wm * 64 + i * 32 + (lane & 31);
+      for (int i = 0; i < MI; ++i) {
+        const int arow = wm * (BM / 2) + i * 32 + (lane & 31);
         const h8 ah = *reinterpret_cast<const h8*>(&As[buf][0][arow * MLD + kc]);
 #pragma unroll
         for (int t = 0; t < 2; ++t) acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bf[t], acc[i][t], 0, 0, 0);
@@ -202,16 +222,16 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
         }
       }
     }
-    if (kt + 1 < KT) store_tiles(buf ^ 1);
+    if (kt + 1 < KT) store_tiles(buf ^ 1, buf ^ 1);
     __syncthreads();
   }
 
   // epilogue: lane holds D[m][n] for n = lane % 32, m = (r / 4) * 8 + (lane / 32) * 4 + r % 4
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      const int m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
       if (m >= g.M) continue;
       float v[2];
 #pragma unroll
@@ -237,8 +257,16 @@ bool gemm_mfma_supported(const GemmArgs& g) { return g.K % MBK == 0 && g.lda % 4
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s) {
   if (!gemm_mfma_supported(g)) return hipErrorInvalidValue;
   const int bn = epi == EPI_SWIGLU ? MBN / 2 : MBN;
-  const dim3 grid((g.N + bn - 1) / bn, (g.M + MBM - 1) / MBM), block(256);
-#define SOC_MFMA_CASE(E, SP) hipLaunchKernelGGL((k_gemm_mfma<E, SP>), grid, block, 0, s, g)
+  const int ntiles = (g.N + bn - 1) / bn;
+  // 64-row tiles when 128-row tiles would not give every CU a block
+  const bool small = ntiles * ((g.M + 127) / 128) < 256;
+  const int bm = small ? 64 : 128;
+  const dim3 grid(ntiles * ((g.M + bm - 1) / bm)), block(256);
+#define SOC_MFMA_CASE(E, SP)                                                     \
+  do {                                                                           \
+    if (small) hipLaunchKernelGGL((k_gemm_mfma<E, SP, 64>), grid, block, 0, s, g); \
+    else hipLaunchKernelGGL((k_gemm_mfma<E, SP, 128>), grid, block, 0, s, g);     \
+  } while (0)
   if (split) {
     if (epi == EPI_STORE) SOC_MFMA_CASE(EPI_STORE, true);
     else if (epi == EPI_RESIDUAL) SOC_MFMA_CASE(EPI_RESIDUAL, true);
