@@ -10,6 +10,8 @@
 // fp16 before use so that decode and prefill see identical keys.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace soc {
 
 namespace {
@@ -305,8 +307,9 @@ __global__ __launch_bounds__(256) void k_embed(const int32_t* ids, const f16* ta
   for (int i = threadIdx.x; i < H; i += 256) x[static_cast<size_t>(t) * H + i] = static_cast<float>(src[i]);
 }
 
+// yh = f16(y); with ylo also set, ylo = f16((y - yh) * 2^11): the hi/lo activation pair of the MFMA GEMMs.
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, int H, const f16* gain, float eps, float* yf,
-                                                      f16* yh) {
+                                                      f16* yh, f16* ylo) {
   __shared__ float red[4];
   const float* xr = x + static_cast<size_t>(blockIdx.x) * H;
   float ss = 0.0f;
@@ -315,8 +318,22 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, int H, con
   const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
   for (int i = threadIdx.x; i < H; i += 256) {
     const float y = xr[i] * scale * static_cast<float>(gain[i]);
-    if (yf) yf[static_cast<size_t>(blockIdx.x) * H + i] = y;
-    if (yh) yh[static_cast<size_t>(blockIdx.x) * H + i] = static_cast<f16>(y);
+    const size_t o = static_cast<size_t>(blockIdx.x) * H + i;
+    if (yf) yf[o] = y;
+    if (yh) {
+      const f16 hi = static_cast<f16>(y);
+      yh[o] = hi;
+      if (ylo) ylo[o] = static_cast<f16>((y - static_cast<float>(hi)) * 2048.0f);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_split_f16(const float* x, size_t n, f16* hi, f16* lo) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+    const float v = x[i];
+    const f16 h = static_cast<f16>(v);
+    hi[i] = h;
+    lo[i] = static_cast<f16>((v - static_cast<float>(h)) * 2048.0f);
   }
 }
 
@@ -486,7 +503,7 @@ __global__ __launch_bounds__(256) void k_attention_prefill_mfma(AttnArgs a) {
 
   const float lt = l + __shfl_xor(l, 32);
   if (t < a.B) {
-    float* dst = a.out + static_cast<size_t>(t) * a.ld_out + head * HD;
+    const size_t row = static_cast<size_t>(t) * a.ld_out + head * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -494,7 +511,18 @@ __global__ __launch_bounds__(256) void k_attention_prefill_mfma(AttnArgs a) {
         f32x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = o[db][r4 * 4 + i] / lt;
-        *reinterpret_cast<f32x4*>(dst + db * 32 + r4 * 8 + hb * 4) = v;
+        const size_t off = row + db * 32 + r4 * 8 + hb * 4;
+        if (a.out != nullptr) *reinterpret_cast<f32x4*>(a.out + off) = v;
+        if (a.out_hi != nullptr) {  // the hi/lo activation pair of the o projection
+          f16x4 hi, lo;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hi[i] = static_cast<f16>(v[i]);
+            lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
+          }
+          *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
+          *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
+        }
       }
   }
 }
@@ -503,6 +531,8 @@ hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;
   if (a.ld_qkv % 4 != 0 || a.ld_out % 4 != 0) return hipErrorInvalidValue;
+  if ((a.out_hi == nullptr) != (a.out_lo == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
+    return hipErrorInvalidValue;
 #define SOC_FA_CASE(GG)                                                                        \
   if (G == GG) {                                                                               \
     const dim3 grid((a.B + 32 * (4 / GG) - 1) / (32 * (4 / GG)), a.nkv);                       \
@@ -550,8 +580,16 @@ hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, floa
 }
 
 hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const f16* gain, float eps, float* yf, f16* yh,
-                               hipStream_t s) {
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, H, gain, eps, yf, yh);
+                               f16* ylo, hipStream_t s) {
+  if (ylo != nullptr && yh == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, H, gain, eps, yf, yh, ylo);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_f16(const float* x, size_t n, f16* hi, f16* lo, hipStream_t s) {
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_split_f16, dim3(static_cast<unsigned>(std::max<size_t>(blocks, 1))), dim3(256), 0, s, x, n, hi,
+                     lo);
   return hipGetLastError();
 }
 

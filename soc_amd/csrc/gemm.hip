@@ -252,6 +252,213 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// MFMA GEMM on pre-split activations: A arrives as hi and lo fp16 arrays (written by the producing kernel with the
+// same split as above), so no register staging is needed and all three operands go global -> LDS with
+// global_load_lds_dwordx4 (16 bytes per lane into 1 KB of LDS per wave instruction) through an ST-stage ring: the
+// loads of slice kt + ST - 1 are issued right after the barrier that retires slice kt - 1, and a wave waits only
+// for its own loads of slice kt (vmcnt) before that barrier, so each slice has ST - 1 slices of MFMA work to arrive
+// in. Rows are 64 bytes (32 halves) with the 16-byte chunk c of row r stored at slot c ^ ((r >> 1) & 3): the 8
+// rows a b128 read phase touches land on 8 different bank groups. BM x BN tile per 4-wave block (2 x 2 waves of
+// (BM/2) x (BN/2), v_mfma_f32_32x32x16_f16). The products and their order match k_gemm_mfma<EPI, true, .>
+// exactly. EPI_SWIGLU with ch/cl set writes silu(g) * u as the hi/lo pair the down projection consumes.
+// ------------------------------------------------------------------------------------------------------------
+namespace {
+constexpr int SBK = 32;
+__device__ __forceinline__ int chunk_slot(int r, int c) { return c ^ ((r >> 1) & 3); }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8));  // expcnt and lgkmcnt not waited on
+}
+}  // namespace
+
+template <int EPI, int BM, int BN, int ST, int MINB>
+__global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g) {
+  constexpr int MI = BM / 64, NJ = BN / 64;  // 32x32 MFMA tiles per wave
+  constexpr int AI = BM / 64, WI = BN / 64;  // DMA instructions per wave per slice: each A part, W
+  constexpr int IPT = 2 * AI + WI;
+  constexpr int STAGE_H = (2 * BM + BN) * SBK;
+  static_assert(EPI != EPI_SWIGLU || NJ == 2, "SwiGLU pairs one gate and one up tile per wave");
+  extern __shared__ __attribute__((aligned(16))) _Float16 slds[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  // XCD-aware tile order (see k_gemm_mfma)
+  const int mt = (g.M + BM - 1) / BM, nt = gridDim.x / mt;
+  int mtile, ntile;
+  if (nt % 8 == 0) {
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, per = nt >> 3;
+    ntile = xcd * per + j % per;
+    mtile = j / per;
+  } else {
+    ntile = blockIdx.x % nt;
+    mtile = blockIdx.x / nt;
+  }
+  const int m0 = mtile * BM;
+  const int n0 = ntile * (EPI == EPI_SWIGLU ? BN / 2 : BN);
+  const int KT = g.K / SBK;
+  auto issue = [&](int kt, int st) {
+    _Float16* base = slds + st * STAGE_H;
+    const int k0 = kt * SBK;
+#pragma unroll
+    for (int h = 0; h < AI; ++h) {
+      const int rb = (wid * AI + h) * 16;  // 16 rows x 64 B = one wave instruction
+      const int r = rb + (lane >> 2);
+      const int c = chunk_slot(r, lane & 3);
+      const size_t off = static_cast<size_t>(min(m0 + r, g.M - 1)) * g.lda + k0 + c * 8;
+      __builtin_amdgcn_global_load_lds(g.ah + off, base + rb * SBK, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(g.al + off, base + BM * SBK + rb * SBK, 16, 0, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < WI; ++h) {
+      const int rb = (wid * WI + h) * 16;
+      const int r = rb + (lane >> 2);
+      const int c = chunk_slot(r, lane & 3);
+      int n;
+      const f16* src;
+      if constexpr (EPI == EPI_SWIGLU) {
+        n = n0 + (r % (BN / 2));
+        src = r < BN / 2 ? g.w : g.w2;
+      } else {
+        n = n0 + r;
+        src = g.w;
+      }
+      n = min(n, g.N - 1);
+      __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(n) * g.K + k0 + c * 8, base + 2 * BM * SBK + rb * SBK,
+                                       16, 0, 0);
+    }
+  };
+
+  f32x16 acc[MI][NJ], acc_lo[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+        acc_lo[i][j][r] = 0.0f;
+      }
+  // W rows of the wave's 32-column tiles: plain wn*(BN/2) + t*32; SwiGLU: gate wn*32, up BN/2 + wn*32
+  int brow[NJ];
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) brow[t] = EPI == EPI_SWIGLU ? t * (BN / 2) + wn * 32 : wn * (BN / 2) + t * 32;
+
+#pragma unroll
+  for (int p = 0; p < ST - 1; ++p)
+    if (p < KT) issue(p, p);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int after = min(ST - 2, KT - 1 - kt);  // slices this wave has issued after slice kt
+    if (after >= 2) wait_vmcnt<2 * IPT>();
+    else if (after == 1) wait_vmcnt<IPT>();
+    else wait_vmcnt<0>();
+    // a plain barrier: a fenced one would also wait for the loads of the later slices still in flight
+    __builtin_amdgcn_s_barrier();
+    if (kt + ST - 1 < KT) issue(kt + ST - 1, (kt + ST - 1) % ST);  // the stage of slice kt - 1, retired above
+    const _Float16* Ah = slds + (kt % ST) * STAGE_H;
+    const _Float16* Al = Ah + BM * SBK;
+    const _Float16* Ws = Ah + 2 * BM * SBK;
+#pragma unroll
+    for (int ks = 0; ks < SBK / 16; ++ks) {
+      const int c = 2 * ks + (lane >> 5);
+      h8 bf[NJ];
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) {
+        const int r = brow[t] + (lane & 31);
+        bf[t] = *reinterpret_cast<const h8*>(Ws + r * SBK + chunk_slot(r, c) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * (BM / 2) + i * 32 + (lane & 31);
+        const int off = r * SBK + chunk_slot(r, c) * 8;
+        const h8 ah = *reinterpret_cast<const h8*>(Ah + off);
+        const h8 al = *reinterpret_cast<const h8*>(Al + off);
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) {
+          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bf[t], acc[i][t], 0, 0, 0);
+          acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bf[t], acc_lo[i][t], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // epilogue: lane holds D[m][n] for n = lane % 32, m = (r / 4) * 8 + (lane / 32) * 4 + r % 4
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (m >= g.M) continue;
+      float v[NJ];
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) v[t] = acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f);
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int n = n0 + wn * 32 + (lane & 31);
+        if (n < g.N) {
+          const float y = silu_ref(v[0]) * v[1];
+          const size_t o = static_cast<size_t>(m) * g.ldc + n;
+          if (g.ch != nullptr) {
+            const _Float16 hi = static_cast<_Float16>(y);
+            g.ch[o] = hi;
+            g.cl[o] = static_cast<_Float16>((y - static_cast<float>(hi)) * 2048.0f);
+          } else {
+            g.c[o] = y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) {
+          const int n = n0 + wn * (BN / 2) + t * 32 + (lane & 31);
+          if (n < g.N) {
+            float* dst = g.c + static_cast<size_t>(m) * g.ldc + n;
+            *dst = EPI == EPI_RESIDUAL ? *dst + v[t] : v[t];
+          }
+        }
+      }
+    }
+}
+
+namespace {
+template <int EPI, int BM, int BN, int ST, int MINB>
+hipError_t launch_split_cfg(const GemmSplitArgs& g, hipStream_t s) {
+  const int bn = EPI == EPI_SWIGLU ? BN / 2 : BN;
+  const dim3 grid(((g.N + bn - 1) / bn) * ((g.M + BM - 1) / BM)), block(256);
+  const size_t lds = static_cast<size_t>(ST) * (2 * BM + BN) * SBK * sizeof(_Float16);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(lds));
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB>), grid, block, lds, s, g);
+  return hipGetLastError();
+}
+}  // namespace
+
+bool gemm_split_supported(const GemmSplitArgs& g) {
+  return g.K % SBK == 0 && g.lda % 8 == 0 && g.M > 0 && g.N > 0 &&
+         (reinterpret_cast<uintptr_t>(g.ah) | reinterpret_cast<uintptr_t>(g.al) |
+          reinterpret_cast<uintptr_t>(g.w) | reinterpret_cast<uintptr_t>(g.w2)) % 16 == 0;
+}
+
+// 128 x 128 tiles with a 3-stage ring (two blocks per CU) when they give every CU at least one block, else
+// 64 x 128 tiles with a 4-stage ring (measured on the Qwen3-0.6B prefill shapes at 2048 tokens).
+hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s) {
+  if (!gemm_split_supported(g)) return hipErrorInvalidValue;
+  if (epi == EPI_SWIGLU && (g.w2 == nullptr || (g.ch == nullptr) != (g.cl == nullptr))) return hipErrorInvalidValue;
+  const int bn = epi == EPI_SWIGLU ? 64 : 128;
+  const bool big = ((g.N + bn - 1) / bn) * ((g.M + 127) / 128) >= 256;
+  switch (epi) {
+    case EPI_STORE:
+      return big ? launch_split_cfg<EPI_STORE, 128, 128, 3, 2>(g, s) : launch_split_cfg<EPI_STORE, 64, 128, 4, 2>(g, s);
+    case EPI_RESIDUAL:
+      return big ? launch_split_cfg<EPI_RESIDUAL, 128, 128, 3, 2>(g, s)
+                 : launch_split_cfg<EPI_RESIDUAL, 64, 128, 4, 2>(g, s);
+    case EPI_SWIGLU:
+      return big ? launch_split_cfg<EPI_SWIGLU, 128, 128, 3, 2>(g, s)
+                 : launch_split_cfg<EPI_SWIGLU, 64, 128, 4, 2>(g, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 bool gemm_mfma_supported(const GemmArgs& g) { return g.K % MBK == 0 && g.lda % 4 == 0; }
 
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s) {

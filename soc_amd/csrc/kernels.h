@@ -68,8 +68,10 @@ struct AttnArgs {
   const int32_t* slot;   // [B] KV slot of each row, nullptr = slot_base for every row
   int slot_base;
   int pos_base;          // added to pos[] (prefill rows use pos = nullptr and pos_base + row)
-  float* out;            // [B][nq*d]
+  float* out;            // [B][nq*d] (prefill MFMA kernel: may be null when out_hi / out_lo are set)
   int ld_out;
+  f16* out_hi;           // prefill MFMA kernel: optional hi = f16(o), lo = f16((o - hi) * 2^11) copies [B][ld_out]
+  f16* out_lo;
   float* part;           // split partials [B][nq][max_split][d + 2]
   int* counters;         // [B][nkv] zero-initialised
   int B, nq, nkv, max_split, chunk;
@@ -147,7 +149,9 @@ hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream
 hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, float* x, hipStream_t s);
 // y[t] = RMSNorm(x[t]) with an fp16 gain; y may be fp32 (yf) or fp16 (yh), whichever is non-null.
 hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const f16* gain, float eps, float* yf, f16* yh,
-                               hipStream_t s);
+                               f16* ylo, hipStream_t s);
+// hi = f16(x), lo = f16((x - hi) * 2^11) of n fp32 values (the activation split of the MFMA GEMMs).
+hipError_t launch_split_f16(const float* x, size_t n, f16* hi, f16* lo, hipStream_t s);
 
 // C[M][N] (epilogue) = A[M][K] . W[N][K]^T, fp32 activations, fp16 weights, fp32 accumulation.
 struct GemmArgs {
@@ -163,6 +167,22 @@ hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
 // Same contract on MFMA (fp16 inputs, fp32 accumulation); split = hi/lo fp16 parts of the fp32 activations.
 bool gemm_mfma_supported(const GemmArgs& g);
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s);
+// Same products on activations pre-split into hi = f16(a) and lo = f16((a - hi) * 2^11) arrays [M][lda]
+// (lda % 8 == 0, K % 32 == 0, 16-byte aligned). EPI_SWIGLU writes c, or the hi/lo pair ch/cl when set.
+struct GemmSplitArgs {
+  const f16* ah;
+  const f16* al;
+  int lda;
+  const f16* w;     // [N][K]
+  const f16* w2;    // EPI_SWIGLU up rows
+  float* c;         // [M][ldc]
+  f16* ch;          // EPI_SWIGLU split output [M][ldc] (or null)
+  f16* cl;
+  int ldc;
+  int M, N, K;
+};
+bool gemm_split_supported(const GemmSplitArgs& g);
+hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s);
 
 // Skinny projection of a ragged decode batch: c[M][.] (epi) x[M][K] . [w | w2]^T for 1 <= M <= 16, K % 256 == 0.
 // Rows 0..N0-1 come from w, rows N0..Ntot-1 from w2 (SwiGLU: Ntot = 2 N0, c = silu(gate) * up over N0 outputs;

@@ -90,6 +90,8 @@ struct PrefillWs {
   int cap_logit_rows = 0;
   std::vector<void*> allocs;
   float* skpart = nullptr;  // split-K partials of the skinny batch projections
+  // hi/lo fp16 activation pairs of the prefill projections: p = normed input / attention output, q = SwiGLU output
+  soc::f16 *ph = nullptr, *pl = nullptr, *qh = nullptr, *ql = nullptr;
 };
 
 // Per-row state of a ragged decode batch (device arrays of `cap` rows).
@@ -260,6 +262,11 @@ int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * m->qd, &w.q));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * m->qd, &w.attn));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.intermediate_size, &w.h));
+  const size_t pw = static_cast<size_t>(R) * std::max<size_t>(H, m->qd);
+  SOC_TRY(dev_alloc_t(w.allocs, pw, &w.ph));
+  SOC_TRY(dev_alloc_t(w.allocs, pw, &w.pl));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.intermediate_size, &w.qh));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.intermediate_size, &w.ql));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(LR) * c.vocab_size, &w.logits));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(R) * c.num_attention_heads * SP * (128 + 2), &w.part));
   SOC_TRY(dev_alloc_t(w.allocs, R, &w.ids));
@@ -573,6 +580,36 @@ hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
   return soc::launch_gemm_f32a(g, epi, s);
 }
 
+// The prefill layers use the pre-split-activation GEMM (direct-to-LDS pipeline) on the default MFMA + hi/lo path
+// when the shapes allow; SOC_PREFILL_GEMM=fma, SOC_PREFILL_GEMM=staged (the register-staged MFMA kernel, same
+// products) and SOC_PREFILL_SPLIT=0 keep the fp32-activation kernels.
+bool prefill_split_path(const soc_model* m) {
+  const char* mode = std::getenv("SOC_PREFILL_GEMM");
+  if (mode != nullptr && (std::strcmp(mode, "fma") == 0 || std::strcmp(mode, "staged") == 0)) return false;
+  const char* sp = std::getenv("SOC_PREFILL_SPLIT");
+  if (sp != nullptr && sp[0] == '0') return false;
+  const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
+  return H % 32 == 0 && m->qd % 32 == 0 && I % 32 == 0;
+}
+
+hipError_t split_gemm(const soc::f16* ah, const soc::f16* al, int lda, const soc::f16* w, const soc::f16* w2,
+                      float* c, soc::f16* ch, soc::f16* cl, int ldc, int M, int N, int K, int epi, hipStream_t s) {
+  soc::GemmSplitArgs g{};
+  g.ah = ah;
+  g.al = al;
+  g.lda = lda;
+  g.w = w;
+  g.w2 = w2;
+  g.c = c;
+  g.ch = ch;
+  g.cl = cl;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return soc::launch_gemm_split(g, epi, s);
+}
+
 // Projections of a ragged decode batch (M = rows of the batch): the skinny MFMA kernel in slabs of 16 rows up to
 // 64 rows (SOC_BATCH_GEMM=tile selects the 128x128-tile GEMM of the prefill path).
 hipError_t batch_gemm(const soc::GemmArgs& g, int epi, float* part, hipStream_t s) {
@@ -613,12 +650,19 @@ size_t skinny_scratch_floats(const soc_model* m) {
 }
 
 // Prefill attention runs the MFMA flash kernel where the head grouping allows (SOC_PREFILL_ATTN=rows selects the
-// per-row split-key kernel that decode also uses).
-hipError_t prefill_attention(const soc::AttnArgs& a, hipStream_t s) {
+// per-row split-key kernel that decode also uses). With a.out_hi / a.out_lo set, the row kernel writes fp32 into
+// `scratch` and a split pass produces the hi/lo pair.
+hipError_t prefill_attention(const soc::AttnArgs& a, float* scratch, hipStream_t s) {
   const char* mode = std::getenv("SOC_PREFILL_ATTN");
   const bool rows = mode != nullptr && std::strcmp(mode, "rows") == 0;
   if (!rows && soc::attention_prefill_mfma_supported(a.nq, a.nkv)) return soc::launch_attention_prefill_mfma(a, s);
-  return soc::launch_attention(a, 0, s);
+  if (a.out_hi == nullptr) return soc::launch_attention(a, 0, s);
+  soc::AttnArgs b = a;
+  b.out = scratch;
+  b.out_hi = b.out_lo = nullptr;
+  const hipError_t e = soc::launch_attention(b, 0, s);
+  if (e != hipSuccess) return e;
+  return soc::launch_split_f16(scratch, static_cast<size_t>(a.B) * a.ld_out, a.out_hi, a.out_lo, s);
 }
 
 int validate_ids(const soc_model* m, const int32_t* ids, int n) {
@@ -684,7 +728,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
   if ((e = soc::launch_embed(b.ids, n, m->embed, H, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
   for (int l = 0; l < c.num_hidden_layers; ++l) {
     const DevLayer& L = m->layers[l];
-    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     soc::GemmArgs g{};
     g.a = w.xn;
@@ -739,7 +783,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.N = H;
     g.K = m->qd;
     if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm o");
-    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
     g.a = w.xn;
@@ -763,7 +807,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.K = c.intermediate_size;
     if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm down");
   }
-  if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+  if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
     return hip_fail(e, "rmsnorm");
   soc::GemmArgs g{};
   g.a = w.xn;
@@ -1236,20 +1280,29 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync ids");
   if ((e = soc::launch_embed(w.ids, n, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
   const int H = c.hidden_size;
+  const bool split = prefill_split_path(m);
   for (int l = 0; l < c.num_hidden_layers; ++l) {
     const DevLayer& L = m->layers[l];
-    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
-      return hip_fail(e, "rmsnorm");
     soc::GemmArgs g{};
-    g.a = w.xn;
-    g.lda = H;
-    g.w = L.wqkv;
-    g.c = w.qkv;
-    g.ldc = m->qkv_rows;
-    g.M = n;
-    g.N = m->qkv_rows;
-    g.K = H;
-    if ((e = prefill_gemm(g,soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    if (split) {
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, w.pl, s)) != hipSuccess)
+        return hip_fail(e, "rmsnorm");
+      if ((e = split_gemm(w.ph, w.pl, H, L.wqkv, nullptr, w.qkv, nullptr, nullptr, m->qkv_rows, n, m->qkv_rows, H,
+                          soc::EPI_STORE, s)) != hipSuccess)
+        return hip_fail(e, "gemm qkv");
+    } else {
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
+        return hip_fail(e, "rmsnorm");
+      g.a = w.xn;
+      g.lda = H;
+      g.w = L.wqkv;
+      g.c = w.qkv;
+      g.ldc = m->qkv_rows;
+      g.M = n;
+      g.N = m->qkv_rows;
+      g.K = H;
+      if ((e = prefill_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+    }
     soc::QkNormRopeArgs q{};
     q.qkv = w.qkv;
     q.ld_qkv = m->qkv_rows;
@@ -1278,13 +1331,30 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     a.slot = nullptr;
     a.slot_base = slot;
     a.pos_base = pos_off;
-    a.out = w.attn;
+    a.out = split ? nullptr : w.attn;
+    a.out_hi = split ? w.ph : nullptr;
+    a.out_lo = split ? w.pl : nullptr;
     a.ld_out = m->qd;
     a.part = w.part;
     a.counters = w.attn_counters;
     a.B = n;
     a.max_split = (pos_off + n + kAttnChunk - 1) / kAttnChunk;
-    if ((e = prefill_attention(a, s)) != hipSuccess) return hip_fail(e, "attention prefill");
+    if ((e = prefill_attention(a, w.attn, s)) != hipSuccess) return hip_fail(e, "attention prefill");
+    const int I = c.intermediate_size;
+    if (split) {
+      if ((e = split_gemm(w.ph, w.pl, m->qd, L.wo, nullptr, w.x, nullptr, nullptr, H, n, H, m->qd, soc::EPI_RESIDUAL,
+                          s)) != hipSuccess)
+        return hip_fail(e, "gemm o");
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, nullptr, w.ph, w.pl, s)) != hipSuccess)
+        return hip_fail(e, "rmsnorm");
+      if ((e = split_gemm(w.ph, w.pl, H, L.wgate, L.wup, nullptr, w.qh, w.ql, I, n, I, H, soc::EPI_SWIGLU, s)) !=
+          hipSuccess)
+        return hip_fail(e, "gemm gate/up");
+      if ((e = split_gemm(w.qh, w.ql, I, L.wdown, nullptr, w.x, nullptr, nullptr, H, n, H, I, soc::EPI_RESIDUAL, s)) !=
+          hipSuccess)
+        return hip_fail(e, "gemm down");
+      continue;
+    }
     g = soc::GemmArgs{};
     g.a = w.attn;
     g.lda = m->qd;
@@ -1294,8 +1364,8 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = H;
     g.K = m->qd;
-    if ((e = prefill_gemm(g,soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
-    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
     g.a = w.xn;
@@ -1303,21 +1373,21 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.w = L.wgate;
     g.w2 = L.wup;
     g.c = w.h;
-    g.ldc = c.intermediate_size;
+    g.ldc = I;
     g.M = n;
-    g.N = c.intermediate_size;
+    g.N = I;
     g.K = H;
-    if ((e = prefill_gemm(g,soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    if ((e = prefill_gemm(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
     g = soc::GemmArgs{};
     g.a = w.h;
-    g.lda = c.intermediate_size;
+    g.lda = I;
     g.w = L.wdown;
     g.c = w.x;
     g.ldc = H;
     g.M = n;
     g.N = H;
-    g.K = c.intermediate_size;
-    if ((e = prefill_gemm(g,soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+    g.K = I;
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
   }
   // logits of the last row (with the greedy token), then of the other requested rows
   soc::LmHeadArgs h{};
@@ -1336,7 +1406,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   if (logit_rows > 1) {
     const int rows = logit_rows - 1;
     const float* xr = w.x + static_cast<size_t>(n - logit_rows) * H;
-    if ((e = soc::launch_rmsnorm_rows(xr, rows, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, s)) != hipSuccess)
+    if ((e = soc::launch_rmsnorm_rows(xr, rows, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     soc::GemmArgs g{};
     g.a = w.xn;

@@ -125,6 +125,39 @@ def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv
         m.close()
 
 
+@pytest.mark.parametrize("n", [150, 300])
+def test_prefill_split_gemm_matches_staged_kernel(gpu_ctx, monkeypatch, n):
+    """The prefill projections on pre-split activations (hi/lo written by RMSNorm, attention and the SwiGLU
+    epilogue; direct-to-LDS pipeline) form the same products in the same order as the register-staged MFMA kernel
+    that splits the fp32 activations itself: logits are bit-identical, for a single prefill (row counts off the
+    64/128-row tiles) and a chunked one. Qwen3-0.6B-wide layers (hidden 1024, 16 q / 8 kv heads, 3072)."""
+    cfg = S.QwenConfig(vocab_size=512, hidden_size=1024, num_hidden_layers=2, num_attention_heads=16,
+                       num_key_value_heads=8, intermediate_size=3072, tie_word_embeddings=True)
+    m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, 21))
+    ids = S.synth_tokens(22, "split", cfg.vocab_size, n)
+    runs = {}
+    try:
+        for mode in ("staged", "split"):
+            if mode == "staged":
+                monkeypatch.setenv("SOC_PREFILL_GEMM", "staged")
+            else:
+                monkeypatch.delenv("SOC_PREFILL_GEMM", raising=False)
+            kv = S.KVCache(m, 1, n + 8)
+            try:
+                full, tok = S.prefill(m, kv, 0, ids, 0, logit_rows=n)
+                kv.reset(0)
+                S.prefill(m, kv, 0, ids[:77], 0, logit_rows=0)
+                part, tok2 = S.prefill(m, kv, 0, ids[77:], 77, logit_rows=n - 77)
+            finally:
+                kv.close()
+            runs[mode] = (full, tok, part, tok2)
+        for i in (0, 2):
+            np.testing.assert_array_equal(runs["split"][i], runs["staged"][i])
+        assert runs["split"][1] == runs["staged"][1] and runs["split"][3] == runs["staged"][3]
+    finally:
+        m.close()
+
+
 def test_decode_steps_equal_decode_loop(gpu_ctx):
     cfg, seed, _, _ = SMALL_MODELS["tiny_untied"]
     m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
