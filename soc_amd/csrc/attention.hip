@@ -364,7 +364,7 @@ __device__ __forceinline__ int fa_swizzle(int k) { return (k & ~12) | ((k & 4) <
 }  // namespace
 
 template <int G>
-__global__ __launch_bounds__(256) void k_attention_prefill_mfma(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
   constexpr int SUB = 4 / G;     // 32-row sub-tiles per block
   constexpr int BP = 32 * SUB;   // query rows per block
   __shared__ _Float16 Ks[2][FA_KT * FA_KLD];
