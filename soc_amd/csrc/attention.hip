@@ -435,6 +435,8 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+  // the online softmax runs in base 2: scores carry log2(e), so exp(s - m) = 2^(s' - m') is one v_exp_f32
+  const float scale2 = a.scale * 1.4426950408889634f;
   float m = -INFINITY, l = 0.0f;
 
   load_tile(0);
@@ -462,13 +464,13 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
-        const float v = (sh[r] + sl[r] * (1.0f / 2048.0f)) * a.scale;
+        const float v = (sh[r] + sl[r] * (1.0f / 2048.0f)) * scale2;
         s[r] = key <= qpos ? v : -INFINITY;
         mt = fmaxf(mt, s[r]);
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
       const float mn = fmaxf(m, mt);  // finite: key 0 is visible to every row and tile 0 comes first
-      const float corr = expf(m - mn);
+      const float corr = __builtin_amdgcn_exp2f(m - mn);
       m = mn;
       l *= corr;
 #pragma unroll
@@ -477,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
         for (int r = 0; r < 16; ++r) o[db][r] *= corr;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = expf(s[r] - mn);
+        s[r] = __builtin_amdgcn_exp2f(s[r] - mn);
         l += s[r];
       }
 #pragma unroll
