@@ -437,6 +437,7 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
     for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
   // the online softmax runs in base 2: scores carry log2(e), so exp(s - m) = 2^(s' - m') is one v_exp_f32
   const float scale2 = a.scale * 1.4426950408889634f;
+  const int wave_min_pos = a.pos_base + min(t0, a.B - 1);  // smallest query position among the wave's rows
   float m = -INFINITY, l = 0.0f;
 
   load_tile(0);
@@ -461,22 +462,32 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
       // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
       float s[16];
       float mt = -INFINITY;
+      if (kt * FA_KT + FA_KT - 1 <= wave_min_pos) {  // every key of the tile is visible to every row of the wave
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
-        const float v = (sh[r] + sl[r] * (1.0f / 2048.0f)) * scale2;
-        s[r] = key <= qpos ? v : -INFINITY;
-        mt = fmaxf(mt, s[r]);
+        for (int r = 0; r < 16; ++r) {
+          s[r] = (sh[r] + sl[r] * (1.0f / 2048.0f)) * scale2;
+          mt = fmaxf(mt, s[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
+          const float v = (sh[r] + sl[r] * (1.0f / 2048.0f)) * scale2;
+          s[r] = key <= qpos ? v : -INFINITY;
+          mt = fmaxf(mt, s[r]);
+        }
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
       const float mn = fmaxf(m, mt);  // finite: key 0 is visible to every row and tile 0 comes first
       const float corr = __builtin_amdgcn_exp2f(m - mn);
       m = mn;
       l *= corr;
+      if (!__all(corr == 1.0f)) {  // no row's running max moved: nothing to rescale
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+          for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[r] = __builtin_amdgcn_exp2f(s[r] - mn);
