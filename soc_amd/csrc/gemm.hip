@@ -255,65 +255,95 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
 // ------------------------------------------------------------------------------------------------------------
 // MFMA GEMM on pre-split activations: A arrives as hi and lo fp16 arrays (written by the producing kernel with the
 // same split as above), so no register staging is needed and all three operands go global -> LDS with
-// global_load_lds_dwordx4 (16 bytes per lane into 1 KB of LDS per wave instruction) through an ST-stage ring: the
-// loads of slice kt + ST - 1 are issued right after the barrier that retires slice kt - 1, and a wave waits only
-// for its own loads of slice kt (vmcnt) before that barrier, so each slice has ST - 1 slices of MFMA work to arrive
-// in. Rows are 64 bytes (32 halves) with the 16-byte chunk c of row r stored at slot c ^ ((r >> 1) & 3): the 8
-// rows a b128 read phase touches land on 8 different bank groups. BM x BN tile per 4-wave block (2 x 2 waves of
-// (BM/2) x (BN/2), v_mfma_f32_32x32x16_f16). The products and their order match k_gemm_mfma<EPI, true, .>
-// exactly. EPI_SWIGLU with ch/cl set writes silu(g) * u as the hi/lo pair the down projection consumes.
+// global_load_lds_dwordx4 (16 bytes per lane into 1 KB of LDS per wave instruction) through an ST-slot ring of
+// BK-deep K slices. A slot is refilled (slice kt + ST) by the barrier that follows the last LDS read of slice kt,
+// so ST slices are in flight while a slice's last 16-deep step runs; before that barrier a wave waits only for its
+// own loads of slice kt + 1 (vmcnt) and for its LDS reads (lgkmcnt). The MFMA operands of the next 16-deep step are
+// read from LDS while the current step's MFMAs run (two register sets used in turn), one read issued after each
+// MFMA. Rows are BK halves with the 16-byte chunk c of row r stored at slot c ^ ((r >> 1) & 3) (BK = 32) or
+// c ^ (r & 7) (BK = 64): the rows a b128 read phase touches land on different bank groups.
+// BM x BN tile per 4-wave block (2 x 2 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_f16). Tiles are dealt to the
+// eight XCDs as an mx x (8 / mx) grid of rectangles (block b runs on XCD b % 8), mx chosen to minimise the bytes
+// of A and W each XCD's L2 has to fetch. The products and their order match k_gemm_mfma<EPI, true, .> exactly.
+// EPI_SWIGLU with ch/cl set writes silu(g) * u as the hi/lo pair the down projection consumes.
 // ------------------------------------------------------------------------------------------------------------
 namespace {
-constexpr int SBK = 32;
-__device__ __forceinline__ int chunk_slot(int r, int c) { return c ^ ((r >> 1) & 3); }
+template <int BK>
+__device__ __forceinline__ int chunk_slot(int r, int c) {
+  if constexpr (BK == 32) return c ^ ((r >> 1) & 3);
+  else return c ^ (r & 7);
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8));  // expcnt and lgkmcnt not waited on
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  // vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt not waited on
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// wait until at most n slices (of IPT loads each) issued after the awaited one are in flight, n <= MAXN
+template <int IPT, int MAXN>
+__device__ __forceinline__ void wait_slices(int n) {
+  if constexpr (MAXN <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= MAXN) wait_vmcnt<MAXN * IPT>();
+    else wait_slices<IPT, MAXN - 1>(n);
+  }
+}
+// a barrier with no fence (a fenced one would also wait for the loads of later slices still in flight); the
+// signal fences keep the compiler from moving LDS accesses across it
+__device__ __forceinline__ void block_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 }  // namespace
 
-template <int EPI, int BM, int BN, int ST, int MINB>
-__global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g) {
+template <int EPI, int BM, int BN, int ST, int MINB, int BK>
+__global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int mx) {
   constexpr int MI = BM / 64, NJ = BN / 64;  // 32x32 MFMA tiles per wave
-  constexpr int AI = BM / 64, WI = BN / 64;  // DMA instructions per wave per slice: each A part, W
+  constexpr int RPI = 1024 / (BK * 2);       // rows per 1 KB wave instruction
+  constexpr int CPR = BK / 8;                // 16-byte chunks per row
+  constexpr int AI = BM / RPI / 4, WI = BN / RPI / 4;  // DMA instructions per wave per slice: each A part, W
   constexpr int IPT = 2 * AI + WI;
-  constexpr int STAGE_H = (2 * BM + BN) * SBK;
+  constexpr int KS = BK / 16;  // 16-deep MFMA steps per slice
+  constexpr int STAGE_H = (2 * BM + BN) * BK;
   static_assert(EPI != EPI_SWIGLU || NJ == 2, "SwiGLU pairs one gate and one up tile per wave");
+  static_assert(KS % 2 == 0 && ST >= 2 && AI >= 1 && WI >= 1, "tile shape");
   extern __shared__ __attribute__((aligned(16))) _Float16 slds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
-  // XCD-aware tile order (see k_gemm_mfma)
   const int mt = (g.M + BM - 1) / BM, nt = gridDim.x / mt;
   int mtile, ntile;
-  if (nt % 8 == 0) {
-    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, per = nt >> 3;
-    ntile = xcd * per + j % per;
-    mtile = j / per;
+  if (mx > 0) {  // XCD rectangle (b % 8) of (mt / mx) x (nt / nx) tiles, walked along N
+    const int nx = 8 / mx, grp = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int tm = mt / mx, tn = nt / nx;
+    mtile = (grp / nx) * tm + j / tn;
+    ntile = (grp % nx) * tn + j % tn;
   } else {
     ntile = blockIdx.x % nt;
     mtile = blockIdx.x / nt;
   }
   const int m0 = mtile * BM;
   const int n0 = ntile * (EPI == EPI_SWIGLU ? BN / 2 : BN);
-  const int KT = g.K / SBK;
+  const int KT = g.K / BK;
   auto issue = [&](int kt, int st) {
     _Float16* base = slds + st * STAGE_H;
-    const int k0 = kt * SBK;
+    const int k0 = kt * BK;
 #pragma unroll
     for (int h = 0; h < AI; ++h) {
-      const int rb = (wid * AI + h) * 16;  // 16 rows x 64 B = one wave instruction
-      const int r = rb + (lane >> 2);
-      const int c = chunk_slot(r, lane & 3);
+      const int rb = (wid * AI + h) * RPI;
+      const int r = rb + lane / CPR;
+      const int c = chunk_slot<BK>(r, lane % CPR);
       const size_t off = static_cast<size_t>(min(m0 + r, g.M - 1)) * g.lda + k0 + c * 8;
-      __builtin_amdgcn_global_load_lds(g.ah + off, base + rb * SBK, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(g.al + off, base + BM * SBK + rb * SBK, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(g.ah + off, base + rb * BK, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(g.al + off, base + BM * BK + rb * BK, 16, 0, 0);
     }
 #pragma unroll
     for (int h = 0; h < WI; ++h) {
-      const int rb = (wid * WI + h) * 16;
-      const int r = rb + (lane >> 2);
-      const int c = chunk_slot(r, lane & 3);
+      const int rb = (wid * WI + h) * RPI;
+      const int r = rb + lane / CPR;
+      const int c = chunk_slot<BK>(r, lane % CPR);
       int n;
       const f16* src;
       if constexpr (EPI == EPI_SWIGLU) {
@@ -324,7 +354,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g) {
         src = g.w;
       }
       n = min(n, g.N - 1);
-      __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(n) * g.K + k0 + c * 8, base + 2 * BM * SBK + rb * SBK,
+      __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(n) * g.K + k0 + c * 8, base + 2 * BM * BK + rb * BK,
                                        16, 0, 0);
     }
   };
@@ -344,40 +374,70 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g) {
 #pragma unroll
   for (int t = 0; t < NJ; ++t) brow[t] = EPI == EPI_SWIGLU ? t * (BN / 2) + wn * 32 : wn * (BN / 2) + t * 32;
 
+  h8 a0[MI][2], b0[NJ], a1[MI][2], b1[NJ];  // the two operand sets
+  auto read = [&](h8 (&fa)[MI][2], h8 (&fb)[NJ], int st, int ks) {
+    const _Float16* Ah = slds + st * STAGE_H;
+    const _Float16* Al = Ah + BM * BK;
+    const _Float16* Ws = Ah + 2 * BM * BK;
+    const int c = 2 * ks + (lane >> 5);
 #pragma unroll
-  for (int p = 0; p < ST - 1; ++p)
-    if (p < KT) issue(p, p);
-  for (int kt = 0; kt < KT; ++kt) {
-    const int after = min(ST - 2, KT - 1 - kt);  // slices this wave has issued after slice kt
-    if (after >= 2) wait_vmcnt<2 * IPT>();
-    else if (after == 1) wait_vmcnt<IPT>();
-    else wait_vmcnt<0>();
-    // a plain barrier: a fenced one would also wait for the loads of the later slices still in flight
-    __builtin_amdgcn_s_barrier();
-    if (kt + ST - 1 < KT) issue(kt + ST - 1, (kt + ST - 1) % ST);  // the stage of slice kt - 1, retired above
-    const _Float16* Ah = slds + (kt % ST) * STAGE_H;
-    const _Float16* Al = Ah + BM * SBK;
-    const _Float16* Ws = Ah + 2 * BM * SBK;
+    for (int t = 0; t < NJ; ++t) {
+      const int r = brow[t] + (lane & 31);
+      fb[t] = *reinterpret_cast<const h8*>(Ws + r * BK + chunk_slot<BK>(r, c) * 8);
+    }
 #pragma unroll
-    for (int ks = 0; ks < SBK / 16; ++ks) {
-      const int c = 2 * ks + (lane >> 5);
-      h8 bf[NJ];
+    for (int i = 0; i < MI; ++i) {
+      const int r = wm * (BM / 2) + i * 32 + (lane & 31);
+      const int off = r * BK + chunk_slot<BK>(r, c) * 8;
+      fa[i][0] = *reinterpret_cast<const h8*>(Ah + off);
+      fa[i][1] = *reinterpret_cast<const h8*>(Al + off);
+    }
+  };
+  auto mma = [&](const h8 (&fa)[MI][2], const h8 (&fb)[NJ]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const int r = brow[t] + (lane & 31);
-        bf[t] = *reinterpret_cast<const h8*>(Ws + r * SBK + chunk_slot(r, c) * 8);
+        acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][0], fb[t], acc[i][t], 0, 0, 0);
+        acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][1], fb[t], acc_lo[i][t], 0, 0, 0);
       }
+  };
+  // one MFMA, one LDS read, ... then the remaining MFMAs
+  auto interleave = [&]() {
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int r = wm * (BM / 2) + i * 32 + (lane & 31);
-        const int off = r * SBK + chunk_slot(r, c) * 8;
-        const h8 ah = *reinterpret_cast<const h8*>(Ah + off);
-        const h8 al = *reinterpret_cast<const h8*>(Al + off);
+    for (int q = 0; q < 2 * MI + NJ; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MI * NJ - (2 * MI + NJ), 0);
+  };
+
 #pragma unroll
-        for (int t = 0; t < NJ; ++t) {
-          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bf[t], acc[i][t], 0, 0, 0);
-          acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bf[t], acc_lo[i][t], 0, 0, 0);
+  for (int p = 0; p < ST; ++p)
+    if (p < KT) issue(p, p);
+  wait_slices<IPT, ST - 1>(KT - 1);
+  block_barrier();
+  read(a0, b0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int st = kt % ST;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks += 2) {
+      read(a1, b1, st, ks + 1);
+      mma(a0, b0);
+      interleave();
+      if (ks + 2 < KS) {
+        read(a0, b0, st, ks + 2);
+        mma(a1, b1);
+        interleave();
+      } else {
+        if (kt + 1 < KT) {
+          wait_slices<IPT, ST - 2>(KT - 2 - kt);  // own loads of slice kt + 1 landed
+          wait_lgkmcnt0();                         // own reads of slot st done
+          block_barrier();
+          if (kt + ST < KT) issue(kt + ST, st);
+          read(a0, b0, (kt + 1) % ST, 0);
         }
+        mma(a1, b1);
       }
     }
   }
@@ -418,44 +478,58 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g) {
 }
 
 namespace {
-template <int EPI, int BM, int BN, int ST, int MINB>
+// mx for the XCD rectangles: the split of the mt x nt tile grid into mx x (8 / mx) parts that minimises the bytes
+// of A (4 per element: hi + lo) and W (2 per element) per XCD; 0 (row-major tile order) when none divides evenly.
+int xcd_split(int mt, int nt, double abytes, double wbytes) {
+  int best = 0;
+  double cost = 0.0;
+  for (int mx = 1; mx <= 8; mx *= 2) {
+    if (mt % mx != 0 || nt % (8 / mx) != 0) continue;
+    const double c = abytes / mx + wbytes / (8 / mx);
+    if (best == 0 || c < cost) {
+      best = mx;
+      cost = c;
+    }
+  }
+  return best;
+}
+
+template <int EPI, int BM, int BN, int ST, int MINB, int BK>
 hipError_t launch_split_cfg(const GemmSplitArgs& g, hipStream_t s) {
   const int bn = EPI == EPI_SWIGLU ? BN / 2 : BN;
-  const dim3 grid(((g.N + bn - 1) / bn) * ((g.M + BM - 1) / BM)), block(256);
-  const size_t lds = static_cast<size_t>(ST) * (2 * BM + BN) * SBK * sizeof(_Float16);
+  const int mt = (g.M + BM - 1) / BM, nt = (g.N + bn - 1) / bn;
+  const int mx = xcd_split(mt, nt, 4.0 * g.M * g.K, 2.0 * (EPI == EPI_SWIGLU ? 2 : 1) * g.N * g.K);
+  const size_t lds = static_cast<size_t>(ST) * (2 * BM + BN) * BK * sizeof(_Float16);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB>), hipFuncAttributeMaxDynamicSharedMemorySize,
-      static_cast<int>(lds));
+      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB, BK>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB>), grid, block, lds, s, g);
+  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB, BK>), dim3(mt * nt), dim3(256), lds, s, g, mx);
   return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_split_epi(const GemmSplitArgs& g, hipStream_t s) {
+  // 64 x 128 tiles, two blocks per CU: 64-deep slices in a 2-slot ring, or 32-deep ones in a 4-slot ring when K
+  // is not a multiple of 64 (measured on the Qwen3-0.6B prefill shapes at 2048 tokens)
+  return g.K % 64 == 0 ? launch_split_cfg<EPI, 64, 128, 2, 2, 64>(g, s) : launch_split_cfg<EPI, 64, 128, 4, 2, 32>(g, s);
 }
 }  // namespace
 
 bool gemm_split_supported(const GemmSplitArgs& g) {
-  return g.K % SBK == 0 && g.lda % 8 == 0 && g.M > 0 && g.N > 0 &&
+  return g.K % 32 == 0 && g.lda % 8 == 0 && g.M > 0 && g.N > 0 &&
          (reinterpret_cast<uintptr_t>(g.ah) | reinterpret_cast<uintptr_t>(g.al) |
           reinterpret_cast<uintptr_t>(g.w) | reinterpret_cast<uintptr_t>(g.w2)) % 16 == 0;
 }
 
-// 128 x 128 tiles with a 3-stage ring (two blocks per CU) when they give every CU at least one block, else
-// 64 x 128 tiles with a 4-stage ring (measured on the Qwen3-0.6B prefill shapes at 2048 tokens).
 hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s) {
   if (!gemm_split_supported(g)) return hipErrorInvalidValue;
   if (epi == EPI_SWIGLU && (g.w2 == nullptr || (g.ch == nullptr) != (g.cl == nullptr))) return hipErrorInvalidValue;
-  const int bn = epi == EPI_SWIGLU ? 64 : 128;
-  const bool big = ((g.N + bn - 1) / bn) * ((g.M + 127) / 128) >= 256;
   switch (epi) {
-    case EPI_STORE:
-      return big ? launch_split_cfg<EPI_STORE, 128, 128, 3, 2>(g, s) : launch_split_cfg<EPI_STORE, 64, 128, 4, 2>(g, s);
-    case EPI_RESIDUAL:
-      return big ? launch_split_cfg<EPI_RESIDUAL, 128, 128, 3, 2>(g, s)
-                 : launch_split_cfg<EPI_RESIDUAL, 64, 128, 4, 2>(g, s);
-    case EPI_SWIGLU:
-      return big ? launch_split_cfg<EPI_SWIGLU, 128, 128, 3, 2>(g, s)
-                 : launch_split_cfg<EPI_SWIGLU, 64, 128, 4, 2>(g, s);
-    default:
-      return hipErrorInvalidValue;
+    case EPI_STORE: return launch_split_epi<EPI_STORE>(g, s);
+    case EPI_RESIDUAL: return launch_split_epi<EPI_RESIDUAL>(g, s);
+    case EPI_SWIGLU: return launch_split_epi<EPI_SWIGLU>(g, s);
+    default: return hipErrorInvalidValue;
   }
 }
 

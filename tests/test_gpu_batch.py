@@ -70,6 +70,34 @@ def test_batch_rows_equal_single_sequence_decode(gpu_ctx, nq, nkv):
         m.close()
 
 
+def test_batch_many_rows_slabs_and_tiled_path(gpu_ctx):
+    """20 rows (two 16-row slabs of the skinny projection) and 70 rows (the tiled GEMM on the same pre-split
+    activations): every row agrees with single-sequence decode of its slot within the model tolerance, with the
+    same greedy token."""
+    cfg = small_cfg()
+    m = S.Model(gpu_ctx, cfg).load(S.synth_weights(cfg, 33))
+    nslots = 70
+    kvs = [S.KVCache(m, nslots, 32) for _ in range(2)]
+    try:
+        last = np.zeros(nslots, np.int32)
+        for kv in kvs:
+            for slot in range(nslots):
+                ids = S.synth_tokens(40 + slot, "batch.many", cfg.vocab_size, 1 + slot % 7)
+                _, last[slot] = S.prefill(m, kv, slot, ids, 0, logit_rows=0)
+        for n in (20, 70):
+            slots = np.arange(n, dtype=np.int32)[::-1].copy()
+            lg, nxt = S.decode_batch(m, kvs[0], slots, last[slots])
+            for i, slot in enumerate(slots):
+                ref, t = S.decode(m, kvs[1], int(slot), int(last[slot]))
+                assert_logits_close(lg[i], ref, f"{n} rows, row {i} (slot {slot})")
+                assert int(nxt[i]) == t
+            last[slots] = nxt
+    finally:
+        for kv in kvs:
+            kv.close()
+        m.close()
+
+
 def test_batch_permutation_invariance_and_steps(gpu_ctx):
     cfg = small_cfg()
     m = S.Model(gpu_ctx, cfg).load(S.synth_weights(cfg, 32))
