@@ -540,6 +540,295 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Causal GQA attention for a prefill chunk, balanced: a block takes two 32-row query tiles of one KV head, tile j
+// and tile nqt - 1 - j, one after the other, so every block sees about the same number of visible keys. Its 8 waves
+// are HB query heads (the whole group of the KV head) x R = 8 / HB key residues: key tile kt goes to the waves of
+// residue kt % R, and each step stages R tiles. At the end of a query tile the R partial (max, sum, weighted values)
+// of each row are merged through LDS.
+// Per tile a wave does what k_attention_prefill_mfma does (S^T = K . Q^T on MFMA, one query per lane, P^T straight
+// from registers into O^T = V^T . P^T with V^T stored key-swizzled), with three changes:
+//  * q is pre-multiplied by scale * log2(e) before its hi/lo split, so a score is sh + sl 2^-11;
+//  * the running max is lazy: it moves only when a score exceeds it by more than 8 (log2 units), so p <= 2^8 and
+//    the 64 accumulators are rescaled rarely; the result is the same softmax (every partial keeps its own max and
+//    the merge rescales exactly);
+//  * p = hi + lo with hi = p with its low 13 mantissa bits cleared (exact in fp16 for p >= 2^-14) and lo = p - hi.
+// K tiles go global -> LDS with global_load_lds_dwordx4 (32 rows x 256 B, 16-byte chunk c of row r at slot
+// c ^ (r & 15)); V goes through registers (transposed on the store). Keys past the chunk's last row read the last
+// key (K) or zeros (V) and are masked.
+// grid = (ceil(ceil(B / 32) / 2), nkv), block = 512, dynamic LDS = max(staging, merge).
+// ------------------------------------------------------------------------------------------------------------
+namespace {
+constexpr int FP_KD = FA_KT * HD;     // K tile in halves (unpadded, swizzled)
+constexpr int FP_VT = HD * FA_VLD;    // V^T tile in halves
+template <int HB, int R>
+constexpr size_t pairs_lds_bytes() {
+  const size_t staging = static_cast<size_t>(2) * R * (FP_KD + FP_VT) * sizeof(_Float16);
+  const size_t merge = static_cast<size_t>(HB) * (R - 1) * 66 * 64 * sizeof(float);
+  return staging > merge ? staging : merge;
+}
+}  // namespace
+
+template <int HB, int R>
+__global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) {
+  static_assert(HB * R == 8, "8 waves");
+  extern __shared__ __attribute__((aligned(16))) _Float16 plds[];
+  _Float16* Ksb = plds;                  // [2][R][FP_KD]
+  _Float16* Vtb = plds + 2 * R * FP_KD;  // [2][R][FP_VT]
+  float* xs = reinterpret_cast<float*>(plds);  // merge area [HB][R - 1][66][64], after the key loop
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int hh = wid % HB, res = wid / HB;
+  const int g = blockIdx.y;
+  const int head = g * HB + hh;
+  const int ql = lane & 31, hb = lane >> 5;
+  const int nqt = (a.B + 31) / 32;
+  const int j = blockIdx.x;
+  const size_t head_base = static_cast<size_t>(a.slot_base) * a.slot_stride +
+                           static_cast<size_t>(a.layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+  const f16* kb = a.kcache + head_base;
+  const f16* vb = a.vcache + head_base;
+  const float scale2 = a.scale * 1.4426950408889634f;
+
+  for (int ph = 0; ph < 2; ++ph) {
+    if (ph == 1 && nqt - 1 - j == j) break;  // odd tile count: the middle tile has no partner
+    const int qt = ph == 0 ? j : nqt - 1 - j;
+    const int t0 = qt * 32;
+    const int t = t0 + ql;
+    const int tq = min(t, a.B - 1);  // rows past the chunk compute a copy of the last row, never stored
+    const int qpos = a.pos_base + tq;
+    const int last = a.pos_base + min(t0 + 31, a.B - 1);  // last key any row of the tile sees
+    const int ntiles = last / FA_KT + 1;
+    const int nsteps = (ntiles + R - 1) / R;
+    const int wave_min_pos = a.pos_base + t0;
+
+    // Q^T operand (lane holds q[t][16 ks + 8 hb + i]) of q * scale * log2(e)
+    fa_h8 qh[8], qlo[8];
+    {
+      const float* qrow = a.qkv + static_cast<size_t>(tq) * a.ld_qkv + head * HD;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8 + 4);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float v = (i < 4 ? v0[i] : v1[i - 4]) * scale2;
+          // keep the rounded fp32 product in a register: otherwise the compiler may fold the product into the
+          // fp16 conversion of hi (one rounding) but not into lo, and hi + lo would no longer equal v
+          __asm__ volatile("" : "+v"(v));
+          const _Float16 h = static_cast<_Float16>(v);
+          qh[ks][i] = h;
+          qlo[ks][i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
+        }
+      }
+    }
+    u32x4 rv[R];
+    auto load_step = [&](int step, int buf) {
+#pragma unroll
+      for (int p = 0; p < R; ++p) {  // K: wave w writes rows 4w..4w+3 of tile p
+        const int r = 4 * wid + (lane >> 4);
+        const int key = min((R * step + p) * FA_KT + r, last);
+        const int c = (lane & 15) ^ (r & 15);
+        __builtin_amdgcn_global_load_lds(kb + static_cast<size_t>(key) * HD + c * 8,
+                                         Ksb + (buf * R + p) * FP_KD + 4 * wid * HD, 16, 0, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < R; ++p) {  // V: thread = (key tid % 32, dims 8 (tid / 32))
+        const int key = (R * step + p) * FA_KT + (tid & 31);
+        const size_t off = static_cast<size_t>(key) * HD + (tid >> 5) * 8;
+        rv[p] = key <= last ? load16(vb + off) : u32x4{0, 0, 0, 0};
+      }
+    };
+    auto store_step = [&](int buf) {
+#pragma unroll
+      for (int p = 0; p < R; ++p) {
+        const int key = tid & 31, d0 = (tid >> 5) * 8;
+        _Float16* Vt = Vtb + (buf * R + p) * FP_VT;
+        const fa_h8 v = __builtin_bit_cast(fa_h8, rv[p]);
+        const int col = fa_swizzle(key);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) Vt[(d0 + i) * FA_VLD + col] = v[i];
+      }
+    };
+
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    load_step(0, 0);
+    store_step(0);
+    __syncthreads();  // also waits for the K tiles (vmcnt)
+    for (int step = 0; step < nsteps; ++step) {
+      const int buf = step & 1;
+      if (step + 1 < nsteps) load_step(step + 1, buf ^ 1);
+      const int kt = R * step + res;
+      if (kt < ntiles) {
+        const _Float16* Ks = Ksb + (buf * R + res) * FP_KD;
+        const _Float16* Vt = Vtb + (buf * R + res) * FP_VT;
+        f32x16 sh, sl;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sh[r] = 0.0f;
+          sl[r] = 0.0f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          const fa_h8 ka = *reinterpret_cast<const fa_h8*>(&Ks[ql * HD + ((2 * ks + hb) ^ (ql & 15)) * 8]);
+          sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
+          sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sl, 0, 0, 0);
+        }
+        // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
+        float sv[16];
+        float mt = -INFINITY;
+        if (kt * FA_KT + FA_KT - 1 <= wave_min_pos) {  // every key of the tile is visible to every row
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            sv[r] = sh[r] + sl[r] * (1.0f / 2048.0f);
+            mt = fmaxf(mt, sv[r]);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
+            const float v = sh[r] + sl[r] * (1.0f / 2048.0f);
+            sv[r] = key <= qpos ? v : -INFINITY;
+            mt = fmaxf(mt, sv[r]);
+          }
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const bool up = mt > m + 8.0f;  // rows with no visible key yet keep m = -inf (and p = 0)
+        if (__any(up)) {
+          const float corr = up ? __builtin_amdgcn_exp2f(m - mt) : 1.0f;
+          if (up) m = mt;
+          l *= corr;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+        }
+        const float mref = m == -INFINITY ? 0.0f : m;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sv[r] = __builtin_amdgcn_exp2f(sv[r] - mref);
+          l += sv[r];
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          fa_h8 ph8, pl8;
+#pragma unroll
+          for (int i = 0; i < 8; i += 2) {
+            const float p0 = sv[k2 * 8 + i], p1 = sv[k2 * 8 + i + 1];
+            const float h0 = __uint_as_float(__float_as_uint(p0) & 0xFFFFE000u);
+            const float h1 = __uint_as_float(__float_as_uint(p1) & 0xFFFFE000u);
+            const auto hv = __builtin_amdgcn_cvt_pkrtz(h0, h1);
+            const auto lv = __builtin_amdgcn_cvt_pkrtz(p0 - h0, p1 - h1);
+            ph8[i] = hv[0];
+            ph8[i + 1] = hv[1];
+            pl8[i] = lv[0];
+            pl8[i + 1] = lv[1];
+          }
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            const fa_h8 va = *reinterpret_cast<const fa_h8*>(&Vt[(db * 32 + ql) * FA_VLD + k2 * 16 + hb * 8]);
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph8, o[db], 0, 0, 0);
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl8, o[db], 0, 0, 0);
+          }
+        }
+      }
+      if (step + 1 < nsteps) store_step(buf ^ 1);
+      __syncthreads();
+    }
+
+    // merge the R residues of each (head, row): residues 1..R-1 park (m, l, o) in LDS
+    const float lt = l + __shfl_xor(l, 32);
+    if (res > 0) {
+      float* dst = xs + (hh * (R - 1) + res - 1) * 66 * 64 + lane;
+      dst[0] = m;
+      dst[64] = lt;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(2 + db * 16 + r) * 64] = o[db][r];
+    }
+    __syncthreads();
+    if (res == 0) {
+      const float* part = xs + hh * (R - 1) * 66 * 64 + lane;
+      float M = m;
+#pragma unroll
+      for (int q = 0; q < R - 1; ++q) M = fmaxf(M, part[q * 66 * 64]);
+      const float ca = __builtin_amdgcn_exp2f(m - M);  // m is finite: key 0 is in residue 0's first tile
+      float cq[R - 1];
+      float L = lt * ca;
+#pragma unroll
+      for (int q = 0; q < R - 1; ++q) {
+        const float mq = part[q * 66 * 64];
+        cq[q] = mq == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mq - M);
+        L += part[q * 66 * 64 + 64] * cq[q];
+      }
+      if (t < a.B) {
+        const size_t row = static_cast<size_t>(t) * a.ld_out + head * HD;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = r4 * 4 + i;
+              float acc = o[db][r] * ca;
+#pragma unroll
+              for (int q = 0; q < R - 1; ++q) acc += part[q * 66 * 64 + (2 + db * 16 + r) * 64] * cq[q];
+              v[i] = acc / L;
+            }
+            const size_t off = row + db * 32 + r4 * 8 + hb * 4;
+            if (a.out != nullptr) *reinterpret_cast<f32x4*>(a.out + off) = v;
+            if (a.out_hi != nullptr) {  // the hi/lo activation pair of the o projection
+              f16x4 hi, lo;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                hi[i] = static_cast<f16>(v[i]);
+                lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
+              }
+              *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
+              *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
+            }
+          }
+      }
+    }
+    __syncthreads();  // the merge area is the next query tile's staging area
+  }
+}
+
+namespace {
+template <int HB>
+hipError_t launch_pairs(const AttnArgs& a, hipStream_t s) {
+  constexpr int R = 8 / HB;
+  constexpr size_t lds = pairs_lds_bytes<HB, R>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_prefill_pairs<HB, R>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(lds));
+  if (attr != hipSuccess) return attr;
+  const int nqt = (a.B + 31) / 32;
+  hipLaunchKernelGGL((k_attention_prefill_pairs<HB, R>), dim3((nqt + 1) / 2, a.nkv), dim3(512), lds, s, a);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attention_prefill_pairs(const AttnArgs& a, hipStream_t s) {
+  const int G = a.nq / a.nkv;
+  if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nkv <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;
+  if (a.ld_qkv % 4 != 0 || a.ld_out % 4 != 0) return hipErrorInvalidValue;
+  if ((a.out_hi == nullptr) != (a.out_lo == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
+    return hipErrorInvalidValue;
+  if (G == 2) return launch_pairs<2>(a, s);
+  if (G == 4) return launch_pairs<4>(a, s);
+  return hipErrorInvalidValue;
+}
+
+bool attention_prefill_pairs_supported(int nq, int nkv) { return nkv > 0 && nq % nkv == 0 && (nq / nkv == 2 || nq / nkv == 4); }
+
 hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;

@@ -83,6 +83,9 @@ hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s);
 // already hold the chunk's own keys. Supports nq/nkv in {1, 2, 4}; `part`, `counters`, `max_split`, `chunk` unused.
 hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s);
 bool attention_prefill_mfma_supported(int nq, int nkv);
+// Same contract, load-balanced over pairs of query tiles; nq/nkv in {2, 4}.
+hipError_t launch_attention_prefill_pairs(const AttnArgs& a, hipStream_t s);
+bool attention_prefill_pairs_supported(int nq, int nkv);
 
 // q/k RMSNorm over each head + RoPE + KV-cache append for T new rows at positions pos_base + t (prefill).
 struct QkNormRopeArgs {

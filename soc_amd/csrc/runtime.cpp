@@ -649,12 +649,16 @@ size_t skinny_scratch_floats(const soc_model* m) {
   return need;
 }
 
-// Prefill attention runs the MFMA flash kernel where the head grouping allows (SOC_PREFILL_ATTN=rows selects the
-// per-row split-key kernel that decode also uses). With a.out_hi / a.out_lo set, the row kernel writes fp32 into
-// `scratch` and a split pass produces the hi/lo pair.
+// Prefill attention runs the load-balanced MFMA flash kernel (query-tile pairs) where the head grouping allows,
+// else the per-tile MFMA flash kernel (SOC_PREFILL_ATTN=tiles forces the latter, SOC_PREFILL_ATTN=rows the per-row
+// split-key kernel that decode also uses). With a.out_hi / a.out_lo set, the row kernel writes fp32 into `scratch`
+// and a split pass produces the hi/lo pair.
 hipError_t prefill_attention(const soc::AttnArgs& a, float* scratch, hipStream_t s) {
   const char* mode = std::getenv("SOC_PREFILL_ATTN");
   const bool rows = mode != nullptr && std::strcmp(mode, "rows") == 0;
+  const bool tiles = mode != nullptr && std::strcmp(mode, "tiles") == 0;
+  if (!rows && !tiles && soc::attention_prefill_pairs_supported(a.nq, a.nkv))
+    return soc::launch_attention_prefill_pairs(a, s);
   if (!rows && soc::attention_prefill_mfma_supported(a.nq, a.nkv)) return soc::launch_attention_prefill_mfma(a, s);
   if (a.out_hi == nullptr) return soc::launch_attention(a, 0, s);
   soc::AttnArgs b = a;

@@ -93,20 +93,22 @@ def test_decode_matches_prefill_rows(gpu_ctx):
 
 @pytest.mark.parametrize("nq,nkv", [(2, 2), (4, 2), (8, 2)])
 def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv):
-    """The MFMA flash prefill attention (q and p carried as fp16 hi/lo pairs) agrees with the per-row fp32 kernel to
-    well inside fp32 noise x depth: max |diff| <= 1e-3 * max |logit| over every row, for a single prefill and for a
-    chunked one whose chunk starts off the 32-key tile grid (positions 70.., rows 0..79 of the chunk)."""
+    """Both MFMA flash prefill attention kernels (q and p carried as fp16 hi/lo pairs; the default one balances
+    pairs of query tiles for 2 or 4 q heads per kv head, SOC_PREFILL_ATTN=tiles selects the per-tile one) agree with
+    the per-row fp32 kernel to well inside fp32 noise x depth: max |diff| <= 1e-3 * max |logit| over every row, for
+    a single prefill and for a chunked one whose chunk starts off the 32-key tile grid (positions 70.., rows 0..79
+    of the chunk)."""
     cfg = S.QwenConfig(vocab_size=384, hidden_size=256, num_hidden_layers=2, num_attention_heads=nq,
                        num_key_value_heads=nkv, intermediate_size=512, tie_word_embeddings=False)
     m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, 11))
     ids = S.synth_tokens(12, "fa", cfg.vocab_size, 150)
     runs = {}
     try:
-        for mode in ("rows", "mfma"):
-            if mode == "rows":
-                monkeypatch.setenv("SOC_PREFILL_ATTN", "rows")
-            else:
+        for mode in ("rows", "tiles", "mfma"):
+            if mode == "mfma":
                 monkeypatch.delenv("SOC_PREFILL_ATTN", raising=False)
+            else:
+                monkeypatch.setenv("SOC_PREFILL_ATTN", mode)
             kv = S.KVCache(m, 1, 160)
             try:
                 full, tok = S.prefill(m, kv, 0, ids, 0, logit_rows=150)
@@ -116,11 +118,12 @@ def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv
             finally:
                 kv.close()
             runs[mode] = (full, tok, part, tok2)
-        for i, what in ((0, "single prefill"), (2, "chunked prefill")):
-            got, ref = runs["mfma"][i], runs["rows"][i]
-            err = float(np.max(np.abs(got - ref)))
-            assert err <= 1e-3 * float(np.max(np.abs(ref))), f"{what}: max abs diff {err:.3e}"
-        assert runs["mfma"][1] == runs["rows"][1] and runs["mfma"][3] == runs["rows"][3]
+        for mode in ("tiles", "mfma"):
+            for i, what in ((0, "single prefill"), (2, "chunked prefill")):
+                got, ref = runs[mode][i], runs["rows"][i]
+                err = float(np.max(np.abs(got - ref)))
+                assert err <= 1e-3 * float(np.max(np.abs(ref))), f"{mode}, {what}: max abs diff {err:.3e}"
+            assert runs[mode][1] == runs["rows"][1] and runs[mode][3] == runs["rows"][3]
     finally:
         m.close()
 
