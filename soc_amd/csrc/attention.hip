@@ -553,17 +553,20 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
 //    the 64 accumulators are rescaled rarely; the result is the same softmax (every partial keeps its own max and
 //    the merge rescales exactly);
 //  * p = hi + lo with hi = p with its low 13 mantissa bits cleared (exact in fp16 for p >= 2^-14) and lo = p - hi.
-// K tiles go global -> LDS with global_load_lds_dwordx4 (32 rows x 256 B, 16-byte chunk c of row r at slot
-// c ^ (r & 15)); V goes through registers (transposed on the store). Keys past the chunk's last row read the last
-// key (K) or zeros (V) and are masked.
-// grid = (ceil(ceil(B / 32) / 2), nkv), block = 512, dynamic LDS = max(staging, merge).
+// K and V tiles go global -> LDS row-major with global_load_lds_dwordx4 (32 rows x 256 B; 16-byte chunk c of row r
+// at slot c ^ (r & 15) for K, c ^ 2 (r & 7) for V) and V^T operands come out of LDS through the transposing read
+// ds_read_b64_tr_b16 (in each 16-lane group, lane j names 8 bytes = 4 dims of one key, and lane i receives dim i
+// of 4 consecutive keys), so no register staging or transposed stores are needed. Keys past the chunk's last row
+// read the last key and are masked (p = 0 against finite values).
+// grid = ceil(ceil(B / 32) / 2) * nkv blocks (block b: KV head b % nkv, so with 8 KV heads each XCD's L2 holds one
+// head), block = 512, dynamic LDS = max(staging, merge).
 // ------------------------------------------------------------------------------------------------------------
 namespace {
-constexpr int FP_KD = FA_KT * HD;     // K tile in halves (unpadded, swizzled)
-constexpr int FP_VT = HD * FA_VLD;    // V^T tile in halves
+constexpr int FP_KD = FA_KT * HD;     // K or V tile in halves (row-major, swizzled)
+typedef __fp16 fp_hv4 __attribute__((__vector_size__(4 * sizeof(__fp16))));  // operand type of the transposing read
 template <int HB, int R>
 constexpr size_t pairs_lds_bytes() {
-  const size_t staging = static_cast<size_t>(2) * R * (FP_KD + FP_VT) * sizeof(_Float16);
+  const size_t staging = static_cast<size_t>(2) * R * 2 * FP_KD * sizeof(_Float16);
   const size_t merge = static_cast<size_t>(HB) * (R - 1) * 66 * 64 * sizeof(float);
   return staging > merge ? staging : merge;
 }
@@ -574,15 +577,15 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
   static_assert(HB * R == 8, "8 waves");
   extern __shared__ __attribute__((aligned(16))) _Float16 plds[];
   _Float16* Ksb = plds;                  // [2][R][FP_KD]
-  _Float16* Vtb = plds + 2 * R * FP_KD;  // [2][R][FP_VT]
+  _Float16* Vb = plds + 2 * R * FP_KD;   // [2][R][FP_KD]
   float* xs = reinterpret_cast<float*>(plds);  // merge area [HB][R - 1][66][64], after the key loop
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int hh = wid % HB, res = wid / HB;
-  const int g = blockIdx.y;
+  const int g = static_cast<int>(blockIdx.x % a.nkv);
   const int head = g * HB + hh;
   const int ql = lane & 31, hb = lane >> 5;
   const int nqt = (a.B + 31) / 32;
-  const int j = blockIdx.x;
+  const int j = static_cast<int>(blockIdx.x / a.nkv);
   const size_t head_base = static_cast<size_t>(a.slot_base) * a.slot_stride +
                            static_cast<size_t>(a.layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
   const f16* kb = a.kcache + head_base;
@@ -621,33 +624,38 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
         }
       }
     }
-    u32x4 rv[R];
     auto load_step = [&](int step, int buf) {
+      const int r = 4 * wid + (lane >> 4);
 #pragma unroll
-      for (int p = 0; p < R; ++p) {  // K: wave w writes rows 4w..4w+3 of tile p
-        const int r = 4 * wid + (lane >> 4);
+      for (int p = 0; p < R; ++p) {  // K and V: wave w writes rows 4w..4w+3 of tile p
         const int key = min((R * step + p) * FA_KT + r, last);
-        const int c = (lane & 15) ^ (r & 15);
-        __builtin_amdgcn_global_load_lds(kb + static_cast<size_t>(key) * HD + c * 8,
+        const int ck = (lane & 15) ^ (r & 15);
+        const int cv = (lane & 15) ^ (2 * (r & 7));
+        __builtin_amdgcn_global_load_lds(kb + static_cast<size_t>(key) * HD + ck * 8,
                                          Ksb + (buf * R + p) * FP_KD + 4 * wid * HD, 16, 0, 0);
-      }
-#pragma unroll
-      for (int p = 0; p < R; ++p) {  // V: thread = (key tid % 32, dims 8 (tid / 32))
-        const int key = (R * step + p) * FA_KT + (tid & 31);
-        const size_t off = static_cast<size_t>(key) * HD + (tid >> 5) * 8;
-        rv[p] = key <= last ? load16(vb + off) : u32x4{0, 0, 0, 0};
+        __builtin_amdgcn_global_load_lds(vb + static_cast<size_t>(key) * HD + cv * 8,
+                                         Vb + (buf * R + p) * FP_KD + 4 * wid * HD, 16, 0, 0);
       }
     };
-    auto store_step = [&](int buf) {
+    // A operand of O^T = V^T . P^T for dims db*32.. and the 16-key step k2: lane (dim l % 32, hb) needs keys
+    // hb*4 + 0..3 and 8 + hb*4 + 0..3 of the step (the key order of the P^T operand); 16-lane group grp covers dims
+    // (grp & 1) * 16.. and keys (grp >> 1) * 4..
+    const int grp = lane >> 4, jj = lane & 15;
+    auto read_vt = [&](const _Float16* Vt, int db, int k2) {
+      fa_h8 out;
 #pragma unroll
-      for (int p = 0; p < R; ++p) {
-        const int key = tid & 31, d0 = (tid >> 5) * 8;
-        _Float16* Vt = Vtb + (buf * R + p) * FP_VT;
-        const fa_h8 v = __builtin_bit_cast(fa_h8, rv[p]);
-        const int col = fa_swizzle(key);
+      for (int half = 0; half < 2; ++half) {
+        const int row = k2 * 16 + half * 8 + (grp >> 1) * 4 + (jj >> 2);
+        const int dim = db * 32 + (grp & 1) * 16 + 4 * (jj & 3);
+        const int slot = (dim >> 3) ^ (2 * (row & 7));
+        const _Float16* p = Vt + row * HD + slot * 8 + (dim & 4);
+        const fp_hv4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (__attribute__((address_space(3))) fp_hv4*)((__attribute__((address_space(3))) _Float16*)(p)));
+        const f16x4 w = __builtin_bit_cast(f16x4, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) Vt[(d0 + i) * FA_VLD + col] = v[i];
+        for (int q = 0; q < 4; ++q) out[half * 4 + q] = w[q];
       }
+      return out;
     };
 
     f32x16 o[4];
@@ -658,15 +666,14 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
     float m = -INFINITY, l = 0.0f;
 
     load_step(0, 0);
-    store_step(0);
-    __syncthreads();  // also waits for the K tiles (vmcnt)
+    __syncthreads();  // also waits for the tiles (vmcnt)
     for (int step = 0; step < nsteps; ++step) {
       const int buf = step & 1;
       if (step + 1 < nsteps) load_step(step + 1, buf ^ 1);
       const int kt = R * step + res;
       if (kt < ntiles) {
         const _Float16* Ks = Ksb + (buf * R + res) * FP_KD;
-        const _Float16* Vt = Vtb + (buf * R + res) * FP_VT;
+        const _Float16* Vt = Vb + (buf * R + res) * FP_KD;
         f32x16 sh, sl;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -731,13 +738,12 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
           }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            const fa_h8 va = *reinterpret_cast<const fa_h8*>(&Vt[(db * 32 + ql) * FA_VLD + k2 * 16 + hb * 8]);
+            const fa_h8 va = read_vt(Vt, db, k2);
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph8, o[db], 0, 0, 0);
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl8, o[db], 0, 0, 0);
           }
         }
       }
-      if (step + 1 < nsteps) store_step(buf ^ 1);
       __syncthreads();
     }
 
@@ -811,7 +817,7 @@ hipError_t launch_pairs(const AttnArgs& a, hipStream_t s) {
                                                      static_cast<int>(lds));
   if (attr != hipSuccess) return attr;
   const int nqt = (a.B + 31) / 32;
-  hipLaunchKernelGGL((k_attention_prefill_pairs<HB, R>), dim3((nqt + 1) / 2, a.nkv), dim3(512), lds, s, a);
+  hipLaunchKernelGGL((k_attention_prefill_pairs<HB, R>), dim3(((nqt + 1) / 2) * a.nkv), dim3(512), lds, s, a);
   return hipGetLastError();
 }
 }  // namespace
