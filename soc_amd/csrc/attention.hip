@@ -105,33 +105,39 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) qreg[j][i] = qs[j][sub * 8 + i];
 
-  // scores: 16 lanes per key (8 dims each), 4 keys per wave step, 16 keys per block step
-  for (int base = 0; base < n; base += 64) {
-    u32x4 kraw[4];
+  // scores: 16 lanes per key (8 dims each), 4 keys per wave step, 16 keys per block step. The whole chunk's keys
+  // (at most 256, a.chunk <= 256 is checked at launch: 16 per lane) are loaded before any is used, and its values
+  // right after the scores, so each block waits for memory twice instead of once per 64 keys.
+  u32x4 raw[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = base + u * 16 + wid * 4 + r;
-      kraw[u] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+  for (int u = 0; u < 16; ++u) {
+    const int p = u * 16 + wid * 4 + r;
+    raw[u] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int p = u * 16 + wid * 4 + r;
+    if (u * 16 >= n) break;  // block-uniform: no key of this step is in the chunk
+    float kf[8];
+    if (FUSED && c0 + p == qpos) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
+    } else {
+      f16x8_to_f32(raw[u], kf);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = base + u * 16 + wid * 4 + r;
-      float kf[8];
-      if (FUSED && c0 + p == qpos) {
+    for (int j = 0; j < G; ++j) {
+      float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-      } else {
-        f16x8_to_f32(kraw[u], kf);
-      }
-#pragma unroll
-      for (int j = 0; j < G; ++j) {
-        float d = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
-        d = group_sum<16>(d);
-        if (sub == 0 && p < n) sc[j][p] = d * a.scale;
-      }
+      for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
+      d = group_sum<16>(d);
+      if (sub == 0 && p < n) sc[j][p] = d * a.scale;
     }
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int p = u * 16 + wid * 4 + r;
+    raw[u] = (p < n) ? load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
   }
   __syncthreads();
 
@@ -160,30 +166,23 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   for (int j = 0; j < G; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
-  for (int base = 0; base < n; base += 64) {
-    u32x4 vraw[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = base + u * 16 + wid * 4 + r;
-      vraw[u] = (p < n) ? load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
-    }
+  for (int u = 0; u < 16; ++u) {
+    const int p = u * 16 + wid * 4 + r;
+    if (u * 16 >= n) break;
+    if (p < n) {
+      float vf[8];
+      if (FUSED && c0 + p == qpos) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = base + u * 16 + wid * 4 + r;
-      if (p < n) {
-        float vf[8];
-        if (FUSED && c0 + p == qpos) {
+        for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+      } else {
+        f16x8_to_f32(raw[u], vf);
+      }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
-        } else {
-          f16x8_to_f32(vraw[u], vf);
-        }
+      for (int j = 0; j < G; ++j) {
+        const float w = sc[j][p];
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-          const float w = sc[j][p];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
-        }
+        for (int i = 0; i < 8; ++i) acc[j][i] += w * vf[i];
       }
     }
   }
