@@ -327,6 +327,51 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, int H, con
   }
 }
 
+// One wave per row for H % 4 == 0 (4 rows per block): the row's 16-byte pieces i = lane + 64 e (e < MAXV) are all
+// loaded before the sum of squares (per lane in e order, then across the wave); otherwise as k_rmsnorm_rows.
+template <int MAXV>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_v(const float* x, int T, int H, const f16* gain, float eps,
+                                                        float* yf, f16* yh, f16* ylo) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int nv = H / 4;
+  const float* xr = x + static_cast<size_t>(t) * H;
+  f32x4 v[MAXV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < MAXV; ++e) {
+    const int i = lane + 64 * e;
+    v[e] = i < nv ? *reinterpret_cast<const f32x4*>(xr + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int e = 0; e < MAXV; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ss += v[e][c] * v[e][c];
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int e = 0; e < MAXV; ++e) {
+    const int i = lane + 64 * e;
+    if (i >= nv) break;
+    const f16x4 gv = *reinterpret_cast<const f16x4*>(gain + 4 * i);
+    f32x4 y;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[c] = v[e][c] * scale * static_cast<float>(gv[c]);
+    const size_t o = static_cast<size_t>(t) * H + 4 * i;
+    if (yf) *reinterpret_cast<f32x4*>(yf + o) = y;
+    if (yh) {
+      f16x4 hi, lo;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        hi[c] = static_cast<f16>(y[c]);
+        lo[c] = static_cast<f16>((y[c] - static_cast<float>(hi[c])) * 2048.0f);
+      }
+      *reinterpret_cast<f16x4*>(yh + o) = hi;
+      if (ylo) *reinterpret_cast<f16x4*>(ylo + o) = lo;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_split_f16(const float* x, size_t n, f16* hi, f16* lo) {
   for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
     const float v = x[i];
@@ -889,7 +934,19 @@ hipError_t launch_embed(const int32_t* ids, int T, const f16* table, int H, floa
 hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const f16* gain, float eps, float* yf, f16* yh,
                                f16* ylo, hipStream_t s) {
   if (ylo != nullptr && yh == nullptr) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, H, gain, eps, yf, yh, ylo);
+  const int nv = H / 4;
+  const bool vec = H % 4 == 0 && nv <= 64 * 32 &&
+                   (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gain) | reinterpret_cast<uintptr_t>(yf) |
+                    reinterpret_cast<uintptr_t>(yh) | reinterpret_cast<uintptr_t>(ylo)) % 16 == 0;
+  if (!vec) {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, H, gain, eps, yf, yh, ylo);
+    return hipGetLastError();
+  }
+  const dim3 grid((T + 3) / 4);
+  if (nv <= 64 * 4) hipLaunchKernelGGL(k_rmsnorm_rows_v<4>, grid, dim3(256), 0, s, x, T, H, gain, eps, yf, yh, ylo);
+  else if (nv <= 64 * 8) hipLaunchKernelGGL(k_rmsnorm_rows_v<8>, grid, dim3(256), 0, s, x, T, H, gain, eps, yf, yh, ylo);
+  else if (nv <= 64 * 16) hipLaunchKernelGGL(k_rmsnorm_rows_v<16>, grid, dim3(256), 0, s, x, T, H, gain, eps, yf, yh, ylo);
+  else hipLaunchKernelGGL(k_rmsnorm_rows_v<32>, grid, dim3(256), 0, s, x, T, H, gain, eps, yf, yh, ylo);
   return hipGetLastError();
 }
 
