@@ -13,6 +13,8 @@
 // residual add, or SwiGLU of the gate/up halves.
 #include "kernels.h"
 
+#include <cmath>
+
 namespace soc {
 
 namespace {
@@ -22,16 +24,28 @@ constexpr int SK_MAX_KB = 1280; // K per block at most (LDS: 2 x 16 x (1280 + 8)
 typedef _Float16 sk_h8 __attribute__((ext_vector_type(8)));
 }  // namespace
 
-// Split count for a stacked matrix of `rows` rows and depth K (K % 256 == 0): the fewest splits (a divisor of
-// K / 256, at most SK_MAX_KB deep each) that give at least 256 blocks, else the most splits.
+// Split count for a stacked matrix of `rows` rows and depth K (K % 256 == 0): the divisor d of K / 256 (at most
+// SK_MAX_KB of K per block) with the least estimated traffic time: weight bytes over the evenness with which the
+// d * tiles blocks fill the chip's block slots (blocks / slots over its ceiling; 2 blocks per CU when the block's LDS
+// allows, the kernel's registers allow 2) plus the partial sums written and read back (16 rows x 4 bytes x rows x d,
+// twice).
 int skinny_splits(int rows, int K) {
   const int n256 = K / SK_CHUNK;
   const int tiles = (rows + SK_ROWS - 1) / SK_ROWS;
   int best = n256;
+  double best_cost = 0.0;
   for (int d = 1; d <= n256; ++d) {
-    if (n256 % d != 0 || K / d > SK_MAX_KB) continue;
-    best = d;
-    if (tiles * d >= 256) break;
+    const int kb = K / d;
+    if (n256 % d != 0 || kb > SK_MAX_KB) continue;
+    const size_t lds = static_cast<size_t>(2) * 16 * (kb + 8) * sizeof(_Float16);
+    const int slots = 256 * (2 * lds <= 160 * 1024 ? 2 : 1);
+    const double waves = static_cast<double>(tiles) * d / slots;
+    const double eff = waves / std::ceil(waves);
+    const double cost = 2.0 * rows * K / eff + 2.0 * 16 * 4 * static_cast<double>(rows) * d;
+    if (best_cost == 0.0 || cost < best_cost) {
+      best = d;
+      best_cost = cost;
+    }
   }
   return best;
 }
