@@ -19,19 +19,6 @@ namespace {
 constexpr int HD = 128;  // head_dim handled by these kernels
 constexpr int kMaxCombine = 160;  // key chunks one attention row may be split into (160 x 256 = 40960 keys)
 
-// Lane l of a wave holds dims (l, l + 64) of one head vector: RMSNorm over the 128 values and rotate-half RoPE at
-// table row `pos` (cos/sin precomputed on the host in double, then rounded to float, like rope.cpp:77-79).
-__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const f16* gain, float eps, const float* cosr,
-                                               const float* sinr, int lane) {
-  const float ss = wave_sum(x0 * x0 + x1 * x1);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(HD) + eps);
-  const float y0 = x0 * scale * static_cast<float>(gain[lane]);
-  const float y1 = x1 * scale * static_cast<float>(gain[lane + 64]);
-  const float c = cosr[lane], s = sinr[lane];
-  x0 = y0 * c - y1 * s;
-  x1 = y0 * s + y1 * c;
-}
-
 }  // namespace
 
 // grid = (max_split, nkv, B), block = 256 (4 waves). Each block: one KV head g, its G query heads, one batch row,

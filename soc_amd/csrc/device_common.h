@@ -97,6 +97,25 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// Lane l of a wave holds dims (l, l + 64) of one 128-dim head vector: RMSNorm over the 128 values and rotate-half
+// RoPE at one table row (cos/sin precomputed on the host in double, then rounded to float, like rope.cpp:77-79).
+// The multiply-adds are written as explicit fmaf so that every kernel that inlines this computes the same bits
+// (the QKV GEMM epilogue and the stand-alone q/k-norm kernel must agree exactly).
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const f16* gain, float eps, const float* cosr,
+                                               const float* sinr, int lane) {
+  const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+  const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float y0 = x0 * scale * static_cast<float>(gain[lane]);
+  const float y1 = x1 * scale * static_cast<float>(gain[lane + 64]);
+  const float c = cosr[lane], s = sinr[lane];
+  x0 = fmaf(y0, c, -(y1 * s));
+  x1 = fmaf(y0, s, y1 * c);
+  // Materialise the fp32 results: otherwise a caller's f16 conversion can be folded into the fma
+  // (v_fma_mixlo_f16, one rounding straight to f16), which differs from rounding to fp32 first in rare cases and
+  // would make the cached keys depend on which kernel wrote them.
+  __asm__ volatile("" : "+v"(x0), "+v"(x1));
+}
+
 // SiLU exactly as the reference writes it: v / (1 + exp(-v)) (Mac/cpu/src/qwen_mlp.cpp:31).
 __device__ __forceinline__ float silu_ref(float v) { return v / (1.0f + expf(-v)); }
 

@@ -442,6 +442,51 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
     }
   }
   // epilogue: lane holds D[m][n] for n = lane % 32, m = (r / 4) * 8 + (lane / 32) * 4 + r % 4
+  if constexpr (EPI == EPI_QKV) {
+    // the tile's 128 columns are one head: park the tile in LDS, then each wave takes BM / 4 of its rows with lane l
+    // holding dims (l, l + 64), as the q/k-norm kernel does, so q, k and v come out bit-identical to it
+    static_assert(BN == 128, "one 128-dim head per tile");
+    constexpr int LDX = BN + 1;
+    float* xs = reinterpret_cast<float*>(slds);
+    __syncthreads();  // every wave's MFMA operand reads of the ring are done
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+#pragma unroll
+        for (int t = 0; t < NJ; ++t)
+          xs[ml * LDX + wn * (BN / 2) + t * 32 + (lane & 31)] = acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f);
+      }
+    __syncthreads();
+    const GemmSplitArgs::Qkv& q = g.qkv;
+    const int head = n0 / BN;  // q heads, then k heads, then v heads
+    for (int rr = 0; rr < BM / 4; ++rr) {
+      const int ml = wid * (BM / 4) + rr, m = m0 + ml;
+      if (m >= g.M) break;  // wave-uniform
+      float x0 = xs[ml * LDX + lane], x1 = xs[ml * LDX + lane + 64];
+      const int pos = q.pos_base + m;
+      if (head < q.nq + q.nkv) {
+        const float* cr = q.rope_cos + static_cast<size_t>(pos) * 64;
+        const float* sr = q.rope_sin + static_cast<size_t>(pos) * 64;
+        norm_rope_pair(x0, x1, head < q.nq ? q.q_gain : q.k_gain, q.eps, cr, sr, lane);
+      }
+      if (head < q.nq) {
+        float* dst = q.q_out + static_cast<size_t>(m) * q.nq * 128 + head * 128;
+        dst[lane] = x0;
+        dst[lane + 64] = x1;
+      } else {
+        const bool is_k = head < q.nq + q.nkv;
+        const int kvh = is_k ? head - q.nq : head - q.nq - q.nkv;
+        const size_t base = static_cast<size_t>(q.slot) * q.slot_stride + static_cast<size_t>(q.layer) * q.layer_stride +
+                            (static_cast<size_t>(kvh) * q.cap + pos) * 128;
+        f16* cache = is_k ? q.kcache : q.vcache;
+        cache[base + lane] = static_cast<f16>(x0);
+        cache[base + lane + 64] = static_cast<f16>(x1);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -525,10 +570,14 @@ bool gemm_split_supported(const GemmSplitArgs& g) {
 hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s) {
   if (!gemm_split_supported(g)) return hipErrorInvalidValue;
   if (epi == EPI_SWIGLU && (g.w2 == nullptr || (g.ch == nullptr) != (g.cl == nullptr))) return hipErrorInvalidValue;
+  if (epi == EPI_QKV && (g.N != (g.qkv.nq + 2 * g.qkv.nkv) * 128 || g.qkv.q_out == nullptr ||
+                         g.qkv.kcache == nullptr || g.qkv.vcache == nullptr))
+    return hipErrorInvalidValue;
   switch (epi) {
     case EPI_STORE: return launch_split_epi<EPI_STORE>(g, s);
     case EPI_RESIDUAL: return launch_split_epi<EPI_RESIDUAL>(g, s);
     case EPI_SWIGLU: return launch_split_epi<EPI_SWIGLU>(g, s);
+    case EPI_QKV: return launch_split_epi<EPI_QKV>(g, s);
     default: return hipErrorInvalidValue;
   }
 }

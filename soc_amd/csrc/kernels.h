@@ -8,7 +8,7 @@
 
 namespace soc {
 
-enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 // ---- decode GEMV (batch 1) ----
 struct GemvArgs {
@@ -183,6 +183,20 @@ struct GemmSplitArgs {
   f16* cl;
   int ldc;
   int M, N, K;
+  // EPI_QKV (fused projection rows q | k | v, 128-column heads): per-head RMSNorm + RoPE of the q and k heads at
+  // positions pos_base + row; q -> q_out [M][nq * 128] (fp32), k and v -> the fp16 cache rows of `slot`
+  struct Qkv {
+    float* q_out;
+    f16* kcache;
+    f16* vcache;
+    const f16* q_gain;
+    const f16* k_gain;
+    const float* rope_cos;
+    const float* rope_sin;
+    long long slot_stride, layer_stride;
+    int slot, layer, cap, pos_base, nq, nkv;
+    float eps;
+  } qkv;
 };
 bool gemm_split_supported(const GemmSplitArgs& g);
 hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s);

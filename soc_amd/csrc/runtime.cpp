@@ -1288,11 +1288,43 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   for (int l = 0; l < c.num_hidden_layers; ++l) {
     const DevLayer& L = m->layers[l];
     soc::GemmArgs g{};
+    bool qkv_fused = false;
     if (split) {
       if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, w.pl, s)) != hipSuccess)
         return hip_fail(e, "rmsnorm");
-      if ((e = split_gemm(w.ph, w.pl, H, L.wqkv, nullptr, w.qkv, nullptr, nullptr, m->qkv_rows, n, m->qkv_rows, H,
-                          soc::EPI_STORE, s)) != hipSuccess)
+      // QKV projection with the per-head q/k RMSNorm + RoPE, q output and K/V cache append in its epilogue
+      // (SOC_PREFILL_QKV=separate: plain projection, then the q/k-norm kernel)
+      const char* qm = std::getenv("SOC_PREFILL_QKV");
+      qkv_fused = qm == nullptr || std::strcmp(qm, "separate") != 0;
+      soc::GemmSplitArgs g3{};
+      g3.ah = w.ph;
+      g3.al = w.pl;
+      g3.lda = H;
+      g3.w = L.wqkv;
+      g3.c = w.qkv;
+      g3.ldc = m->qkv_rows;
+      g3.M = n;
+      g3.N = m->qkv_rows;
+      g3.K = H;
+      if (qkv_fused) {
+        g3.qkv.q_out = w.q;
+        g3.qkv.kcache = kv->k;
+        g3.qkv.vcache = kv->v;
+        g3.qkv.q_gain = L.q_norm;
+        g3.qkv.k_gain = L.k_norm;
+        g3.qkv.rope_cos = m->rope_cos;
+        g3.qkv.rope_sin = m->rope_sin;
+        g3.qkv.slot_stride = kv->slot_stride;
+        g3.qkv.layer_stride = kv->layer_stride;
+        g3.qkv.slot = slot;
+        g3.qkv.layer = l;
+        g3.qkv.cap = kv->cap;
+        g3.qkv.pos_base = pos_off;
+        g3.qkv.nq = c.num_attention_heads;
+        g3.qkv.nkv = c.num_key_value_heads;
+        g3.qkv.eps = c.rms_norm_eps;
+      }
+      if ((e = soc::launch_gemm_split(g3, qkv_fused ? soc::EPI_QKV : soc::EPI_STORE, s)) != hipSuccess)
         return hip_fail(e, "gemm qkv");
     } else {
       if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
@@ -1327,7 +1359,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     q.T = n;
     q.nq = c.num_attention_heads;
     q.nkv = c.num_key_value_heads;
-    if ((e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
+    if (!qkv_fused && (e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
     soc::AttnArgs a = attn_args(m, kv, l);
     a.qkv = w.q;
     a.ld_qkv = m->qd;
