@@ -79,9 +79,10 @@ int soc_model_synthesize(soc_model* model, uint64_t seed, float sigma);
 int soc_model_finalize(soc_model* model);
 /* Bytes of weights held on the device. */
 int soc_model_weight_bytes(const soc_model* model, int64_t* bytes);
-/* Which decode implementation soc_decode / soc_decode_steps use on this device: 1 = one persistent kernel launch per
- * token (k_decode_persistent), 0 = the per-operator kernel sequence replayed as a HIP graph. Diagnostics only; the
- * reference has no counterpart (it has one decode implementation per backend). */
+/* Which decode implementation soc_decode / soc_decode_steps use on this device: 2 = one kernel launch per token with
+ * every layer split over the 8 XCDs (k_decode_xcd; models with 8 KV heads), 1 = one kernel launch per token with
+ * dedicated attention blocks (k_decode_persistent), 0 = the per-operator kernel sequence replayed as a HIP graph.
+ * Diagnostics only; the reference has no counterpart (it has one decode implementation per backend). */
 int soc_model_decode_path(soc_model* model, int32_t* path);
 
 /* ---- KV cache: replaces KVCache (Mac/gpu/include/runtime/kv_cache.h:23-79; kv_cache.mm:32-204).

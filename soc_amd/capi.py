@@ -289,10 +289,11 @@ class Model:
         return v.value
 
     def decode_path(self) -> str:
-        """"persistent" (one k_decode_persistent launch per token) or "graph" (per-operator kernels)."""
+        """"xcd" (one k_decode_xcd launch per token, each layer split over the 8 XCDs), "persistent" (one
+        k_decode_persistent launch per token) or "graph" (per-operator kernels)."""
         v = C.c_int32()
         check(lib().soc_model_decode_path(self.h, C.byref(v)))
-        return "persistent" if v.value == 1 else "graph"
+        return {2: "xcd", 1: "persistent"}.get(v.value, "graph")
 
     def close(self) -> None:
         if self.h:

@@ -8,10 +8,13 @@
 //   P3 x' = x + Wo . attn                                    every projection block
 //   P4 h = silu(RMSNorm(x') . Wg^T) * (RMSNorm(x') . Wu^T)   every projection block
 //   P5 x'' = x' + Wd . h                                     every projection block
-// Activations move between phases through small exchange vectors written with 8-byte stores that carry the value
-// and a tag unique to (step, layer): a reader spins until every element carries the expected tag. An aligned 8-byte
-// store is single-copy atomic, so a value is never seen without its tag, and no barrier or cache flush is needed.
-// Loads and stores of the exchange vectors are relaxed device-scope atomics (coherent across XCDs).
+// Activations move between phases through small exchange vectors of 32-bit tagged words: the fp32 value rounded
+// to 21 mantissa bits with a 2-bit phase tag in the two low bits (phase = (step - 1) * L + layer, mod 4). A reader
+// spins until every element carries the expected tag. An aligned 4-byte store is single-copy atomic, so a value is
+// never seen without its tag, and no barrier or cache flush is needed. Two bits are enough because every element is
+// written once per phase and a producer can only reach phase p + 1 after every reader has consumed phase p (each
+// phase needs all outputs of the one before it), so a reader waiting for phase p can find only phase p - 1 or p.
+// Loads and stores of the exchange vectors are relaxed device-scope accesses (coherent across XCDs).
 //
 // Each block splits into seven compute waves and one receiver wave (wave 7). For the inputs that are RMSNorm-ed
 // (P1, P4, the LM head) the receiver alone waits, applies the norm in its registers (or, in attention blocks, the
@@ -23,6 +26,7 @@
 // its own rows. Every wait is bounded: on timeout the block raises an error flag and the whole grid drains.
 #include <algorithm>
 
+#include "exchange.h"
 #include "kernels.h"
 
 namespace soc {
@@ -33,47 +37,23 @@ constexpr int NT = 512;          // threads per block
 constexpr int NC = 448;          // compute threads: waves 0..6
 constexpr int RECV = 7;          // receiver wave
 constexpr int HD = 128;
-constexpr uint64_t kSpinTicks = 20000000ull;  // 200 ms of the 100 MHz real-time counter per wait
-
-__device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
-
-__device__ __forceinline__ void ll_store(uint64_t* p, float v, uint32_t tag) {
-  const uint64_t u = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
-  __hip_atomic_store(p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t ll_peek(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ bool err_raised(int* err) {
-  return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-}
-
-__device__ __forceinline__ uint32_t tag_of(uint64_t v) { return static_cast<uint32_t>(v >> 32); }
-
-// Back-off between polling rounds: fewer re-reads of lines that producers are about to write.
-__device__ __forceinline__ void poll_pause(int n) {
-  for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(1);
-}
-__device__ __forceinline__ float val_of(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 
 // Receiver wave: elements i = lane + 64 e (e < MAXE) of a tagged vector, re-read until every one carries `tag`.
 // `addr(i)` gives the source of element i < n. Returns false (wave-uniform) on timeout or a raised error flag.
 template <int MAXE, typename Addr>
-__device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err, int pause) {
+__device__ __forceinline__ bool recv_wait(uint32_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err, int pause) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int e = 0; e < MAXE; ++e) {
     const int i = lane + 64 * e;
-    v[e] = i < n ? ll_peek(addr(i)) : (static_cast<uint64_t>(tag) << 32);
+    v[e] = i < n ? ll_peek(addr(i)) : tag;
   }
   const uint64_t t0 = now_ticks();
   uint32_t spins = 0;
   while (true) {
     bool all = true;
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) all = all && tag_of(v[e]) == tag;
+    for (int e = 0; e < MAXE; ++e) all = all && tw_tag(v[e]) == tag;
     if (__all(all)) return true;
     if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -83,49 +63,40 @@ __device__ __forceinline__ bool recv_wait(uint64_t (&v)[MAXE], int n, uint32_t t
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) {
       const int i = lane + 64 * e;
-      if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek(addr(i));
+      if (i < n && tw_tag(v[e]) != tag) v[e] = ll_peek(addr(i));
     }
   }
-}
-
-// Relaxed device-scope read of one tagged word through a buffer resource (sc1: coherent across XCDs). The lane's
-// byte offset stays in one register and the per-element part folds into the instruction's offset fields, so a
-// receiver polling thousands of elements needs no per-element address registers. An aligned 8-byte load is
-// single-copy atomic.
-__device__ __forceinline__ uint64_t ll_peek_buf(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 16);
-  return (static_cast<uint64_t>(v.y) << 32) | v.x;
 }
 
 // Receiver: the tagged vector src[0..n) into dst; with NORM, RMSNorm-ed with `gain`
 // (Mac/cpu/src/rms_norm_module.cpp:56-64: ms = sum x^2 / n; y = x * (1 / sqrt(ms + eps)) * g).
-template <int MAXE, bool NORM>
-__device__ __forceinline__ bool recv_vec(const uint64_t* src, int n, uint32_t tag, float* dst, const f16* gain,
+// Lane l polls the quads q = l + 64 e (elements 4q..4q+3) with one 16-byte load each; n is a multiple of 4.
+template <int MAXQ, bool NORM>
+__device__ __forceinline__ bool recv_vec(const uint32_t* src, int n, uint32_t tag, float* dst, const f16* gain,
                                          float eps, int* err, int pause) {
   const int lane = threadIdx.x & 63;
-  float g[NORM ? MAXE : 1];
+  const int nq = n / 4;
+  f16x4 g[NORM ? MAXQ : 1];
   if constexpr (NORM) {
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-      const int i = lane + 64 * e;
-      g[e] = i < n ? static_cast<float>(gain[i]) : 0.0f;
+    for (int e = 0; e < MAXQ; ++e) {
+      const int q = lane + 64 * e;
+      g[e] = q < nq ? ld_global(reinterpret_cast<const f16x4*>(gain), q) : f16x4{0, 0, 0, 0};
     }
   }
   const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(src), 0, n * 8, 0x00020000);
-  uint64_t v[MAXE];
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, n * 4, 0x00020000);
+  const u32x4 filler = {tag, tag, tag, tag};
+  u32x4 v[MAXQ];
 #pragma unroll
-  for (int e = 0; e < MAXE; ++e) {
-    const int i = lane + 64 * e;
-    v[e] = i < n ? ll_peek_buf(rsrc, lane * 8 + 512 * e) : (static_cast<uint64_t>(tag) << 32);
-  }
+  for (int e = 0; e < MAXQ; ++e) v[e] = lane + 64 * e < nq ? ll_peek_buf4(rsrc, lane * 16 + 1024 * e) : filler;
   const uint64_t t0 = now_ticks();
   uint32_t spins = 0;
   bool ok = true;
   while (true) {
     bool all = true;
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) all = all && tag_of(v[e]) == tag;
+    for (int e = 0; e < MAXQ; ++e) all = all && tw_quad_ok(v[e], tag);
     if (__all(all)) break;
     if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -134,31 +105,40 @@ __device__ __forceinline__ bool recv_vec(const uint64_t* src, int n, uint32_t ta
     }
     poll_pause(pause);
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-      const int i = lane + 64 * e;
-      if (i < n && tag_of(v[e]) != tag) v[e] = ll_peek_buf(rsrc, lane * 8 + 512 * e);
-    }
+    for (int e = 0; e < MAXQ; ++e)
+      if (lane + 64 * e < nq && !tw_quad_ok(v[e], tag)) v[e] = ll_peek_buf4(rsrc, lane * 16 + 1024 * e);
   }
   if (!ok) return false;
+  float x[MAXQ][4];
+#pragma unroll
+  for (int e = 0; e < MAXQ; ++e) {
+    x[e][0] = tw_val(v[e].x);
+    x[e][1] = tw_val(v[e].y);
+    x[e][2] = tw_val(v[e].z);
+    x[e][3] = tw_val(v[e].w);
+  }
   if constexpr (!NORM) {
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-      const int i = lane + 64 * e;
-      if (i < n) dst[i] = val_of(v[e]);
+    for (int e = 0; e < MAXQ; ++e) {
+      const int q = lane + 64 * e;
+      if (q < nq) *reinterpret_cast<f32x4*>(dst + 4 * q) = f32x4{x[e][0], x[e][1], x[e][2], x[e][3]};
     }
   } else {
     float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-      const float x = lane + 64 * e < n ? val_of(v[e]) : 0.0f;
-      ss += x * x;
-    }
+    for (int e = 0; e < MAXQ; ++e)
+      if (lane + 64 * e < nq) ss += x[e][0] * x[e][0] + x[e][1] * x[e][1] + x[e][2] * x[e][2] + x[e][3] * x[e][3];
     ss = wave_sum(ss);
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e) {
-      const int i = lane + 64 * e;
-      if (i < n) dst[i] = val_of(v[e]) * scale * g[e];
+    for (int e = 0; e < MAXQ; ++e) {
+      const int q = lane + 64 * e;
+      if (q < nq) {
+        f32x4 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = x[e][j] * scale * static_cast<float>(g[e][j]);
+        *reinterpret_cast<f32x4*>(dst + 4 * q) = y;
+      }
     }
   }
   return true;
@@ -181,7 +161,7 @@ __device__ __forceinline__ void recv_embed(const f16* row, int n, float* dst, co
 #pragma unroll
   for (int e = 0; e < MAXE; ++e) {
     const int i = lane + 64 * e;
-    if (i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
+    if (i < n) dst[i] = x[e] * scale * static_cast<float>(ld_global(gain, i));
   }
 }
 
@@ -230,7 +210,7 @@ constexpr int TPR_O = 64, CPT_O = 4;       // K = q_dim
 constexpr int TPR_GU = 32, CPT_GU = 4;     // K = H
 constexpr int TPR_D = 64, CPT_D = 6;       // K = I
 constexpr int TPR_LM = 32, CPT_LM = 4;     // LM head, NC / 32 = 14 rows per fragment
-constexpr int MAXE_H = 16;                // receiver elements per lane: H <= 64 x MAXE_H
+constexpr int MAXQ_H = 4;                 // receiver quads per lane: H <= 256 x MAXQ_H
 constexpr int KCH = 224;                   // attention keys per chunk: 28 groups of 16 lanes x 8 keys
 
 }  // namespace
@@ -261,7 +241,7 @@ namespace {
 struct Ctx {
   const PersistArgs& a;
   int b, ng, token, pos;
-  uint32_t step;
+  uint32_t phase0;  // (step - 1) * L: the tag of layer l is (phase0 + l) & 3
   float* xs0;   // [xs_cap] phase inputs, double buffered
   float* xs1;
   int* flag;    // [2] block-uniform status
@@ -281,18 +261,20 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
   const PersistArgs& a = c.a;
   const int lane = threadIdx.x & 63;
   for (int layer = 0; layer < a.L; ++layer) {
-    const f16* const* W = a.layer_w + layer * 9;
-    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    const f16* W[9];  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+#pragma unroll
+    for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     f16* kb = a.kcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
     f16* vb = a.vcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
     // q heads, key and value of KV head g: (G + 2) x 128 tagged elements, two per lane per head
     constexpr int E = 2 * (G + 2);
-    uint64_t v[E];
-    const uint64_t* q_src = a.qkv + g * G * HD;
-    const uint64_t* k_src = a.qkv + a.qd + g * HD;
-    const uint64_t* v_src = a.qkv + a.qd + a.nkv * HD + g * HD;
-    const float qg0 = static_cast<float>(W[2][lane]), qg1 = static_cast<float>(W[2][lane + 64]);
-    const float kg0 = static_cast<float>(W[3][lane]), kg1 = static_cast<float>(W[3][lane + 64]);
+    uint32_t v[E];
+    const uint32_t* q_src = a.qkv + g * G * HD;
+    const uint32_t* k_src = a.qkv + a.qd + g * HD;
+    const uint32_t* v_src = a.qkv + a.qd + a.nkv * HD + g * HD;
+    const float qg0 = static_cast<float>(ld_global(W[2], lane)), qg1 = static_cast<float>(ld_global(W[2], lane + 64));
+    const float kg0 = static_cast<float>(ld_global(W[3], lane)), kg1 = static_cast<float>(ld_global(W[3], lane + 64));
     const float rc = a.rope_cos[static_cast<size_t>(c.pos) * (HD / 2) + lane];
     const float rs = a.rope_sin[static_cast<size_t>(c.pos) * (HD / 2) + lane];
     const bool ok = recv_wait<E>(v, E * 64, tag,
@@ -306,7 +288,7 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
       // (lane, lane + 64) of each head; the key and value are rounded to fp16 and appended at `pos`
 #pragma unroll
       for (int hh = 0; hh <= G; ++hh) {
-        const float x0 = val_of(v[2 * hh]), x1 = val_of(v[2 * hh + 1]);
+        const float x0 = tw_val(v[2 * hh]), x1 = tw_val(v[2 * hh + 1]);
         const float ssum = wave_sum(x0 * x0 + x1 * x1);
         const float sc = 1.0f / sqrtf(ssum / static_cast<float>(HD) + a.eps);
         const float y0 = x0 * sc * (hh < G ? qg0 : kg0);
@@ -324,7 +306,7 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
           kn[lane + 64] = static_cast<float>(h1v);
         }
       }
-      const f16 v0h = static_cast<f16>(val_of(v[2 * G + 2])), v1h = static_cast<f16>(val_of(v[2 * G + 3]));
+      const f16 v0h = static_cast<f16>(tw_val(v[2 * G + 2])), v1h = static_cast<f16>(tw_val(v[2 * G + 3]));
       vb[static_cast<size_t>(c.pos) * HD + lane] = v0h;
       vb[static_cast<size_t>(c.pos) * HD + lane + 64] = v1h;
       vn[lane] = static_cast<float>(v0h);
@@ -352,7 +334,7 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
   const int pos = c.pos, S = pos + 1;
   u32x4 kreg[8], vreg[8];
   for (int layer = 0; layer < a.L; ++layer) {
-    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     const f16* kb = a.kcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
     const f16* vb = a.vcache + static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
     auto kv_fetch = [&](int c0) {
@@ -484,100 +466,46 @@ __device__ __forceinline__ bool attn_compute(const Ctx& c, int g, const float* q
   return true;
 }
 
-// ---------------- multi-wave receive (waves w0..7; used where those waves have no loads or stores in flight) -----
-// Element pairs of the tagged vector src[0..n) are spread over the polling threads and go to dst; with NORM, the
-// block then applies the RMSNorm with `gain` (a block-wide sum of squares through LDS). Every wave takes part in
-// the barriers: two with NORM, one without. (A single polling wave sees the first data sooner, but more polling
-// threads see the last element sooner when the vector is long; which wins is a per-phase measurement.)
-template <bool NORM>
-__device__ __forceinline__ bool block_recv(const Ctx& c, const uint64_t* src, const f16* embed_row, int n,
-                                           uint32_t tag, float* dst, const f16* gain, float eps, int w0) {
-  constexpr int MP = 3;  // pairs of elements per polling thread
-  constexpr int MB = 2 * MP;
-  const int tid = threadIdx.x, wid = tid >> 6;
-  const bool polls = wid >= w0;
-  const int tp = tid - 64 * w0, np = NT - 64 * w0;  // polling thread index and count
-  // polling thread tp owns the element pairs (2 tp + 2 np e, + 1): one 16-byte load reads both tagged words
-  auto elem = [&](int e) { return 2 * tp + (e & 1) + 2 * np * (e >> 1); };
-  float x[MB];
+// ---------------- multi-wave receive (all eight waves; used where no wave has loads or stores in flight) -----
+// Quads of the tagged vector src[0..n) are spread over the block's threads and go to dst; one block barrier
+// follows. (A single polling wave sees the first data sooner, but more polling threads see the last element sooner
+// when the vector is long; which wins is a per-phase measurement.)
+__device__ __forceinline__ bool block_recv(const Ctx& c, const uint32_t* src, int n, uint32_t tag, float* dst) {
+  constexpr int MQ = 2;  // quads per thread: n <= 4 x MQ x NT
+  const int tid = threadIdx.x;
+  const int nq = n / 4;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, n * 4, 0x00020000);
+  const u32x4 filler = {tag, tag, tag, tag};
+  u32x4 v[MQ];
+#pragma unroll
+  for (int e = 0; e < MQ; ++e) v[e] = tid + NT * e < nq ? ll_peek_buf4(rsrc, tid * 16 + NT * 16 * e) : filler;
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
   bool ok = true;
-  if (!polls) {
+  while (true) {
+    bool all = true;
 #pragma unroll
-    for (int e = 0; e < MB; ++e) x[e] = 0.0f;
-  } else if (embed_row != nullptr) {
-    // layer 0: the embedding row itself (embedding.cpp:51-77)
-#pragma unroll
-    for (int e = 0; e < MB; ++e) {
-      const int i = elem(e);
-      x[e] = i < n ? static_cast<float>(embed_row[i]) : 0.0f;
+    for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
+    if (__all(all)) break;
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+      __hip_atomic_store(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = false;
+      break;
     }
-  } else {
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(src), 0, n * 8, 0x00020000);
-    u32x4 v[MP];
-    auto done = [&](const u32x4& w, int e) {  // both words of pair e carry the tag (or lie past n)
-      const int i = 2 * tp + 2 * np * e;
-      return (i >= n || w.y == tag) && (i + 1 >= n || w.w == tag);
-    };
+    poll_pause(c.a.spin_sleep);
 #pragma unroll
-    for (int e = 0; e < MP; ++e) {
-      const int i = 2 * tp + 2 * np * e;
-      v[e] = i < n ? __builtin_amdgcn_raw_buffer_load_b128(rsrc, tp * 16 + np * 16 * e, 0, 16)
-                   : u32x4{0, tag, 0, tag};
-    }
-    const uint64_t t0 = now_ticks();
-    uint32_t spins = 0;
-    while (true) {
-      bool all = true;
-#pragma unroll
-      for (int e = 0; e < MP; ++e) all = all && done(v[e], e);
-      if (__all(all)) break;
-      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-        __hip_atomic_store(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = false;
-        break;
-      }
-      poll_pause(c.a.spin_sleep);
-#pragma unroll
-      for (int e = 0; e < MP; ++e)
-        if (!done(v[e], e)) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tp * 16 + np * 16 * e, 0, 16);
-    }
-#pragma unroll
-    for (int e = 0; e < MP; ++e) {
-      x[2 * e] = __uint_as_float(v[e].x);
-      x[2 * e + 1] = __uint_as_float(v[e].z);
-    }
+    for (int e = 0; e < MQ; ++e)
+      if (tid + NT * e < nq && !tw_quad_ok(v[e], tag)) v[e] = ll_peek_buf4(rsrc, tid * 16 + NT * 16 * e);
   }
   if (!ok && (tid & 63) == 0) c.flag[0] = 1;
-  float* red = reinterpret_cast<float*>(c.bv);  // [8] wave partial sums (argmax scratch is idle until the LM head)
-  if constexpr (!NORM) {
 #pragma unroll
-    for (int e = 0; e < MB; ++e) {
-      const int i = elem(e);
-      if (polls && i < n) dst[i] = x[e];
-    }
-    SOC_SYNC();
-  } else {
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < MB; ++e) {
-      const int i = elem(e);
-      ss += polls && i < n ? x[e] * x[e] : 0.0f;
-    }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[wid] = ss;
-    SOC_SYNC();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NT / 64; ++w) tot += red[w];
-    const float scale = 1.0f / sqrtf(tot / static_cast<float>(n) + eps);
-#pragma unroll
-    for (int e = 0; e < MB; ++e) {
-      const int i = elem(e);
-      if (polls && i < n) dst[i] = x[e] * scale * static_cast<float>(gain[i]);
-    }
-    SOC_SYNC();
+  for (int e = 0; e < MQ; ++e) {
+    const int q = tid + NT * e;
+    if (ok && q < nq)
+      *reinterpret_cast<f32x4*>(dst + 4 * q) = f32x4{tw_val(v[e].x), tw_val(v[e].y), tw_val(v[e].z), tw_val(v[e].w)};
   }
+  SOC_SYNC();
   return true;
 }
 
@@ -586,15 +514,17 @@ __device__ __forceinline__ bool proj_receiver(const Ctx& c) {
   const PersistArgs& a = c.a;
   const int H = a.H;
   for (int layer = 0; layer < a.L; ++layer) {
-    const f16* const* W = a.layer_w + layer * 9;
-    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
-    if (layer == 0) recv_embed<MAXE_H>(a.embed + static_cast<size_t>(c.token) * H, H, c.xs0, W[0], a.eps);
-    else report(c, recv_vec<MAXE_H, true>(a.xb, H, tag - 1, c.xs0, W[0], a.eps, a.err, a.spin_sleep));
+    const f16* W[9];  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+#pragma unroll
+    for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
+    if (layer == 0) recv_embed<4 * MAXQ_H>(a.embed + static_cast<size_t>(c.token) * H, H, c.xs0, W[0], a.eps);
+    else report(c, recv_vec<MAXQ_H, true>(a.xb, H, (tag - 1u) & 3u, c.xs0, W[0], a.eps, a.err, a.spin_sleep));
     SOC_SYNC();                                    // P1 input
-    if (!block_recv<false>(c, a.attn, nullptr, a.qd, tag, c.xs1, nullptr, a.eps, 0)) return false;  // P3 input
-    report(c, recv_vec<MAXE_H, true>(a.xa, H, tag, c.xs0, W[1], a.eps, a.err, a.spin_sleep));
+    if (!block_recv(c, a.attn, a.qd, tag, c.xs1)) return false;  // P3 input
+    report(c, recv_vec<MAXQ_H, true>(a.xa, H, tag, c.xs0, W[1], a.eps, a.err, a.spin_sleep));
     SOC_SYNC();                                    // P4 input (receiver alone: its first sight of the data is earliest)
-    if (!block_recv<false>(c, a.h, nullptr, a.I, tag, c.xs1, nullptr, a.eps, 0)) return false;      // P5 input
+    if (!block_recv(c, a.h, a.I, tag, c.xs1)) return false;      // P5 input
   }
   return true;
 }
@@ -616,11 +546,13 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
   // residual stream value of this slot's H-row; layer 0 starts from the embedding row (embedding.cpp:51-77)
   const int hrow = h0 + slot_h;
   float xres = hrow < h1 ? static_cast<float>(a.embed[static_cast<size_t>(c.token) * H + hrow]) : 0.0f;
-  slice_load(sq, a.layer_w[4], H, q0, q1);
+  slice_load(sq, ld_global(a.layer_w, 4), H, q0, q1);
   SOC_TRACE(0);
   for (int layer = 0; layer < a.L; ++layer) {
-    const f16* const* W = a.layer_w + layer * 9;  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
-    const uint32_t tag = c.step * 64u + static_cast<uint32_t>(layer) + 1u;
+    const f16* W[9];  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+#pragma unroll
+    for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);  // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     // ---- P1: RMSNorm + QKV projection ----
     SOC_SYNC();
     SOC_TRACE(1 + 8 * layer);
@@ -635,11 +567,11 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     slice_load(sg, W[6], H, i0, i1);
     slice_load(su, W[7], H, i0, i1);
     slice_load(sd, W[8], I, h0, h1);
-    if (layer + 1 < a.L) slice_load(sq, a.layer_w[(layer + 1) * 9 + 4], H, q0, q1);
+    if (layer + 1 < a.L) slice_load(sq, ld_global(a.layer_w, static_cast<size_t>(layer + 1) * 9 + 4), H, q0, q1);
     if (a.trace != nullptr) __builtin_amdgcn_s_waitcnt(0);  // diagnostics: point 2 = the weight stream has landed
     SOC_TRACE(2 + 8 * layer);
     // ---- P3: o_proj + residual (the attention output is 2048 elements: every wave polls a share) ----
-    if (!block_recv<false>(c, a.attn, nullptr, qd, tag, c.xs1, nullptr, a.eps, 0)) return false;
+    if (!block_recv(c, a.attn, qd, tag, c.xs1)) return false;
     SOC_TRACE(3 + 8 * layer);
     {
       const float out = slice_dot(so, c.xs1, qd);
@@ -658,7 +590,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
     }
     SOC_TRACE(6 + 8 * layer);
     // ---- P5: down + residual ----
-    if (!block_recv<false>(c, a.h, nullptr, I, tag, c.xs1, nullptr, a.eps, 0)) return false;
+    if (!block_recv(c, a.h, I, tag, c.xs1)) return false;
     SOC_TRACE(7 + 8 * layer);
     {
       const float out = slice_dot(sd, c.xs1, I);
@@ -673,8 +605,8 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
 // ---------------- LM head: receiver wave gets the final hidden state ----------------
 __device__ __forceinline__ bool lm_receiver(const Ctx& c) {
   const PersistArgs& a = c.a;
-  const uint32_t last_tag = c.step * 64u + static_cast<uint32_t>(a.L);
-  report(c, recv_vec<MAXE_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err, a.spin_sleep));
+  const uint32_t last_tag = (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u;
+  report(c, recv_vec<MAXQ_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err, a.spin_sleep));
   SOC_SYNC();
   return true;
 }
@@ -731,7 +663,8 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
   float* red = lds + 2 * a.xs_cap;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
   const int ng = static_cast<int>(gridDim.x) - a.nkv;
-  Ctx c{a, static_cast<int>(blockIdx.x), ng, a.state[0], a.state[1], static_cast<uint32_t>(a.state[2]),
+  Ctx c{a, static_cast<int>(blockIdx.x), ng, a.state[0], a.state[1],
+        (static_cast<uint32_t>(a.state[2]) - 1u) * static_cast<uint32_t>(a.L),
         lds, lds + a.xs_cap, reinterpret_cast<int*>(red + 16), red + 32, reinterpret_cast<int*>(red + 48), red + 96};
   if (tid == 0) c.flag[0] = 0;
   __syncthreads();
@@ -802,7 +735,7 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
     const int tok = c.bi[0] == 0x7fffffff ? 0 : c.bi[0];
     a.state[0] = tok;
     a.state[1] = c.pos + 1;
-    a.state[2] = static_cast<int>(c.step + 1);
+    a.state[2] += 1;
     if (a.ring != nullptr) {
       a.ring[*a.ring_pos] = tok;
       *a.ring_pos += 1;
@@ -858,7 +791,7 @@ bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, i
   if (G != 1 && G != 2 && G != 4) return false;
   if (H > CPT_QKV * TPR_QKV * 8 || H > CPT_GU * TPR_GU * 8 || qd > CPT_O * TPR_O * 8 || I > CPT_D * TPR_D * 8)
     return false;
-  if (H > 64 * MAXE_H || qd > 6 * NT || I > 6 * NT || H > 6 * NT) return false;
+  if (H > 256 * MAXQ_H || qd > 8 * NT || I > 8 * NT) return false;
   if (H % 8 || qd % 8 || I % 8) return false;
   const int ng = nblocks - nkv;
   if (ng < 1) return false;

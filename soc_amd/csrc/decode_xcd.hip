@@ -1,0 +1,818 @@
+// decode_xcd.hip - one-launch decode step for batch 1 with every layer partitioned over the eight XCDs of MI355X.
+//
+// Block (g, j): XCD g, read from the XCC_ID hardware register, and rank j < 32 among the blocks of this launch that
+// arrived on it. XCD g owns KV head g (every Qwen3 model has 8 KV heads) with its G = nq / 8 query heads and 1/8 of
+// every matrix: the q/k/v rows of its heads, the o_proj columns of its query heads, the gate/up rows and down_proj
+// columns of its eighth of the intermediate dimension. Per layer (reference: QwenBlock::ForwardCached,
+// Mac/cpu/src/qwen_block.cpp:63-73, with QwenAttention::ForwardCached and QwenMLP::Forward):
+//   A  x = x' + sum_k D_k over the eight XCDs' partial down outputs (cross-XCD), RMSNorm(x)
+//   B  the block's q/k/v rows of the XCD's heads                               -> XCD-local exchange
+//   C  the XCD's q/k/v; per-head QK-RMSNorm + RoPE; rank 0 appends k and v to the cache
+//   D  causal attention over the block's 1/32 of the keys: per query head (max, sum, weighted values)
+//   E  the XCD's 32 partials (XCD-local), log-sum-exp merge
+//   F  O_g = Wo[the block's rows][the XCD's query columns] . attn              -> cross-XCD exchange
+//   G  x' = x + sum_k O_k (cross-XCD), RMSNorm(x')
+//   H  h = silu(gate) * up on the block's share of the XCD's intermediate slice -> XCD-local exchange
+//   I  the XCD's h slice (XCD-local)
+//   J  D_g = Wd[the block's rows][the slice's columns] . h                     -> cross-XCD exchange
+// So a layer has two cross-XCD hand-offs (device-scope stores; every block reads 8 x H words) and three XCD-local
+// ones (plain stores served by the XCD's own L2 at half the latency, see exchange.h). Every block keeps the whole
+// residual stream x / x' in LDS, computed in the same order from the same words, so all blocks hold identical bits.
+// Weight rows live in registers: after B a block issues the loads of the layer's o/gate/up/down rows and of the next
+// layer's q/k/v rows, which land while C..E run. Every wait is bounded; a timeout raises the error flag and the
+// grid drains.
+#include <algorithm>
+
+#include "exchange.h"
+#include "kernels.h"
+
+namespace soc {
+
+namespace {
+
+constexpr int NT = 512;   // threads per block
+constexpr int NC = 256;   // compute threads: waves 0..3; waves 4..7 are receivers
+constexpr int HD = 128;   // head dim
+constexpr int NX = kXcdGroups, NBX = kXcdBlocks;
+constexpr int HMAX = 1024;        // hidden size covered by the register tiling
+constexpr int IMAX = 3072;        // intermediate size covered: I / 256 <= 12 gate/up pairs per block
+constexpr int PW = HD + 4;        // words per (block, query head) attention partial: 128 values, max, sum, 2 pad
+constexpr float kNoKeys = -1e30f; // running max of a block that owns no key (finite: a tag bit must not make a NaN)
+
+// A block's rows of one weight matrix in registers: slot s = tid / TPR owns one row; thread t of the slot holds the
+// 8-half chunks at k = 8 (t + TPR c), c < CPT.
+template <int TPR, int CPT>
+struct Slice {
+  u32x4 w[CPT];
+};
+
+template <int TPR, int CPT>
+__device__ __forceinline__ void slice_load(Slice<TPR, CPT>& s, const f16* row, int K) {
+  const int t = threadIdx.x % TPR;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int k = (t + TPR * c) * 8;
+    s.w[c] = (row != nullptr && k < K) ? load_stream16(row + k) : u32x4{0, 0, 0, 0};
+  }
+}
+
+// Row sum of the slot's row with xs[0..K); every thread of the slot gets it.
+template <int TPR, int CPT>
+__device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float* xs, int K) {
+  static_assert(TPR <= 64, "a slot must not span waves");
+  const int t = threadIdx.x % TPR;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int k = (t + TPR * c) * 8;
+    if (k < K) {
+      float wf[8], xv[8];
+      f16x8_to_f32(s.w[c], wf);
+      *reinterpret_cast<f32x4*>(xv) = *reinterpret_cast<const f32x4*>(xs + k);
+      *reinterpret_cast<f32x4*>(xv + 4) = *reinterpret_cast<const f32x4*>(xs + k + 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += xv[i] * wf[i];
+    }
+  }
+  return group_sum<TPR>(acc);
+}
+
+// Word of element e of XCD k's partial in a cross-XCD vector [8][H]: block j of XCD k writes its H / 32 rows as whole
+// aligned lines (32-byte pieces per wave), so no line is written piecewise by several XCDs.
+__device__ __forceinline__ int cross_idx(int e, int k, int H) { return k * H + e; }
+
+// Register tiling of the 256 compute threads (waves 0..3). Rows per block: q/k/v (G + 2) * 4, o/down H / 32, gate/up
+// pairs I / 256. The LM head runs on all 512 threads.
+template <int G>
+struct Tiling {
+  static constexpr int RQ = (G + 2) * 4;
+  static constexpr int TPR_Q = 16, CPT_Q = HMAX / (TPR_Q * 8);     // 16 slots, K = H
+  static constexpr int TPR_O = 8, CPT_O = G * HD / (TPR_O * 8);    // 32 slots, K = G * 128 columns of o_proj
+  static constexpr int TPR_GU = 16, CPT_GU = HMAX / (TPR_GU * 8);  // 16 slots, K = H
+  static constexpr int TPR_D = 8, CPT_D = IMAX / 8 / (TPR_D * 8);  // 32 slots, K = I / 8 columns of down_proj
+  static constexpr int TPR_LM = 32, CPT_LM = HMAX / (TPR_LM * 8);  // 16 rows per fragment
+  static constexpr int NA_MAX = 32;                                // attention blocks per XCD at most
+  static constexpr int MQ_E = (NA_MAX * PW / 4 + 63) / 64;         // one head's partial quads per receiver lane
+  static_assert(RQ <= NC / TPR_Q && HMAX / NBX <= NC / TPR_O && IMAX / (NX * NBX) <= NC / TPR_GU, "slots");
+  static_assert(TPR_D == TPR_O, "o_proj and down_proj rows share the slot mapping");
+};
+
+// LDS carve-up (floats).
+template <int G>
+struct Lds {
+  static constexpr int XRES = 0;                   // [HMAX] residual stream x / x' (receivers)
+  static constexpr int XN = XRES + HMAX;           // [HMAX] x * gain of the next RMSNorm (the scale is applied later)
+  static constexpr int RED = XN + HMAX;            // [8] the waves' partial sums of x^2
+  static constexpr int HS = RED + 8;               // [IMAX / 8] the XCD's h slice
+  static constexpr int ATT = HS + IMAX / 8;        // [G][HD] merged attention output
+  static constexpr int QS = ATT + G * HD;          // [G][HD] normed, rotated queries
+  static constexpr int KN = QS + G * HD;           // [HD] new key (fp16-rounded)
+  static constexpr int VN = KN + HD;               // [HD] new value (fp16-rounded)
+  static constexpr int RAW = VN + HD;              // [(G + 2) HD] the XCD's raw q/k/v (receivers)
+  static constexpr int WPART = RAW + (G + 2) * HD; // [16][G][PW] the receiver groups' attention partials
+  static constexpr int BPART = WPART + 16 * G * PW; // [G][NA_MAX PW] words: the XCD's block partials per head
+  static constexpr int FLAG = BPART + G * Tiling<G>::NA_MAX * PW;  // [8] ints: status, g, j, last block, D counter
+  static constexpr int BV = FLAG + 8;              // [16] argmax values per slot
+  static constexpr int BI = BV + 16;               // [16] argmax indices
+  static constexpr int TOTAL = BI + 16;
+};
+
+struct Ctx {
+  const PersistArgs& a;
+  int g, j, token, pos;
+  uint32_t phase0;  // (step - 1) * L: the tag of layer l is (phase0 + l) & 3
+  float* lds;
+  int* flag;
+};
+
+// Attention blocks of the XCD for S keys (about 16 keys each, one per 16-lane group of the receiver waves, at most
+// 32 blocks) and keys per block; na is recomputed from the chunk so that every block j < na owns at least one key.
+__device__ __forceinline__ void attn_split(int S, int& na, int& chunk) {
+  na = min(NBX, (S + 15) / 16);
+  chunk = (S + na - 1) / na;
+  na = (S + chunk - 1) / chunk;
+}
+
+// RMSNorm scale 1 / sqrt(sum x^2 / n + eps) from the eight waves' partial sums, added in a fixed order.
+__device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
+  const float s = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+  return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
+}
+
+// Optional phase timestamps (diagnostics): the middle layer's 11 phase points of every block go to
+// trace[block * 16 + point] (receiver points from wave 4, compute points from wave 0); block (0, 0) also writes each
+// layer's start, the final norm and the step's end into trace[256 * 16 + i].
+#define XTRACE(pt)                                                                                           \
+  do {                                                                                                       \
+    if (c.a.trace != nullptr && (threadIdx.x == 0 || threadIdx.x == NC) && layer == c.a.L / 2)               \
+      c.a.trace[(c.g * NBX + c.j) * 16 + (pt)] = now_ticks();                                                \
+  } while (0)
+#define XTRACE0(i, t)                                                                                        \
+  do {                                                                                                       \
+    if (c.a.trace != nullptr && threadIdx.x == (t) && c.g == 0 && c.j == 0)                                  \
+      c.a.trace[NX * NBX * 16 + (i)] = now_ticks();                                                          \
+  } while (0)
+
+// Block barrier; afterwards every thread leaves if a receiver reported a failed wait (flag[0] != 0).
+#define XSYNC()                       \
+  do {                                \
+    __syncthreads();                  \
+    if (c.flag[0] != 0) return false; \
+  } while (0)
+
+// Receiver wave: polls MQ quads per lane (byte offsets off[e] into r, or -1 for none) of a tagged vector until every
+// one carries `tag`. Returns false (wave-uniform) on timeout or a raised error flag, after recording it in flag[0].
+template <int MQ>
+__device__ __forceinline__ bool poll_quads(const Ctx& c, __amdgpu_buffer_rsrc_t r, const int (&off)[MQ], uint32_t tag,
+                                           u32x4 (&v)[MQ]) {
+  const u32x4 filler = {tag, tag, tag, tag};
+#pragma unroll
+  for (int e = 0; e < MQ; ++e) v[e] = off[e] >= 0 ? ll_peek_buf4(r, off[e]) : filler;
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
+  while (true) {
+    bool all = true;
+#pragma unroll
+    for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
+    if (__all(all)) return true;
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+      __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error (2)
+      c.flag[0] = 1;
+      return false;
+    }
+#pragma unroll
+    for (int e = 0; e < MQ; ++e)
+      if (off[e] >= 0 && !tw_quad_ok(v[e], tag)) v[e] = ll_peek_buf4(r, off[e]);
+  }
+}
+
+// Sum over aligned groups of 8 lanes that is bit-identical in every lane of the group: each step adds two values
+// that are equal in both partner lanes up to the order of one addition, and IEEE addition commutes exactly.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_mov<0xB1>(v);   // lane ^ 1
+  v += dpp_mov<0x4E>(v);   // lane ^ 2
+  v += dpp_mov<0x141>(v);  // lane ^ 7 within 8: the other (now uniform) quad
+  return v;
+}
+
+// Wave w < 8 of the block (all eight take part; the cross-XCD vectors are polled when no wave has weight loads in
+// flight): its eighth of x = x + sum_k partial_k over the eight XCDs (layer 0: x = the embedding row), then x * gain
+// into xn and its partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is completed by
+// rms_scale). The wave owns the element quads w * H / 32 .. + H / 32; its load i brings 8 of them from all eight
+// partials (lane l: quad i * 8 + l / 8 of partial l % 8) and the 8 lanes of a quad add their partials with sum8.
+__device__ __forceinline__ bool recv_cross(const Ctx& c, int rw, const uint32_t* src, uint32_t tag,
+                                           const f16* embed_row, const f16* gain, float* xres, float* xn, float* red) {
+  constexpr int NI = HMAX / 256;
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
+  const int k = lane & 7;
+  const int H = c.a.H, ni = H / 256, line0 = rw * (H / 32);
+  float ss = 0.0f;
+  if (embed_row != nullptr) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = line0 + i * 8 + (lane >> 3);
+      if (i < ni && k == 0) {
+        const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
+        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+        f32x4 x, y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = static_cast<float>(e4[e]);
+          y[e] = x[e] * static_cast<float>(g4[e]);
+          ss += x[e] * x[e];
+        }
+        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+      }
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
+    int off[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) off[i] = i < ni ? k * H * 4 + (line0 + i * 8 + (lane >> 3)) * 16 : -1;
+    u32x4 v[NI];
+    if (!poll_quads<NI>(c, r, off, tag, v)) return false;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = line0 + i * 8 + (lane >> 3);
+      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
+      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
+      if (i < ni && k == 0) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(xres + 4 * q);
+        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+        x[0] += s0;
+        x[1] += s1;
+        x[2] += s2;
+        x[3] += s3;
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[e] = x[e] * static_cast<float>(g4[e]);
+          ss += x[e] * x[e];
+        }
+        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[rw] = ss;
+  return true;
+}
+
+// Receiver wave: the quads qi = lane + 64 e < nq of the XCD-local tagged words src[0 .. 4 nq) into dst[4 qi ..] (raw
+// words: the tags are kept). Load e of a lane is at byte 16 lane + 1024 e: one register offset for all loads.
+template <int MQ>
+__device__ __forceinline__ bool recv_contig(const Ctx& c, const uint32_t* src, int nq, uint32_t tag, uint32_t* dst) {
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, nq * 16, 0x00020000);
+  const u32x4 filler = {tag, tag, tag, tag};
+  u32x4 v[MQ];
+#pragma unroll
+  for (int e = 0; e < MQ; ++e)
+    v[e] = lane + 64 * e < nq ? __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, e * 1024, 16) : filler;
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
+  while (true) {
+    bool all = true;
+#pragma unroll
+    for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
+    if (__all(all)) break;
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+      __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error (2)
+      c.flag[0] = 1;
+      return false;
+    }
+#pragma unroll
+    for (int e = 0; e < MQ; ++e)
+      if (lane + 64 * e < nq && !tw_quad_ok(v[e], tag))
+        v[e] = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, e * 1024, 16);
+  }
+#pragma unroll
+  for (int e = 0; e < MQ; ++e)
+    if (lane + 64 * e < nq) *reinterpret_cast<u32x4*>(dst + 4 * (lane + 64 * e)) = v[e];
+  return true;
+}
+
+// Receiver waves (4..7): every poll, the RMSNorm inputs, QK-norm/RoPE and attention merge of the layers, then the
+// final hidden state. They issue no weight loads, so their polls never queue behind the weight stream; no receiver
+// needs another receiver's data.
+template <int G>
+__device__ __forceinline__ bool recv_layers(const Ctx& c) {
+  using LD = Lds<G>;
+  const PersistArgs& a = c.a;
+  const int rw = (threadIdx.x >> 6) - NC / 64;
+  const int g = c.g, j = c.j, pos = c.pos, S = pos + 1;
+  const int H = a.H, IS = a.I / NX;
+  float* lds = c.lds;
+  float* xres = lds + LD::XRES;
+  float* xn = lds + LD::XN;
+  float* red = lds + LD::RED;
+  float* hs = lds + LD::HS;
+  float* att = lds + LD::ATT;
+  float* qs = lds + LD::QS;
+  float* kn = lds + LD::KN;
+  float* vn = lds + LD::VN;
+  uint32_t* raw = reinterpret_cast<uint32_t*>(lds + LD::RAW);
+  uint32_t* bpart = reinterpret_cast<uint32_t*>(lds + LD::BPART) + rw * (Tiling<G>::NA_MAX * PW);
+  const uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
+  const uint32_t* loc_qkv = loc;
+  const uint32_t* loc_att = loc + (((G + 2) * HD + 63) & ~63);
+  const uint32_t* loc_h = loc_att + ((NBX * G * PW + 63) & ~63);
+  int na, chunk;
+  attn_split(S, na, chunk);
+  // attention: block j < na takes keys [k0, k1); group grp (16 lanes, 8 dims each) takes keys k0 + grp + 16 u
+  const int k0 = j < na ? min(S, j * chunk) : S, k1 = j < na ? min(S, k0 + chunk) : S;
+  int lane = threadIdx.x & 63, grp = (threadIdx.x - NC) >> 4, sub = threadIdx.x & 15;
+  constexpr int NG = (NT - NC) / 16;
+  float* wpart = lds + LD::WPART;
+  uint32_t* loc_att_w = a.loc + static_cast<size_t>(g) * a.loc_stride + (((G + 2) * HD + 63) & ~63);
+  u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
+  auto kv_fetch = [&](int layer, int p) {  // cached key/value p (< pos) of this layer, 8 dims per lane
+    if (p < k1 && p < pos) {
+      const size_t base = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD +
+                          static_cast<size_t>(p) * HD + sub * 8;
+      kr = load16(a.kcache + base);
+      vr = load16(a.vcache + base);
+    }
+  };
+  const float* rc = a.rope_cos + static_cast<size_t>(pos) * (HD / 2);
+  const float* rs = a.rope_sin + static_cast<size_t>(pos) * (HD / 2);
+  for (int layer = 0; layer < a.L; ++layer) {
+    const f16* W[4];  // in_norm, post_norm, q_norm, k_norm
+#pragma unroll
+    for (int i = 0; i < 4; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
+    // per layer: keeps the compiler from hoisting per-lane addresses out of the loop (register pressure)
+    __asm__ volatile("" : "+v"(lane), "+v"(grp), "+v"(sub));
+    // this layer's first cached key/value of the group, issued before A's poll: the previous layer's outputs take
+    // longer to arrive than these loads, so the poll (which returns after them) loses nothing
+    kv_fetch(layer, k0 + grp);
+    XTRACE0(layer, NC);
+    XTRACE(0);
+    // ---- A: x (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
+    recv_cross(c, NC / 64 + rw, a.xd, (tag - 1u) & 3u,
+               layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0], xres, xn, red);
+    XTRACE(1);
+    XSYNC();  // #1
+    // ---- C: head rw of the XCD's q/k/v; QK-RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171, rope.cpp:81-84)
+    if (rw < G + 2) {
+      const int hh = rw;
+      if (recv_contig<1>(c, loc_qkv + hh * HD, HD / 4, tag, raw + hh * HD)) {
+        float x0 = tw_val(raw[hh * HD + lane]), x1 = tw_val(raw[hh * HD + lane + 64]);
+        if (hh <= G) norm_rope_pair(x0, x1, hh < G ? W[2] : W[3], a.eps, rc, rs, lane);
+        if (hh < G) {
+          qs[hh * HD + lane] = x0;
+          qs[hh * HD + lane + 64] = x1;
+        } else {
+          // key and value rounded to the cache's fp16 before use; rank 0 appends them at `pos`
+          const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
+          float* dst = hh == G ? kn : vn;
+          dst[lane] = static_cast<float>(h0);
+          dst[lane + 64] = static_cast<float>(h1);
+          if (j == 0) {
+            f16* cache = (hh == G ? a.kcache : a.vcache) + static_cast<size_t>(layer) * a.layer_stride +
+                         static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(pos) * HD;
+            cache[lane] = h0;
+            cache[lane + 64] = h1;
+          }
+        }
+      }
+    }
+    XTRACE(3);
+    XSYNC();  // #2: qs, kn, vn
+    // ---- D: attention over keys [k0, k1) (online softmax of grouped_query_attention.cpp:105-136) ----
+    if (j < na) {
+      float qreg[G][8], o[G][8], mrun[G], lrun[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        mrun[h] = kNoKeys;
+        lrun[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          qreg[h][i] = qs[h * HD + sub * 8 + i];
+          o[h][i] = 0.0f;
+        }
+      }
+      for (int p = k0 + grp; p < k1; p += NG) {
+        float kf[8], vf[8];
+        if (p == pos) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            kf[i] = kn[sub * 8 + i];
+            vf[i] = vn[sub * 8 + i];
+          }
+        } else {
+          f16x8_to_f32(kr, kf);
+          f16x8_to_f32(vr, vf);
+        }
+        kv_fetch(layer, p + NG);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          float d = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
+          const float sc = group_sum<16>(d) * a.scale;
+          const float mn = fmaxf(mrun[h], sc);
+          const float corr = expf(mrun[h] - mn);
+          const float pw = expf(sc - mn);
+          lrun[h] = lrun[h] * corr + pw;
+          mrun[h] = mn;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[h][i] = o[h][i] * corr + pw * vf[i];
+        }
+      }
+      // the group's partial (its keys' max, sum and weighted values per head) to LDS
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wpart[(grp * G + h) * PW + sub * 8 + i] = o[h][i];
+        if (sub == 0) {
+          wpart[(grp * G + h) * PW + HD] = mrun[h];
+          wpart[(grp * G + h) * PW + HD + 1] = lrun[h];
+        }
+      }
+    }
+    XSYNC();  // #2b: the block's 16 group partials
+    if (j < na) {
+      // receiver thread t merges output t (head t / 128, dim t % 128) over the 16 groups and publishes it, relative
+      // to the max as the exchange word will carry it (a group without keys adds nothing)
+      const int rt = threadIdx.x - NC;
+      for (int t = rt; t < G * HD; t += NT - NC) {
+        const int h = t / HD, d = t % HD;
+        float mg[16];
+        float M = kNoKeys;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          mg[q] = wpart[(q * G + h) * PW + HD];
+          M = fmaxf(M, mg[q]);
+        }
+        if (M != kNoKeys) M = tw_val(tw_pack(M, 0u));
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const float e = mg[q] == kNoKeys ? 0.0f : expf(mg[q] - M);
+          L += wpart[(q * G + h) * PW + HD + 1] * e;
+          O += wpart[(q * G + h) * PW + d] * e;
+        }
+        const int w0 = (h * NBX + j) * PW;  // [head][block][PW]
+        ll_store_local(loc_att_w, w0 + d, O, tag);
+        if (d < 4) ll_store_local(loc_att_w, w0 + HD + d, d == 0 ? M : (d == 1 ? L : 0.0f), tag);
+      }
+      if (c.a.trace != nullptr && rt == 0 && layer == c.a.L / 2) c.a.trace[(g * NBX + j) * 16 + 12] = now_ticks();
+    }
+    XTRACE(4);
+    // ---- E: head rw's partials of the XCD's attention blocks, merged in a fixed order ----
+    if (rw < G) {
+      const int h = rw;
+      // head h's partials of blocks 0..na-1 are contiguous: [h][block][PW]
+      if (recv_contig<Tiling<G>::MQ_E>(c, loc_att + h * NBX * PW, na * (PW / 4), tag, bpart)) {
+        if (c.a.trace != nullptr && lane == 0 && h == 0 && layer == c.a.L / 2)
+          c.a.trace[(g * NBX + j) * 16 + 11] = now_ticks();
+        // lane r < na holds block r's max and sum; the weights e_r are broadcast with readlane
+        const float mr = lane < na ? tw_val(bpart[lane * PW + HD]) : kNoKeys;
+        const float lr = lane < na ? tw_val(bpart[lane * PW + HD + 1]) : 0.0f;
+        const float M = wave_max(mr);
+        const float er = mr < 0.5f * kNoKeys ? 0.0f : expf(mr - M);  // a block without keys adds nothing
+        const float L = wave_sum(lr * er);
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          const int d = lane + 64 * dd;
+          float O = 0.0f;
+#pragma unroll
+          for (int r = 0; r < NBX; ++r)
+            if (r < na) O += tw_val(bpart[r * PW + d]) * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er), r));
+          att[h * HD + d] = O / L;
+        }
+      }
+    }
+    XTRACE(5);
+    XSYNC();  // #3
+    // ---- G: x' = x + sum_k O_k, RMSNorm input ----
+    recv_cross(c, NC / 64 + rw, a.xo, tag, nullptr, W[1], xres, xn, red);
+    XTRACE(7);
+    XSYNC();  // #4
+    // ---- I: the XCD's h slice ----
+    if (rw * 64 < IS / 4 &&
+        recv_contig<1>(c, loc_h + rw * 256, min(64, IS / 4 - rw * 64), tag, reinterpret_cast<uint32_t*>(hs) + rw * 256)) {
+      // the words this lane brought, as floats
+      const int q = rw * 64 + lane;
+      if (q < IS / 4) {
+        uint32_t* w4 = reinterpret_cast<uint32_t*>(hs) + 4 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hs[4 * q + e] = tw_val(w4[e]);
+      }
+    }
+    XTRACE(9);
+    XSYNC();  // #5
+  }
+  // final hidden state x = x' + sum_k D_k, RMSNorm input with the final gain
+  recv_cross(c, NC / 64 + rw, a.xd, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xn,
+             red);
+  XTRACE0(a.L, NC);
+  XSYNC();  // #F
+  return true;
+}
+
+// Compute waves (0..3): the block's weight rows in registers and the projections.
+template <int G>
+__device__ __forceinline__ bool comp_layers(const Ctx& c) {
+  using T = Tiling<G>;
+  using LD = Lds<G>;
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x;
+  const int g = c.g, j = c.j;
+  const int H = a.H, I = a.I, qd = a.qd;
+  const int RH = H / NBX;          // o/down rows per block
+  const int IS = I / NX;           // intermediate slice of the XCD
+  const int RI = IS / NBX;         // gate/up pairs per block
+  float* lds = c.lds;
+  const float* xn = lds + LD::XN;
+  const float* red = lds + LD::RED;
+  const float* hs = lds + LD::HS;
+  const float* att = lds + LD::ATT;
+  float* xres = lds + LD::XRES;
+  float* xnw = lds + LD::XN;
+  float* redw = lds + LD::RED;
+  const int wid = tid >> 6;
+  uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
+  uint32_t* loc_qkv = loc;
+  uint32_t* loc_h = loc + (((G + 2) * HD + 63) & ~63) + ((NBX * G * PW + 63) & ~63);
+  // this block's q/k/v row: local row lr of the XCD's (G + 2) * 128 (q heads, key, value)
+  const int q_slot = tid / T::TPR_Q;
+  const int q_lr = j * T::RQ + q_slot;
+  const bool q_live = q_slot < T::RQ;
+  const int q_row = q_lr < G * HD ? g * G * HD + q_lr
+                                  : (q_lr < (G + 1) * HD ? qd + g * HD + (q_lr - G * HD)
+                                                         : qd + a.nkv * HD + g * HD + (q_lr - (G + 1) * HD));
+  const int o_slot = tid / T::TPR_O, gu_slot = tid / T::TPR_GU;
+  const int hrow = j * RH + o_slot;           // o/down output row
+  const bool h_live = o_slot < RH;
+  const int iidx = g * IS + j * RI + gu_slot; // gate/up row
+  const bool i_live = gu_slot < RI;
+
+  Slice<T::TPR_Q, T::CPT_Q> sq;
+  Slice<T::TPR_O, T::CPT_O> so;
+  Slice<T::TPR_GU, T::CPT_GU> sg, su;
+  Slice<T::TPR_D, T::CPT_D> sd;
+  slice_load(sq, q_live ? ld_global(a.layer_w, 4) + static_cast<size_t>(q_row) * H : nullptr, H);
+
+  for (int layer = 0; layer < a.L; ++layer) {
+    // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
+    const f16* W[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
+    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
+    // ---- A (this wave's eighth) ----
+    recv_cross(c, wid, a.xd, (tag - 1u) & 3u, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0],
+               xres, xnw, redw);
+    XSYNC();  // #1: xn = x * gain, red = partial sums of x^2
+    // ---- B: q/k/v rows of RMSNorm(x) ----
+    {
+      const float out = slice_dot(sq, xn, H) * rms_scale(red, H, a.eps);
+      if (q_live && tid % T::TPR_Q == 0) ll_store_local(loc_qkv, q_lr, out, tag);
+    }
+    XTRACE(2);
+    // the layer's other rows in the order the phases use them, then the next layer's q/k/v rows
+    auto issue_weights = [&]() {
+      slice_load(so, h_live ? W[5] + static_cast<size_t>(hrow) * qd + g * G * HD : nullptr, G * HD);
+      slice_load(sg, i_live ? W[6] + static_cast<size_t>(iidx) * H : nullptr, H);
+      slice_load(su, i_live ? W[7] + static_cast<size_t>(iidx) * H : nullptr, H);
+      slice_load(sd, h_live ? W[8] + static_cast<size_t>(hrow) * I + g * IS : nullptr, IS);
+      if (layer + 1 < a.L)
+        slice_load(sq,
+                   q_live ? ld_global(a.layer_w, static_cast<size_t>(layer + 1) * 9 + 4) + static_cast<size_t>(q_row) * H
+                          : nullptr,
+                   H);
+    };
+    if (a.weights_sync != 2) issue_weights();
+    if (a.weights_sync == 1) wait_mem();
+    XSYNC();  // #2
+    if (a.weights_sync == 2) issue_weights();
+    XSYNC();  // #2b
+    XSYNC();  // #3: merged attention output
+    // ---- F: partial o_proj over the XCD's query columns ----
+    {
+      const float out = slice_dot(so, att, G * HD);
+      if (h_live && tid % T::TPR_O == 0) ll_store(a.xo + cross_idx(hrow, g, H), out, tag);
+    }
+    XTRACE(6);
+    // ---- G (this wave's eighth) ----
+    recv_cross(c, wid, a.xo, tag, nullptr, W[1], xres, xnw, redw);
+    XSYNC();  // #4: xn = x' * gain, red
+    // ---- H: gate/up of RMSNorm(x') + SwiGLU (qwen_mlp.cpp:31) on the block's share of the XCD's slice ----
+    {
+      const float scale = rms_scale(red, H, a.eps);
+      const float og = slice_dot(sg, xn, H) * scale;
+      const float ou = slice_dot(su, xn, H) * scale;
+      if (i_live && tid % T::TPR_GU == 0) ll_store_local(loc_h, j * RI + gu_slot, silu_ref(og) * ou, tag);
+    }
+    XTRACE(8);
+    XSYNC();  // #5: the XCD's h slice
+    // ---- J: partial down_proj over the slice's columns ----
+    {
+      const float out = slice_dot(sd, hs, IS);
+      if (h_live && tid % T::TPR_D == 0) ll_store(a.xd + cross_idx(hrow, g, H), out, tag);
+    }
+    XTRACE(10);
+  }
+  recv_cross(c, wid, a.xd, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xnw, redw);
+  XSYNC();  // #F: xn = x * final gain, red
+  return true;
+}
+
+// LM head rows of block b = 32 g + j on all 512 threads, best (value, index) per 32-lane slot into bv/bi. The logits
+// are RMSNorm(x) . W = (x * gain) . W * scale.
+template <int G>
+__device__ __forceinline__ void lm_head(const Ctx& c) {
+  using T = Tiling<G>;
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x, slot = tid / T::TPR_LM;
+  const bool lead = (tid % T::TPR_LM) == 0;
+  const float* xn = c.lds + Lds<G>::XN;
+  const float scale = rms_scale(c.lds + Lds<G>::RED, a.H, a.eps);
+  const int b = c.g * NBX + c.j;
+  const int rv = (a.V + NX * NBX - 1) / (NX * NBX);
+  const int v0 = b * rv, v1 = min(a.V, v0 + rv);
+  constexpr int STEP = NT / T::TPR_LM;
+  Slice<T::TPR_LM, T::CPT_LM> f0, f1;
+  auto rowp = [&](int r) { return r < v1 ? a.lm_head + static_cast<size_t>(r) * a.H : nullptr; };
+  slice_load(f0, rowp(v0 + slot), a.H);
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  auto consume = [&](const Slice<T::TPR_LM, T::CPT_LM>& f, int r0) {
+    const float out = slice_dot(f, xn, a.H) * scale;
+    const int row = r0 + slot;
+    if (row < v1) {
+      if (lead && a.logits != nullptr) a.logits[row] = out;
+      if (out > best) {  // a slot's rows ascend: strict > keeps the lowest index
+        best = out;
+        best_i = row;
+      }
+    }
+  };
+  for (int r0 = v0; r0 < v1; r0 += 2 * STEP) {
+    slice_load(f1, rowp(r0 + STEP + slot), a.H);
+    consume(f0, r0);
+    slice_load(f0, rowp(r0 + 2 * STEP + slot), a.H);
+    consume(f1, r0 + STEP);
+  }
+  float* bv = c.lds + Lds<G>::BV;
+  int* bi = reinterpret_cast<int*>(c.lds + Lds<G>::BI);
+  if (lead) {
+    bv[slot] = best;
+    bi[slot] = best_i;
+  }
+}
+
+}  // namespace
+
+template <int G>
+__global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
+  extern __shared__ float lds[];
+  using LD = Lds<G>;
+  int* flag = reinterpret_cast<int*>(lds + LD::FLAG);
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const uint32_t step = static_cast<uint32_t>(a.state[2]);
+  if (tid == 0) {
+    const int xcc = static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
+    const int rank = xcc < NX ? atomicAdd(a.xcd_ctr + (step & 1u) * NX + xcc, 1) : NBX;
+    flag[0] = 0;
+    flag[1] = xcc;
+    flag[2] = rank;
+  }
+  __syncthreads();
+  const int g = flag[1], j = flag[2];
+  if (j >= NBX) {  // not the expected 32 blocks per XCD: fail the step (every other block's wait then times out)
+    if (tid == 0) __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  Ctx c{a, g, j, a.state[0], a.state[1], (step - 1u) * static_cast<uint32_t>(a.L), lds, flag};
+  if (wid >= NC / 64) {
+    if (!recv_layers<G>(c)) return;
+  } else {
+    if (!comp_layers<G>(c)) return;
+  }
+  lm_head<G>(c);
+  XTRACE0(a.L + 1, 0);
+
+  // ---- greedy argmax over the blocks' candidates (sampler.cpp:26-61 with top_k = 1) ----
+  float* bv = lds + LD::BV;
+  int* bi = reinterpret_cast<int*>(lds + LD::BI);
+  const int b = g * NBX + j, nb = NX * NBX;
+  __syncthreads();
+  if (tid == 0) {
+    float v = bv[0];
+    int i = bi[0];
+    for (int w = 1; w < NT / Tiling<G>::TPR_LM; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < i)) {
+        v = bv[w];
+        i = bi[w];
+      }
+    st_dev(a.part_val + b, v);
+    st_dev(a.part_idx + b, i);
+    wait_mem();  // the block's candidate is visible device-wide before it is counted
+    const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag[3] = (done == nb - 1);
+  }
+  __syncthreads();
+  if (flag[3] == 0) return;
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int q = tid; q < nb; q += NT) {
+    const float pv = ld_dev(a.part_val + q);
+    const int pi = ld_dev(a.part_idx + q);
+    if (pv > v || (pv == v && pi < i)) {
+      v = pv;
+      i = pi;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(i, off, kWave);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    bv[wid] = v;
+    bi[wid] = i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < NT / 64; ++w)
+      if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
+        bv[0] = bv[w];
+        bi[0] = bi[w];
+      }
+    const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
+    a.state[0] = tok;
+    a.state[1] = c.pos + 1;
+    a.state[2] = static_cast<int>(step + 1u);
+    if (a.ring != nullptr) {
+      a.ring[*a.ring_pos] = tok;
+      *a.ring_pos += 1;
+    }
+    for (int k = 0; k < NX; ++k) a.xcd_ctr[((step + 1u) & 1u) * NX + k] = 0;  // the next step's arrival counters
+    __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+#undef XSYNC
+#undef XTRACE
+#undef XTRACE0
+
+namespace {
+template <int G>
+hipError_t launch_g(const PersistArgs& a, hipStream_t s) {
+  // more than 80 KB of LDS per block: one block per CU, so 32 blocks land on each XCD
+  const size_t lds = std::max<size_t>(Lds<G>::TOTAL * sizeof(float), 96 * 1024);
+  static size_t attr_lds = 0;
+  if (attr_lds < lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_decode_xcd<G>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    attr_lds = lds;
+  }
+  hipLaunchKernelGGL(k_decode_xcd<G>, dim3(NX * NBX), dim3(NT), lds, s, a);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_decode_xcd(const PersistArgs& a, hipStream_t s) {
+  const int G = a.nq / a.nkv;
+  if (G == 1) return launch_g<1>(a, s);
+  if (G == 2) return launch_g<2>(a, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t xcd_blocks_per_cu(int G, int* blocks) {
+  *blocks = 0;
+  const size_t lds = 96 * 1024;
+  if (G == 1) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<1>, NT, lds);
+  if (G == 2) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<2>, NT, lds);
+  return hipErrorInvalidValue;
+}
+
+int xcd_loc_stride(int G, int I) {
+  return (((G + 2) * HD + 63) & ~63) + ((NBX * G * PW + 63) & ~63) + ((I / NX + 63) & ~63);
+}
+
+// Shapes the partition and the register tiling cover: 8 KV heads of 128 dims (one per XCD), G = 1 or 2 query heads
+// per KV head, hidden size a multiple of 256 up to 1024, intermediate size a multiple of 256 up to 3072, and a device
+// of 8 XCDs x 32 CUs.
+bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus) {
+  if (num_cus != NX * NBX || nkv != NX || head_dim != HD) return false;
+  const int G = nq / nkv;
+  if (nq % nkv != 0 || (G != 1 && G != 2)) return false;
+  if (H % 256 != 0 || H > HMAX) return false;  // each of a block's 8 waves reduces whole 8-line loads
+  if (I % (NX * NBX) != 0 || I > IMAX) return false;
+  return true;
+}
+
+}  // namespace soc

@@ -20,11 +20,21 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// 16-byte streaming load that does not keep the line in the caches (weights are read once per step).
-__device__ __forceinline__ u32x4 load_stream16(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// Global-memory view of a pointer. Pointers read from device memory (per-layer weight tables) are generic to the
+// compiler, which then emits FLAT loads; FLAT loads also count against lgkmcnt, so every later LDS wait of the wave
+// would wait for them too. These helpers are only used on global memory.
+typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+
+// 16-byte streaming load from global memory that does not keep the line in the caches (weights are read once per
+// step).
+__device__ __forceinline__ u32x4 load_stream16(const void* p) { return __builtin_nontemporal_load((gu32x4*)p); }
+__device__ __forceinline__ u32x4 load16(const void* p) { return *(gu32x4*)p; }
+
+// Element i of a table in global memory (weight-pointer tables, norm gains) through a global load.
+template <typename T>
+__device__ __forceinline__ T ld_global(const T* p, size_t i) {
+  return ((const __attribute__((address_space(1))) T*)p)[i];
 }
-__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
@@ -105,8 +115,8 @@ __device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const f16* 
                                                const float* sinr, int lane) {
   const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
   const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
-  const float y0 = x0 * scale * static_cast<float>(gain[lane]);
-  const float y1 = x1 * scale * static_cast<float>(gain[lane + 64]);
+  const float y0 = x0 * scale * static_cast<float>(ld_global(gain, lane));
+  const float y1 = x1 * scale * static_cast<float>(ld_global(gain, lane + 64));
   const float c = cosr[lane], s = sinr[lane];
   x0 = fmaf(y0, c, -(y1 * s));
   x1 = fmaf(y0, s, y1 * c);

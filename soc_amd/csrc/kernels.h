@@ -126,11 +126,11 @@ struct PersistArgs {
   int cap;
   int L, H, I, V, nq, nkv, qkv_rows, qd, xs_cap;
   float eps, scale;
-  uint64_t* xa;               // exchange vectors: {value, tag} per element
-  uint64_t* xb;
-  uint64_t* qkv;
-  uint64_t* attn;
-  uint64_t* h;
+  uint32_t* xa;               // exchange vectors: one tagged 32-bit word per element (value, 2-bit phase tag)
+  uint32_t* xb;
+  uint32_t* qkv;
+  uint32_t* attn;
+  uint32_t* h;
   float* logits;              // [V] or nullptr
   float* part_val;            // [nblocks]
   int* part_idx;              // [nblocks]
@@ -141,11 +141,26 @@ struct PersistArgs {
   int* err;                   // raised when a wait times out
   uint64_t* trace;            // nullable: phase timestamps (diagnostics)
   int spin_sleep;             // back-off between polling rounds, in units of s_sleep 1 (about 64 clocks)
+  // XCD-partitioned kernel only (k_decode_xcd):
+  uint32_t* xo;               // [H/4][8][4] tagged partial o_proj outputs of the eight XCD groups (cross-XCD)
+  uint32_t* xd;               // [H/4][8][4] tagged partial down_proj outputs (cross-XCD)
+  uint32_t* loc;              // [8][loc_stride] per-XCD hand-off regions (q/k/v, attention partials, h)
+  int loc_stride;             // words per region
+  int* xcd_ctr;               // [2][8] arrivals per XCD, by step parity (zero; the next step's pair is reset)
+  int weights_sync;           // k_decode_xcd weight-stream schedule: 0 = issued after B, 1 = and awaited there,
+                              //   2 = issued after the q/k/v hand-off
 };
 bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks);
 size_t persistent_lds_bytes(const PersistArgs& a, int G);
 hipError_t persistent_blocks_per_cu(int G, int* blocks);
 hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream_t s);
+
+// XCD-partitioned one-launch decode step: 256 blocks, 32 on each of the 8 XCDs, XCD g owns KV head g.
+constexpr int kXcdGroups = 8, kXcdBlocks = 32;
+bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus);
+int xcd_loc_stride(int G, int I);  // words per per-XCD hand-off region
+hipError_t xcd_blocks_per_cu(int G, int* blocks);
+hipError_t launch_decode_xcd(const PersistArgs& a, hipStream_t s);
 
 // ---- prefill helpers ----
 // x[t][:] = float(table[ids[t]][:]) for t < T (Mac/cpu/src/embedding.cpp:51-77).

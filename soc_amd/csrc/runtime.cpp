@@ -74,8 +74,12 @@ struct DecodeWs {
   int *lm_idx = nullptr, *lm_counter = nullptr, *attn_counters = nullptr, *state = nullptr, *ring = nullptr,
       *ring_pos = nullptr;
   int max_split = 0, ring_cap = 0;
-  // persistent decode kernel: exchange vectors ({value, tag} per element), argmax partials, error flag
-  uint64_t *xa = nullptr, *xb = nullptr, *qkv_x = nullptr, *attn_x = nullptr, *h_x = nullptr;
+  // persistent decode kernel: exchange vectors (tagged 32-bit word per element), argmax partials, error flag
+  uint32_t *xa = nullptr, *xb = nullptr, *qkv_x = nullptr, *attn_x = nullptr, *h_x = nullptr;
+  // XCD-partitioned decode kernel: cross-XCD partial vectors, per-XCD hand-off regions, arrival counters
+  uint32_t *xo = nullptr, *xd = nullptr, *loc = nullptr;
+  int loc_stride = 0;
+  int* xcd_ctr = nullptr;
   float* pv = nullptr;
   int *pi = nullptr, *err = nullptr;
   int nblocks = 0;
@@ -126,6 +130,7 @@ struct soc_model {
   PrefillWs pws;
   BatchWs bws;
   bool finalized = false;
+  bool xcd_off = false;  // the XCD-partitioned decode step failed its block placement once: not used again
 };
 
 struct soc_kv {
@@ -220,21 +225,32 @@ int ensure_decode_ws(soc_model* m, int cap) {
     return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.state, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.ring_pos, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
-  // persistent-kernel state: zeroed exchange vectors (tag 0 is never expected), step counter starts at 1
+  // persistent-kernel state: exchange vectors filled with 0xff bytes (tag 3; the first phase expects tag 0), step
+  // counter starts at 1
   w.nblocks = m->ctx->num_cus;
   SOC_TRY(dev_alloc_t(w.allocs, c.hidden_size, &w.xa));
   SOC_TRY(dev_alloc_t(w.allocs, c.hidden_size, &w.xb));
   SOC_TRY(dev_alloc_t(w.allocs, m->qkv_rows, &w.qkv_x));
   SOC_TRY(dev_alloc_t(w.allocs, m->qd, &w.attn_x));
   SOC_TRY(dev_alloc_t(w.allocs, c.intermediate_size, &w.h_x));
-  SOC_TRY(dev_alloc_t(w.allocs, w.nblocks, &w.pv));
-  SOC_TRY(dev_alloc_t(w.allocs, w.nblocks, &w.pi));
+  const int G = c.num_attention_heads / c.num_key_value_heads;
+  w.loc_stride = soc::xcd_loc_stride(G, c.intermediate_size);
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * c.hidden_size, &w.xo));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * c.hidden_size, &w.xd));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * w.loc_stride, &w.loc));
+  SOC_TRY(dev_alloc_t(w.allocs, 2 * soc::kXcdGroups, &w.xcd_ctr));
+  SOC_TRY(dev_alloc_t(w.allocs, std::max(w.nblocks, soc::kXcdGroups * soc::kXcdBlocks), &w.pv));
+  SOC_TRY(dev_alloc_t(w.allocs, std::max(w.nblocks, soc::kXcdGroups * soc::kXcdBlocks), &w.pi));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.err));
   for (auto pr : {std::make_pair((void*)w.xa, (size_t)c.hidden_size), std::make_pair((void*)w.xb, (size_t)c.hidden_size),
                   std::make_pair((void*)w.qkv_x, (size_t)m->qkv_rows), std::make_pair((void*)w.attn_x, (size_t)m->qd),
-                  std::make_pair((void*)w.h_x, (size_t)c.intermediate_size)})
-    if ((e = hipMemset(pr.first, 0, pr.second * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
+                  std::make_pair((void*)w.h_x, (size_t)c.intermediate_size),
+                  std::make_pair((void*)w.xo, (size_t)soc::kXcdGroups * c.hidden_size),
+                  std::make_pair((void*)w.xd, (size_t)soc::kXcdGroups * c.hidden_size),
+                  std::make_pair((void*)w.loc, (size_t)soc::kXcdGroups * w.loc_stride)})
+    if ((e = hipMemset(pr.first, 0xff, pr.second * sizeof(uint32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.err, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
+  if ((e = hipMemset(w.xcd_ctr, 0, 2 * soc::kXcdGroups * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
   const int32_t step1 = 1;
   if ((e = hipMemcpy(w.state + 2, &step1, 4, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy");
   w.ready = true;
@@ -434,11 +450,25 @@ int get_decode_graph(soc_model* m, soc_kv* kv, int slot, hipGraphExec_t* out) {
   return SOC_OK;
 }
 
-// The persistent one-launch decode step is used when the shapes fit its register tiling and every block can be
-// resident at once; SOC_DECODE=graph selects the per-op kernels replayed from a HIP graph instead.
+// Decode implementation for batch 1: the XCD-partitioned one-launch step when the model has one KV head per XCD and
+// fits its tiling (2), else the one-launch step with attention blocks (1), else the per-op kernels replayed from a
+// HIP graph (0). SOC_DECODE=xcd / persistent / graph restricts the choice (an unsupported choice falls back).
+bool use_xcd(soc_model* m) {
+  const char* mode = std::getenv("SOC_DECODE");
+  if (mode != nullptr && std::strcmp(mode, "xcd") != 0) return false;
+  if (env_flag("SOC_EAGER") || m->xcd_off) return false;
+  const soc_qwen_config& c = m->cfg;
+  if (!soc::xcd_supported(c.hidden_size, c.intermediate_size, c.num_attention_heads, c.num_key_value_heads,
+                          c.head_dim, m->ctx->num_cus))
+    return false;
+  int per_cu = 0;
+  if (soc::xcd_blocks_per_cu(c.num_attention_heads / c.num_key_value_heads, &per_cu) != hipSuccess) return false;
+  return per_cu >= 1;
+}
+
 bool use_persistent(soc_model* m) {
   const char* mode = std::getenv("SOC_DECODE");
-  if (mode != nullptr && std::strcmp(mode, "persistent") != 0) return false;
+  if (mode != nullptr && std::strcmp(mode, "persistent") != 0 && std::strcmp(mode, "xcd") != 0) return false;
   if (env_flag("SOC_EAGER")) return false;
   const soc_qwen_config& c = m->cfg;
   const int nb = m->ctx->num_cus;
@@ -488,6 +518,12 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
   p.ring = w.ring;
   p.ring_pos = w.ring_pos;
   p.err = w.err;
+  p.xo = w.xo;
+  p.xd = w.xd;
+  p.loc = w.loc;
+  p.loc_stride = w.loc_stride;
+  p.xcd_ctr = w.xcd_ctr;
+  if (const char* ws = std::getenv("SOC_XCD_WEIGHTS")) p.weights_sync = std::atoi(ws);
   if (const char* sl = std::getenv("SOC_SPIN_SLEEP")) p.spin_sleep = std::max(0, std::atoi(sl));
   return p;
 }
@@ -501,18 +537,21 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
   const int32_t zero = 0;
   if ((e = hipMemcpyAsync(w.ring_pos, &zero, sizeof(zero), hipMemcpyHostToDevice, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync ring");
-  if (use_persistent(m)) {
+  const bool xcd = use_xcd(m);
+  if (xcd || use_persistent(m)) {
     soc::PersistArgs p = persist_args(m, kv, slot);
     // SOC_TRACE_FILE=<path>: append the last step's per-phase timestamps (diagnostics)
     const char* trace_path = std::getenv("SOC_TRACE_FILE");
     const size_t trace_roles = 2 * (4 + 8 * static_cast<size_t>(m->cfg.num_hidden_layers));
-    const size_t trace_n = trace_roles + static_cast<size_t>(w.nblocks) * 8;
+    const size_t xcd_nb = static_cast<size_t>(soc::kXcdGroups) * soc::kXcdBlocks;
+    const size_t trace_n = xcd ? xcd_nb * 16 + m->cfg.num_hidden_layers + 4
+                               : trace_roles + static_cast<size_t>(w.nblocks) * 8;
     if (trace_path != nullptr) {
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
       if ((e = hipMemset(p.trace, 0, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
     }
     for (int i = 0; i < steps; ++i)
-      if ((e = soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
+      if ((e = xcd ? soc::launch_decode_xcd(p, s) : soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
         return hip_fail(e, "persistent decode launch");
     int32_t err = 0;
     if ((e = hipMemcpyAsync(&err, w.err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
@@ -523,7 +562,49 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       e = hipMemcpy(t.data(), p.trace, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost);
       (void)hipFree(p.trace);
       if (e != hipSuccess) return hip_fail(e, "hipMemcpy trace");
-      if (FILE* f = std::fopen(trace_path, "a")) {
+      FILE* f = std::fopen(trace_path, "a");
+      if (f != nullptr && xcd) {
+        // block (0, 0): layer durations, LM head; then the middle layer's phase points over all blocks
+        const int L = m->cfg.num_hidden_layers;
+        const uint64_t* t0p = t.data() + xcd_nb * 16;
+        std::fprintf(f, "xcd block(0,0) layer us:");
+        for (int l = 1; l <= L; ++l) std::fprintf(f, " %.2f", (static_cast<double>(t0p[l]) - t0p[l - 1]) * 0.01);
+        std::fprintf(f, " | lm head %.2f\n", (static_cast<double>(t0p[L + 1]) - t0p[L]) * 0.01);
+        uint64_t tmin = ~0ull;
+        for (size_t b = 0; b < xcd_nb; ++b)
+          if (t[b * 16] != 0) tmin = std::min(tmin, t[b * 16]);
+        std::fprintf(f, "xcd middle layer (us from earliest start):");
+        for (int pnt = 0; pnt < 13; ++pnt) {
+          std::vector<double> v;
+          for (size_t b = 0; b < xcd_nb; ++b)
+            if (t[b * 16 + pnt] != 0) v.push_back((static_cast<double>(t[b * 16 + pnt]) - tmin) * 0.01);
+          std::sort(v.begin(), v.end());
+          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJep"[pnt], v.front(), v[v.size() / 2], v.back());
+        }
+        std::fprintf(f, "\n");
+        // per XCD: latest published attention partial (point p) and its block, earliest / latest E poll return (e)
+        for (int g = 0; g < soc::kXcdGroups; ++g) {
+          double pmax = -1, emin = 1e30, emax = -1;
+          int jmax = -1;
+          for (int j = 0; j < soc::kXcdBlocks; ++j) {
+            const size_t b = static_cast<size_t>(g) * soc::kXcdBlocks + j;
+            if (t[b * 16 + 12] != 0) {
+              const double v = (static_cast<double>(t[b * 16 + 12]) - tmin) * 0.01;
+              if (v > pmax) { pmax = v; jmax = j; }
+            }
+            if (t[b * 16 + 11] != 0) {
+              const double v = (static_cast<double>(t[b * 16 + 11]) - tmin) * 0.01;
+              emin = std::min(emin, v);
+              emax = std::max(emax, v);
+            }
+          }
+          std::fprintf(f, " xcd%d: p_max %.2f (j %d) e[%.2f %.2f]", g, pmax, jmax, emin, emax);
+        }
+        std::fprintf(f, "\n");
+        std::fclose(f);
+        f = nullptr;
+      }
+      if (f != nullptr) {
         const size_t per = trace_roles / 2;
         for (int which = 0; which < 2; ++which) {
           std::fprintf(f, "%s:", which == 0 ? "block0" : "blockN");
@@ -554,6 +635,10 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     if (err != 0) {
       // a bounded wait expired: drop the exchange state so the next call starts clean
       m->dws.ready = false;
+      if (xcd && err == 2) {
+        m->xcd_off = true;
+        return soc::fail(SOC_ERR_HIP, "XCD decode: the launch did not place 32 blocks on each of the 8 XCDs");
+      }
       return soc::fail(SOC_ERR_HIP, "persistent decode: a cross-block wait timed out (grid not co-resident?)");
     }
   } else if (env_flag("SOC_EAGER")) {
@@ -1115,7 +1200,7 @@ int soc_model_decode_path(soc_model* m, int32_t* path) {
   SOC_API_BEGIN
   if (m == nullptr || path == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
-  *path = use_persistent(m) ? 1 : 0;
+  *path = use_xcd(m) ? 2 : (use_persistent(m) ? 1 : 0);
   return SOC_OK;
   SOC_API_END
 }

@@ -41,6 +41,9 @@ SMALL_MODELS = {
                                num_key_value_heads=2, intermediate_size=384, tie_word_embeddings=False), 12, 9, 10),
     "tiny_g4": (QwenConfig(vocab_size=640, hidden_size=512, num_hidden_layers=2, num_attention_heads=8,
                            num_key_value_heads=2, intermediate_size=1024, tie_word_embeddings=False), 13, 20, 6),
+    # eight KV heads like every Qwen3 model: decode takes the XCD-partitioned kernel on MI355X
+    "tiny_kv8": (QwenConfig(vocab_size=512, hidden_size=256, num_hidden_layers=2, num_attention_heads=16,
+                            num_key_value_heads=8, intermediate_size=768, tie_word_embeddings=False), 14, 11, 9),
 }
 
 

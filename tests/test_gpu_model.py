@@ -183,16 +183,19 @@ def test_decode_steps_equal_decode_loop(gpu_ctx):
         m.close()
 
 
-@pytest.mark.parametrize("name", ["tiny_untied", "tiny_g4"])
+@pytest.mark.parametrize("name", ["tiny_untied", "tiny_g4", "tiny_kv8"])
 def test_persistent_decode_matches_graph_decode(gpu_ctx, name, monkeypatch):
-    """The one-launch persistent decode step and the per-op kernels (graph replay) agree on every step."""
+    """The one-launch decode steps (with attention blocks; for 8 KV heads also the XCD-partitioned one) and the
+    per-op kernels (graph replay) agree on every step."""
     cfg, seed, _, _ = SMALL_MODELS[name]
     m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, seed))
     ids = S.synth_tokens(9, "paths", cfg.vocab_size, 13)
+    modes = ("graph", "persistent", "xcd") if cfg.num_key_value_heads == 8 else ("graph", "persistent")
     runs = {}
     try:
-        for mode in ("graph", "persistent"):
+        for mode in modes:
             monkeypatch.setenv("SOC_DECODE", mode)
+            assert m.decode_path() == mode, f"SOC_DECODE={mode} fell back to {m.decode_path()}"
             kv = S.KVCache(m, 1, 300)
             _, t = S.prefill(m, kv, 0, ids)
             rows, toks = [], [t]
@@ -204,9 +207,10 @@ def test_persistent_decode_matches_graph_decode(gpu_ctx, name, monkeypatch):
             more = S.decode_steps(m, kv, 0, toks[-1], 270)
             kv.close()
             runs[mode] = (np.stack(rows), toks, more)
-        assert runs["graph"][1] == runs["persistent"][1]
-        assert_logits_close(runs["persistent"][0], runs["graph"][0], f"{name} persistent vs graph")
-        assert np.array_equal(runs["graph"][2], runs["persistent"][2])
+        for mode in modes[1:]:
+            assert runs["graph"][1] == runs[mode][1], mode
+            assert_logits_close(runs[mode][0], runs["graph"][0], f"{name} {mode} vs graph")
+            assert np.array_equal(runs["graph"][2], runs[mode][2]), mode
     finally:
         m.close()
 
@@ -239,13 +243,17 @@ def test_prefill_against_live_oracle_long_prompt(gpu_ctx, oracle_mod):
         m.close()
 
 
-def test_qwen3_0p6b_greedy_matches_reference(gpu_ctx, golden):
-    """Qwen3-0.6B, random-init fp16 N(0,0.02) seed 1, 32-token prompt, 16 greedy tokens at batch 1."""
+@pytest.mark.parametrize("mode", ["xcd", "persistent"])
+def test_qwen3_0p6b_greedy_matches_reference(gpu_ctx, golden, mode, monkeypatch):
+    """Qwen3-0.6B, random-init fp16 N(0,0.02) seed 1, 32-token prompt, 16 greedy tokens at batch 1, through each
+    one-launch decode kernel."""
     g = golden("qwen3_0p6b.npz")
     cfg = S.QWEN3_0_6B
+    monkeypatch.setenv("SOC_DECODE", mode)
     m = S.Model(gpu_ctx, cfg).synthesize(int(g["weight_seed"]), 0.02)
     kv = S.KVCache(m, 1, 64)
     try:
+        assert m.decode_path() == mode
         prompt = g["prompt"]
         logits, tok = S.prefill(m, kv, 0, prompt)
         rows = [logits[0]]
