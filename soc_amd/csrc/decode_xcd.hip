@@ -1,26 +1,28 @@
-// decode_xcd.hip - one-launch decode step for batch 1 with every layer partitioned over the eight XCDs of MI355X.
+// decode_xcd.hip - one-launch decode step for batch 1 with every layer partitioned over the eight XCDs of MI355X, the
+// layers alternating between two groups of blocks.
 //
 // Block (g, j): XCD g, read from the XCC_ID hardware register, and rank j < 32 among the blocks of this launch that
-// arrived on it. XCD g owns KV head g (every Qwen3 model has 8 KV heads) with its G = nq / 8 query heads and 1/8 of
-// every matrix: the q/k/v rows of its heads, the o_proj columns of its query heads, the gate/up rows and down_proj
-// columns of its eighth of the intermediate dimension. Per layer (reference: QwenBlock::ForwardCached,
-// Mac/cpu/src/qwen_block.cpp:63-73, with QwenAttention::ForwardCached and QwenMLP::Forward):
-//   A  x = x' + sum_k D_k over the eight XCDs' partial down outputs (cross-XCD), RMSNorm(x)
-//   B  the block's q/k/v rows of the XCD's heads                               -> XCD-local exchange
+// arrived on it. Group p = j / 16 computes the layers l with l % 2 == p while the other group streams the weight rows
+// of its next layer into registers: a CU never waits on hand-offs while its own weight loads are in flight (its
+// vector memory requests would queue behind them). XCD g owns KV head g (every Qwen3 model has 8 KV heads) with its
+// G = nq / 8 query heads and 1/8 of every matrix: the q/k/v rows of its heads, the o_proj columns of its query heads,
+// the gate/up rows and down_proj columns of its eighth of the intermediate dimension; the group's 16 blocks of the
+// XCD split that share. Per layer (reference: QwenBlock::ForwardCached, Mac/cpu/src/qwen_block.cpp:63-73, with
+// QwenAttention::ForwardCached and QwenMLP::Forward):
+//   A  x = x' + sum_k D_k: the previous layer's residual and its eight XCDs' partial down outputs (cross-XCD), RMSNorm
+//   B  the block's q/k/v rows of the XCD's heads                                   -> XCD-local exchange
 //   C  the XCD's q/k/v; per-head QK-RMSNorm + RoPE; rank 0 appends k and v to the cache
-//   D  causal attention over the block's 1/32 of the keys: per query head (max, sum, weighted values)
-//   E  the XCD's 32 partials (XCD-local), log-sum-exp merge
-//   F  O_g = Wo[the block's rows][the XCD's query columns] . attn              -> cross-XCD exchange
-//   G  x' = x + sum_k O_k (cross-XCD), RMSNorm(x')
-//   H  h = silu(gate) * up on the block's share of the XCD's intermediate slice -> XCD-local exchange
+//   D  causal attention over the block's share of the keys; the 32 lane groups' partials merged in LDS
+//   E  the XCD's block partials (XCD-local), log-sum-exp merge
+//   F  O_g = Wo[the block's rows][the XCD's query columns] . attn                  -> cross-XCD exchange
+//   G  x' = x + sum_k O_k (cross-XCD), RMSNorm; the block publishes its rows of x' for the other group
+//   H  h = silu(gate) * up on the block's share of the XCD's intermediate slice     -> XCD-local exchange
 //   I  the XCD's h slice (XCD-local)
-//   J  D_g = Wd[the block's rows][the slice's columns] . h                     -> cross-XCD exchange
-// So a layer has two cross-XCD hand-offs (device-scope stores; every block reads 8 x H words) and three XCD-local
-// ones (plain stores served by the XCD's own L2 at half the latency, see exchange.h). Every block keeps the whole
-// residual stream x / x' in LDS, computed in the same order from the same words, so all blocks hold identical bits.
-// Weight rows live in registers: after B a block issues the loads of the layer's o/gate/up/down rows and of the next
-// layer's q/k/v rows, which land while C..E run. Every wait is bounded; a timeout raises the error flag and the
-// grid drains.
+//   J  D_g = Wd[the block's rows][the slice's columns] . h                         -> cross-XCD exchange
+// Cross-XCD words are written with device-scope stores; XCD-local ones with plain stores served by the XCD's own L2
+// (see exchange.h). Every block of the computing group holds the whole residual stream in LDS, computed in the same
+// order from the same words, so all blocks hold identical bits. All eight waves of a block poll, compute and hold
+// weight rows. Every wait is bounded; a timeout raises the error flag and the grid drains.
 #include <algorithm>
 
 #include "exchange.h"
@@ -31,13 +33,14 @@ namespace soc {
 namespace {
 
 constexpr int NT = 512;   // threads per block
-constexpr int NC = 256;   // compute threads: waves 0..3; waves 4..7 are receivers
 constexpr int HD = 128;   // head dim
 constexpr int NX = kXcdGroups, NBX = kXcdBlocks;
+constexpr int NBG = NBX / 2;      // blocks of one group on one XCD
 constexpr int HMAX = 1024;        // hidden size covered by the register tiling
-constexpr int IMAX = 3072;        // intermediate size covered: I / 256 <= 12 gate/up pairs per block
+constexpr int IMAX = 3072;        // intermediate size covered: I / 128 <= 24 gate/up pairs per block
 constexpr int PW = HD + 4;        // words per (block, query head) attention partial: 128 values, max, sum, 2 pad
-constexpr float kNoKeys = -1e30f; // running max of a block that owns no key (finite: a tag bit must not make a NaN)
+constexpr int NGRP = NT / 16;     // attention lane groups per block (16 lanes, 8 dims each)
+constexpr float kNoKeys = -1e30f; // running max of a group that owns no key (finite: a tag bit must not make a NaN)
 
 // A block's rows of one weight matrix in registers: slot s = tid / TPR owns one row; thread t of the slot holds the
 // 8-half chunks at k = 8 (t + TPR c), c < CPT.
@@ -77,43 +80,70 @@ __device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float
   return group_sum<TPR>(acc);
 }
 
-// Word of element e of XCD k's partial in a cross-XCD vector [8][H]: block j of XCD k writes its H / 32 rows as whole
-// aligned lines (32-byte pieces per wave), so no line is written piecewise by several XCDs.
-__device__ __forceinline__ int cross_idx(int e, int k, int H) { return k * H + e; }
+// A block of `rows` rows of `K` halves (row r at src + r * ld) straight to LDS (dst[r * K ..]) with 16-byte
+// global -> LDS loads, one 1 KB wave instruction per 64 chunks; waves w < 8 take every eighth instruction.
+__device__ __forceinline__ void rows_to_lds(const f16* src, size_t ld, int rows, int K, f16* dst) {
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int cpr = K / 8, nch = rows * cpr;
+  for (int c0 = wid * 64; c0 < nch; c0 += 512) {
+    const int ch = min(c0 + lane, nch - 1), row = ch / cpr, col = ch % cpr;
+    __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(row) * ld + col * 8,
+                                     (__attribute__((address_space(3))) void*)(dst + c0 * 8), 16, 0, 0);
+  }
+}
 
-// Register tiling of the 256 compute threads (waves 0..3). Rows per block: q/k/v (G + 2) * 4, o/down H / 32, gate/up
-// pairs I / 256. The LM head runs on all 512 threads.
+// Row sum of an LDS row (K halves) with xs[0..K): TPR threads per row, thread t takes the chunks t + TPR c.
+template <int TPR, int CPT>
+__device__ __forceinline__ float lds_row_dot(const f16* rowp, const float* xs, int K) {
+  const int t = threadIdx.x % TPR;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int k = (t + TPR * c) * 8;
+    if (k < K) {
+      float wf[8];
+      f16x8_to_f32(*reinterpret_cast<const u32x4*>(rowp + k), wf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += xs[k + i] * wf[i];
+    }
+  }
+  return group_sum<TPR>(acc);
+}
+
+// Register tiling of a block's share of one layer (512 threads). Rows per block: q/k/v (G + 2) * 8, o/down H / 16,
+// gate/up pairs I / 128.
 template <int G>
 struct Tiling {
-  static constexpr int RQ = (G + 2) * 4;
-  static constexpr int TPR_Q = 16, CPT_Q = HMAX / (TPR_Q * 8);     // 16 slots, K = H
-  static constexpr int TPR_O = 8, CPT_O = G * HD / (TPR_O * 8);    // 32 slots, K = G * 128 columns of o_proj
-  static constexpr int TPR_GU = 16, CPT_GU = HMAX / (TPR_GU * 8);  // 16 slots, K = H
-  static constexpr int TPR_D = 8, CPT_D = IMAX / 8 / (TPR_D * 8);  // 32 slots, K = I / 8 columns of down_proj
+  static constexpr int RQ = (G + 2) * 8;
+  static constexpr int TPR_Q = 16, CPT_Q = HMAX / (TPR_Q * 8);     // 32 slots, K = H
+  static constexpr int TPR_O = 8, CPT_O = G * HD / (TPR_O * 8);    // 64 slots, K = G * 128 columns of o_proj (LDS)
+  static constexpr int TPR_GU = 16, CPT_GU = HMAX / (TPR_GU * 8);  // 32 slots, K = H
+  static constexpr int TPR_D = 8, CPT_D = IMAX / 8 / (TPR_D * 8);  // 64 slots, K = I / 8 columns of down_proj (LDS)
   static constexpr int TPR_LM = 32, CPT_LM = HMAX / (TPR_LM * 8);  // 16 rows per fragment
-  static constexpr int NA_MAX = 32;                                // attention blocks per XCD at most
-  static constexpr int MQ_E = (NA_MAX * PW / 4 + 63) / 64;         // one head's partial quads per receiver lane
-  static_assert(RQ <= NC / TPR_Q && HMAX / NBX <= NC / TPR_O && IMAX / (NX * NBX) <= NC / TPR_GU, "slots");
+  static constexpr int MQ_E = (NBG * PW / 4 + 63) / 64;            // one head's partial quads per lane
+  static_assert(RQ <= NT / TPR_Q && HMAX / NBG <= NT / TPR_O && IMAX / (NX * NBG) <= NT / TPR_GU, "slots");
   static_assert(TPR_D == TPR_O, "o_proj and down_proj rows share the slot mapping");
 };
 
 // LDS carve-up (floats).
 template <int G>
 struct Lds {
-  static constexpr int XRES = 0;                   // [HMAX] residual stream x / x' (receivers)
-  static constexpr int XN = XRES + HMAX;           // [HMAX] x * gain of the next RMSNorm (the scale is applied later)
-  static constexpr int RED = XN + HMAX;            // [8] the waves' partial sums of x^2
-  static constexpr int HS = RED + 8;               // [IMAX / 8] the XCD's h slice
-  static constexpr int ATT = HS + IMAX / 8;        // [G][HD] merged attention output
-  static constexpr int QS = ATT + G * HD;          // [G][HD] normed, rotated queries
-  static constexpr int KN = QS + G * HD;           // [HD] new key (fp16-rounded)
-  static constexpr int VN = KN + HD;               // [HD] new value (fp16-rounded)
-  static constexpr int RAW = VN + HD;              // [(G + 2) HD] the XCD's raw q/k/v (receivers)
-  static constexpr int WPART = RAW + (G + 2) * HD; // [16][G][PW] the receiver groups' attention partials
-  static constexpr int BPART = WPART + 16 * G * PW; // [G][NA_MAX PW] words: the XCD's block partials per head
-  static constexpr int FLAG = BPART + G * Tiling<G>::NA_MAX * PW;  // [8] ints: status, g, j, last block, D counter
-  static constexpr int BV = FLAG + 8;              // [16] argmax values per slot
-  static constexpr int BI = BV + 16;               // [16] argmax indices
+  static constexpr int XRES = 0;                     // [HMAX] residual stream x / x'
+  static constexpr int XN = XRES + HMAX;             // [HMAX] x * gain of the next RMSNorm (the scale is applied later)
+  static constexpr int RED = XN + HMAX;              // [8] the waves' partial sums of x^2
+  static constexpr int HS = RED + 8;                 // [IMAX / 8] the XCD's h slice
+  static constexpr int ATT = HS + IMAX / 8;          // [G][HD] merged attention output
+  static constexpr int QS = ATT + G * HD;            // [G][HD] normed, rotated queries
+  static constexpr int KN = QS + G * HD;             // [HD] new key (fp16-rounded)
+  static constexpr int VN = KN + HD;                 // [HD] new value (fp16-rounded)
+  static constexpr int RAW = VN + HD;                // [(G + 2) HD] the XCD's raw q/k/v
+  static constexpr int GPART = RAW + (G + 2) * HD;   // [32][G][PW] lane-group partials, [8][G] maxima, [256][2] sums
+  static constexpr int BPART = GPART + NGRP * G * PW + 8 * G + NT;  // [G][NBG PW] words: the XCD's block partials
+  static constexpr int WD = BPART + G * NBG * PW;    // [HMAX / 16][IMAX / 8] halves: the block's down_proj rows
+  static constexpr int WO = WD + HMAX / 16 * IMAX / 8 / 2;  // [HMAX / 16][G HD] halves: the block's o_proj rows
+  static constexpr int FLAG = WO + HMAX / 16 * G * HD / 2;  // [8] ints: status, g, j, last block
+  static constexpr int BV = FLAG + 8;                // [16] argmax values per slot
+  static constexpr int BI = BV + 16;                 // [16] argmax indices
   static constexpr int TOTAL = BI + 16;
 };
 
@@ -125,10 +155,10 @@ struct Ctx {
   int* flag;
 };
 
-// Attention blocks of the XCD for S keys (about 16 keys each, one per 16-lane group of the receiver waves, at most
-// 32 blocks) and keys per block; na is recomputed from the chunk so that every block j < na owns at least one key.
+// Attention blocks of the XCD's computing group for S keys (about 32 keys each, one per lane group, at most 16
+// blocks) and keys per block; na is recomputed from the chunk so that every block jj < na owns at least one key.
 __device__ __forceinline__ void attn_split(int S, int& na, int& chunk) {
-  na = min(NBX, (S + 15) / 16);
+  na = min(NBG, (S + NGRP - 1) / NGRP);
   chunk = (S + na - 1) / na;
   na = (S + chunk - 1) / chunk;
 }
@@ -139,28 +169,28 @@ __device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
   return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
 }
 
-// Optional phase timestamps (diagnostics): the middle layer's 11 phase points of every block go to
-// trace[block * 16 + point] (receiver points from wave 4, compute points from wave 0); block (0, 0) also writes each
-// layer's start, the final norm and the step's end into trace[256 * 16 + i].
+// Optional phase timestamps (diagnostics): the middle layer's phase points of every block of its group go to
+// trace[block * 16 + point]; block 0 of each group on XCD 0 also writes its layers' starts, the final norm and the
+// step's end into trace[256 * 16 + i].
 #define XTRACE(pt)                                                                                           \
   do {                                                                                                       \
-    if (c.a.trace != nullptr && (threadIdx.x == 0 || threadIdx.x == NC) && layer == c.a.L / 2)               \
+    if (c.a.trace != nullptr && threadIdx.x == 0 && layer == c.a.L / 2)                                      \
       c.a.trace[(c.g * NBX + c.j) * 16 + (pt)] = now_ticks();                                                \
   } while (0)
-#define XTRACE0(i, t)                                                                                        \
+#define XTRACE0(i)                                                                                           \
   do {                                                                                                       \
-    if (c.a.trace != nullptr && threadIdx.x == (t) && c.g == 0 && c.j == 0)                                  \
+    if (c.a.trace != nullptr && threadIdx.x == 0 && c.g == 0 && c.j % NBG == 0)                              \
       c.a.trace[NX * NBX * 16 + (i)] = now_ticks();                                                          \
   } while (0)
 
-// Block barrier; afterwards every thread leaves if a receiver reported a failed wait (flag[0] != 0).
+// Block barrier; afterwards every thread leaves if a wave reported a failed wait (flag[0] != 0).
 #define XSYNC()                       \
   do {                                \
     __syncthreads();                  \
     if (c.flag[0] != 0) return false; \
   } while (0)
 
-// Receiver wave: polls MQ quads per lane (byte offsets off[e] into r, or -1 for none) of a tagged vector until every
+// Wave: polls MQ quads per lane (byte offsets off[e] into r, or -1 for none) of a tagged vector until every
 // one carries `tag`. Returns false (wave-uniform) on timeout or a raised error flag, after recording it in flag[0].
 template <int MQ>
 __device__ __forceinline__ bool poll_quads(const Ctx& c, __amdgpu_buffer_rsrc_t r, const int (&off)[MQ], uint32_t tag,
@@ -186,83 +216,7 @@ __device__ __forceinline__ bool poll_quads(const Ctx& c, __amdgpu_buffer_rsrc_t 
   }
 }
 
-// Sum over aligned groups of 8 lanes that is bit-identical in every lane of the group: each step adds two values
-// that are equal in both partner lanes up to the order of one addition, and IEEE addition commutes exactly.
-__device__ __forceinline__ float sum8(float v) {
-  v += dpp_mov<0xB1>(v);   // lane ^ 1
-  v += dpp_mov<0x4E>(v);   // lane ^ 2
-  v += dpp_mov<0x141>(v);  // lane ^ 7 within 8: the other (now uniform) quad
-  return v;
-}
-
-// Wave w < 8 of the block (all eight take part; the cross-XCD vectors are polled when no wave has weight loads in
-// flight): its eighth of x = x + sum_k partial_k over the eight XCDs (layer 0: x = the embedding row), then x * gain
-// into xn and its partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is completed by
-// rms_scale). The wave owns the element quads w * H / 32 .. + H / 32; its load i brings 8 of them from all eight
-// partials (lane l: quad i * 8 + l / 8 of partial l % 8) and the 8 lanes of a quad add their partials with sum8.
-__device__ __forceinline__ bool recv_cross(const Ctx& c, int rw, const uint32_t* src, uint32_t tag,
-                                           const f16* embed_row, const f16* gain, float* xres, float* xn, float* red) {
-  constexpr int NI = HMAX / 256;
-  int lane = threadIdx.x & 63;
-  __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
-  const int k = lane & 7;
-  const int H = c.a.H, ni = H / 256, line0 = rw * (H / 32);
-  float ss = 0.0f;
-  if (embed_row != nullptr) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int q = line0 + i * 8 + (lane >> 3);
-      if (i < ni && k == 0) {
-        const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
-        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
-        f32x4 x, y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = static_cast<float>(e4[e]);
-          y[e] = x[e] * static_cast<float>(g4[e]);
-          ss += x[e] * x[e];
-        }
-        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
-        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
-      }
-    }
-  } else {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
-    int off[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) off[i] = i < ni ? k * H * 4 + (line0 + i * 8 + (lane >> 3)) * 16 : -1;
-    u32x4 v[NI];
-    if (!poll_quads<NI>(c, r, off, tag, v)) return false;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int q = line0 + i * 8 + (lane >> 3);
-      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
-      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
-      if (i < ni && k == 0) {
-        f32x4 x = *reinterpret_cast<const f32x4*>(xres + 4 * q);
-        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
-        x[0] += s0;
-        x[1] += s1;
-        x[2] += s2;
-        x[3] += s3;
-        f32x4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          y[e] = x[e] * static_cast<float>(g4[e]);
-          ss += x[e] * x[e];
-        }
-        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
-        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
-      }
-    }
-  }
-  ss = wave_sum(ss);
-  if (lane == 0) red[rw] = ss;
-  return true;
-}
-
-// Receiver wave: the quads qi = lane + 64 e < nq of the XCD-local tagged words src[0 .. 4 nq) into dst[4 qi ..] (raw
+// Wave: the quads qi = lane + 64 e < nq of the XCD-local tagged words src[0 .. 4 nq) into dst[4 qi ..] (raw
 // words: the tags are kept). Load e of a lane is at byte 16 lane + 1024 e: one register offset for all loads.
 template <int MQ>
 __device__ __forceinline__ bool recv_contig(const Ctx& c, const uint32_t* src, int nq, uint32_t tag, uint32_t* dst) {
@@ -297,16 +251,123 @@ __device__ __forceinline__ bool recv_contig(const Ctx& c, const uint32_t* src, i
   return true;
 }
 
-// Receiver waves (4..7): every poll, the RMSNorm inputs, QK-norm/RoPE and attention merge of the layers, then the
-// final hidden state. They issue no weight loads, so their polls never queue behind the weight stream; no receiver
-// needs another receiver's data.
+// Sum over aligned groups of 8 lanes that is bit-identical in every lane of the group: each step adds two values
+// that are equal in both partner lanes up to the order of one addition, and IEEE addition commutes exactly.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_mov<0xB1>(v);   // lane ^ 1
+  v += dpp_mov<0x4E>(v);   // lane ^ 2
+  v += dpp_mov<0x141>(v);  // lane ^ 7 within 8: the other (now uniform) quad
+  return v;
+}
+
+// Wave w < 8 of the block: its eighth of x = base + sum_k partial_k over the eight XCDs, then x * gain into xn and its
+// partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is completed by rms_scale). The base is
+// the tagged vector xbase (the previous layer's residual published by the other group) or, when xbase is null, the
+// residual in LDS; for layer 0 the embedding row replaces it all. The wave owns the element quads w * H / 32 ..
+// + H / 32; its load i brings 8 of them from all eight partials (lane l: quad i * 8 + l / 8 of partial l % 8) and
+// the 8 lanes of a quad add their partials with sum8; lanes l % 8 == 0 also load the base quad.
+__device__ __forceinline__ bool cross_reduce(const Ctx& c, int w, const uint32_t* src, const uint32_t* xbase,
+                                             uint32_t tag, const f16* embed_row, const f16* gain, float* xres,
+                                             float* xn, float* red) {
+  constexpr int NI = HMAX / 256;
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
+  const int k = lane & 7;
+  const int H = c.a.H, ni = H / 256, q0 = w * (H / 32);
+  float ss = 0.0f;
+  if (embed_row != nullptr) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = q0 + i * 8 + (lane >> 3);
+      if (i < ni && k == 0) {
+        const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
+        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+        f32x4 x, y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = static_cast<float>(e4[e]);
+          y[e] = x[e] * static_cast<float>(g4[e]);
+          ss += x[e] * x[e];
+        }
+        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+      }
+    }
+  } else {
+    // one poll for the partials and, when given, the base quads (lanes l % 8 == 0): the base is published earlier,
+    // so it costs no extra round trip
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(xbase != nullptr ? xbase : src), 0, H * 4, 0x00020000);
+    const u32x4 filler = {tag, tag, tag, tag};
+    u32x4 v[NI], bq[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const bool live = i < ni, blive = live && xbase != nullptr && k == 0;
+      v[i] = live ? ll_peek_buf4(r, k * H * 4 + (q0 + i * 8 + (lane >> 3)) * 16) : filler;
+      bq[i] = blive ? ll_peek_buf4(rb, (q0 + i * 8 + (lane >> 3)) * 16) : filler;
+    }
+    const uint64_t t0 = now_ticks();
+    uint32_t spins = 0;
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) all = all && tw_quad_ok(v[i], tag) && tw_quad_ok(bq[i], tag);
+      if (__all(all)) break;
+      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+        __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error
+        c.flag[0] = 1;
+        return false;
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const bool live = i < ni, blive = live && xbase != nullptr && k == 0;
+        if (live && !tw_quad_ok(v[i], tag)) v[i] = ll_peek_buf4(r, k * H * 4 + (q0 + i * 8 + (lane >> 3)) * 16);
+        if (blive && !tw_quad_ok(bq[i], tag)) bq[i] = ll_peek_buf4(rb, (q0 + i * 8 + (lane >> 3)) * 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int q = q0 + i * 8 + (lane >> 3);
+      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
+      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
+      if (i < ni && k == 0) {
+        f32x4 x = xbase != nullptr ? f32x4{tw_val(bq[i].x), tw_val(bq[i].y), tw_val(bq[i].z), tw_val(bq[i].w)}
+                                   : *reinterpret_cast<const f32x4*>(xres + 4 * q);
+        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+        x[0] += s0;
+        x[1] += s1;
+        x[2] += s2;
+        x[3] += s3;
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[e] = x[e] * static_cast<float>(g4[e]);
+          ss += x[e] * x[e];
+        }
+        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[w] = ss;
+  return true;
+}
+
+// The layers l % 2 == p of one decode step for a block of group p, then the final hidden state (all blocks).
 template <int G>
-__device__ __forceinline__ bool recv_layers(const Ctx& c) {
+__device__ __forceinline__ bool run_layers(const Ctx& c) {
+  using T = Tiling<G>;
   using LD = Lds<G>;
   const PersistArgs& a = c.a;
-  const int rw = (threadIdx.x >> 6) - NC / 64;
-  const int g = c.g, j = c.j, pos = c.pos, S = pos + 1;
-  const int H = a.H, IS = a.I / NX;
+  const int tid = threadIdx.x, wid = tid >> 6;
+  const int g = c.g, pgrp = c.j / NBG, jj = c.j % NBG, pos = c.pos, S = pos + 1;
+  const int H = a.H, I = a.I, qd = a.qd;
+  const int RH = H / NBG;   // o/down rows per block
+  const int IS = I / NX;    // intermediate slice of the XCD
+  const int RI = IS / NBG;  // gate/up pairs per block
   float* lds = c.lds;
   float* xres = lds + LD::XRES;
   float* xn = lds + LD::XN;
@@ -317,19 +378,34 @@ __device__ __forceinline__ bool recv_layers(const Ctx& c) {
   float* kn = lds + LD::KN;
   float* vn = lds + LD::VN;
   uint32_t* raw = reinterpret_cast<uint32_t*>(lds + LD::RAW);
-  uint32_t* bpart = reinterpret_cast<uint32_t*>(lds + LD::BPART) + rw * (Tiling<G>::NA_MAX * PW);
-  const uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
-  const uint32_t* loc_qkv = loc;
-  const uint32_t* loc_att = loc + (((G + 2) * HD + 63) & ~63);
-  const uint32_t* loc_h = loc_att + ((NBX * G * PW + 63) & ~63);
+  float* gpart = lds + LD::GPART;
+  uint32_t* bpart = reinterpret_cast<uint32_t*>(lds + LD::BPART);
+  f16* wd = reinterpret_cast<f16*>(lds + LD::WD);
+  f16* wo = reinterpret_cast<f16*>(lds + LD::WO);
+  uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
+  uint32_t* loc_qkv = loc;                                  // [(G + 2) HD]
+  uint32_t* loc_att = loc + (((G + 2) * HD + 63) & ~63);    // [G][NBX][PW]
+  uint32_t* loc_h = loc_att + ((NBX * G * PW + 63) & ~63);  // [IS]
+  // this block's q/k/v row: local row lr of the XCD's (G + 2) * 128 (q heads, key, value)
+  const int q_slot = tid / T::TPR_Q;
+  const int q_lr = jj * T::RQ + q_slot;
+  const bool q_live = q_slot < T::RQ;
+  const int q_row = q_lr < G * HD ? g * G * HD + q_lr
+                                  : (q_lr < (G + 1) * HD ? qd + g * HD + (q_lr - G * HD)
+                                                         : qd + a.nkv * HD + g * HD + (q_lr - (G + 1) * HD));
+  const int o_slot = tid / T::TPR_O, gu_slot = tid / T::TPR_GU;
+  const int hrow = jj * RH + o_slot;           // o/down output row
+  const bool h_live = o_slot < RH;
+  const int iidx = g * IS + jj * RI + gu_slot; // gate/up row
+  const bool i_live = gu_slot < RI;
+  // attention: block jj < na takes keys [k0, k1); lane group grp takes keys k0 + grp + 32 u
   int na, chunk;
   attn_split(S, na, chunk);
-  // attention: block j < na takes keys [k0, k1); group grp (16 lanes, 8 dims each) takes keys k0 + grp + 16 u
-  const int k0 = j < na ? min(S, j * chunk) : S, k1 = j < na ? min(S, k0 + chunk) : S;
-  int lane = threadIdx.x & 63, grp = (threadIdx.x - NC) >> 4, sub = threadIdx.x & 15;
-  constexpr int NG = (NT - NC) / 16;
-  float* wpart = lds + LD::WPART;
-  uint32_t* loc_att_w = a.loc + static_cast<size_t>(g) * a.loc_stride + (((G + 2) * HD + 63) & ~63);
+  const int k0 = jj < na ? min(S, jj * chunk) : S, k1 = jj < na ? min(S, k0 + chunk) : S;
+  int lane = tid & 63, grp = tid >> 4, sub = tid & 15;
+
+  Slice<T::TPR_Q, T::CPT_Q> sq;
+  Slice<T::TPR_GU, T::CPT_GU> sg, su;
   u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
   auto kv_fetch = [&](int layer, int p) {  // cached key/value p (< pos) of this layer, 8 dims per lane
     if (p < k1 && p < pos) {
@@ -339,41 +415,64 @@ __device__ __forceinline__ bool recv_layers(const Ctx& c) {
       vr = load16(a.vcache + base);
     }
   };
-  const float* rc = a.rope_cos + static_cast<size_t>(pos) * (HD / 2);
-  const float* rs = a.rope_sin + static_cast<size_t>(pos) * (HD / 2);
-  for (int layer = 0; layer < a.L; ++layer) {
+  // the weight rows of layer `layer` and its first cached key/value of this lane group
+  auto stream = [&](int layer) {
+    // recomputed per call: keeps the 64-bit row offsets from staying live across the layer loop
+    int qr = q_row, hr = jj * RH, ir = iidx;
+    __asm__ volatile("" : "+v"(qr), "+v"(ir), "+s"(hr));
+    const f16* W4 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 4);
+    const f16* W5 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 5);
+    const f16* W6 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 6);
+    const f16* W7 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 7);
+    const f16* W8 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 8);
+    slice_load(sq, q_live ? W4 + static_cast<size_t>(qr) * H : nullptr, H);
+    rows_to_lds(W5 + static_cast<size_t>(hr) * qd + g * G * HD, qd, RH, G * HD, wo);
+    slice_load(sg, i_live ? W6 + static_cast<size_t>(ir) * H : nullptr, H);
+    slice_load(su, i_live ? W7 + static_cast<size_t>(ir) * H : nullptr, H);
+    rows_to_lds(W8 + static_cast<size_t>(hr) * I + g * IS, I, RH, IS, wd);
+    kv_fetch(layer, k0 + grp);
+  };
+  if (pgrp < a.L) stream(pgrp);
+
+  for (int layer = pgrp; layer < a.L; layer += 2) {
     const f16* W[4];  // in_norm, post_norm, q_norm, k_norm
 #pragma unroll
     for (int i = 0; i < 4; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
     const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     // per layer: keeps the compiler from hoisting per-lane addresses out of the loop (register pressure)
     __asm__ volatile("" : "+v"(lane), "+v"(grp), "+v"(sub));
-    // this layer's first cached key/value of the group, issued before A's poll: the previous layer's outputs take
-    // longer to arrive than these loads, so the poll (which returns after them) loses nothing
-    kv_fetch(layer, k0 + grp);
-    XTRACE0(layer, NC);
+    XTRACE0(layer);
     XTRACE(0);
-    // ---- A: x (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
-    recv_cross(c, NC / 64 + rw, a.xd, (tag - 1u) & 3u,
-               layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0], xres, xn, red);
+    // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
+    wait_mem();  // this wave's rows of the layer have landed (its LDS rows are published by the barrier below)
+    cross_reduce(c, wid, a.xd, a.xp, (tag - 1u) & 3u,
+                 layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0], xres, xn, red);
     XTRACE(1);
     XSYNC();  // #1
-    // ---- C: head rw of the XCD's q/k/v; QK-RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171, rope.cpp:81-84)
-    if (rw < G + 2) {
-      const int hh = rw;
+    // ---- B: q/k/v rows of RMSNorm(x) ----
+    {
+      const float out = slice_dot(sq, xn, H) * rms_scale(red, H, a.eps);
+      if (q_live && tid % T::TPR_Q == 0) ll_store_local(loc_qkv, q_lr, out, tag);
+    }
+    XTRACE(2);
+    // ---- C: head wid of the XCD's q/k/v; QK-RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171,
+    //      rope.cpp:81-84); rank 0 appends the key and value, rounded to the cache's fp16, at `pos` ----
+    if (wid < G + 2) {
+      const int hh = wid;
       if (recv_contig<1>(c, loc_qkv + hh * HD, HD / 4, tag, raw + hh * HD)) {
         float x0 = tw_val(raw[hh * HD + lane]), x1 = tw_val(raw[hh * HD + lane + 64]);
-        if (hh <= G) norm_rope_pair(x0, x1, hh < G ? W[2] : W[3], a.eps, rc, rs, lane);
+        if (hh <= G)
+          norm_rope_pair(x0, x1, hh < G ? W[2] : W[3], a.eps, a.rope_cos + static_cast<size_t>(pos) * (HD / 2),
+                         a.rope_sin + static_cast<size_t>(pos) * (HD / 2), lane);
         if (hh < G) {
           qs[hh * HD + lane] = x0;
           qs[hh * HD + lane + 64] = x1;
         } else {
-          // key and value rounded to the cache's fp16 before use; rank 0 appends them at `pos`
           const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
           float* dst = hh == G ? kn : vn;
           dst[lane] = static_cast<float>(h0);
           dst[lane + 64] = static_cast<float>(h1);
-          if (j == 0) {
+          if (jj == 0) {
             f16* cache = (hh == G ? a.kcache : a.vcache) + static_cast<size_t>(layer) * a.layer_stride +
                          static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(pos) * HD;
             cache[lane] = h0;
@@ -384,243 +483,209 @@ __device__ __forceinline__ bool recv_layers(const Ctx& c) {
     }
     XTRACE(3);
     XSYNC();  // #2: qs, kn, vn
-    // ---- D: attention over keys [k0, k1) (online softmax of grouped_query_attention.cpp:105-136) ----
-    if (j < na) {
-      float qreg[G][8], o[G][8], mrun[G], lrun[G];
+    // ---- D: attention over keys [k0, k1) (the softmax of grouped_query_attention.cpp:105-136) in two passes over the
+    //      block's keys: scores and the block's max per head, then base-2 weights relative to that max, so that the
+    //      lane groups' partials merge by plain sums. q is prescaled by scale * log2(e). ----
+    float qreg[G][8], mblk[G];
+    {
+      const float qscale = a.scale * 1.44269504088896341f;
+      float mloc[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        mrun[h] = kNoKeys;
-        lrun[h] = 0.0f;
+        mloc[h] = kNoKeys;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          qreg[h][i] = qs[h * HD + sub * 8 + i];
-          o[h][i] = 0.0f;
-        }
+        for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
       }
-      for (int p = k0 + grp; p < k1; p += NG) {
-        float kf[8], vf[8];
+      // the score of key p for every head (every lane of the group gets it)
+      auto scores = [&](int p, int u, float (&sc)[G]) {
+        float kf[8];
         if (p == pos) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            kf[i] = kn[sub * 8 + i];
-            vf[i] = vn[sub * 8 + i];
-          }
+          for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
         } else {
-          f16x8_to_f32(kr, kf);
-          f16x8_to_f32(vr, vf);
+          const u32x4 kw = u == 0 ? kr
+                                  : load16(a.kcache + static_cast<size_t>(layer) * a.layer_stride +
+                                           static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(p) * HD + sub * 8);
+          f16x8_to_f32(kw, kf);
         }
-        kv_fetch(layer, p + NG);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           float d = 0.0f;
 #pragma unroll
           for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
-          const float sc = group_sum<16>(d) * a.scale;
-          const float mn = fmaxf(mrun[h], sc);
-          const float corr = expf(mrun[h] - mn);
-          const float pw = expf(sc - mn);
-          lrun[h] = lrun[h] * corr + pw;
-          mrun[h] = mn;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[h][i] = o[h][i] * corr + pw * vf[i];
+          sc[h] = group_sum<16>(d);
         }
+      };
+      if (jj < na)
+        for (int p = k0 + grp, u = 0; p < k1; p += NGRP, ++u) {
+          float sc[G];
+          scores(p, u, sc);
+#pragma unroll
+          for (int h = 0; h < G; ++h) mloc[h] = fmaxf(mloc[h], sc[h]);
+        }
+      // the block's max per head: wave maxima, then the 8 waves' through LDS
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float mw = wave_max(mloc[h]);
+        if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
       }
-      // the group's partial (its keys' max, sum and weighted values per head) to LDS
+      XSYNC();  // #2a: wave maxima
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float M = kNoKeys;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
+        mblk[h] = M == kNoKeys ? M : tw_val(tw_pack(M, 0u));  // as the exchange word will carry it
+      }
+      float o[G][8], l[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        l[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
+      }
+      if (jj < na)
+        for (int p = k0 + grp, u = 0; p < k1; p += NGRP, ++u) {
+          float sc[G], vf[8];
+          scores(p, u, sc);
+          if (p == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+          } else {
+            const u32x4 vw = u == 0 ? vr
+                                    : load16(a.vcache + static_cast<size_t>(layer) * a.layer_stride +
+                                             static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(p) * HD + sub * 8);
+            f16x8_to_f32(vw, vf);
+          }
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            const float pw = __builtin_amdgcn_exp2f(sc[h] - mblk[h]);
+            l[h] += pw;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
+          }
+        }
+      // the group's partial sums (relative to the block max) to LDS
 #pragma unroll
       for (int h = 0; h < G; ++h) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wpart[(grp * G + h) * PW + sub * 8 + i] = o[h][i];
-        if (sub == 0) {
-          wpart[(grp * G + h) * PW + HD] = mrun[h];
-          wpart[(grp * G + h) * PW + HD + 1] = lrun[h];
-        }
+        for (int i = 0; i < 8; ++i) gpart[(grp * G + h) * PW + sub * 8 + i] = o[h][i];
+        if (sub == 0) gpart[(grp * G + h) * PW + HD + 1] = l[h];
       }
     }
-    XSYNC();  // #2b: the block's 16 group partials
-    if (j < na) {
-      // receiver thread t merges output t (head t / 128, dim t % 128) over the 16 groups and publishes it, relative
-      // to the max as the exchange word will carry it (a group without keys adds nothing)
-      const int rt = threadIdx.x - NC;
-      for (int t = rt; t < G * HD; t += NT - NC) {
-        const int h = t / HD, d = t % HD;
-        float mg[16];
-        float M = kNoKeys;
+    XTRACE(11);
+    XSYNC();  // #2b: the block's lane-group partials
+    XTRACE(12);
+    if (jj < na) {
+      // output t (head t / 128, dim t % 128) is the sum over the 32 groups in a fixed order: threads t and t + 256 of
+      // the same lane add groups 0..15 and 16..31, and the lower half adds the upper half's sum through LDS
+      static_assert(G * HD <= NT / 2, "two threads per output");
+      const int t = tid & (NT / 2 - 1), half = tid / (NT / 2);
+      const int h = t / HD, d = t % HD;
+      float L = 0.0f, O = 0.0f;
+      if (t < G * HD) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          mg[q] = wpart[(q * G + h) * PW + HD];
-          M = fmaxf(M, mg[q]);
+        for (int q = 0; q < NGRP / 2; ++q) {
+          const int qq = half * (NGRP / 2) + q;
+          L += gpart[(qq * G + h) * PW + HD + 1];
+          O += gpart[(qq * G + h) * PW + d];
         }
-        if (M != kNoKeys) M = tw_val(tw_pack(M, 0u));
-        float L = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const float e = mg[q] == kNoKeys ? 0.0f : expf(mg[q] - M);
-          L += wpart[(q * G + h) * PW + HD + 1] * e;
-          O += wpart[(q * G + h) * PW + d] * e;
-        }
-        const int w0 = (h * NBX + j) * PW;  // [head][block][PW]
-        ll_store_local(loc_att_w, w0 + d, O, tag);
-        if (d < 4) ll_store_local(loc_att_w, w0 + HD + d, d == 0 ? M : (d == 1 ? L : 0.0f), tag);
       }
-      if (c.a.trace != nullptr && rt == 0 && layer == c.a.L / 2) c.a.trace[(g * NBX + j) * 16 + 12] = now_ticks();
+      float* hsum = gpart + NGRP * G * PW + 8 * G;  // [NT / 2][2] the upper halves' sums (spare LDS after the maxima)
+      if (half == 1 && t < G * HD) {
+        hsum[2 * t] = O;
+        hsum[2 * t + 1] = L;
+      }
+      __syncthreads();  // every thread of the block reaches this barrier (jj < na is block-uniform)
+      if (half == 0 && t < G * HD) {
+        O += hsum[2 * t];
+        L += hsum[2 * t + 1];
+        const int w0 = (h * NBX + jj) * PW;  // [head][block][PW]
+        ll_store_local(loc_att, w0 + d, O, tag);
+        if (d < 4) ll_store_local(loc_att, w0 + HD + d, d == 0 ? mblk[h] : (d == 1 ? L : 0.0f), tag);
+      }
     }
     XTRACE(4);
-    // ---- E: head rw's partials of the XCD's attention blocks, merged in a fixed order ----
-    if (rw < G) {
-      const int h = rw;
-      // head h's partials of blocks 0..na-1 are contiguous: [h][block][PW]
-      if (recv_contig<Tiling<G>::MQ_E>(c, loc_att + h * NBX * PW, na * (PW / 4), tag, bpart)) {
-        if (c.a.trace != nullptr && lane == 0 && h == 0 && layer == c.a.L / 2)
-          c.a.trace[(g * NBX + j) * 16 + 11] = now_ticks();
+    // ---- E: head wid's block partials of the XCD, merged in a fixed order ----
+    if (wid < G) {
+      const int h = wid;
+      if (recv_contig<T::MQ_E>(c, loc_att + h * NBX * PW, na * (PW / 4), tag, bpart + h * (NBG * PW))) {
+        XTRACE(13);
+        const uint32_t* bp = bpart + h * (NBG * PW);
         // lane r < na holds block r's max and sum; the weights e_r are broadcast with readlane
-        const float mr = lane < na ? tw_val(bpart[lane * PW + HD]) : kNoKeys;
-        const float lr = lane < na ? tw_val(bpart[lane * PW + HD + 1]) : 0.0f;
+        const float mr = lane < na ? tw_val(bp[lane * PW + HD]) : kNoKeys;
+        const float lr = lane < na ? tw_val(bp[lane * PW + HD + 1]) : 0.0f;
         const float M = wave_max(mr);
-        const float er = mr < 0.5f * kNoKeys ? 0.0f : expf(mr - M);  // a block without keys adds nothing
+        const float er = mr < 0.5f * kNoKeys ? 0.0f : __builtin_amdgcn_exp2f(mr - M);  // base 2; a keyless block adds 0
         const float L = wave_sum(lr * er);
 #pragma unroll
         for (int dd = 0; dd < 2; ++dd) {
           const int d = lane + 64 * dd;
           float O = 0.0f;
 #pragma unroll
-          for (int r = 0; r < NBX; ++r)
-            if (r < na) O += tw_val(bpart[r * PW + d]) * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er), r));
+          for (int r = 0; r < NBG; ++r)
+            if (r < na) O += tw_val(bp[r * PW + d]) * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er), r));
           att[h * HD + d] = O / L;
         }
       }
     }
     XTRACE(5);
-    XSYNC();  // #3
-    // ---- G: x' = x + sum_k O_k, RMSNorm input ----
-    recv_cross(c, NC / 64 + rw, a.xo, tag, nullptr, W[1], xres, xn, red);
-    XTRACE(7);
-    XSYNC();  // #4
-    // ---- I: the XCD's h slice ----
-    if (rw * 64 < IS / 4 &&
-        recv_contig<1>(c, loc_h + rw * 256, min(64, IS / 4 - rw * 64), tag, reinterpret_cast<uint32_t*>(hs) + rw * 256)) {
-      // the words this lane brought, as floats
-      const int q = rw * 64 + lane;
-      if (q < IS / 4) {
-        uint32_t* w4 = reinterpret_cast<uint32_t*>(hs) + 4 * q;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hs[4 * q + e] = tw_val(w4[e]);
-      }
-    }
-    XTRACE(9);
-    XSYNC();  // #5
-  }
-  // final hidden state x = x' + sum_k D_k, RMSNorm input with the final gain
-  recv_cross(c, NC / 64 + rw, a.xd, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xn,
-             red);
-  XTRACE0(a.L, NC);
-  XSYNC();  // #F
-  return true;
-}
-
-// Compute waves (0..3): the block's weight rows in registers and the projections.
-template <int G>
-__device__ __forceinline__ bool comp_layers(const Ctx& c) {
-  using T = Tiling<G>;
-  using LD = Lds<G>;
-  const PersistArgs& a = c.a;
-  const int tid = threadIdx.x;
-  const int g = c.g, j = c.j;
-  const int H = a.H, I = a.I, qd = a.qd;
-  const int RH = H / NBX;          // o/down rows per block
-  const int IS = I / NX;           // intermediate slice of the XCD
-  const int RI = IS / NBX;         // gate/up pairs per block
-  float* lds = c.lds;
-  const float* xn = lds + LD::XN;
-  const float* red = lds + LD::RED;
-  const float* hs = lds + LD::HS;
-  const float* att = lds + LD::ATT;
-  float* xres = lds + LD::XRES;
-  float* xnw = lds + LD::XN;
-  float* redw = lds + LD::RED;
-  const int wid = tid >> 6;
-  uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
-  uint32_t* loc_qkv = loc;
-  uint32_t* loc_h = loc + (((G + 2) * HD + 63) & ~63) + ((NBX * G * PW + 63) & ~63);
-  // this block's q/k/v row: local row lr of the XCD's (G + 2) * 128 (q heads, key, value)
-  const int q_slot = tid / T::TPR_Q;
-  const int q_lr = j * T::RQ + q_slot;
-  const bool q_live = q_slot < T::RQ;
-  const int q_row = q_lr < G * HD ? g * G * HD + q_lr
-                                  : (q_lr < (G + 1) * HD ? qd + g * HD + (q_lr - G * HD)
-                                                         : qd + a.nkv * HD + g * HD + (q_lr - (G + 1) * HD));
-  const int o_slot = tid / T::TPR_O, gu_slot = tid / T::TPR_GU;
-  const int hrow = j * RH + o_slot;           // o/down output row
-  const bool h_live = o_slot < RH;
-  const int iidx = g * IS + j * RI + gu_slot; // gate/up row
-  const bool i_live = gu_slot < RI;
-
-  Slice<T::TPR_Q, T::CPT_Q> sq;
-  Slice<T::TPR_O, T::CPT_O> so;
-  Slice<T::TPR_GU, T::CPT_GU> sg, su;
-  Slice<T::TPR_D, T::CPT_D> sd;
-  slice_load(sq, q_live ? ld_global(a.layer_w, 4) + static_cast<size_t>(q_row) * H : nullptr, H);
-
-  for (int layer = 0; layer < a.L; ++layer) {
-    // in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown
-    const f16* W[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
-    const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
-    // ---- A (this wave's eighth) ----
-    recv_cross(c, wid, a.xd, (tag - 1u) & 3u, layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0],
-               xres, xnw, redw);
-    XSYNC();  // #1: xn = x * gain, red = partial sums of x^2
-    // ---- B: q/k/v rows of RMSNorm(x) ----
-    {
-      const float out = slice_dot(sq, xn, H) * rms_scale(red, H, a.eps);
-      if (q_live && tid % T::TPR_Q == 0) ll_store_local(loc_qkv, q_lr, out, tag);
-    }
-    XTRACE(2);
-    // the layer's other rows in the order the phases use them, then the next layer's q/k/v rows
-    auto issue_weights = [&]() {
-      slice_load(so, h_live ? W[5] + static_cast<size_t>(hrow) * qd + g * G * HD : nullptr, G * HD);
-      slice_load(sg, i_live ? W[6] + static_cast<size_t>(iidx) * H : nullptr, H);
-      slice_load(su, i_live ? W[7] + static_cast<size_t>(iidx) * H : nullptr, H);
-      slice_load(sd, h_live ? W[8] + static_cast<size_t>(hrow) * I + g * IS : nullptr, IS);
-      if (layer + 1 < a.L)
-        slice_load(sq,
-                   q_live ? ld_global(a.layer_w, static_cast<size_t>(layer + 1) * 9 + 4) + static_cast<size_t>(q_row) * H
-                          : nullptr,
-                   H);
-    };
-    if (a.weights_sync != 2) issue_weights();
-    if (a.weights_sync == 1) wait_mem();
-    XSYNC();  // #2
-    if (a.weights_sync == 2) issue_weights();
-    XSYNC();  // #2b
     XSYNC();  // #3: merged attention output
     // ---- F: partial o_proj over the XCD's query columns ----
     {
-      const float out = slice_dot(so, att, G * HD);
-      if (h_live && tid % T::TPR_O == 0) ll_store(a.xo + cross_idx(hrow, g, H), out, tag);
+      const float out = lds_row_dot<T::TPR_O, T::CPT_O>(wo + (h_live ? o_slot : 0) * (G * HD), att, G * HD);
+      if (h_live && tid % T::TPR_O == 0) ll_store_buf(a.xo, g * H + hrow, out, tag);
     }
     XTRACE(6);
-    // ---- G (this wave's eighth) ----
-    recv_cross(c, wid, a.xo, tag, nullptr, W[1], xres, xnw, redw);
-    XSYNC();  // #4: xn = x' * gain, red
+    // ---- G: x' = x + sum_k O_k, RMSNorm input ----
+    cross_reduce(c, wid, a.xo, nullptr, tag, nullptr, W[1], xres, xn, red);
+    XTRACE(7);
+    XSYNC();  // #4
+    // the block's rows of x' for the other group's next layer
+    {
+      const int rows = H / (NX * NBG), r0 = (g * NBG + jj) * rows;
+      if (tid < rows) ll_store_buf(a.xp, r0 + tid, xres[r0 + tid], tag);
+    }
     // ---- H: gate/up of RMSNorm(x') + SwiGLU (qwen_mlp.cpp:31) on the block's share of the XCD's slice ----
     {
       const float scale = rms_scale(red, H, a.eps);
       const float og = slice_dot(sg, xn, H) * scale;
       const float ou = slice_dot(su, xn, H) * scale;
-      if (i_live && tid % T::TPR_GU == 0) ll_store_local(loc_h, j * RI + gu_slot, silu_ref(og) * ou, tag);
+      if (i_live && tid % T::TPR_GU == 0) ll_store_local(loc_h, jj * RI + gu_slot, silu_ref(og) * ou, tag);
     }
     XTRACE(8);
-    XSYNC();  // #5: the XCD's h slice
+    // ---- I: the XCD's h slice ----
+    if (wid * 64 < IS / 4 &&
+        recv_contig<1>(c, loc_h + wid * 256, min(64, IS / 4 - wid * 64), tag, reinterpret_cast<uint32_t*>(hs) + wid * 256)) {
+      const int q = wid * 64 + lane;  // the words this lane brought, as floats
+      if (q < IS / 4) {
+        const uint32_t* w4 = reinterpret_cast<const uint32_t*>(hs) + 4 * q;
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = tw_val(w4[e]);
+        *reinterpret_cast<f32x4*>(hs + 4 * q) = f32x4{f[0], f[1], f[2], f[3]};
+      }
+    }
+    XTRACE(9);
+    XSYNC();  // #5
     // ---- J: partial down_proj over the slice's columns ----
     {
-      const float out = slice_dot(sd, hs, IS);
-      if (h_live && tid % T::TPR_D == 0) ll_store(a.xd + cross_idx(hrow, g, H), out, tag);
+      const float out = lds_row_dot<T::TPR_D, T::CPT_D>(wd + (h_live ? o_slot : 0) * IS, hs, IS);
+      if (h_live && tid % T::TPR_D == 0) ll_store_buf(a.xd, g * H + hrow, out, tag);
     }
     XTRACE(10);
+    // the group's next layer: its weight rows stream into registers and LDS while the other group computes (after a
+    // barrier: no wave may still read this layer's rows in LDS)
+    if (layer + 2 < a.L) {
+      XSYNC();
+      stream(layer + 2);
+    }
   }
-  recv_cross(c, wid, a.xd, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xnw, redw);
-  XSYNC();  // #F: xn = x * final gain, red
+  // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks)
+  cross_reduce(c, wid, a.xd, a.xp, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xn,
+               red);
+  XTRACE0(a.L);
+  XSYNC();
   return true;
 }
 
@@ -691,13 +756,9 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
     return;
   }
   Ctx c{a, g, j, a.state[0], a.state[1], (step - 1u) * static_cast<uint32_t>(a.L), lds, flag};
-  if (wid >= NC / 64) {
-    if (!recv_layers<G>(c)) return;
-  } else {
-    if (!comp_layers<G>(c)) return;
-  }
+  if (!run_layers<G>(c)) return;
   lm_head<G>(c);
-  XTRACE0(a.L + 1, 0);
+  XTRACE0(a.L + 1);
 
   // ---- greedy argmax over the blocks' candidates (sampler.cpp:26-61 with top_k = 1) ----
   float* bv = lds + LD::BV;
@@ -793,7 +854,7 @@ hipError_t launch_decode_xcd(const PersistArgs& a, hipStream_t s) {
 
 hipError_t xcd_blocks_per_cu(int G, int* blocks) {
   *blocks = 0;
-  const size_t lds = 96 * 1024;
+  const size_t lds = std::max<size_t>((G == 1 ? Lds<1>::TOTAL : Lds<2>::TOTAL) * sizeof(float), 96 * 1024);
   if (G == 1) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<1>, NT, lds);
   if (G == 2) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<2>, NT, lds);
   return hipErrorInvalidValue;

@@ -52,6 +52,13 @@ __device__ __forceinline__ void ll_store_local(uint32_t* base, int idx, float v,
   __builtin_amdgcn_raw_buffer_store_b32(tw_pack(v, tag), r, idx * 4, 0, 0);
 }
 
+// Device-scope (sc1) store of a tagged word to word `idx` of the region at `base` (block-uniform): visible to sc1
+// loads on every XCD. The base stays in scalar registers and the lane needs only a 32-bit offset.
+__device__ __forceinline__ void ll_store_buf(uint32_t* base, int idx, float v, uint32_t tag) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b32(tw_pack(v, tag), r, idx * 4, 0, 16);
+}
+
 // Relaxed device-scope read of four tagged words through a buffer resource (sc1: coherent across XCDs). The lane's
 // byte offset stays in one register and the per-chunk part folds into the instruction's offset fields, so a
 // receiver polling thousands of elements needs no per-element address registers. Each aligned 4-byte word of the

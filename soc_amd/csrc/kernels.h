@@ -142,20 +142,20 @@ struct PersistArgs {
   uint64_t* trace;            // nullable: phase timestamps (diagnostics)
   int spin_sleep;             // back-off between polling rounds, in units of s_sleep 1 (about 64 clocks)
   // XCD-partitioned kernel only (k_decode_xcd):
-  uint32_t* xo;               // [H/4][8][4] tagged partial o_proj outputs of the eight XCD groups (cross-XCD)
-  uint32_t* xd;               // [H/4][8][4] tagged partial down_proj outputs (cross-XCD)
+  uint32_t* xo;               // [8][H] tagged partial o_proj outputs of the eight XCDs (cross-XCD)
+  uint32_t* xd;               // [8][H] tagged partial down_proj outputs (cross-XCD)
+  uint32_t* xp;               // [H] tagged residual x' of the last layer, for the other block group
   uint32_t* loc;              // [8][loc_stride] per-XCD hand-off regions (q/k/v, attention partials, h)
   int loc_stride;             // words per region
   int* xcd_ctr;               // [2][8] arrivals per XCD, by step parity (zero; the next step's pair is reset)
-  int weights_sync;           // k_decode_xcd weight-stream schedule: 0 = issued after B, 1 = and awaited there,
-                              //   2 = issued after the q/k/v hand-off
 };
 bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks);
 size_t persistent_lds_bytes(const PersistArgs& a, int G);
 hipError_t persistent_blocks_per_cu(int G, int* blocks);
 hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream_t s);
 
-// XCD-partitioned one-launch decode step: 256 blocks, 32 on each of the 8 XCDs, XCD g owns KV head g.
+// XCD-partitioned one-launch decode step: 256 blocks, 32 on each of the 8 XCDs, XCD g owns KV head g; two groups of
+// 16 blocks per XCD take alternate layers.
 constexpr int kXcdGroups = 8, kXcdBlocks = 32;
 bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus);
 int xcd_loc_stride(int G, int I);  // words per per-XCD hand-off region

@@ -77,7 +77,7 @@ struct DecodeWs {
   // persistent decode kernel: exchange vectors (tagged 32-bit word per element), argmax partials, error flag
   uint32_t *xa = nullptr, *xb = nullptr, *qkv_x = nullptr, *attn_x = nullptr, *h_x = nullptr;
   // XCD-partitioned decode kernel: cross-XCD partial vectors, per-XCD hand-off regions, arrival counters
-  uint32_t *xo = nullptr, *xd = nullptr, *loc = nullptr;
+  uint32_t *xo = nullptr, *xd = nullptr, *xp = nullptr, *loc = nullptr;
   int loc_stride = 0;
   int* xcd_ctr = nullptr;
   float* pv = nullptr;
@@ -237,6 +237,7 @@ int ensure_decode_ws(soc_model* m, int cap) {
   w.loc_stride = soc::xcd_loc_stride(G, c.intermediate_size);
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * c.hidden_size, &w.xo));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * c.hidden_size, &w.xd));
+  SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(c.hidden_size), &w.xp));
   SOC_TRY(dev_alloc_t(w.allocs, static_cast<size_t>(soc::kXcdGroups) * w.loc_stride, &w.loc));
   SOC_TRY(dev_alloc_t(w.allocs, 2 * soc::kXcdGroups, &w.xcd_ctr));
   SOC_TRY(dev_alloc_t(w.allocs, std::max(w.nblocks, soc::kXcdGroups * soc::kXcdBlocks), &w.pv));
@@ -247,6 +248,7 @@ int ensure_decode_ws(soc_model* m, int cap) {
                   std::make_pair((void*)w.h_x, (size_t)c.intermediate_size),
                   std::make_pair((void*)w.xo, (size_t)soc::kXcdGroups * c.hidden_size),
                   std::make_pair((void*)w.xd, (size_t)soc::kXcdGroups * c.hidden_size),
+                  std::make_pair((void*)w.xp, (size_t)c.hidden_size),
                   std::make_pair((void*)w.loc, (size_t)soc::kXcdGroups * w.loc_stride)})
     if ((e = hipMemset(pr.first, 0xff, pr.second * sizeof(uint32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.err, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
@@ -520,10 +522,10 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
   p.err = w.err;
   p.xo = w.xo;
   p.xd = w.xd;
+  p.xp = w.xp;
   p.loc = w.loc;
   p.loc_stride = w.loc_stride;
   p.xcd_ctr = w.xcd_ctr;
-  if (const char* ws = std::getenv("SOC_XCD_WEIGHTS")) p.weights_sync = std::atoi(ws);
   if (const char* sl = std::getenv("SOC_SPIN_SLEEP")) p.spin_sleep = std::max(0, std::atoi(sl));
   return p;
 }
@@ -574,31 +576,23 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
         for (size_t b = 0; b < xcd_nb; ++b)
           if (t[b * 16] != 0) tmin = std::min(tmin, t[b * 16]);
         std::fprintf(f, "xcd middle layer (us from earliest start):");
-        for (int pnt = 0; pnt < 13; ++pnt) {
+        for (int pnt = 0; pnt < 14; ++pnt) {
           std::vector<double> v;
           for (size_t b = 0; b < xcd_nb; ++b)
             if (t[b * 16 + pnt] != 0) v.push_back((static_cast<double>(t[b * 16 + pnt]) - tmin) * 0.01);
           std::sort(v.begin(), v.end());
-          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJep"[pnt], v.front(), v[v.size() / 2], v.back());
+          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJkbe"[pnt], v.front(), v[v.size() / 2], v.back());
         }
         std::fprintf(f, "\n");
-        // per XCD: latest published attention partial (point p) and its block, earliest / latest E poll return (e)
-        for (int g = 0; g < soc::kXcdGroups; ++g) {
-          double pmax = -1, emin = 1e30, emax = -1;
-          int jmax = -1;
-          for (int j = 0; j < soc::kXcdBlocks; ++j) {
+        // per block rank j (max over the XCDs) of point D and the first blocks with the latest D
+        std::fprintf(f, "D by rank:");
+        for (int j = 0; j < soc::kXcdBlocks; ++j) {
+          double dmax = -1;
+          for (int g = 0; g < soc::kXcdGroups; ++g) {
             const size_t b = static_cast<size_t>(g) * soc::kXcdBlocks + j;
-            if (t[b * 16 + 12] != 0) {
-              const double v = (static_cast<double>(t[b * 16 + 12]) - tmin) * 0.01;
-              if (v > pmax) { pmax = v; jmax = j; }
-            }
-            if (t[b * 16 + 11] != 0) {
-              const double v = (static_cast<double>(t[b * 16 + 11]) - tmin) * 0.01;
-              emin = std::min(emin, v);
-              emax = std::max(emax, v);
-            }
+            if (t[b * 16 + 4] != 0) dmax = std::max(dmax, (static_cast<double>(t[b * 16 + 4]) - tmin) * 0.01);
           }
-          std::fprintf(f, " xcd%d: p_max %.2f (j %d) e[%.2f %.2f]", g, pmax, jmax, emin, emax);
+          if (dmax >= 0) std::fprintf(f, " j%d:%.2f", j, dmax);
         }
         std::fprintf(f, "\n");
         std::fclose(f);
