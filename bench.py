@@ -5,8 +5,9 @@ Workload (headline): Qwen3-0.6B architecture, random-init fp16 weights N(0, 0.02
 prompt is prefilled (untimed), then W warmup and K timed greedy decode steps run with the sampled token fed back on
 the device. A "step" is one decode token. Also measured in the same run:
   * prefill of a 2048-token prompt (tok/s),
-  * the dominant decode kernel: k_decode_persistent (one launch = one whole token) when the device runs the
-    persistent decode, timed with HIP events on the stream it is launched on; the fused RMSNorm + QKV GEMV
+  * the dominant decode kernel: k_decode_xcd (one launch = one whole token, every layer split over the 8 XCDs) or
+    k_decode_persistent when the device runs that one, timed with HIP events on the stream it is launched on; the
+    fused RMSNorm + QKV GEMV
     (4096 x 1024 fp16, over weight copies larger than the 256 MB Infinity Cache) is reported beside it,
   * every decode projection shape (q, k/v, o, gate/up, down, LM head) as an fp16 GEMV at batch 1 and as the
     int8 / int4 group-quantized matmul (group 64, fp16 scales) at batch 1 and 8, in GB/s against 8 TB/s,
@@ -252,11 +253,12 @@ def cpu_baseline(cfg: S.QwenConfig, budget_s: float = 20.0):
                       f"(one decode step each; median {sec:.3f} s), 1 host thread of {os.cpu_count()}"}
 
 
-TRAFFIC_SUMMARY = ROOT / "profiles" / "k_decode_persistent_qwen3_0p6b_traffic.md"
+TRAFFIC_SUMMARY = {"xcd": ROOT / "profiles" / "k_decode_xcd_qwen3_0p6b_traffic.md",
+                   "persistent": ROOT / "profiles" / "k_decode_persistent_qwen3_0p6b_traffic.md"}
 
 
-def measured_traffic(path: Path = TRAFFIC_SUMMARY):
-    """HBM bytes per launch of the persistent decode kernel from the committed rocprofv3 counter summary
+def measured_traffic(path: Path):
+    """HBM bytes per launch of a one-launch decode kernel from its committed rocprofv3 counter summary
     (line `traffic_bytes_per_launch: <int>`), or None when no summary exists."""
     try:
         for line in path.read_text().splitlines():
@@ -318,12 +320,13 @@ def main() -> None:
     ragged = None if args.no_ragged else bench_ragged(ctx)
     ctx.close()
 
-    if path == "persistent":
+    if path in ("xcd", "persistent"):
         # one launch per token: the events around the K launches give the average launch duration (the short
         # gaps between back-to-back launches included)
-        roofline = {"kernel": "k_decode_persistent (whole decode token: 28 layers + LM head + argmax)",
+        kname = "k_decode_xcd" if path == "xcd" else "k_decode_persistent"
+        roofline = {"kernel": f"{kname} (whole decode token: 28 layers + LM head + argmax)",
                     "bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                    "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(TRAFFIC_SUMMARY[path]),
                     "avg_launch_us": round(ms_per_step * 1e3, 3), "alg_bytes_per_launch": int(bpt)}
     else:
         roofline = {"kernel": "k_gemv<4,2,EPI_STORE> (decode QKV projection 4096x1024 fp16)", "bound": "hbm",
