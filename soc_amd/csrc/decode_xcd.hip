@@ -40,6 +40,7 @@ constexpr int HMAX = 1024;        // hidden size covered by the register tiling
 constexpr int IMAX = 3072;        // intermediate size covered: I / 128 <= 24 gate/up pairs per block
 constexpr int PW = HD + 4;        // words per (block, query head) attention partial: 128 values, max, sum, 2 pad
 constexpr int NGRP = NT / 16;     // attention lane groups per block (16 lanes, 8 dims each)
+constexpr int KPG = 8;            // keys per lane group when every block takes all keys (S <= NGRP * KPG)
 constexpr float kNoKeys = -1e30f; // running max of a group that owns no key (finite: a tag bit must not make a NaN)
 
 // A block's rows of one weight matrix in registers: slot s = tid / TPR owns one row; thread t of the slot holds the
@@ -260,6 +261,16 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// Sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48) with the gfx950 cross-row swaps: with
+// both operands equal, the two results of v_permlane32_swap hold v[l] and v[l ^ 32] (in some order) in every lane,
+// and likewise for v_permlane16_swap with l ^ 16; no LDS round trip.
+__device__ __forceinline__ float sum_rows4(float v) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+}
+
 // Wave w < 8 of the block: its eighth of x = base + sum_k partial_k over the eight XCDs, then x * gain into xn and its
 // partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is completed by rms_scale). The base is
 // the tagged vector xbase (the previous layer's residual published by the other group) or, when xbase is null, the
@@ -398,10 +409,13 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   const bool h_live = o_slot < RH;
   const int iidx = g * IS + jj * RI + gu_slot; // gate/up row
   const bool i_live = gu_slot < RI;
-  // attention: block jj < na takes keys [k0, k1); lane group grp takes keys k0 + grp + 32 u
+  // attention: up to NGRP * KPG keys every block takes all keys (lane group grp: keys grp + 32 u); beyond that block
+  // jj < na takes keys [k0, k1) (lane group grp: keys k0 + grp + 32 u) and the blocks' partials are exchanged
+  const bool allkeys = S <= NGRP * KPG;
   int na, chunk;
   attn_split(S, na, chunk);
-  const int k0 = jj < na ? min(S, jj * chunk) : S, k1 = jj < na ? min(S, k0 + chunk) : S;
+  const int k0 = allkeys ? 0 : (jj < na ? min(S, jj * chunk) : S);
+  const int k1 = allkeys ? S : (jj < na ? min(S, k0 + chunk) : S);
   int lane = tid & 63, grp = tid >> 4, sub = tid & 15;
 
   Slice<T::TPR_Q, T::CPT_Q> sq;
@@ -431,6 +445,20 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     slice_load(su, i_live ? W7 + static_cast<size_t>(ir) * H : nullptr, H);
     rows_to_lds(W8 + static_cast<size_t>(hr) * I + g * IS, I, RH, IS, wd);
     kv_fetch(layer, k0 + grp);
+    if (allkeys) {
+      // this block's share of KV head g's cached keys and values into the XCD's L2 (keys jj + 16 m): every block
+      // of the group then reads them from there
+      const int p = jj + NBG * (tid >> 4);
+      if (p < pos) {
+        const size_t base = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD +
+                            static_cast<size_t>(p) * HD + sub * 8;
+        const u32x4 pfk = load16(a.kcache + base);
+        const u32x4 pfv = load16(a.vcache + base);
+        // the words are only kept alive (a compare that is practically never true, and harmless if it is); the
+        // wait this implies is free: the group has nothing to do until the other group's layer is done
+        if (pfk.x == 0x9e3779b9u && pfv.y == 0x7f7f7f7fu && pfk.z == pfv.w) c.flag[7] = 1;
+      }
+    }
   };
   if (pgrp < a.L) stream(pgrp);
 
@@ -483,6 +511,120 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     }
     XTRACE(3);
     XSYNC();  // #2: qs, kn, vn
+    if (allkeys) {
+      // ---- D, up to 256 keys: every block takes all S keys of KV head g (the softmax of
+      //      grouped_query_attention.cpp:105-136): scores and the block max per head, then base-2 weights; the 4
+      //      lane groups of a wave add with cross-row swaps, the 8 waves through LDS. No hand-off between blocks. ----
+      const float qscale = a.scale * 1.44269504088896341f;
+      // the head's cached keys/values through buffer resources (scalar base, 32-bit lane offsets; keys at or past
+      // `pos` read as zero)
+      const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache + kvb, 0, pos * HD * 2, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache + kvb, 0, pos * HD * 2, 0x00020000);
+      const int kvo = (grp * HD + sub * 8) * 2;
+      float qreg[G][8], sc[KPG][G], mloc[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        mloc[h] = kNoKeys;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
+      }
+#pragma unroll
+      for (int u0 = 0; u0 < KPG; u0 += 4) {
+        u32x4 kw[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          kw[v] = (u0 + v == 0) ? kr : __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, NGRP * (u0 + v) * HD * 2, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int p = grp + NGRP * (u0 + v);
+          float kf[8];
+          if (p == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
+          } else {
+            f16x8_to_f32(kw[v], kf);
+          }
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
+            const float sv = group_sum<16>(d);
+            sc[u0 + v][h] = p < S ? sv : kNoKeys;
+            mloc[h] = fmaxf(mloc[h], sc[u0 + v][h]);
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float mw = wave_max(mloc[h]);
+        if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
+      }
+      XSYNC();  // #2a: wave maxima
+      float mblk[G], o[G][8], l[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float M = kNoKeys;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
+        mblk[h] = M;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
+      }
+#pragma unroll
+      for (int u0 = 0; u0 < KPG; u0 += 4) {
+        u32x4 vw[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int p = grp + NGRP * (u0 + v);
+          if (p < S) {
+            float vf[8];
+            if (p == pos) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+            } else {
+              f16x8_to_f32(vw[v], vf);
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+              const float pw = __builtin_amdgcn_exp2f(sc[u0 + v][h] - mblk[h]);
+              l[h] += pw;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
+            }
+          }
+        }
+      }
+      // the wave's 4 lane groups added across rows; row 0 writes the wave's sums
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float ov = sum_rows4(o[h][i]);
+          if (lane < 16) gpart[(wid * G + h) * PW + sub * 8 + i] = ov;
+        }
+        const float lv = sum_rows4(l[h]);
+        if (lane == 0) gpart[(wid * G + h) * PW + HD + 1] = lv;
+      }
+      XSYNC();  // #2b: the 8 waves' sums
+      for (int t = tid; t < G * HD; t += NT) {
+        const int h = t / HD, d = t % HD;
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) {
+          L += gpart[(w * G + h) * PW + HD + 1];
+          O += gpart[(w * G + h) * PW + d];
+        }
+        att[h * HD + d] = O / L;
+      }
+    } else {
     // ---- D: attention over keys [k0, k1) (the softmax of grouped_query_attention.cpp:105-136) in two passes over the
     //      block's keys: scores and the block's max per head, then base-2 weights relative to that max, so that the
     //      lane groups' partials merge by plain sums. q is prescaled by scale * log2(e). ----
@@ -630,6 +772,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       }
     }
     XTRACE(5);
+    }  // the split path
     XSYNC();  // #3: merged attention output
     // ---- F: partial o_proj over the XCD's query columns ----
     {
