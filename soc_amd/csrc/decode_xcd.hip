@@ -512,118 +512,125 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     XTRACE(3);
     XSYNC();  // #2: qs, kn, vn
     if (allkeys) {
-      // ---- D, up to 256 keys: every block takes all S keys of KV head g (the softmax of
-      //      grouped_query_attention.cpp:105-136): scores and the block max per head, then base-2 weights; the 4
-      //      lane groups of a wave add with cross-row swaps, the 8 waves through LDS. No hand-off between blocks. ----
-      const float qscale = a.scale * 1.44269504088896341f;
-      // the head's cached keys/values through buffer resources (scalar base, 32-bit lane offsets; keys at or past
-      // `pos` read as zero)
-      const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
-      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache + kvb, 0, pos * HD * 2, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache + kvb, 0, pos * HD * 2, 0x00020000);
-      const int kvo = (grp * HD + sub * 8) * 2;
-      float qreg[G][8], sc[KPG][G], mloc[G];
+      // NK keys per lane group (4 or 8): a straight-line body for each, chosen by the uniform S
+      auto all_keys = [&](auto nk) {
+        constexpr int NK = decltype(nk)::value;
+        // ---- D, up to 256 keys: every block takes all S keys of KV head g (the softmax of
+        //      grouped_query_attention.cpp:105-136): scores and the block max per head, then base-2 weights; the 4
+        //      lane groups of a wave add with cross-row swaps, the 8 waves through LDS. No hand-off between blocks. ----
+        const float qscale = a.scale * 1.44269504088896341f;
+        // the head's cached keys/values through buffer resources (scalar base, 32-bit lane offsets; keys at or past
+        // `pos` read as zero)
+        const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache + kvb, 0, pos * HD * 2, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache + kvb, 0, pos * HD * 2, 0x00020000);
+        const int kvo = (grp * HD + sub * 8) * 2;
+        float qreg[G][8], sc[NK][G], mloc[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        mloc[h] = kNoKeys;
+        for (int h = 0; h < G; ++h) {
+          mloc[h] = kNoKeys;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
-      }
-#pragma unroll
-      for (int u0 = 0; u0 < KPG; u0 += 4) {
-        u32x4 kw[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          kw[v] = (u0 + v == 0) ? kr : __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, NGRP * (u0 + v) * HD * 2, 0);
+          for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
         }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int p = grp + NGRP * (u0 + v);
-          float kf[8];
-          if (p == pos) {
+        for (int u0 = 0; u0 < NK; u0 += 4) {
+          u32x4 kw[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-          } else {
-            f16x8_to_f32(kw[v], kf);
+          for (int v = 0; v < 4; ++v) {
+            kw[v] = (u0 + v == 0) ? kr : __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, NGRP * (u0 + v) * HD * 2, 0);
           }
 #pragma unroll
-          for (int h = 0; h < G; ++h) {
-            float d = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
-            const float sv = group_sum<16>(d);
-            sc[u0 + v][h] = p < S ? sv : kNoKeys;
-            mloc[h] = fmaxf(mloc[h], sc[u0 + v][h]);
-          }
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float mw = wave_max(mloc[h]);
-        if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
-      }
-      XSYNC();  // #2a: wave maxima
-      float mblk[G], o[G][8], l[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float M = kNoKeys;
-#pragma unroll
-        for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
-        mblk[h] = M;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
-      }
-#pragma unroll
-      for (int u0 = 0; u0 < KPG; u0 += 4) {
-        u32x4 vw[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int p = grp + NGRP * (u0 + v);
-          if (p < S) {
-            float vf[8];
+          for (int v = 0; v < 4; ++v) {
+            const int p = grp + NGRP * (u0 + v);
+            float kf[8];
             if (p == pos) {
 #pragma unroll
-              for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+              for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
             } else {
-              f16x8_to_f32(vw[v], vf);
+              f16x8_to_f32(kw[v], kf);
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-              const float pw = __builtin_amdgcn_exp2f(sc[u0 + v][h] - mblk[h]);
-              l[h] += pw;
+              float d = 0.0f;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
+              for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
+              const float sv = group_sum<16>(d);
+              sc[u0 + v][h] = p < S ? sv : kNoKeys;
+              mloc[h] = fmaxf(mloc[h], sc[u0 + v][h]);
             }
           }
         }
-      }
-      // the wave's 4 lane groups added across rows; row 0 writes the wave's sums
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float ov = sum_rows4(o[h][i]);
-          if (lane < 16) gpart[(wid * G + h) * PW + sub * 8 + i] = ov;
+        for (int h = 0; h < G; ++h) {
+          const float mw = wave_max(mloc[h]);
+          if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
         }
-        const float lv = sum_rows4(l[h]);
-        if (lane == 0) gpart[(wid * G + h) * PW + HD + 1] = lv;
-      }
-      XSYNC();  // #2b: the 8 waves' sums
-      for (int t = tid; t < G * HD; t += NT) {
-        const int h = t / HD, d = t % HD;
-        float L = 0.0f, O = 0.0f;
+        XSYNC();  // #2a: wave maxima
+        float mblk[G], o[G][8], l[G];
 #pragma unroll
-        for (int w = 0; w < NT / 64; ++w) {
-          L += gpart[(w * G + h) * PW + HD + 1];
-          O += gpart[(w * G + h) * PW + d];
+        for (int h = 0; h < G; ++h) {
+          float M = kNoKeys;
+#pragma unroll
+          for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
+          mblk[h] = M;
+          l[h] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
         }
-        att[h * HD + d] = O / L;
-      }
+#pragma unroll
+        for (int u0 = 0; u0 < NK; u0 += 4) {
+          u32x4 vw[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int p = grp + NGRP * (u0 + v);
+            if (p < S) {
+              float vf[8];
+              if (p == pos) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+              } else {
+                f16x8_to_f32(vw[v], vf);
+              }
+#pragma unroll
+              for (int h = 0; h < G; ++h) {
+                const float pw = __builtin_amdgcn_exp2f(sc[u0 + v][h] - mblk[h]);
+                l[h] += pw;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
+              }
+            }
+          }
+        }
+        // the wave's 4 lane groups added across rows; row 0 writes the wave's sums
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float ov = sum_rows4(o[h][i]);
+            if (lane < 16) gpart[(wid * G + h) * PW + sub * 8 + i] = ov;
+          }
+          const float lv = sum_rows4(l[h]);
+          if (lane == 0) gpart[(wid * G + h) * PW + HD + 1] = lv;
+        }
+        XSYNC();  // #2b: the 8 waves' sums
+        for (int t = tid; t < G * HD; t += NT) {
+          const int h = t / HD, d = t % HD;
+          float L = 0.0f, O = 0.0f;
+#pragma unroll
+          for (int w = 0; w < NT / 64; ++w) {
+            L += gpart[(w * G + h) * PW + HD + 1];
+            O += gpart[(w * G + h) * PW + d];
+          }
+          att[h * HD + d] = O / L;
+        }
+        return true;
+      };
+      if (!(S <= NGRP * 4 ? all_keys(std::integral_constant<int, 4>{}) : all_keys(std::integral_constant<int, KPG>{})))
+        return false;
     } else {
     // ---- D: attention over keys [k0, k1) (the softmax of grouped_query_attention.cpp:105-136) in two passes over the
     //      block's keys: scores and the block's max per head, then base-2 weights relative to that max, so that the
