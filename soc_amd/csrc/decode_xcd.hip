@@ -532,12 +532,18 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
         }
+        u32x4 vw0[4];
 #pragma unroll
         for (int u0 = 0; u0 < NK; u0 += 4) {
           u32x4 kw[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             kw[v] = (u0 + v == 0) ? kr : __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, NGRP * (u0 + v) * HD * 2, 0);
+          }
+          if constexpr (NK == 4) {  // one round: its values are requested with the keys
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              vw0[v] = v == 0 ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * v * HD * 2, 0);
           }
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
@@ -565,7 +571,9 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
           const float mw = wave_max(mloc[h]);
           if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
         }
+        XTRACE(4);
         XSYNC();  // #2a: wave maxima
+        XTRACE(5);
         float mblk[G], o[G][8], l[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
@@ -582,7 +590,10 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
           u32x4 vw[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
+            if constexpr (NK == 4)
+              vw[v] = vw0[v];
+            else
+              vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
           }
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
@@ -616,7 +627,9 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
           const float lv = sum_rows4(l[h]);
           if (lane == 0) gpart[(wid * G + h) * PW + HD + 1] = lv;
         }
+        XTRACE(11);
         XSYNC();  // #2b: the 8 waves' sums
+        XTRACE(12);
         for (int t = tid; t < G * HD; t += NT) {
           const int h = t / HD, d = t % HD;
           float L = 0.0f, O = 0.0f;
@@ -627,6 +640,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
           }
           att[h * HD + d] = O / L;
         }
+        XTRACE(13);
         return true;
       };
       if (!(S <= NGRP * 4 ? all_keys(std::integral_constant<int, 4>{}) : all_keys(std::integral_constant<int, KPG>{})))
