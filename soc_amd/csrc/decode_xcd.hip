@@ -367,6 +367,117 @@ __device__ __forceinline__ bool cross_reduce(const Ctx& c, int w, const uint32_t
   return true;
 }
 
+// Two-stage form of the same reduction, x = base + sum_k P_k over the eight XCDs' partials P_k (src, [8][H] words),
+// that reads each remote partial once per XCD instead of once per block:
+// stage 1 (wave 0 of a block with do1): the block's 1/16 of the elements, quads jj * H/64 ..; base from base_loc
+//   (XCD-local words) or, if null, from xres; x goes to out[0, H) and the block's sum of squares of x to out[H + jj],
+//   as XCD-local words with the same tag;
+// stage 2 (every wave): all of x and the 16 sums from out; x into xres, x * gain into xn, red[0..7] = pair sums of the
+//   16 sums (rms_scale adds them in a fixed order). Every block reads the same words, so x and the norm agree in every
+//   block of every XCD. The caller's barrier publishes xres, xn and red.
+__device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool do1, const uint32_t* src,
+                                              const uint32_t* base_loc, uint32_t tag, uint32_t* out, const f16* gain,
+                                              float* xres, float* xn, float* red) {
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
+  const int H = c.a.H;
+  const u32x4 filler = {tag, tag, tag, tag};
+  const uint64_t t0 = now_ticks();
+  auto failed = [&]() {
+    __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c.flag[0] = 1;
+  };
+  if (w == 0 && do1) {
+    const int k = lane & 7, nq1 = H / 64, qb = jj * nq1;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(base_loc != nullptr ? base_loc : src), 0, H * 4, 0x00020000);
+    u32x4 v[2], bq[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int qi = (lane >> 3) + 8 * i;
+      const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
+      v[i] = live ? ll_peek_buf4(r, (k * H + 4 * (qb + qi)) * 4) : filler;
+      bq[i] = blive ? ll_peek_buf4(rb, (qb + qi) * 16) : filler;
+    }
+    uint32_t spins = 0;
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) all = all && tw_quad_ok(v[i], tag) && tw_quad_ok(bq[i], tag);
+      if (__all(all)) break;
+      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+        failed();
+        return false;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int qi = (lane >> 3) + 8 * i;
+        const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
+        if (live && !tw_quad_ok(v[i], tag)) v[i] = ll_peek_buf4(r, (k * H + 4 * (qb + qi)) * 4);
+        if (blive && !tw_quad_ok(bq[i], tag)) bq[i] = ll_peek_buf4(rb, (qb + qi) * 16);
+      }
+    }
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int qi = (lane >> 3) + 8 * i, q = qb + qi;
+      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
+      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
+      if (qi < nq1 && k == 0) {
+        f32x4 x = base_loc != nullptr ? f32x4{tw_val(bq[i].x), tw_val(bq[i].y), tw_val(bq[i].z), tw_val(bq[i].w)}
+                                      : *reinterpret_cast<const f32x4*>(xres + 4 * q);
+        x[0] += s0;
+        x[1] += s1;
+        x[2] += s2;
+        x[3] += s3;
+        u32x4 wq;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wq[e] = tw_pack(x[e], tag);
+          const float xr = tw_val(wq[e]);
+          ss += xr * xr;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(wq, ro, q * 16, 0, 0);
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) ll_store_local(out, H + jj, ss, tag);
+  }
+  // stage 2: wave w takes quads w * H/32 + lane of x; wave 0's lanes 32..35 take the 16 sums
+  const int per = H / 32;
+  const bool xlive = lane < per, slive = w == 0 && lane >= 32 && lane < 36;
+  const int off = xlive ? (w * per + lane) * 16 : (H + 4 * (lane - 32)) * 4;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
+  u32x4 v = (xlive || slive) ? ll_peek_buf4(ro, off) : filler;
+  uint32_t spins = 0;
+  while (!__all(tw_quad_ok(v, tag))) {
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+      failed();
+      return false;
+    }
+    if (!tw_quad_ok(v, tag)) v = ll_peek_buf4(ro, off);
+  }
+  if (xlive) {
+    const int q = w * per + lane;
+    const f32x4 x = {tw_val(v.x), tw_val(v.y), tw_val(v.z), tw_val(v.w)};
+    const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = x[e] * static_cast<float>(g4[e]);
+    *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+    *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+  }
+  if (slive) {
+    const int m = lane - 32;
+    red[2 * m] = tw_val(v.x) + tw_val(v.y);
+    red[2 * m + 1] = tw_val(v.z) + tw_val(v.w);
+  }
+  return true;
+}
+
 // The layers l % 2 == p of one decode step for a block of group p, then the final hidden state (all blocks).
 template <int G>
 __device__ __forceinline__ bool run_layers(const Ctx& c) {
@@ -397,6 +508,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   uint32_t* loc_qkv = loc;                                  // [(G + 2) HD]
   uint32_t* loc_att = loc + (((G + 2) * HD + 63) & ~63);    // [G][NBX][PW]
   uint32_t* loc_h = loc_att + ((NBX * G * PW + 63) & ~63);  // [IS]
+  uint32_t* loc_xa = loc_h + ((IS + 63) & ~63);               // [H + 16]: x after the attention-input reduction
+  uint32_t* loc_xg = loc_xa + HMAX + 64;                      // [H + 16]: x' after the o_proj reduction
   // this block's q/k/v row: local row lr of the XCD's (G + 2) * 128 (q heads, key, value)
   const int q_slot = tid / T::TPR_Q;
   const int q_lr = jj * T::RQ + q_slot;
@@ -473,8 +586,10 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     XTRACE(0);
     // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
     wait_mem();  // this wave's rows of the layer have landed (its LDS rows are published by the barrier below)
-    cross_reduce(c, wid, a.xd, a.xp, (tag - 1u) & 3u,
-                 layer == 0 ? a.embed + static_cast<size_t>(c.token) * H : nullptr, W[0], xres, xn, red);
+    if (layer == 0)
+      cross_reduce(c, wid, a.xd, nullptr, tag, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xn, red);
+    else
+      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xn, red);
     XTRACE(1);
     XSYNC();  // #1
     // ---- B: q/k/v rows of RMSNorm(x) ----
@@ -802,14 +917,9 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     }
     XTRACE(6);
     // ---- G: x' = x + sum_k O_k, RMSNorm input ----
-    cross_reduce(c, wid, a.xo, nullptr, tag, nullptr, W[1], xres, xn, red);
+    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xn, red);  // x' also for the other group
     XTRACE(7);
     XSYNC();  // #4
-    // the block's rows of x' for the other group's next layer
-    {
-      const int rows = H / (NX * NBG), r0 = (g * NBG + jj) * rows;
-      if (tid < rows) ll_store_buf(a.xp, r0 + tid, xres[r0 + tid], tag);
-    }
     // ---- H: gate/up of RMSNorm(x') + SwiGLU (qwen_mlp.cpp:31) on the block's share of the XCD's slice ----
     {
       const float scale = rms_scale(red, H, a.eps);
@@ -846,8 +956,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     }
   }
   // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks)
-  cross_reduce(c, wid, a.xd, a.xp, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, nullptr, a.final_norm, xres, xn,
-               red);
+  cross_reduce2(c, wid, jj, pgrp == 0, a.xd, loc_xg, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, loc_xa,
+                a.final_norm, xres, xn, red);
   XTRACE0(a.L);
   XSYNC();
   return true;
@@ -1025,7 +1135,7 @@ hipError_t xcd_blocks_per_cu(int G, int* blocks) {
 }
 
 int xcd_loc_stride(int G, int I) {
-  return (((G + 2) * HD + 63) & ~63) + ((NBX * G * PW + 63) & ~63) + ((I / NX + 63) & ~63);
+  return (((G + 2) * HD + 63) & ~63) + ((NBX * G * PW + 63) & ~63) + ((I / NX + 63) & ~63) + 2 * (HMAX + 64);
 }
 
 // Shapes the partition and the register tiling cover: 8 KV heads of 128 dims (one per XCD), G = 1 or 2 query heads
