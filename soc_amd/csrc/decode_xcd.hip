@@ -377,7 +377,7 @@ __device__ __forceinline__ bool cross_reduce(const Ctx& c, int w, const uint32_t
 //   block of every XCD. The caller's barrier publishes xres, xn and red.
 __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool do1, const uint32_t* src,
                                               const uint32_t* base_loc, uint32_t tag, uint32_t* out, const f16* gain,
-                                              float* xres, float* xn, float* red) {
+                                              float* xres, float* xn, float* red, int trace_pt = -1) {
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
   const int H = c.a.H;
@@ -445,6 +445,8 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
     }
     ss = wave_sum(ss);
     if (lane == 0) ll_store_local(out, H + jj, ss, tag);
+    if (trace_pt >= 0 && c.a.trace != nullptr && threadIdx.x == 0)
+      c.a.trace[(c.g * NBX + c.j) * 16 + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
   }
   // stage 2: wave w takes quads w * H/32 + lane of x; wave 0's lanes 32..35 take the 16 sums
   const int per = H / 32;
@@ -589,7 +591,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     if (layer == 0)
       cross_reduce(c, wid, a.xd, nullptr, tag, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xn, red);
     else
-      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xn, red);
+      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xn, red,
+                    layer == a.L / 2 ? 15 : -1);
     XTRACE(1);
     XSYNC();  // #1
     // ---- B: q/k/v rows of RMSNorm(x) ----
@@ -681,21 +684,12 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
             }
           }
         }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float mw = wave_max(mloc[h]);
-          if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
-        }
+        // weights relative to the wave's max (no block barrier); the 8 waves' sums are rescaled when merged
         XTRACE(4);
-        XSYNC();  // #2a: wave maxima
-        XTRACE(5);
         float mblk[G], o[G][8], l[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          float M = kNoKeys;
-#pragma unroll
-          for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
-          mblk[h] = M;
+          mblk[h] = wave_max(mloc[h]);
           l[h] = 0.0f;
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
@@ -740,18 +734,25 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
             if (lane < 16) gpart[(wid * G + h) * PW + sub * 8 + i] = ov;
           }
           const float lv = sum_rows4(l[h]);
-          if (lane == 0) gpart[(wid * G + h) * PW + HD + 1] = lv;
+          if (lane == 0) {
+            gpart[(wid * G + h) * PW + HD + 1] = lv;
+            gpart[(wid * G + h) * PW + HD + 2] = mblk[h];
+          }
         }
         XTRACE(11);
         XSYNC();  // #2b: the 8 waves' sums
         XTRACE(12);
         for (int t = tid; t < G * HD; t += NT) {
           const int h = t / HD, d = t % HD;
+          float M = kNoKeys;
+#pragma unroll
+          for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[(w * G + h) * PW + HD + 2]);
           float L = 0.0f, O = 0.0f;
 #pragma unroll
           for (int w = 0; w < NT / 64; ++w) {
-            L += gpart[(w * G + h) * PW + HD + 1];
-            O += gpart[(w * G + h) * PW + d];
+            const float f = __builtin_amdgcn_exp2f(gpart[(w * G + h) * PW + HD + 2] - M);  // 0 for a wave without keys
+            L += gpart[(w * G + h) * PW + HD + 1] * f;
+            O += gpart[(w * G + h) * PW + d] * f;
           }
           att[h * HD + d] = O / L;
         }
@@ -917,7 +918,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     }
     XTRACE(6);
     // ---- G: x' = x + sum_k O_k, RMSNorm input ----
-    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xn, red);  // x' also for the other group
+    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xn, red,  // x' also for the other group
+                  layer == a.L / 2 ? 14 : -1);
     XTRACE(7);
     XSYNC();  // #4
     // ---- H: gate/up of RMSNorm(x') + SwiGLU (qwen_mlp.cpp:31) on the block's share of the XCD's slice ----

@@ -576,12 +576,12 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
         for (size_t b = 0; b < xcd_nb; ++b)
           if (t[b * 16] != 0) tmin = std::min(tmin, t[b * 16]);
         std::fprintf(f, "xcd middle layer (us from earliest start):");
-        for (int pnt = 0; pnt < 14; ++pnt) {
+        for (int pnt = 0; pnt < 16; ++pnt) {
           std::vector<double> v;
           for (size_t b = 0; b < xcd_nb; ++b)
             if (t[b * 16 + pnt] != 0) v.push_back((static_cast<double>(t[b * 16 + pnt]) - tmin) * 0.01);
           std::sort(v.begin(), v.end());
-          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJkbe"[pnt], v.front(), v[v.size() / 2], v.back());
+          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJkbega"[pnt], v.front(), v[v.size() / 2], v.back());
         }
         std::fprintf(f, "\n");
         // per block rank j (max over the XCDs) of point D and the first blocks with the latest D
