@@ -957,33 +957,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       stream(layer + 2);
     }
   }
-  // the group that does not compute the last layer reads its blocks' LM-head rows once, in 128 KB rounds for at most
-  // 14 us, while the other group computes it: the head then finds those lines in the memory-side cache
-  const int last_grp = (a.L - 1) % 2;
-  if (pgrp != last_grp) {
-    const int b = g * NBX + c.j, rv = (a.V + NX * NBX - 1) / (NX * NBX);
-    const int v0 = min(a.V, b * rv), v1 = min(a.V, v0 + rv);
-    const char* base = reinterpret_cast<const char*>(a.lm_head) + static_cast<size_t>(v0) * H * 2;
-    const int bytes = (v1 - v0) * H * 2;
-    const uint64_t t0 = now_ticks();
-    uint32_t acc = 0;
-    for (int off = 0; off < bytes; off += NT * 16 * 16) {
-      u32x4 w[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int o = off + (i * NT + tid) * 16;
-        w[i] = o < bytes ? load16(base + o) : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc ^= w[i].x ^ w[i].w;
-      if (now_ticks() - t0 > 1400) break;
-    }
-    // keeps the loads (a compare that is practically never true, and harmless if it is)
-    if (acc == 0x9e3779b9u) c.flag[7] = 1;
-  }
-  // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks; stage 1 by
-  // the group that computed the last layer)
-  cross_reduce2(c, wid, jj, pgrp == last_grp, a.xd, loc_xg, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, loc_xa,
+  // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks)
+  cross_reduce2(c, wid, jj, pgrp == 0, a.xd, loc_xg, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, loc_xa,
                 a.final_norm, xres, xn, red);
   XTRACE0(a.L);
   XSYNC();
