@@ -448,10 +448,10 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
     if (trace_pt >= 0 && c.a.trace != nullptr && threadIdx.x == 0)
       c.a.trace[(c.g * NBX + c.j) * 16 + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
   }
-  // stage 2: wave w takes quads w * H/32 + lane of x; wave 0's lanes 32..35 take the 16 sums
-  const int per = H / 32;
-  const bool xlive = lane < per, slive = w == 0 && lane >= 32 && lane < 36;
-  const int off = xlive ? (w * per + lane) * 16 : (H + 4 * (lane - 32)) * 4;
+  // stage 2: waves 0..3 take quad w * H/16 + lane of x, wave 4's lanes 0..3 the 16 sums (fewer waves polling L2)
+  const int per = H / 16;
+  const bool xlive = w < 4 && lane < per, slive = w == 4 && lane < 4;
+  const int off = xlive ? (w * per + lane) * 16 : (H + 4 * lane) * 4;
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
   u32x4 v = (xlive || slive) ? ll_peek_buf4(ro, off) : filler;
   uint32_t spins = 0;
@@ -473,7 +473,7 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
     *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
   }
   if (slive) {
-    const int m = lane - 32;
+    const int m = lane;
     red[2 * m] = tw_val(v.x) + tw_val(v.y);
     red[2 * m + 1] = tw_val(v.z) + tw_val(v.w);
   }
