@@ -666,8 +666,10 @@ __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
   Ctx c{a, static_cast<int>(blockIdx.x), ng, a.state[0], a.state[1],
         (static_cast<uint32_t>(a.state[2]) - 1u) * static_cast<uint32_t>(a.L),
         lds, lds + a.xs_cap, reinterpret_cast<int*>(red + 16), red + 32, reinterpret_cast<int*>(red + 48), red + 96};
-  if (tid == 0) c.flag[0] = 0;
+  // a launch queued behind a failed one leaves at once (the failed step did not advance the step count)
+  if (tid == 0) c.flag[0] = err_raised(a.err) ? 1 : 0;
   __syncthreads();
+  if (c.flag[0] != 0) return;
   const bool recv = wid == RECV;
   bool ok;
   if (c.b >= ng) {

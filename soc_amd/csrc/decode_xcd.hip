@@ -1,28 +1,42 @@
 // decode_xcd.hip - one-launch decode step for batch 1 with every layer partitioned over the eight XCDs of MI355X, the
-// layers alternating between two groups of blocks.
+// layers alternating between two groups of blocks, and every dot product of a layer on the matrix cores.
 //
 // Block (g, j): XCD g, read from the XCC_ID hardware register, and rank j < 32 among the blocks of this launch that
 // arrived on it. Group p = j / 16 computes the layers l with l % 2 == p while the other group streams the weight rows
-// of its next layer into registers: a CU never waits on hand-offs while its own weight loads are in flight (its
-// vector memory requests would queue behind them). XCD g owns KV head g (every Qwen3 model has 8 KV heads) with its
-// G = nq / 8 query heads and 1/8 of every matrix: the q/k/v rows of its heads, the o_proj columns of its query heads,
-// the gate/up rows and down_proj columns of its eighth of the intermediate dimension; the group's 16 blocks of the
-// XCD split that share. Per layer (reference: QwenBlock::ForwardCached, Mac/cpu/src/qwen_block.cpp:63-73, with
+// of its next layer into registers and LDS: a CU never waits on hand-offs while its own weight loads are in flight
+// (its vector memory requests would queue behind them). XCD g owns KV head g (every Qwen3 model has 8 KV heads) with
+// its G = nq / 8 query heads and 1/8 of every matrix: the q/k/v rows of its heads, the o_proj columns of its query
+// heads, the gate/up rows and down_proj columns of its eighth of the intermediate dimension; the group's 16 blocks of
+// the XCD split that share. Per layer (reference: QwenBlock::ForwardCached, Mac/cpu/src/qwen_block.cpp:63-73, with
 // QwenAttention::ForwardCached and QwenMLP::Forward):
 //   A  x = x' + sum_k D_k: the previous layer's residual and its eight XCDs' partial down outputs (cross-XCD), RMSNorm
 //   B  the block's q/k/v rows of the XCD's heads                                   -> XCD-local exchange
 //   C  the XCD's q/k/v; per-head QK-RMSNorm + RoPE; rank 0 appends k and v to the cache
-//   D  causal attention over the block's share of the keys; the 32 lane groups' partials merged in LDS
-//   E  the XCD's block partials (XCD-local), log-sum-exp merge
+//   D  causal attention over the block's share of the keys, 32-key tiles per wave, the waves' partials merged in LDS
+//   E  the XCD's block partials (XCD-local), log-sum-exp merge (more than 256 keys only)
 //   F  O_g = Wo[the block's rows][the XCD's query columns] . attn                  -> cross-XCD exchange
 //   G  x' = x + sum_k O_k (cross-XCD), RMSNorm; the block publishes its rows of x' for the other group
 //   H  h = silu(gate) * up on the block's share of the XCD's intermediate slice     -> XCD-local exchange
 //   I  the XCD's h slice (XCD-local)
 //   J  D_g = Wd[the block's rows][the slice's columns] . h                         -> cross-XCD exchange
+//
+// Matrix cores (v_mfma_f32_16x16x32_f16) for a vector times a matrix: the fp32 vector enters as two fp16 rows of the
+// A operand, hi = f16(v) and lo = f16((v - hi) 2^11) (about 22 bits of v; the weights are exact fp16, every product is
+// exact in fp32 and the sums are fp32), 16 weight rows form the B operand, and lanes 0..15 receive row j's
+// hi-sum and lo-sum, added as hi + lo 2^-11. The other 14 rows of A are zero: at batch 1 the matrix cores are idle
+// most of the time anyway, and one MFMA replaces 512 FMAs and their fp16 conversions on the vector ALUs, which at
+// one 512-thread block per CU were what bounded every compute phase. q/k/v and gate/up rows sit in registers (each
+// wave holds 1/8 of K for all of the block's rows, and the eight partial sums meet in LDS); o_proj and down_proj rows
+// sit in LDS with 16-byte chunks XOR-swizzled by row (conflict-free operand reads) and each wave takes 16 rows over
+// the whole K. Attention: a wave takes 32-key tiles; S^T = q . K^T with q's hi/lo rows (prescaled by scale log2 e) as
+// A and 16 keys straight from the cache as B, base-2 softmax with a running maximum per wave, then O = P . V with P's
+// hi/lo rows as A and V^T from the transposing LDS read of the tile (brought global -> LDS by range-checked buffer
+// loads, so keys at or past `pos` read as zero).
+//
 // Cross-XCD words are written with device-scope stores; XCD-local ones with plain stores served by the XCD's own L2
 // (see exchange.h). Every block of the computing group holds the whole residual stream in LDS, computed in the same
-// order from the same words, so all blocks hold identical bits. All eight waves of a block poll, compute and hold
-// weight rows. Every wait is bounded; a timeout raises the error flag and the grid drains.
+// order from the same words, so all blocks hold identical bits. Every wait is bounded; a timeout raises the error flag
+// and the grid drains.
 #include <algorithm>
 
 #include "exchange.h"
@@ -32,19 +46,31 @@ namespace soc {
 
 namespace {
 
-constexpr int NT = 512;   // threads per block
-constexpr int HD = 128;   // head dim
+constexpr int NT = 512;           // threads per block
+constexpr int NW = NT / 64;       // waves per block
+constexpr int HD = 128;           // head dim
 constexpr int NX = kXcdGroups, NBX = kXcdBlocks;
 constexpr int NBG = NBX / 2;      // blocks of one group on one XCD
 constexpr int HMAX = 1024;        // hidden size covered by the register tiling
 constexpr int IMAX = 3072;        // intermediate size covered: I / 128 <= 24 gate/up pairs per block
+constexpr int ISM = IMAX / NX;    // intermediate slice of an XCD at most
 constexpr int PW = HD + 4;        // words per (block, query head) attention partial: 128 values, max, sum, 2 pad
-constexpr int NGRP = NT / 16;     // attention lane groups per block (16 lanes, 8 dims each)
-constexpr int KPG = 8;            // keys per lane group when every block takes all keys (S <= NGRP * KPG)
-constexpr float kNoKeys = -1e30f; // running max of a group that owns no key (finite: a tag bit must not make a NaN)
+constexpr int KT = 32;            // keys per attention tile (the K depth of one P . V MFMA)
+constexpr int KALL = NW * KT;     // up to this many keys every block computes its KV head's whole attention
+constexpr float kNoKeys = -1e30f; // running max of a wave or block that owns no key (finite: exp2 of it is 0)
+constexpr float kLo = 1.0f / 2048.0f;
 
-// A block's rows of one weight matrix in registers: slot s = tid / TPR owns one row; thread t of the slot holds the
-// 8-half chunks at k = 8 (t + TPR c), c < CPT.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __fp16 hv4 __attribute__((__vector_size__(4 * sizeof(__fp16))));  // operand type of the transposing read
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
+__device__ __forceinline__ f32x4 mfma16(h8 a, h8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// A block's LM-head rows in registers: slot s = tid / TPR owns one row; thread t of the slot holds the 8-half chunks
+// at k = 8 (t + TPR c), c < CPT.
 template <int TPR, int CPT>
 struct Slice {
   u32x4 w[CPT];
@@ -81,86 +107,95 @@ __device__ __forceinline__ float slice_dot(const Slice<TPR, CPT>& s, const float
   return group_sum<TPR>(acc);
 }
 
-// A block of `rows` rows of `K` halves (row r at src + r * ld) straight to LDS (dst[r * K ..]) with 16-byte
-// global -> LDS loads, one 1 KB wave instruction per 64 chunks; waves w < 8 take every eighth instruction.
+// XOR mask of the 16-byte chunk swizzle of an LDS row of `cpr` chunks: chunk c of row r is stored at c ^ (r & mask),
+// with mask + 1 the largest power of two (at most 16) that divides cpr, so the swizzled chunk stays in the row.
+__device__ __forceinline__ int swz_mask(int cpr) { return min(16, cpr & -cpr) - 1; }
+
+// A block of `rows` rows of `K` halves (row r at src + r * ld) straight to LDS with 16-byte global -> LDS loads, one
+// 1 KB wave instruction per 64 chunks, into rows of CPR >= K / 8 chunks: chunk c of row r is stored at slot
+// c ^ (r & swz_mask(CPR)) of dst row r, and slots whose chunk lies past K hold a copy of the row's first chunk (finite
+// values that meet zero operands), so the consumers run a fixed number of MFMA steps for every K.
+template <int CPR>
 __device__ __forceinline__ void rows_to_lds(const f16* src, size_t ld, int rows, int K, f16* dst) {
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int cpr = K / 8, nch = rows * cpr;
-  for (int c0 = wid * 64; c0 < nch; c0 += 512) {
-    const int ch = min(c0 + lane, nch - 1), row = ch / cpr, col = ch % cpr;
-    __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(row) * ld + col * 8,
-                                     (__attribute__((address_space(3))) void*)(dst + c0 * 8), 16, 0, 0);
+  const int cpr = K / 8, nch = rows * CPR, msk = swz_mask(CPR);
+  for (int c0 = wid * 64; c0 < nch; c0 += NT) {
+    const int ch = min(c0 + lane, nch - 1), row = ch / CPR, slot = ch % CPR, col = slot ^ (row & msk);
+    __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(row) * ld + (col < cpr ? col : 0) * 8,
+                                     (lds_void*)(dst + c0 * 8), 16, 0, 0);
   }
 }
 
-// Row sum of an LDS row (K halves) with xs[0..K): TPR threads per row, thread t takes the chunks t + TPR c.
-template <int TPR, int CPT>
-__device__ __forceinline__ float lds_row_dot(const f16* rowp, const float* xs, int K) {
-  const int t = threadIdx.x % TPR;
-  float acc = 0.0f;
+// hl[i .. i+3] = f16(y), hl[ld + i ..] = f16((y - hi) 2^11): the hi/lo rows of a vector operand.
+__device__ __forceinline__ void store_hl4(f16* hl, int ld, int i, f32x4 y) {
+  f16x4 hi, lo;
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int k = (t + TPR * c) * 8;
-    if (k < K) {
-      float wf[8];
-      f16x8_to_f32(*reinterpret_cast<const u32x4*>(rowp + k), wf);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc += xs[k + i] * wf[i];
-    }
+  for (int e = 0; e < 4; ++e) {
+    float v = y[e];
+    __asm__ volatile("" : "+v"(v));  // hi and lo come from the same rounded fp32 value
+    hi[e] = static_cast<f16>(v);
+    lo[e] = static_cast<f16>((v - static_cast<float>(hi[e])) * 2048.0f);
   }
-  return group_sum<TPR>(acc);
+  *reinterpret_cast<f16x4*>(hl + i) = hi;
+  *reinterpret_cast<f16x4*>(hl + ld + i) = lo;
 }
 
-// Register tiling of a block's share of one layer (512 threads). Rows per block: q/k/v (G + 2) * 8, o/down H / 16,
-// gate/up pairs I / 128.
+// Register tiling of a block's share of one layer. Each wave holds K slice [w H/8, (w+1) H/8) of all the block's
+// q/k/v rows (QT tiles of 16) and gate/up rows (GT tiles: the gate rows, then the up rows) as MFMA B operands:
+// lane (j, kq) of tile t, step s holds row 16 t + j, halves k0 + 32 s + 8 kq .. + 8.
 template <int G>
 struct Tiling {
-  static constexpr int RQ = (G + 2) * 8;
-  static constexpr int TPR_Q = 16, CPT_Q = HMAX / (TPR_Q * 8);     // 32 slots, K = H
-  static constexpr int TPR_O = 8, CPT_O = G * HD / (TPR_O * 8);    // 64 slots, K = G * 128 columns of o_proj (LDS)
-  static constexpr int TPR_GU = 16, CPT_GU = HMAX / (TPR_GU * 8);  // 32 slots, K = H
-  static constexpr int TPR_D = 8, CPT_D = IMAX / 8 / (TPR_D * 8);  // 64 slots, K = I / 8 columns of down_proj (LDS)
-  static constexpr int TPR_LM = 32, CPT_LM = HMAX / (TPR_LM * 8);  // 16 rows per fragment
-  static constexpr int MQ_E = (NBG * PW / 4 + 63) / 64;            // one head's partial quads per lane
-  static_assert(RQ <= NT / TPR_Q && HMAX / NBG <= NT / TPR_O && IMAX / (NX * NBG) <= NT / TPR_GU, "slots");
-  static_assert(TPR_D == TPR_O, "o_proj and down_proj rows share the slot mapping");
+  static constexpr int RQ = (G + 2) * 8;          // q/k/v rows per block
+  static constexpr int QT = (RQ + 15) / 16;
+  static constexpr int RIM = ISM / NBG;           // gate/up pairs per block at most
+  static constexpr int GT = (2 * RIM + 15) / 16;
+  static constexpr int SW = HMAX / NW / 32;       // MFMA steps of a wave's K slice at most
+  static constexpr int RHM = HMAX / NBG;          // o/down rows per block at most (16 per wave: RHM / 16 waves)
+  static constexpr int GHD = G * HD;              // o_proj columns of the XCD
+  static constexpr int TPR_LM = 32, CPT_LM = HMAX / (TPR_LM * 8);  // LM head: 16 rows per fragment
+  static constexpr int MQ_E = (NBG * PW / 4 + 63) / 64;            // one head's block-partial quads per lane
+  static_assert(RHM / 16 <= NW, "o/down tiles");
 };
 
-// LDS carve-up (floats).
+// LDS carve-up, byte offsets.
 template <int G>
 struct Lds {
-  static constexpr int XRES = 0;                     // [HMAX] residual stream x / x'
-  static constexpr int XN = XRES + HMAX;             // [HMAX] x * gain of the next RMSNorm (the scale is applied later)
-  static constexpr int RED = XN + HMAX;              // [8] the waves' partial sums of x^2
-  static constexpr int HS = RED + 8;                 // [IMAX / 8] the XCD's h slice
-  static constexpr int ATT = HS + IMAX / 8;          // [G][HD] merged attention output
-  static constexpr int QS = ATT + G * HD;            // [G][HD] normed, rotated queries
-  static constexpr int KN = QS + G * HD;             // [HD] new key (fp16-rounded)
-  static constexpr int VN = KN + HD;                 // [HD] new value (fp16-rounded)
-  static constexpr int RAW = VN + HD;                // [(G + 2) HD] the XCD's raw q/k/v
-  static constexpr int GPART = RAW + (G + 2) * HD;   // [32][G][PW] lane-group partials, [8][G] maxima, [256][2] sums
-  static constexpr int BPART = GPART + NGRP * G * PW + 8 * G + NT;  // [G][NBG PW] words: the XCD's block partials
-  static constexpr int WD = BPART + G * NBG * PW;    // [HMAX / 16][IMAX / 8] halves: the block's down_proj rows
-  static constexpr int WO = WD + HMAX / 16 * IMAX / 8 / 2;  // [HMAX / 16][G HD] halves: the block's o_proj rows
-  static constexpr int FLAG = WO + HMAX / 16 * G * HD / 2;  // [8] ints: status, g, j, last block
-  static constexpr int BV = FLAG + 8;                // [16] argmax values per slot
-  static constexpr int BI = BV + 16;                 // [16] argmax indices
-  static constexpr int TOTAL = BI + 16;
+  static constexpr int XRES = 0;                               // fp32 [HMAX] residual stream x / x'
+  static constexpr int XHL = XRES + HMAX * 4;                  // fp16 [2][HMAX] hi/lo of x * gain (next RMSNorm)
+  static constexpr int HHL = XHL + 2 * HMAX * 2;               // fp16 [2][ISM] hi/lo of the XCD's h slice
+  static constexpr int AHL = HHL + 2 * ISM * 2;                // fp16 [2][G HD] hi/lo of the attention output
+  static constexpr int QHL = AHL + 2 * G * HD * 2;             // fp16 [2G][HD] hi/lo rows of q * scale * log2 e
+  static constexpr int KN = QHL + 2 * G * HD * 2;              // fp16 [HD] new key
+  static constexpr int VN = KN + HD * 2;                       // fp16 [HD] new value
+  static constexpr int PT = VN + HD * 2;                       // fp16 [NW][2G][KT] the waves' softmax weights
+  static constexpr int RED = PT + NW * 2 * G * KT * 2;         // fp32 [16] partial sums of squares
+  static constexpr int FLAG = RED + 16 * 4;                    // int [8] status, g, j, last block
+  static constexpr int BV = FLAG + 8 * 4;                      // fp32 [16] argmax values per slot
+  static constexpr int BI = BV + 16 * 4;                       // int [16] argmax indices
+  // fp16 [NW][KT][HD] the waves' V tiles. Phases that never overlap the attention tiles use the same bytes: the
+  // projections' partial sums, the waves' attention partials, E's block partials, the final x * gain of the LM head.
+  static constexpr int VT = BI + 16 * 4;
+  static constexpr int WD = VT + NW * KT * HD * 2;             // fp16 [HMAX / 16][ISM] down_proj rows (swizzled)
+  static constexpr int WO = WD + (HMAX / NBG) * ISM * 2;       // fp16 [HMAX / 16][G HD] o_proj rows (swizzled)
+  static constexpr int TOTAL = WO + (HMAX / NBG) * G * HD * 2;
+  static_assert(VT % 16 == 0 && WD % 16 == 0 && WO % 16 == 0, "16-byte aligned operand rows");
+  static_assert(TOTAL <= 160 * 1024, "LDS of one CU");
+  static_assert(G * NBG * PW * 4 <= NW * KT * HD * 2 && HMAX * 4 <= NW * KT * HD * 2, "VT reuse");
 };
 
 struct Ctx {
   const PersistArgs& a;
   int g, j, token, pos;
   uint32_t phase0;  // (step - 1) * L: the tag of layer l is (phase0 + l) & 3
-  float* lds;
+  char* lds;
   int* flag;
 };
 
-// Attention blocks of the XCD's computing group for S keys (about 32 keys each, one per lane group, at most 16
-// blocks) and keys per block; na is recomputed from the chunk so that every block jj < na owns at least one key.
+// Attention blocks of the XCD's computing group for S keys (at most 16, whole 32-key tiles each) and keys per block;
+// na is recomputed from the chunk so that every block jj < na owns at least one key.
 __device__ __forceinline__ void attn_split(int S, int& na, int& chunk) {
-  na = min(NBG, (S + NGRP - 1) / NGRP);
-  chunk = (S + na - 1) / na;
+  na = min(NBG, (S + KT - 1) / KT);
+  chunk = ((S + na - 1) / na + KT - 1) / KT * KT;
   na = (S + chunk - 1) / chunk;
 }
 
@@ -176,12 +211,19 @@ __device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
 #define XTRACE(pt)                                                                                           \
   do {                                                                                                       \
     if (c.a.trace != nullptr && threadIdx.x == 0 && layer == c.a.L / 2)                                      \
-      c.a.trace[(c.g * NBX + c.j) * 16 + (pt)] = now_ticks();                                                \
+      c.a.trace[(c.g * NBX + c.j) * kTracePts + (pt)] = now_ticks();                                         \
   } while (0)
 #define XTRACE0(i)                                                                                           \
   do {                                                                                                       \
     if (c.a.trace != nullptr && threadIdx.x == 0 && c.g == 0 && c.j % NBG == 0)                              \
-      c.a.trace[NX * NBX * 16 + (i)] = now_ticks();                                                          \
+      c.a.trace[NX * NBX * kTracePts + (i)] = now_ticks();                                                   \
+  } while (0)
+
+// Same, recorded by lane 0 of the wave that takes the first attention tile.
+#define XTRACEW(pt)                                                                                          \
+  do {                                                                                                       \
+    if (c.a.trace != nullptr && (threadIdx.x & 63) == 0 && wr == 0 && layer == c.a.L / 2)                     \
+      c.a.trace[(c.g * NBX + c.j) * kTracePts + (pt)] = now_ticks();                                         \
   } while (0)
 
 // Block barrier; afterwards every thread leaves if a wave reported a failed wait (flag[0] != 0).
@@ -191,30 +233,14 @@ __device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
     if (c.flag[0] != 0) return false; \
   } while (0)
 
-// Wave: polls MQ quads per lane (byte offsets off[e] into r, or -1 for none) of a tagged vector until every
-// one carries `tag`. Returns false (wave-uniform) on timeout or a raised error flag, after recording it in flag[0].
-template <int MQ>
-__device__ __forceinline__ bool poll_quads(const Ctx& c, __amdgpu_buffer_rsrc_t r, const int (&off)[MQ], uint32_t tag,
-                                           u32x4 (&v)[MQ]) {
-  const u32x4 filler = {tag, tag, tag, tag};
-#pragma unroll
-  for (int e = 0; e < MQ; ++e) v[e] = off[e] >= 0 ? ll_peek_buf4(r, off[e]) : filler;
-  const uint64_t t0 = now_ticks();
-  uint32_t spins = 0;
-  while (true) {
-    bool all = true;
-#pragma unroll
-    for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
-    if (__all(all)) return true;
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-      __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error (2)
-      c.flag[0] = 1;
-      return false;
-    }
-#pragma unroll
-    for (int e = 0; e < MQ; ++e)
-      if (off[e] >= 0 && !tw_quad_ok(v[e], tag)) v[e] = ll_peek_buf4(r, off[e]);
-  }
+// A failed wait: the error flag keeps a placement error (2) over a timeout (1); the block leaves at its next barrier.
+__device__ __forceinline__ void wait_failed(const Ctx& c) {
+  __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.flag[0] = 1;
+}
+
+__device__ __forceinline__ bool give_up(const Ctx& c, uint32_t& spins, uint64_t t0) {
+  return (++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err));
 }
 
 // Wave: the quads qi = lane + 64 e < nq of the XCD-local tagged words src[0 .. 4 nq) into dst[4 qi ..] (raw
@@ -236,9 +262,8 @@ __device__ __forceinline__ bool recv_contig(const Ctx& c, const uint32_t* src, i
 #pragma unroll
     for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
     if (__all(all)) break;
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-      __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error (2)
-      c.flag[0] = 1;
+    if (give_up(c, spins, t0)) {
+      wait_failed(c);
       return false;
     }
 #pragma unroll
@@ -252,6 +277,28 @@ __device__ __forceinline__ bool recv_contig(const Ctx& c, const uint32_t* src, i
   return true;
 }
 
+// Wave: words lane and lane + 64 of a 128-word XCD-local tagged vector (one head of the XCD's q/k/v), into registers.
+__device__ __forceinline__ bool recv_head(const Ctx& c, const uint32_t* src, uint32_t tag, float& x0, float& x1) {
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, HD * 4, 0x00020000);
+  uint32_t w0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
+  uint32_t w1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
+  const uint64_t t0 = now_ticks();
+  uint32_t spins = 0;
+  while (!__all(tw_tag(w0) == tag && tw_tag(w1) == tag)) {
+    if (give_up(c, spins, t0)) {
+      wait_failed(c);
+      return false;
+    }
+    if (tw_tag(w0) != tag) w0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
+    if (tw_tag(w1) != tag) w1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
+  }
+  x0 = tw_val(w0);
+  x1 = tw_val(w1);
+  return true;
+}
+
 // Sum over aligned groups of 8 lanes that is bit-identical in every lane of the group: each step adds two values
 // that are equal in both partner lanes up to the order of one addition, and IEEE addition commutes exactly.
 __device__ __forceinline__ float sum8(float v) {
@@ -261,132 +308,54 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
-// Sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48) with the gfx950 cross-row swaps: with
-// both operands equal, the two results of v_permlane32_swap hold v[l] and v[l ^ 32] (in some order) in every lane,
-// and likewise for v_permlane16_swap with l ^ 16; no LDS round trip.
-__device__ __forceinline__ float sum_rows4(float v) {
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-}
-
-// Wave w < 8 of the block: its eighth of x = base + sum_k partial_k over the eight XCDs, then x * gain into xn and its
-// partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is completed by rms_scale). The base is
-// the tagged vector xbase (the previous layer's residual published by the other group) or, when xbase is null, the
-// residual in LDS; for layer 0 the embedding row replaces it all. The wave owns the element quads w * H / 32 ..
-// + H / 32; its load i brings 8 of them from all eight partials (lane l: quad i * 8 + l / 8 of partial l % 8) and
-// the 8 lanes of a quad add their partials with sum8; lanes l % 8 == 0 also load the base quad.
-__device__ __forceinline__ bool cross_reduce(const Ctx& c, int w, const uint32_t* src, const uint32_t* xbase,
-                                             uint32_t tag, const f16* embed_row, const f16* gain, float* xres,
-                                             float* xn, float* red) {
+// Wave w < 8 of the block: its eighth of x = embedding row (layer 0, embedding.cpp:51-77), into xres, the hi/lo
+// rows of x * gain into xhl and its partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is
+// completed by rms_scale). The wave owns the element quads w * H / 32 .. + H / 32.
+__device__ __forceinline__ void embed_row(const Ctx& c, int w, const f16* embed_row, const f16* gain, float* xres,
+                                          f16* xhl, float* red) {
   constexpr int NI = HMAX / 256;
   int lane = threadIdx.x & 63;
-  __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
-  const int k = lane & 7;
+  __asm__ volatile("" : "+v"(lane));
   const int H = c.a.H, ni = H / 256, q0 = w * (H / 32);
   float ss = 0.0f;
-  if (embed_row != nullptr) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int q = q0 + i * 8 + (lane >> 3);
-      if (i < ni && k == 0) {
-        const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
-        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
-        f32x4 x, y;
+  for (int i = 0; i < NI; ++i) {
+    const int q = q0 + i * 8 + (lane >> 3);
+    if (i < ni && (lane & 7) == 0) {
+      const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
+      const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+      f32x4 x, y;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = static_cast<float>(e4[e]);
-          y[e] = x[e] * static_cast<float>(g4[e]);
-          ss += x[e] * x[e];
-        }
-        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
-        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+      for (int e = 0; e < 4; ++e) {
+        x[e] = static_cast<float>(e4[e]);
+        y[e] = x[e] * static_cast<float>(g4[e]);
+        ss += x[e] * x[e];
       }
-    }
-  } else {
-    // one poll for the partials and, when given, the base quads (lanes l % 8 == 0): the base is published earlier,
-    // so it costs no extra round trip
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(xbase != nullptr ? xbase : src), 0, H * 4, 0x00020000);
-    const u32x4 filler = {tag, tag, tag, tag};
-    u32x4 v[NI], bq[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const bool live = i < ni, blive = live && xbase != nullptr && k == 0;
-      v[i] = live ? ll_peek_buf4(r, k * H * 4 + (q0 + i * 8 + (lane >> 3)) * 16) : filler;
-      bq[i] = blive ? ll_peek_buf4(rb, (q0 + i * 8 + (lane >> 3)) * 16) : filler;
-    }
-    const uint64_t t0 = now_ticks();
-    uint32_t spins = 0;
-    while (true) {
-      bool all = true;
-#pragma unroll
-      for (int i = 0; i < NI; ++i) all = all && tw_quad_ok(v[i], tag) && tw_quad_ok(bq[i], tag);
-      if (__all(all)) break;
-      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-        __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // keeps a placement error
-        c.flag[0] = 1;
-        return false;
-      }
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const bool live = i < ni, blive = live && xbase != nullptr && k == 0;
-        if (live && !tw_quad_ok(v[i], tag)) v[i] = ll_peek_buf4(r, k * H * 4 + (q0 + i * 8 + (lane >> 3)) * 16);
-        if (blive && !tw_quad_ok(bq[i], tag)) bq[i] = ll_peek_buf4(rb, (q0 + i * 8 + (lane >> 3)) * 16);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int q = q0 + i * 8 + (lane >> 3);
-      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
-      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
-      if (i < ni && k == 0) {
-        f32x4 x = xbase != nullptr ? f32x4{tw_val(bq[i].x), tw_val(bq[i].y), tw_val(bq[i].z), tw_val(bq[i].w)}
-                                   : *reinterpret_cast<const f32x4*>(xres + 4 * q);
-        const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
-        x[0] += s0;
-        x[1] += s1;
-        x[2] += s2;
-        x[3] += s3;
-        f32x4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          y[e] = x[e] * static_cast<float>(g4[e]);
-          ss += x[e] * x[e];
-        }
-        *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
-        *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
-      }
+      *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
+      store_hl4(xhl, HMAX, 4 * q, y);
     }
   }
   ss = wave_sum(ss);
   if (lane == 0) red[w] = ss;
-  return true;
 }
 
-// Two-stage form of the same reduction, x = base + sum_k P_k over the eight XCDs' partials P_k (src, [8][H] words),
-// that reads each remote partial once per XCD instead of once per block:
+// x = base + sum_k P_k over the eight XCDs' partials P_k (src, [8][H] words), reading each remote partial once per
+// XCD instead of once per block:
 // stage 1 (wave 0 of a block with do1): the block's 1/16 of the elements, quads jj * H/64 ..; base from base_loc
 //   (XCD-local words) or, if null, from xres; x goes to out[0, H) and the block's sum of squares of x to out[H + jj],
 //   as XCD-local words with the same tag;
-// stage 2 (every wave): all of x and the 16 sums from out; x into xres, x * gain into xn, red[0..7] = pair sums of the
-//   16 sums (rms_scale adds them in a fixed order). Every block reads the same words, so x and the norm agree in every
-//   block of every XCD. The caller's barrier publishes xres, xn and red.
+// stage 2 (every wave): all of x and the 16 sums from out; x into xres, the hi/lo rows of x * gain into xhl (or, with
+//   xn32 set, x * gain in fp32 into xn32), red[0..7] = pair sums of the 16 sums (rms_scale adds them in a fixed
+//   order). Every block reads the same words, so x and the norm agree in every block of every XCD. The caller's
+//   barrier publishes xres, xhl / xn32 and red.
 __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool do1, const uint32_t* src,
                                               const uint32_t* base_loc, uint32_t tag, uint32_t* out, const f16* gain,
-                                              float* xres, float* xn, float* red, int trace_pt = -1) {
+                                              float* xres, f16* xhl, float* xn32, float* red, int trace_pt = -1) {
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
   const int H = c.a.H;
   const u32x4 filler = {tag, tag, tag, tag};
   const uint64_t t0 = now_ticks();
-  auto failed = [&]() {
-    __hip_atomic_fetch_max(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    c.flag[0] = 1;
-  };
   if (w == 0 && do1) {
     const int k = lane & 7, nq1 = H / 64, qb = jj * nq1;
     const __amdgpu_buffer_rsrc_t r =
@@ -407,8 +376,8 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
 #pragma unroll
       for (int i = 0; i < 2; ++i) all = all && tw_quad_ok(v[i], tag) && tw_quad_ok(bq[i], tag);
       if (__all(all)) break;
-      if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-        failed();
+      if (give_up(c, spins, t0)) {
+        wait_failed(c);
         return false;
       }
 #pragma unroll
@@ -446,7 +415,7 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
     ss = wave_sum(ss);
     if (lane == 0) ll_store_local(out, H + jj, ss, tag);
     if (trace_pt >= 0 && c.a.trace != nullptr && threadIdx.x == 0)
-      c.a.trace[(c.g * NBX + c.j) * 16 + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
+      c.a.trace[(c.g * NBX + c.j) * kTracePts + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
   }
   // stage 2: waves 0..3 take quad w * H/16 + lane of x, wave 4's lanes 0..3 the 16 sums (fewer waves polling L2)
   const int per = H / 16;
@@ -456,8 +425,8 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
   u32x4 v = (xlive || slive) ? ll_peek_buf4(ro, off) : filler;
   uint32_t spins = 0;
   while (!__all(tw_quad_ok(v, tag))) {
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
-      failed();
+    if (give_up(c, spins, t0)) {
+      wait_failed(c);
       return false;
     }
     if (!tw_quad_ok(v, tag)) v = ll_peek_buf4(ro, off);
@@ -470,7 +439,10 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = x[e] * static_cast<float>(g4[e]);
     *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
-    *reinterpret_cast<f32x4*>(xn + 4 * q) = y;
+    if (xn32 != nullptr)
+      *reinterpret_cast<f32x4*>(xn32 + 4 * q) = y;
+    else
+      store_hl4(xhl, HMAX, 4 * q, y);
   }
   if (slive) {
     const int m = lane;
@@ -486,95 +458,96 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   using T = Tiling<G>;
   using LD = Lds<G>;
   const PersistArgs& a = c.a;
-  const int tid = threadIdx.x, wid = tid >> 6;
+  const int tid = threadIdx.x, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
   const int g = c.g, pgrp = c.j / NBG, jj = c.j % NBG, pos = c.pos, S = pos + 1;
   const int H = a.H, I = a.I, qd = a.qd;
-  const int RH = H / NBG;   // o/down rows per block
-  const int IS = I / NX;    // intermediate slice of the XCD
-  const int RI = IS / NBG;  // gate/up pairs per block
-  float* lds = c.lds;
-  float* xres = lds + LD::XRES;
-  float* xn = lds + LD::XN;
-  float* red = lds + LD::RED;
-  float* hs = lds + LD::HS;
-  float* att = lds + LD::ATT;
-  float* qs = lds + LD::QS;
-  float* kn = lds + LD::KN;
-  float* vn = lds + LD::VN;
-  uint32_t* raw = reinterpret_cast<uint32_t*>(lds + LD::RAW);
-  float* gpart = lds + LD::GPART;
-  uint32_t* bpart = reinterpret_cast<uint32_t*>(lds + LD::BPART);
-  f16* wd = reinterpret_cast<f16*>(lds + LD::WD);
-  f16* wo = reinterpret_cast<f16*>(lds + LD::WO);
+  const int RH = H / NBG;          // o/down rows per block
+  const int IS = I / NX;           // intermediate slice of the XCD
+  const int RI = IS / NBG;         // gate/up pairs per block
+  const int kw0 = wid * (H / NW);  // this wave's K slice of the projections from the hidden state
+  const int sw = H / NW / 32;      // and its MFMA steps (the registers past them hold zeros)
+  char* L = c.lds;
+  float* xres = reinterpret_cast<float*>(L + LD::XRES);
+  f16* xhl = reinterpret_cast<f16*>(L + LD::XHL);
+  f16* hhl = reinterpret_cast<f16*>(L + LD::HHL);
+  f16* ahl = reinterpret_cast<f16*>(L + LD::AHL);
+  f16* qhl = reinterpret_cast<f16*>(L + LD::QHL);
+  f16* kn = reinterpret_cast<f16*>(L + LD::KN);
+  f16* vn = reinterpret_cast<f16*>(L + LD::VN);
+  f16* pt = reinterpret_cast<f16*>(L + LD::PT) + wid * 2 * G * KT;  // this wave's [2G][KT] softmax weights
+  float* red = reinterpret_cast<float*>(L + LD::RED);
+  char* vtb = L + LD::VT;
+  f16* vt = reinterpret_cast<f16*>(vtb + wid * KT * HD * 2);        // this wave's V tile [KT][HD] (swizzled)
+  float* part = reinterpret_cast<float*>(vtb);                       // [NW][GT 16] projection partial sums
+  f16* wd = reinterpret_cast<f16*>(L + LD::WD);
+  f16* wo = reinterpret_cast<f16*>(L + LD::WO);
   uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
   uint32_t* loc_qkv = loc;                                  // [(G + 2) HD]
   uint32_t* loc_att = loc + (((G + 2) * HD + 63) & ~63);    // [G][NBX][PW]
   uint32_t* loc_h = loc_att + ((NBX * G * PW + 63) & ~63);  // [IS]
   uint32_t* loc_xa = loc_h + ((IS + 63) & ~63);               // [H + 16]: x after the attention-input reduction
   uint32_t* loc_xg = loc_xa + HMAX + 64;                      // [H + 16]: x' after the o_proj reduction
-  // this block's q/k/v row: local row lr of the XCD's (G + 2) * 128 (q heads, key, value)
-  const int q_slot = tid / T::TPR_Q;
-  const int q_lr = jj * T::RQ + q_slot;
-  const bool q_live = q_slot < T::RQ;
-  const int q_row = q_lr < G * HD ? g * G * HD + q_lr
-                                  : (q_lr < (G + 1) * HD ? qd + g * HD + (q_lr - G * HD)
-                                                         : qd + a.nkv * HD + g * HD + (q_lr - (G + 1) * HD));
-  const int o_slot = tid / T::TPR_O, gu_slot = tid / T::TPR_GU;
-  const int hrow = jj * RH + o_slot;           // o/down output row
-  const bool h_live = o_slot < RH;
-  const int iidx = g * IS + jj * RI + gu_slot; // gate/up row
-  const bool i_live = gu_slot < RI;
-  // attention: up to NGRP * KPG keys every block takes all keys (lane group grp: keys grp + 32 u); beyond that block
-  // jj < na takes keys [k0, k1) (lane group grp: keys k0 + grp + 32 u) and the blocks' partials are exchanged
-  const bool allkeys = S <= NGRP * KPG;
+  constexpr int PST = T::GT * 16;                             // partial-sum row stride of a wave
+  // attention: up to KALL keys every block takes all keys; beyond that block jj < na takes keys [k0, k1) and the
+  // blocks' partials are exchanged
+  const bool allkeys = S <= KALL;
   int na, chunk;
   attn_split(S, na, chunk);
   const int k0 = allkeys ? 0 : (jj < na ? min(S, jj * chunk) : S);
   const int k1 = allkeys ? S : (jj < na ? min(S, k0 + chunk) : S);
-  int lane = tid & 63, grp = tid >> 4, sub = tid & 15;
-
-  Slice<T::TPR_Q, T::CPT_Q> sq;
-  Slice<T::TPR_GU, T::CPT_GU> sg, su;
-  u32x4 kr = {0, 0, 0, 0}, vr = {0, 0, 0, 0};
-  auto kv_fetch = [&](int layer, int p) {  // cached key/value p (< pos) of this layer, 8 dims per lane
-    if (p < k1 && p < pos) {
-      const size_t base = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD +
-                          static_cast<size_t>(p) * HD + sub * 8;
-      kr = load16(a.kcache + base);
-      vr = load16(a.vcache + base);
+  int lane = tid & 63, rl = lane & 15, kq = lane >> 4;
+  // this block's local q/k/v row lr of the XCD's (G + 2) * 128 (q heads, key, value) as a row of the fused matrix
+  auto qkv_row = [&](int lr) {
+    return lr < G * HD ? g * G * HD + lr
+                       : (lr < (G + 1) * HD ? qd + g * HD + (lr - G * HD) : qd + a.nkv * HD + g * HD + (lr - (G + 1) * HD));
+  };
+  // The block's slot of the XCD's attention partials when it owns no keys (every block in the short-context path,
+  // blocks jj >= na in the split path): max kNoKeys, sum 0. Every slot is written in every layer, so every word of
+  // the region carries the tag of one of the two latest layers and a later phase can never mistake a stale word for
+  // a fresh one, whatever the layer count and however na changes from step to step.
+  auto keyless_partial = [&](uint32_t tg) {
+    for (int t = tid; t < G * PW; t += NT) {
+      const int h = t / PW, d = t % PW;
+      ll_store_local(loc_att, (h * NBX + jj) * PW + d, d == HD ? kNoKeys : 0.0f, tg);
     }
   };
-  // the weight rows of layer `layer` and its first cached key/value of this lane group
+
+  u32x4 wq[T::QT][T::SW], wg[T::GT][T::SW];
+  // the weight rows of layer `layer`: q/k/v and gate/up slices into registers, o_proj and down_proj rows into LDS
   auto stream = [&](int layer) {
-    // recomputed per call: keeps the 64-bit row offsets from staying live across the layer loop
-    int qr = q_row, hr = jj * RH, ir = iidx;
-    __asm__ volatile("" : "+v"(qr), "+v"(ir), "+s"(hr));
+    int l16 = rl, k8 = kq * 8;
+    __asm__ volatile("" : "+v"(l16), "+v"(k8));  // recomputed per call: no 64-bit row offsets live across layers
     const f16* W4 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 4);
     const f16* W5 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 5);
     const f16* W6 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 6);
     const f16* W7 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 7);
     const f16* W8 = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + 8);
-    slice_load(sq, q_live ? W4 + static_cast<size_t>(qr) * H : nullptr, H);
-    rows_to_lds(W5 + static_cast<size_t>(hr) * qd + g * G * HD, qd, RH, G * HD, wo);
-    slice_load(sg, i_live ? W6 + static_cast<size_t>(ir) * H : nullptr, H);
-    slice_load(su, i_live ? W7 + static_cast<size_t>(ir) * H : nullptr, H);
-    rows_to_lds(W8 + static_cast<size_t>(hr) * I + g * IS, I, RH, IS, wd);
-    kv_fetch(layer, k0 + grp);
-    if (allkeys) {
-      // this block's share of KV head g's cached keys and values into the XCD's L2 (keys jj + 16 m): every block
-      // of the group then reads them from there
-      const int p = jj + NBG * (tid >> 4);
-      if (p < pos) {
-        const size_t base = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD +
-                            static_cast<size_t>(p) * HD + sub * 8;
-        const u32x4 pfk = load16(a.kcache + base);
-        const u32x4 pfv = load16(a.vcache + base);
-        // the words are only kept alive (a compare that is practically never true, and harmless if it is); the
-        // wait this implies is free: the group has nothing to do until the other group's layer is done
-        if (pfk.x == 0x9e3779b9u && pfv.y == 0x7f7f7f7fu && pfk.z == pfv.w) c.flag[7] = 1;
-      }
+#pragma unroll
+    for (int t = 0; t < T::QT; ++t) {
+      const int r = 16 * t + l16;
+      const f16* row = r < T::RQ ? W4 + static_cast<size_t>(qkv_row(jj * T::RQ + r)) * H + kw0 + k8 : nullptr;
+#pragma unroll
+      for (int s = 0; s < T::SW; ++s) wq[t][s] = (row != nullptr && s < sw) ? load_stream16(row + 32 * s) : u32x4{0, 0, 0, 0};
     }
+#pragma unroll
+    for (int t = 0; t < T::GT; ++t) {
+      const int r = 16 * t + l16;
+      const int ir = g * IS + jj * RI + (r < RI ? r : r - RI);
+      const f16* row = r < 2 * RI ? (r < RI ? W6 : W7) + static_cast<size_t>(ir) * H + kw0 + k8 : nullptr;
+#pragma unroll
+      for (int s = 0; s < T::SW; ++s) wg[t][s] = (row != nullptr && s < sw) ? load_stream16(row + 32 * s) : u32x4{0, 0, 0, 0};
+    }
+    rows_to_lds<T::GHD / 8>(W5 + static_cast<size_t>(jj * RH) * qd + g * G * HD, qd, RH, G * HD, wo);
+    rows_to_lds<ISM / 8>(W8 + static_cast<size_t>(jj * RH) * I + g * IS, I, RH, IS, wd);
   };
+  // vector A operand of one MFMA step over columns k .. k + 32: rows 0 and 1 = hi and lo rows of hl (row stride ld),
+  // rows 2..15 zero
+  auto vec_operand = [&](const f16* hl, int ld, int k) -> h8 {
+    return rl < 2 ? *reinterpret_cast<const h8*>(hl + rl * ld + k + 8 * kq) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+  };
+  // the hi/lo rows of x and h are zero past H and IS (the fixed-length MFMA steps read them)
+  for (int i = tid; i < 2 * HMAX; i += NT) xhl[i] = static_cast<f16>(0.0f);
+  for (int i = tid; i < 2 * ISM; i += NT) hhl[i] = static_cast<f16>(0.0f);
   if (pgrp < a.L) stream(pgrp);
 
   for (int layer = pgrp; layer < a.L; layer += 2) {
@@ -583,41 +556,90 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     for (int i = 0; i < 4; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
     const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     // per layer: keeps the compiler from hoisting per-lane addresses out of the loop (register pressure)
-    __asm__ volatile("" : "+v"(lane), "+v"(grp), "+v"(sub));
+    __asm__ volatile("" : "+v"(lane), "+v"(rl), "+v"(kq));
     XTRACE0(layer);
     XTRACE(0);
     // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
     wait_mem();  // this wave's rows of the layer have landed (its LDS rows are published by the barrier below)
     if (layer == 0)
-      cross_reduce(c, wid, a.xd, nullptr, tag, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xn, red);
+      embed_row(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xhl, red);
     else
-      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xn, red,
+      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red,
                     layer == a.L / 2 ? 15 : -1);
     XTRACE(1);
     XSYNC();  // #1
-    // ---- B: q/k/v rows of RMSNorm(x) ----
+    // ---- D's key tiles: wave w takes tiles kb / 32 + (7 - w), + 8, ... ----
+    const int kb = allkeys ? 0 : k0, ke = allkeys ? S : k1;
+    const int wr = NW - 1 - wid;  // the wave's tile rank: tiles kb / KT + wr, + 8, ...
+    const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
+    // keys at or past `pos` read as zero: their whole byte offset is in voffset, which the range check covers
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache + kvb, 0, pos * HD * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache + kvb, 0, pos * HD * 2, 0x00020000);
+    u32x4 kw[2][HD / 32];
+    // K operands of tile t (lane: key 16 sb + rl, dims 32 s + 8 kq ..) into kw; then its V tile -> LDS (instruction n
+    // brings rows 4n .. 4n+3, lane (slot rl, row 4n + kq), chunk rl ^ 2 (row & 7)): loads return in order, and the
+    // scores need only the keys
+    auto load_tile = [&](int t) {
+      const int p0 = t * KT;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+          kw[sb][s] = __builtin_amdgcn_raw_buffer_load_b128(rk, (p0 + 16 * sb + rl) * HD * 2 + (32 * s + 8 * kq) * 2, 0, 0);
+#pragma unroll
+      for (int n = 0; n < KT / 4; ++n) {
+        const int row = 4 * n + kq;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vt + n * 4 * HD), 16,
+                                                 (p0 + row) * HD * 2 + ((rl ^ (2 * (row & 7))) * 16), 0, 0, 0);
+      }
+    };
+    // ---- B: q/k/v rows of RMSNorm(x): each wave its K slice of every row, the partial sums added in LDS ----
     {
-      const float out = slice_dot(sq, xn, H) * rms_scale(red, H, a.eps);
-      if (q_live && tid % T::TPR_Q == 0) ll_store_local(loc_qkv, q_lr, out, tag);
+      h8 xa[T::SW];
+#pragma unroll
+      for (int s = 0; s < T::SW; ++s) xa[s] = vec_operand(xhl, HMAX, kw0 + 32 * s);
+#pragma unroll
+      for (int t = 0; t < T::QT; ++t) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < T::SW; ++s)
+          acc = mfma16(xa[s], as_h8(wq[t][s]), acc);  // steps past H meet zero weights
+        if (kq == 0) part[wid * PST + 16 * t + rl] = acc[0] + acc[1] * kLo;
+      }
+    }
+    XSYNC();  // #1b
+    if (wid == 0 && lane < T::RQ) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += part[w * PST + lane];
+      ll_store_local(loc_qkv, jj * T::RQ + lane, s * rms_scale(red, H, a.eps), tag);
     }
     XTRACE(2);
     // ---- C: head wid of the XCD's q/k/v; QK-RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171,
-    //      rope.cpp:81-84); rank 0 appends the key and value, rounded to the cache's fp16, at `pos` ----
+    //      rope.cpp:81-84); q -> hi/lo rows prescaled by scale * log2(e); k and v rounded to the cache's fp16, and
+    //      rank 0 appends them at `pos` ----
     if (wid < G + 2) {
       const int hh = wid;
-      if (recv_contig<1>(c, loc_qkv + hh * HD, HD / 4, tag, raw + hh * HD)) {
-        float x0 = tw_val(raw[hh * HD + lane]), x1 = tw_val(raw[hh * HD + lane + 64]);
+      float x0, x1;
+      if (recv_head(c, loc_qkv + hh * HD, tag, x0, x1)) {
         if (hh <= G)
           norm_rope_pair(x0, x1, hh < G ? W[2] : W[3], a.eps, a.rope_cos + static_cast<size_t>(pos) * (HD / 2),
                          a.rope_sin + static_cast<size_t>(pos) * (HD / 2), lane);
         if (hh < G) {
-          qs[hh * HD + lane] = x0;
-          qs[hh * HD + lane + 64] = x1;
+          const float qscale = a.scale * 1.44269504088896341f;
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            float v = (half == 0 ? x0 : x1) * qscale;
+            __asm__ volatile("" : "+v"(v));
+            const f16 hi = static_cast<f16>(v);
+            qhl[(2 * hh) * HD + lane + 64 * half] = hi;
+            qhl[(2 * hh + 1) * HD + lane + 64 * half] = static_cast<f16>((v - static_cast<float>(hi)) * 2048.0f);
+          }
         } else {
           const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
-          float* dst = hh == G ? kn : vn;
-          dst[lane] = static_cast<float>(h0);
-          dst[lane + 64] = static_cast<float>(h1);
+          f16* dst = hh == G ? kn : vn;
+          dst[lane] = h0;
+          dst[lane + 64] = h1;
           if (jj == 0) {
             f16* cache = (hh == G ? a.kcache : a.vcache) + static_cast<size_t>(layer) * a.layer_stride +
                          static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(pos) * HD;
@@ -628,326 +650,271 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       }
     }
     XTRACE(3);
-    XSYNC();  // #2: qs, kn, vn
-    if (allkeys) {
-      // NK keys per lane group (4 or 8): a straight-line body for each, chosen by the uniform S
-      auto all_keys = [&](auto nk) {
-        constexpr int NK = decltype(nk)::value;
-        // ---- D, up to 256 keys: every block takes all S keys of KV head g (the softmax of
-        //      grouped_query_attention.cpp:105-136): scores and the block max per head, then base-2 weights; the 4
-        //      lane groups of a wave add with cross-row swaps, the 8 waves through LDS. No hand-off between blocks. ----
-        const float qscale = a.scale * 1.44269504088896341f;
-        // the head's cached keys/values through buffer resources (scalar base, 32-bit lane offsets; keys at or past
-        // `pos` read as zero)
-        const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache + kvb, 0, pos * HD * 2, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache + kvb, 0, pos * HD * 2, 0x00020000);
-        const int kvo = (grp * HD + sub * 8) * 2;
-        float qreg[G][8], sc[NK][G], mloc[G];
+    XSYNC();  // #2: q rows, kn, vn; the projection partials are consumed
+    XTRACE(17);
+    // ---- D: attention over keys [kb, ke) (the softmax of grouped_query_attention.cpp:105-136). Wave w takes the
+    //      32-key tiles kb / 32 + (7 - w), + 8, ...: scores S^T = q . K^T, a running base-2 softmax per wave,
+    //      O += P . V ----
+    {
+      // A operand of step s: rows 2h, 2h + 1 = hi, lo of head h's q; rows >= 2G zero
+      auto q_operand = [&](int s) -> h8 {
+        return rl < 2 * G ? *reinterpret_cast<const h8*>(qhl + rl * HD + 32 * s + 8 * kq) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      };
+      float mrun[G], lsum[G];
+      f32x4 o[HD / 16];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-          mloc[h] = kNoKeys;
+      for (int h = 0; h < G; ++h) {
+        mrun[h] = -INFINITY;
+        lsum[h] = 0.0f;
+      }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
+      for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = kb / KT + wr; t * KT < ke; t += NW) {
+        const int p0 = t * KT;
+        load_tile(t);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+          if (p0 + 16 * sb + rl == pos)
+#pragma unroll
+            for (int s = 0; s < HD / 32; ++s) kw[sb][s] = *reinterpret_cast<const u32x4*>(kn + 32 * s + 8 * kq);
+        f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) {
+          const h8 qa = q_operand(s);
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) sc[sb] = mfma16(qa, as_h8(kw[sb][s]), sc[sb]);
         }
-        u32x4 vw0[4];
-#pragma unroll
-        for (int u0 = 0; u0 < NK; u0 += 4) {
-          u32x4 kw[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            kw[v] = (u0 + v == 0) ? kr : __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, NGRP * (u0 + v) * HD * 2, 0);
-          }
-          if constexpr (NK == 4) {  // one round: its values are requested with the keys
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-              vw0[v] = v == 0 ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * v * HD * 2, 0);
-          }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int p = grp + NGRP * (u0 + v);
-            float kf[8];
-            if (p == pos) {
-#pragma unroll
-              for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-            } else {
-              f16x8_to_f32(kw[v], kf);
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-              float d = 0.0f;
-#pragma unroll
-              for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
-              const float sv = group_sum<16>(d);
-              sc[u0 + v][h] = p < S ? sv : kNoKeys;
-              mloc[h] = fmaxf(mloc[h], sc[u0 + v][h]);
-            }
-          }
-        }
-        // weights relative to the wave's max (no block barrier); the 8 waves' sums are rescaled when merged
-        XTRACE(4);
-        float mblk[G], o[G][8], l[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          mblk[h] = wave_max(mloc[h]);
-          l[h] = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
-        }
-#pragma unroll
-        for (int u0 = 0; u0 < NK; u0 += 4) {
-          u32x4 vw[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            if constexpr (NK == 4)
-              vw[v] = vw0[v];
-            else
-              vw[v] = (u0 + v == 0) ? vr : __builtin_amdgcn_raw_buffer_load_b128(rv, kvo, NGRP * (u0 + v) * HD * 2, 0);
-          }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int p = grp + NGRP * (u0 + v);
-            if (p < S) {
-              float vf[8];
-              if (p == pos) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
-              } else {
-                f16x8_to_f32(vw[v], vf);
-              }
-#pragma unroll
-              for (int h = 0; h < G; ++h) {
-                const float pw = __builtin_amdgcn_exp2f(sc[u0 + v][h] - mblk[h]);
-                l[h] += pw;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
-              }
-            }
-          }
-        }
-        // the wave's 4 lane groups added across rows; row 0 writes the wave's sums
+        if (t == kb / KT + wr) XTRACEW(19);
+        // lanes 0..15 hold the scores of keys p0 + rl and p0 + 16 + rl for every head
+        float pv[2][G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float ov = sum_rows4(o[h][i]);
-            if (lane < 16) gpart[(wid * G + h) * PW + sub * 8 + i] = ov;
+          for (int sb = 0; sb < 2; ++sb)
+            pv[sb][h] = (kq == 0 && p0 + 16 * sb + rl < ke) ? sc[sb][2 * h] + sc[sb][2 * h + 1] * kLo : -INFINITY;
+          const float mt = wave_max(fmaxf(pv[0][h], pv[1][h]));  // finite: key p0 < ke is in the tile
+          const float mnew = fmaxf(mrun[h], mt);
+          const float corr = __builtin_amdgcn_exp2f(mrun[h] - mnew);  // 0 on the first tile
+          mrun[h] = mnew;
+          lsum[h] *= corr;
+#pragma unroll
+          for (int dt = 0; dt < HD / 16; ++dt) {
+            o[dt][2 * h] *= corr;
+            o[dt][2 * h + 1] *= corr;
           }
-          const float lv = sum_rows4(l[h]);
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) pv[sb][h] = __builtin_amdgcn_exp2f(pv[sb][h] - mnew);
+          lsum[h] += pv[0][h] + pv[1][h];
+        }
+        if (t == kb / KT + wr) XTRACEW(18);
+        // P rows 2h, 2h + 1 (hi, lo 2^11) of the tile's 32 keys -> the wave's LDS rows
+        if (kq == 0) {
+#pragma unroll
+          for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+              const float p = pv[sb][h];
+              const f16 hi = static_cast<f16>(p);
+              pt[(2 * h) * KT + 16 * sb + rl] = hi;
+              pt[(2 * h + 1) * KT + 16 * sb + rl] = static_cast<f16>((p - static_cast<float>(hi)) * 2048.0f);
+            }
+        }
+        wait_mem();  // the V tile has landed in LDS
+        if (t == kb / KT + wr) XTRACEW(16);
+        if (pos >= p0 && pos < p0 + KT && lane < 16) {  // the new value is not in the cache (read as zero): its row
+          const int row = pos - p0;
+          *reinterpret_cast<u32x4*>(vt + row * HD + ((lane ^ (2 * (row & 7))) * 8)) =
+              *reinterpret_cast<const u32x4*>(vn + lane * 8);
+        }
+        const h8 pa = rl < 2 * G ? *reinterpret_cast<const h8*>(pt + rl * KT + 8 * kq) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+        // B operand V[8 kq + e][16 dt + rl]: two transposing reads of 4 keys each; in each 16-lane group lane rl names
+        // 4 dims of one key and receives dim rl of the 4 keys. Read (dt, half) is at row 8 kq + 4 half + rl / 4,
+        // dims 16 dt + 4 (rl & 3): chunk 2 dt + (rl & 3) / 2 stored at slot (2 dt + (rl & 3) / 2) ^ 2 (row & 7), i.e.
+        // byte 32 ((dt ^ (rl / 4)) ^ 4 half) + 16 ((rl & 3) / 2) + 8 (rl & 1) of the row
+        const int vbase = (8 * kq + (rl >> 2)) * HD * 2 + ((rl & 3) >> 1) * 16 + (rl & 1) * 8, vsw = (rl >> 2) * 32;
+        hv4 vr[HD / 16][2];
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+          for (int half = 0; half < 2; ++half)
+            vr[dt][half] = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) hv4*)(
+                (__attribute__((address_space(3))) char*)(vt) + vbase + half * 4 * HD * 2 +
+                ((32 * dt) ^ vsw ^ (128 * half))));
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+          const f16x4 w0 = __builtin_bit_cast(f16x4, vr[dt][0]), w1 = __builtin_bit_cast(f16x4, vr[dt][1]);
+          const h8 vb = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+          o[dt] = mfma16(pa, vb, o[dt]);
+        }
+        if (t == kb / KT + wr) XTRACEW(20);
+      }
+      XTRACE(4);
+      // the wave's partial (its max, sum and weighted values per head) into the first bytes of its own V tile
+      {
+        float* gp = reinterpret_cast<float*>(vt);  // [G][HD] values, [G] maxima, [G] sums
+        if (kq == 0) {
+#pragma unroll
+          for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+            for (int h = 0; h < G; ++h) gp[h * HD + 16 * dt + rl] = o[dt][2 * h] + o[dt][2 * h + 1] * kLo;
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float l = wave_sum(lsum[h]);
           if (lane == 0) {
-            gpart[(wid * G + h) * PW + HD + 1] = lv;
-            gpart[(wid * G + h) * PW + HD + 2] = mblk[h];
+            gp[G * HD + h] = mrun[h] == -INFINITY ? kNoKeys : mrun[h];
+            gp[G * HD + G + h] = l;
           }
         }
-        XTRACE(11);
-        XSYNC();  // #2b: the 8 waves' sums
-        XTRACE(12);
+      }
+      XTRACE(11);
+      XSYNC();  // #2b: the 8 waves' partials
+      XTRACE(12);
+      if (allkeys || jj < na) {
+        // output t (head t / 128, dim t % 128): the waves' partials rescaled to the block max, in wave order
         for (int t = tid; t < G * HD; t += NT) {
           const int h = t / HD, d = t % HD;
           float M = kNoKeys;
 #pragma unroll
-          for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[(w * G + h) * PW + HD + 2]);
-          float L = 0.0f, O = 0.0f;
+          for (int w = 0; w < NW; ++w)
+            M = fmaxf(M, reinterpret_cast<const float*>(vtb + w * KT * HD * 2)[G * HD + h]);
+          if (!allkeys) M = tw_val(tw_pack(M, 0u));  // as the exchange word will carry it
+          float O = 0.0f, Lw = 0.0f;
 #pragma unroll
-          for (int w = 0; w < NT / 64; ++w) {
-            const float f = __builtin_amdgcn_exp2f(gpart[(w * G + h) * PW + HD + 2] - M);  // 0 for a wave without keys
-            L += gpart[(w * G + h) * PW + HD + 1] * f;
-            O += gpart[(w * G + h) * PW + d] * f;
+          for (int w = 0; w < NW; ++w) {
+            const float* gw = reinterpret_cast<const float*>(vtb + w * KT * HD * 2);
+            const float f = __builtin_amdgcn_exp2f(gw[G * HD + h] - M);  // 0 for a wave without keys
+            Lw += gw[G * HD + G + h] * f;
+            O += gw[h * HD + d] * f;
           }
-          att[h * HD + d] = O / L;
-        }
-        XTRACE(13);
-        return true;
-      };
-      if (!(S <= NGRP * 4 ? all_keys(std::integral_constant<int, 4>{}) : all_keys(std::integral_constant<int, KPG>{})))
-        return false;
-    } else {
-    // ---- D: attention over keys [k0, k1) (the softmax of grouped_query_attention.cpp:105-136) in two passes over the
-    //      block's keys: scores and the block's max per head, then base-2 weights relative to that max, so that the
-    //      lane groups' partials merge by plain sums. q is prescaled by scale * log2(e). ----
-    float qreg[G][8], mblk[G];
-    {
-      const float qscale = a.scale * 1.44269504088896341f;
-      float mloc[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        mloc[h] = kNoKeys;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qreg[h][i] = qs[h * HD + sub * 8 + i] * qscale;
-      }
-      // the score of key p for every head (every lane of the group gets it)
-      auto scores = [&](int p, int u, float (&sc)[G]) {
-        float kf[8];
-        if (p == pos) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-        } else {
-          const u32x4 kw = u == 0 ? kr
-                                  : load16(a.kcache + static_cast<size_t>(layer) * a.layer_stride +
-                                           static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(p) * HD + sub * 8);
-          f16x8_to_f32(kw, kf);
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          float d = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) d += qreg[h][i] * kf[i];
-          sc[h] = group_sum<16>(d);
-        }
-      };
-      if (jj < na)
-        for (int p = k0 + grp, u = 0; p < k1; p += NGRP, ++u) {
-          float sc[G];
-          scores(p, u, sc);
-#pragma unroll
-          for (int h = 0; h < G; ++h) mloc[h] = fmaxf(mloc[h], sc[h]);
-        }
-      // the block's max per head: wave maxima, then the 8 waves' through LDS
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float mw = wave_max(mloc[h]);
-        if (lane == 0) gpart[NGRP * G * PW + wid * G + h] = mw;
-      }
-      XSYNC();  // #2a: wave maxima
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float M = kNoKeys;
-#pragma unroll
-        for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, gpart[NGRP * G * PW + w * G + h]);
-        mblk[h] = M == kNoKeys ? M : tw_val(tw_pack(M, 0u));  // as the exchange word will carry it
-      }
-      float o[G][8], l[G];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        l[h] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
-      }
-      if (jj < na)
-        for (int p = k0 + grp, u = 0; p < k1; p += NGRP, ++u) {
-          float sc[G], vf[8];
-          scores(p, u, sc);
-          if (p == pos) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vf[i] = vn[sub * 8 + i];
+          if (allkeys) {
+            float v = O / Lw;
+            __asm__ volatile("" : "+v"(v));
+            const f16 hi = static_cast<f16>(v);
+            ahl[t] = hi;
+            ahl[G * HD + t] = static_cast<f16>((v - static_cast<float>(hi)) * 2048.0f);
           } else {
-            const u32x4 vw = u == 0 ? vr
-                                    : load16(a.vcache + static_cast<size_t>(layer) * a.layer_stride +
-                                             static_cast<size_t>(g) * a.cap * HD + static_cast<size_t>(p) * HD + sub * 8);
-            f16x8_to_f32(vw, vf);
-          }
-#pragma unroll
-          for (int h = 0; h < G; ++h) {
-            const float pw = __builtin_amdgcn_exp2f(sc[h] - mblk[h]);
-            l[h] += pw;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[h][i] += pw * vf[i];
+            const int w0 = (h * NBX + jj) * PW;  // [head][block][PW]
+            ll_store_local(loc_att, w0 + d, O, tag);
+            if (d < 4) ll_store_local(loc_att, w0 + HD + d, d == 0 ? M : (d == 1 ? Lw : 0.0f), tag);
           }
         }
-      // the group's partial sums (relative to the block max) to LDS
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) gpart[(grp * G + h) * PW + sub * 8 + i] = o[h][i];
-        if (sub == 0) gpart[(grp * G + h) * PW + HD + 1] = l[h];
       }
+      if (allkeys || jj >= na) keyless_partial(tag);
+      XTRACE(13);
     }
-    XTRACE(11);
-    XSYNC();  // #2b: the block's lane-group partials
-    XTRACE(12);
-    if (jj < na) {
-      // output t (head t / 128, dim t % 128) is the sum over the 32 groups in a fixed order: threads t and t + 256 of
-      // the same lane add groups 0..15 and 16..31, and the lower half adds the upper half's sum through LDS
-      static_assert(G * HD <= NT / 2, "two threads per output");
-      const int t = tid & (NT / 2 - 1), half = tid / (NT / 2);
-      const int h = t / HD, d = t % HD;
-      float L = 0.0f, O = 0.0f;
-      if (t < G * HD) {
+    if (!allkeys) {
+      XSYNC();  // the merge has read the waves' partials: E's block partials may overwrite them
+      // ---- E: head wid's block partials of the XCD, merged in a fixed order ----
+      if (wid < G) {
+        const int h = wid;
+        uint32_t* bpart = reinterpret_cast<uint32_t*>(vtb) + h * (NBG * PW);
+        if (recv_contig<T::MQ_E>(c, loc_att + h * NBX * PW, na * (PW / 4), tag, bpart)) {
+          // lane r < na holds block r's max and sum; the weights e_r are broadcast with readlane
+          const float mr = lane < na ? tw_val(bpart[lane * PW + HD]) : kNoKeys;
+          const float lr = lane < na ? tw_val(bpart[lane * PW + HD + 1]) : 0.0f;
+          const float M = wave_max(mr);
+          const float er = mr < 0.5f * kNoKeys ? 0.0f : __builtin_amdgcn_exp2f(mr - M);  // a keyless block adds 0
+          const float Ls = wave_sum(lr * er);
 #pragma unroll
-        for (int q = 0; q < NGRP / 2; ++q) {
-          const int qq = half * (NGRP / 2) + q;
-          L += gpart[(qq * G + h) * PW + HD + 1];
-          O += gpart[(qq * G + h) * PW + d];
-        }
-      }
-      float* hsum = gpart + NGRP * G * PW + 8 * G;  // [NT / 2][2] the upper halves' sums (spare LDS after the maxima)
-      if (half == 1 && t < G * HD) {
-        hsum[2 * t] = O;
-        hsum[2 * t + 1] = L;
-      }
-      __syncthreads();  // every thread of the block reaches this barrier (jj < na is block-uniform)
-      if (half == 0 && t < G * HD) {
-        O += hsum[2 * t];
-        L += hsum[2 * t + 1];
-        const int w0 = (h * NBX + jj) * PW;  // [head][block][PW]
-        ll_store_local(loc_att, w0 + d, O, tag);
-        if (d < 4) ll_store_local(loc_att, w0 + HD + d, d == 0 ? mblk[h] : (d == 1 ? L : 0.0f), tag);
-      }
-    }
-    XTRACE(4);
-    // ---- E: head wid's block partials of the XCD, merged in a fixed order ----
-    if (wid < G) {
-      const int h = wid;
-      if (recv_contig<T::MQ_E>(c, loc_att + h * NBX * PW, na * (PW / 4), tag, bpart + h * (NBG * PW))) {
-        XTRACE(13);
-        const uint32_t* bp = bpart + h * (NBG * PW);
-        // lane r < na holds block r's max and sum; the weights e_r are broadcast with readlane
-        const float mr = lane < na ? tw_val(bp[lane * PW + HD]) : kNoKeys;
-        const float lr = lane < na ? tw_val(bp[lane * PW + HD + 1]) : 0.0f;
-        const float M = wave_max(mr);
-        const float er = mr < 0.5f * kNoKeys ? 0.0f : __builtin_amdgcn_exp2f(mr - M);  // base 2; a keyless block adds 0
-        const float L = wave_sum(lr * er);
+          for (int dd = 0; dd < 2; ++dd) {
+            const int d = lane + 64 * dd;
+            float O = 0.0f;
 #pragma unroll
-        for (int dd = 0; dd < 2; ++dd) {
-          const int d = lane + 64 * dd;
-          float O = 0.0f;
-#pragma unroll
-          for (int r = 0; r < NBG; ++r)
-            if (r < na) O += tw_val(bp[r * PW + d]) * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er), r));
-          att[h * HD + d] = O / L;
+            for (int r = 0; r < NBG; ++r)
+              if (r < na) O += tw_val(bpart[r * PW + d]) * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er), r));
+            float v = O / Ls;
+            __asm__ volatile("" : "+v"(v));
+            const f16 hi = static_cast<f16>(v);
+            ahl[h * HD + d] = hi;
+            ahl[G * HD + h * HD + d] = static_cast<f16>((v - static_cast<float>(hi)) * 2048.0f);
+          }
         }
       }
     }
     XTRACE(5);
-    }  // the split path
     XSYNC();  // #3: merged attention output
-    // ---- F: partial o_proj over the XCD's query columns ----
-    {
-      const float out = lds_row_dot<T::TPR_O, T::CPT_O>(wo + (h_live ? o_slot : 0) * (G * HD), att, G * HD);
-      if (h_live && tid % T::TPR_O == 0) ll_store_buf(a.xo, g * H + hrow, out, tag);
+    // ---- F: partial o_proj over the XCD's query columns: wave w < RH / 16 takes rows 16 w .. over all G * 128 ----
+    if (wid < RH / 16) {
+      const int row = 16 * wid + rl;
+      constexpr int msk = T::GHD / 8 >= 16 ? 15 : T::GHD / 8 - 1;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < T::GHD / 32; ++s) {
+        const h8 av = vec_operand(ahl, T::GHD, 32 * s);
+        const h8 bv = *reinterpret_cast<const h8*>(wo + row * T::GHD + (((4 * s + kq) ^ (row & msk)) * 8));
+        acc = mfma16(av, bv, acc);
+      }
+      if (kq == 0) ll_store_buf(a.xo, g * H + jj * RH + row, acc[0] + acc[1] * kLo, tag);
     }
     XTRACE(6);
     // ---- G: x' = x + sum_k O_k, RMSNorm input ----
-    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xn, red,  // x' also for the other group
+    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xhl, nullptr, red,  // x' also for the other group
                   layer == a.L / 2 ? 14 : -1);
     XTRACE(7);
     XSYNC();  // #4
     // ---- H: gate/up of RMSNorm(x') + SwiGLU (qwen_mlp.cpp:31) on the block's share of the XCD's slice ----
     {
+      h8 xa[T::SW];
+#pragma unroll
+      for (int s = 0; s < T::SW; ++s) xa[s] = vec_operand(xhl, HMAX, kw0 + 32 * s);
+#pragma unroll
+      for (int t = 0; t < T::GT; ++t) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < T::SW; ++s)
+          acc = mfma16(xa[s], as_h8(wg[t][s]), acc);
+        if (kq == 0) part[wid * PST + 16 * t + rl] = acc[0] + acc[1] * kLo;
+      }
+    }
+    XSYNC();  // #4b
+    if (wid == 0 && lane < RI) {
       const float scale = rms_scale(red, H, a.eps);
-      const float og = slice_dot(sg, xn, H) * scale;
-      const float ou = slice_dot(su, xn, H) * scale;
-      if (i_live && tid % T::TPR_GU == 0) ll_store_local(loc_h, jj * RI + gu_slot, silu_ref(og) * ou, tag);
+      float gs = 0.0f, us = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        gs += part[w * PST + lane];
+        us += part[w * PST + RI + lane];
+      }
+      ll_store_local(loc_h, jj * RI + lane, silu_ref(gs * scale) * (us * scale), tag);
     }
     XTRACE(8);
-    // ---- I: the XCD's h slice ----
-    if (wid * 64 < IS / 4 &&
-        recv_contig<1>(c, loc_h + wid * 256, min(64, IS / 4 - wid * 64), tag, reinterpret_cast<uint32_t*>(hs) + wid * 256)) {
-      const int q = wid * 64 + lane;  // the words this lane brought, as floats
-      if (q < IS / 4) {
-        const uint32_t* w4 = reinterpret_cast<const uint32_t*>(hs) + 4 * q;
-        float f[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = tw_val(w4[e]);
-        *reinterpret_cast<f32x4*>(hs + 4 * q) = f32x4{f[0], f[1], f[2], f[3]};
+    // ---- I: the XCD's h slice, as hi/lo rows ----
+    if (wid * 64 < IS / 4) {
+      int ln = lane;
+      __asm__ volatile("" : "+v"(ln));
+      const int nq = min(64, IS / 4 - wid * 64);
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(loc_h + wid * 256, 0, nq * 16, 0x00020000);
+      const u32x4 filler = {tag, tag, tag, tag};
+      u32x4 v = ln < nq ? ll_peek_buf4(r, ln * 16) : filler;
+      const uint64_t t0 = now_ticks();
+      uint32_t spins = 0;
+      bool ok = true;
+      while (!__all(tw_quad_ok(v, tag))) {
+        if (give_up(c, spins, t0)) {
+          wait_failed(c);
+          ok = false;
+          break;
+        }
+        if (!tw_quad_ok(v, tag)) v = ll_peek_buf4(r, ln * 16);
       }
+      if (ok && ln < nq)
+        store_hl4(hhl, ISM, 4 * (wid * 64 + ln), f32x4{tw_val(v.x), tw_val(v.y), tw_val(v.z), tw_val(v.w)});
     }
     XTRACE(9);
     XSYNC();  // #5
-    // ---- J: partial down_proj over the slice's columns ----
-    {
-      const float out = lds_row_dot<T::TPR_D, T::CPT_D>(wd + (h_live ? o_slot : 0) * IS, hs, IS);
-      if (h_live && tid % T::TPR_D == 0) ll_store_buf(a.xd, g * H + hrow, out, tag);
+    // ---- J: partial down_proj over the slice's columns: wave w < RH / 16 takes rows 16 w .. over all IS ----
+    if (wid < RH / 16) {
+      const int row = 16 * wid + rl;
+      constexpr int msk = ISM / 8 >= 16 ? 15 : ISM / 8 - 1;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < ISM / 32; ++s) {  // steps past IS meet zero operands
+        const h8 av = vec_operand(hhl, ISM, 32 * s);
+        const h8 bv = *reinterpret_cast<const h8*>(wd + row * ISM + (((4 * s + kq) ^ (row & msk)) * 8));
+        acc = mfma16(av, bv, acc);
+      }
+      if (kq == 0) ll_store_buf(a.xd, g * H + jj * RH + row, acc[0] + acc[1] * kLo, tag);
     }
     XTRACE(10);
     // the group's next layer: its weight rows stream into registers and LDS while the other group computes (after a
@@ -957,9 +924,10 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       stream(layer + 2);
     }
   }
-  // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks)
+  // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks), in fp32
+  // for the LM head
   cross_reduce2(c, wid, jj, pgrp == 0, a.xd, loc_xg, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, loc_xa,
-                a.final_norm, xres, xn, red);
+                a.final_norm, xres, xhl, reinterpret_cast<float*>(vtb), red);
   XTRACE0(a.L);
   XSYNC();
   return true;
@@ -970,11 +938,12 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
 template <int G>
 __device__ __forceinline__ void lm_head(const Ctx& c) {
   using T = Tiling<G>;
+  using LD = Lds<G>;
   const PersistArgs& a = c.a;
   const int tid = threadIdx.x, slot = tid / T::TPR_LM;
   const bool lead = (tid % T::TPR_LM) == 0;
-  const float* xn = c.lds + Lds<G>::XN;
-  const float scale = rms_scale(c.lds + Lds<G>::RED, a.H, a.eps);
+  const float* xn = reinterpret_cast<const float*>(c.lds + LD::VT);
+  const float scale = rms_scale(reinterpret_cast<const float*>(c.lds + LD::RED), a.H, a.eps);
   const int b = c.g * NBX + c.j;
   const int rv = (a.V + NX * NBX - 1) / (NX * NBX);
   const int v0 = b * rv, v1 = min(a.V, v0 + rv);
@@ -1001,8 +970,8 @@ __device__ __forceinline__ void lm_head(const Ctx& c) {
     slice_load(f0, rowp(r0 + 2 * STEP + slot), a.H);
     consume(f1, r0 + STEP);
   }
-  float* bv = c.lds + Lds<G>::BV;
-  int* bi = reinterpret_cast<int*>(c.lds + Lds<G>::BI);
+  float* bv = reinterpret_cast<float*>(c.lds + LD::BV);
+  int* bi = reinterpret_cast<int*>(c.lds + LD::BI);
   if (lead) {
     bv[slot] = best;
     bi[slot] = best_i;
@@ -1013,20 +982,25 @@ __device__ __forceinline__ void lm_head(const Ctx& c) {
 
 template <int G>
 __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) char lds[];
   using LD = Lds<G>;
   int* flag = reinterpret_cast<int*>(lds + LD::FLAG);
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
-  const uint32_t step = static_cast<uint32_t>(a.state[2]);
+  const uint32_t step = static_cast<uint32_t>(a.state[3]);  // this kernel's own step count (the legacy one-launch
+                                                             // kernel counts its steps in state[2])
   if (tid == 0) {
+    // a launch queued behind a failed one leaves at once: the failed step did not advance the step count or reset
+    // the arrival counters, so a rank taken now would be meaningless, and the first failure's cause is kept
+    const bool failed = err_raised(a.err);
     const int xcc = static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
-    const int rank = xcc < NX ? atomicAdd(a.xcd_ctr + (step & 1u) * NX + xcc, 1) : NBX;
+    const int rank = failed ? -1 : (xcc < NX ? atomicAdd(a.xcd_ctr + (step & 1u) * NX + xcc, 1) : NBX);
     flag[0] = 0;
     flag[1] = xcc;
     flag[2] = rank;
   }
   __syncthreads();
   const int g = flag[1], j = flag[2];
+  if (j < 0) return;
   if (j >= NBX) {  // not the expected 32 blocks per XCD: fail the step (every other block's wait then times out)
     if (tid == 0) __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -1037,7 +1011,7 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
   XTRACE0(a.L + 1);
 
   // ---- greedy argmax over the blocks' candidates (sampler.cpp:26-61 with top_k = 1) ----
-  float* bv = lds + LD::BV;
+  float* bv = reinterpret_cast<float*>(lds + LD::BV);
   int* bi = reinterpret_cast<int*>(lds + LD::BI);
   const int b = g * NBX + j, nb = NX * NBX;
   __syncthreads();
@@ -1091,7 +1065,7 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
     const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
     a.state[0] = tok;
     a.state[1] = c.pos + 1;
-    a.state[2] = static_cast<int>(step + 1u);
+    a.state[3] = static_cast<int>(step + 1u);
     if (a.ring != nullptr) {
       a.ring[*a.ring_pos] = tok;
       *a.ring_pos += 1;
@@ -1103,12 +1077,13 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
 #undef XSYNC
 #undef XTRACE
 #undef XTRACE0
+#undef XTRACEW
 
 namespace {
 template <int G>
 hipError_t launch_g(const PersistArgs& a, hipStream_t s) {
   // more than 80 KB of LDS per block: one block per CU, so 32 blocks land on each XCD
-  const size_t lds = std::max<size_t>(Lds<G>::TOTAL * sizeof(float), 96 * 1024);
+  const size_t lds = std::max<size_t>(Lds<G>::TOTAL, 96 * 1024);
   static size_t attr_lds = 0;
   if (attr_lds < lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_decode_xcd<G>),
@@ -1130,7 +1105,7 @@ hipError_t launch_decode_xcd(const PersistArgs& a, hipStream_t s) {
 
 hipError_t xcd_blocks_per_cu(int G, int* blocks) {
   *blocks = 0;
-  const size_t lds = std::max<size_t>((G == 1 ? Lds<1>::TOTAL : Lds<2>::TOTAL) * sizeof(float), 96 * 1024);
+  const size_t lds = std::max<size_t>(G == 1 ? Lds<1>::TOTAL : Lds<2>::TOTAL, 96 * 1024);
   if (G == 1) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<1>, NT, lds);
   if (G == 2) return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, k_decode_xcd<2>, NT, lds);
   return hipErrorInvalidValue;
@@ -1147,7 +1122,7 @@ bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus) {
   if (num_cus != NX * NBX || nkv != NX || head_dim != HD) return false;
   const int G = nq / nkv;
   if (nq % nkv != 0 || (G != 1 && G != 2)) return false;
-  if (H % 256 != 0 || H > HMAX) return false;  // each of a block's 8 waves reduces whole 8-line loads
+  if (H % 256 != 0 || H > HMAX) return false;  // each of a block's 8 waves takes whole 32-deep MFMA steps
   if (I % (NX * NBX) != 0 || I > IMAX) return false;
   return true;
 }

@@ -135,7 +135,7 @@ struct PersistArgs {
   float* part_val;            // [nblocks]
   int* part_idx;              // [nblocks]
   int* counter;               // zero; reset by the last block
-  int* state;                 // {token, pos, step}; step starts at 1
+  int* state;                 // {token, pos, step of k_decode_persistent, step of k_decode_xcd}; steps start at 1
   int* ring;                  // nullable
   int* ring_pos;
   int* err;                   // raised when a wait times out
@@ -157,6 +157,7 @@ hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream
 // XCD-partitioned one-launch decode step: 256 blocks, 32 on each of the 8 XCDs, XCD g owns KV head g; two groups of
 // 16 blocks per XCD take alternate layers.
 constexpr int kXcdGroups = 8, kXcdBlocks = 32;
+constexpr int kTracePts = 32;  // diagnostic timestamps per block of k_decode_xcd
 bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus);
 int xcd_loc_stride(int G, int I);  // words per per-XCD hand-off region
 hipError_t xcd_blocks_per_cu(int G, int* blocks);

@@ -253,8 +253,12 @@ int ensure_decode_ws(soc_model* m, int cap) {
     if ((e = hipMemset(pr.first, 0xff, pr.second * sizeof(uint32_t))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.err, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.xcd_ctr, 0, 2 * soc::kXcdGroups * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
-  const int32_t step1 = 1;
-  if ((e = hipMemcpy(w.state + 2, &step1, 4, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "hipMemcpy");
+  // step counters of the two one-launch kernels (state[2]: k_decode_persistent, state[3]: k_decode_xcd): each kernel
+  // derives its exchange tags from its own count, so the tags of its regions advance by one per layer whichever
+  // decode implementation ran in between
+  const int32_t step1[2] = {1, 1};
+  if ((e = hipMemcpy(w.state + 2, step1, sizeof(step1), hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy");
   w.ready = true;
   return SOC_OK;
 }
@@ -546,7 +550,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     const char* trace_path = std::getenv("SOC_TRACE_FILE");
     const size_t trace_roles = 2 * (4 + 8 * static_cast<size_t>(m->cfg.num_hidden_layers));
     const size_t xcd_nb = static_cast<size_t>(soc::kXcdGroups) * soc::kXcdBlocks;
-    const size_t trace_n = xcd ? xcd_nb * 16 + m->cfg.num_hidden_layers + 4
+    const size_t trace_n = xcd ? xcd_nb * soc::kTracePts + m->cfg.num_hidden_layers + 4
                                : trace_roles + static_cast<size_t>(w.nblocks) * 8;
     if (trace_path != nullptr) {
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
@@ -568,20 +572,20 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       if (f != nullptr && xcd) {
         // block (0, 0): layer durations, LM head; then the middle layer's phase points over all blocks
         const int L = m->cfg.num_hidden_layers;
-        const uint64_t* t0p = t.data() + xcd_nb * 16;
+        const uint64_t* t0p = t.data() + xcd_nb * soc::kTracePts;
         std::fprintf(f, "xcd block(0,0) layer us:");
         for (int l = 1; l <= L; ++l) std::fprintf(f, " %.2f", (static_cast<double>(t0p[l]) - t0p[l - 1]) * 0.01);
         std::fprintf(f, " | lm head %.2f\n", (static_cast<double>(t0p[L + 1]) - t0p[L]) * 0.01);
         uint64_t tmin = ~0ull;
         for (size_t b = 0; b < xcd_nb; ++b)
-          if (t[b * 16] != 0) tmin = std::min(tmin, t[b * 16]);
+          if (t[b * soc::kTracePts] != 0) tmin = std::min(tmin, t[b * soc::kTracePts]);
         std::fprintf(f, "xcd middle layer (us from earliest start):");
-        for (int pnt = 0; pnt < 16; ++pnt) {
+        for (int pnt = 0; pnt < soc::kTracePts; ++pnt) {
           std::vector<double> v;
           for (size_t b = 0; b < xcd_nb; ++b)
-            if (t[b * 16 + pnt] != 0) v.push_back((static_cast<double>(t[b * 16 + pnt]) - tmin) * 0.01);
+            if (t[b * soc::kTracePts + pnt] != 0) v.push_back((static_cast<double>(t[b * soc::kTracePts + pnt]) - tmin) * 0.01);
           std::sort(v.begin(), v.end());
-          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJkbega"[pnt], v.front(), v[v.size() / 2], v.back());
+          if (!v.empty()) std::fprintf(f, " %c[%.2f %.2f %.2f]", "0ABCDEFGHIJkbegaLMNOPQRSTUVWXYZ."[pnt], v.front(), v[v.size() / 2], v.back());
         }
         std::fprintf(f, "\n");
         // per block rank j (max over the XCDs) of point D and the first blocks with the latest D
@@ -590,7 +594,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
           double dmax = -1;
           for (int g = 0; g < soc::kXcdGroups; ++g) {
             const size_t b = static_cast<size_t>(g) * soc::kXcdBlocks + j;
-            if (t[b * 16 + 4] != 0) dmax = std::max(dmax, (static_cast<double>(t[b * 16 + 4]) - tmin) * 0.01);
+            if (t[b * soc::kTracePts + 4] != 0) dmax = std::max(dmax, (static_cast<double>(t[b * soc::kTracePts + 4]) - tmin) * 0.01);
           }
           if (dmax >= 0) std::fprintf(f, " j%d:%.2f", j, dmax);
         }
