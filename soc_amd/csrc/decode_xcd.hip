@@ -172,9 +172,11 @@ struct Lds {
   static constexpr int FLAG = RED + 16 * 4;                    // int [8] status, g, j, last block
   static constexpr int BV = FLAG + 8 * 4;                      // fp32 [16] argmax values per slot
   static constexpr int BI = BV + 16 * 4;                       // int [16] argmax indices
-  // fp16 [NW][KT][HD] the waves' V tiles. Phases that never overlap the attention tiles use the same bytes: the
-  // projections' partial sums, the waves' attention partials, E's block partials, the final x * gain of the LM head.
-  static constexpr int VT = BI + 16 * 4;
+  static constexpr int PART = BI + 16 * 4;                     // fp32 [NW][GT 16] the projections' partial sums
+  // fp16 [NW][KT][HD] the waves' V tiles (a wave's first tile is requested at the start of its layer). Phases that
+  // never overlap the attention tiles use the same bytes: the waves' attention partials, E's block partials, the
+  // final x * gain of the LM head.
+  static constexpr int VT = PART + NW * Tiling<G>::GT * 16 * 4;
   static constexpr int WD = VT + NW * KT * HD * 2;             // fp16 [HMAX / 16][ISM] down_proj rows (swizzled)
   static constexpr int WO = WD + (HMAX / NBG) * ISM * 2;       // fp16 [HMAX / 16][G HD] o_proj rows (swizzled)
   static constexpr int TOTAL = WO + (HMAX / NBG) * G * HD * 2;
@@ -205,13 +207,13 @@ __device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
   return 1.0f / sqrtf(s / static_cast<float>(n) + eps);
 }
 
-// Optional phase timestamps (diagnostics): the middle layer's phase points of every block of its group go to
-// trace[block * 16 + point]; block 0 of each group on XCD 0 also writes its layers' starts, the final norm and the
-// step's end into trace[256 * 16 + i].
+// Optional phase timestamps (diagnostics): lane 0 of every wave of the middle layer's group writes its phase points to
+// trace[kTraceWaveBase + (block * 8 + wave) * kTracePts + point]; block 0 of each group on XCD 0 also writes its
+// layers' starts, the final norm and the step's end into trace[256 * kTracePts + i].
+// (The wave's slot, trw, is a wave-uniform pointer computed once per step, nullptr without a trace.)
 #define XTRACE(pt)                                                                                           \
   do {                                                                                                       \
-    if (c.a.trace != nullptr && threadIdx.x == 0 && layer == c.a.L / 2)                                      \
-      c.a.trace[(c.g * NBX + c.j) * kTracePts + (pt)] = now_ticks();                                         \
+    if (trw != nullptr && layer == c.a.L / 2 && (threadIdx.x & 63) == 0) trw[pt] = now_ticks();               \
   } while (0)
 #define XTRACE0(i)                                                                                           \
   do {                                                                                                       \
@@ -220,11 +222,7 @@ __device__ __forceinline__ float rms_scale(const float* red, int n, float eps) {
   } while (0)
 
 // Same, recorded by lane 0 of the wave that takes the first attention tile.
-#define XTRACEW(pt)                                                                                          \
-  do {                                                                                                       \
-    if (c.a.trace != nullptr && (threadIdx.x & 63) == 0 && wr == 0 && layer == c.a.L / 2)                     \
-      c.a.trace[(c.g * NBX + c.j) * kTracePts + (pt)] = now_ticks();                                         \
-  } while (0)
+#define XTRACEW(pt) XTRACE(pt)
 
 // Block barrier; afterwards every thread leaves if a wave reported a failed wait (flag[0] != 0).
 #define XSYNC()                       \
@@ -422,6 +420,8 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
   const bool xlive = w < 4 && lane < per, slive = w == 4 && lane < 4;
   const int off = xlive ? (w * per + lane) * 16 : (H + 4 * lane) * 4;
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
+  // the gains of the lane's quad are requested before the poll: they do not depend on the exchanged words
+  const f16x4 g4 = xlive ? ld_global(reinterpret_cast<const f16x4*>(gain), w * per + lane) : f16x4{0, 0, 0, 0};
   u32x4 v = (xlive || slive) ? ll_peek_buf4(ro, off) : filler;
   uint32_t spins = 0;
   while (!__all(tw_quad_ok(v, tag))) {
@@ -434,7 +434,6 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
   if (xlive) {
     const int q = w * per + lane;
     const f32x4 x = {tw_val(v.x), tw_val(v.y), tw_val(v.z), tw_val(v.w)};
-    const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
     f32x4 y;
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = x[e] * static_cast<float>(g4[e]);
@@ -460,6 +459,8 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   const PersistArgs& a = c.a;
   const int tid = threadIdx.x, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
   const int g = c.g, pgrp = c.j / NBG, jj = c.j % NBG, pos = c.pos, S = pos + 1;
+  uint64_t* const trw =
+      a.trace != nullptr ? a.trace + kTraceWaveBase + ((g * NBX + c.j) * NW + wid) * kTracePts : nullptr;
   const int H = a.H, I = a.I, qd = a.qd;
   const int RH = H / NBG;          // o/down rows per block
   const int IS = I / NX;           // intermediate slice of the XCD
@@ -478,7 +479,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   float* red = reinterpret_cast<float*>(L + LD::RED);
   char* vtb = L + LD::VT;
   f16* vt = reinterpret_cast<f16*>(vtb + wid * KT * HD * 2);        // this wave's V tile [KT][HD] (swizzled)
-  float* part = reinterpret_cast<float*>(vtb);                       // [NW][GT 16] projection partial sums
+  float* part = reinterpret_cast<float*>(L + LD::PART);              // [NW][GT 16] projection partial sums
   f16* wd = reinterpret_cast<f16*>(L + LD::WD);
   f16* wo = reinterpret_cast<f16*>(L + LD::WO);
   uint32_t* loc = a.loc + static_cast<size_t>(g) * a.loc_stride;
@@ -559,16 +560,10 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     __asm__ volatile("" : "+v"(lane), "+v"(rl), "+v"(kq));
     XTRACE0(layer);
     XTRACE(0);
-    // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
     wait_mem();  // this wave's rows of the layer have landed (its LDS rows are published by the barrier below)
-    if (layer == 0)
-      embed_row(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xhl, red);
-    else
-      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red,
-                    layer == a.L / 2 ? 15 : -1);
-    XTRACE(1);
-    XSYNC();  // #1
-    // ---- D's key tiles: wave w takes tiles kb / 32 + (7 - w), + 8, ... ----
+    // ---- D's key tiles: wave w takes tiles kb / 32 + (7 - w), + 8, ... The first is requested here, at the start
+    //      of the layer: the group has nothing to do until the other group's layer ends, and the keys of cached
+    //      positions do not depend on this layer (the first layer of a step has no such slack) ----
     const int kb = allkeys ? 0 : k0, ke = allkeys ? S : k1;
     const int wr = NW - 1 - wid;  // the wave's tile rank: tiles kb / KT + wr, + 8, ...
     const size_t kvb = static_cast<size_t>(layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * HD;
@@ -593,25 +588,40 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
                                                  (p0 + row) * HD * 2 + ((rl ^ (2 * (row & 7))) * 16), 0, 0, 0);
       }
     };
+    const bool early = layer > 0 && (kb / KT + wr) * KT < ke;
+    if (early) load_tile(kb / KT + wr);
+    // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
+    if (layer == 0)
+      embed_row(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xhl, red);
+    else
+      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red,
+                    layer == a.L / 2 ? 15 : -1);
+    XTRACE(1);
+    XSYNC();  // #1
     // ---- B: q/k/v rows of RMSNorm(x): each wave its K slice of every row, the partial sums added in LDS ----
     {
       h8 xa[T::SW];
 #pragma unroll
       for (int s = 0; s < T::SW; ++s) xa[s] = vec_operand(xhl, HMAX, kw0 + 32 * s);
+      f32x4 acc[T::QT];
 #pragma unroll
-      for (int t = 0; t < T::QT; ++t) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < T::QT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < T::SW; ++s)
-          acc = mfma16(xa[s], as_h8(wq[t][s]), acc);  // steps past H meet zero weights
-        if (kq == 0) part[wid * PST + 16 * t + rl] = acc[0] + acc[1] * kLo;
-      }
+      for (int s = 0; s < T::SW; ++s)  // the tiles' chains interleaved; steps past H meet zero weights
+#pragma unroll
+        for (int t = 0; t < T::QT; ++t) acc[t] = mfma16(xa[s], as_h8(wq[t][s]), acc[t]);
+      if (kq == 0)
+#pragma unroll
+        for (int t = 0; t < T::QT; ++t) part[wid * PST + 16 * t + rl] = acc[t][0] + acc[t][1] * kLo;
     }
     XSYNC();  // #1b
     if (wid == 0 && lane < T::RQ) {
+      float p[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) p[w] = part[w * PST + lane];
       float s = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) s += part[w * PST + lane];
+      for (int w = 0; w < NW; ++w) s += p[w];
       ll_store_local(loc_qkv, jj * T::RQ + lane, s * rms_scale(red, H, a.eps), tag);
     }
     XTRACE(2);
@@ -620,11 +630,18 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     //      rank 0 appends them at `pos` ----
     if (wid < G + 2) {
       const int hh = wid;
+      // the head's gains and the RoPE entries are requested before the poll: they do not depend on the exchange
+      float g0 = 1.0f, g1 = 1.0f, rc = 0.0f, rs = 0.0f;
+      if (hh <= G) {
+        const f16* gn = hh < G ? W[2] : W[3];
+        g0 = static_cast<float>(ld_global(gn, lane));
+        g1 = static_cast<float>(ld_global(gn, lane + 64));
+        rc = ld_global(a.rope_cos, static_cast<size_t>(pos) * (HD / 2) + lane);
+        rs = ld_global(a.rope_sin, static_cast<size_t>(pos) * (HD / 2) + lane);
+      }
       float x0, x1;
       if (recv_head(c, loc_qkv + hh * HD, tag, x0, x1)) {
-        if (hh <= G)
-          norm_rope_pair(x0, x1, hh < G ? W[2] : W[3], a.eps, a.rope_cos + static_cast<size_t>(pos) * (HD / 2),
-                         a.rope_sin + static_cast<size_t>(pos) * (HD / 2), lane);
+        if (hh <= G) norm_rope_pair(x0, x1, g0, g1, a.eps, rc, rs);
         if (hh < G) {
           const float qscale = a.scale * 1.44269504088896341f;
 #pragma unroll
@@ -671,7 +688,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int t = kb / KT + wr; t * KT < ke; t += NW) {
         const int p0 = t * KT;
-        load_tile(t);
+        if (!(early && t == kb / KT + wr)) load_tile(t);
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
           if (p0 + 16 * sb + rl == pos)
@@ -838,14 +855,21 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     if (wid < RH / 16) {
       const int row = 16 * wid + rl;
       constexpr int msk = T::GHD / 8 >= 16 ? 15 : T::GHD / 8 - 1;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      constexpr int NS = T::GHD / 32, NH = (NS + 1) / 2;
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int s = 0; s < T::GHD / 32; ++s) {
-        const h8 av = vec_operand(ahl, T::GHD, 32 * s);
-        const h8 bv = *reinterpret_cast<const h8*>(wo + row * T::GHD + (((4 * s + kq) ^ (row & msk)) * 8));
-        acc = mfma16(av, bv, acc);
+      for (int s0 = 0; s0 < NS; s0 += NH) {  // the operands of half the steps requested before their MFMAs
+        h8 av[NH], bv[NH];
+#pragma unroll
+        for (int s = s0; s < s0 + NH && s < NS; ++s) {
+          av[s - s0] = vec_operand(ahl, T::GHD, 32 * s);
+          bv[s - s0] = *reinterpret_cast<const h8*>(wo + row * T::GHD + (((4 * s + kq) ^ (row & msk)) * 8));
+        }
+#pragma unroll
+        for (int s = s0; s < s0 + NH && s < NS; ++s) acc[s & 1] = mfma16(av[s - s0], bv[s - s0], acc[s & 1]);
       }
-      if (kq == 0) ll_store_buf(a.xo, g * H + jj * RH + row, acc[0] + acc[1] * kLo, tag);
+      const f32x4 r = acc[0] + acc[1];
+      if (kq == 0) ll_store_buf(a.xo, g * H + jj * RH + row, r[0] + r[1] * kLo, tag);
     }
     XTRACE(6);
     // ---- G: x' = x + sum_k O_k, RMSNorm input ----
@@ -858,23 +882,31 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       h8 xa[T::SW];
 #pragma unroll
       for (int s = 0; s < T::SW; ++s) xa[s] = vec_operand(xhl, HMAX, kw0 + 32 * s);
+      f32x4 acc[T::GT];
 #pragma unroll
-      for (int t = 0; t < T::GT; ++t) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < T::GT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < T::SW; ++s)
-          acc = mfma16(xa[s], as_h8(wg[t][s]), acc);
-        if (kq == 0) part[wid * PST + 16 * t + rl] = acc[0] + acc[1] * kLo;
-      }
+      for (int s = 0; s < T::SW; ++s)
+#pragma unroll
+        for (int t = 0; t < T::GT; ++t) acc[t] = mfma16(xa[s], as_h8(wg[t][s]), acc[t]);
+      if (kq == 0)
+#pragma unroll
+        for (int t = 0; t < T::GT; ++t) part[wid * PST + 16 * t + rl] = acc[t][0] + acc[t][1] * kLo;
     }
     XSYNC();  // #4b
     if (wid == 0 && lane < RI) {
       const float scale = rms_scale(red, H, a.eps);
+      float pg[NW], pu[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        pg[w] = part[w * PST + lane];
+        pu[w] = part[w * PST + RI + lane];
+      }
       float gs = 0.0f, us = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        gs += part[w * PST + lane];
-        us += part[w * PST + RI + lane];
+        gs += pg[w];
+        us += pu[w];
       }
       ll_store_local(loc_h, jj * RI + lane, silu_ref(gs * scale) * (us * scale), tag);
     }
@@ -907,14 +939,21 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     if (wid < RH / 16) {
       const int row = 16 * wid + rl;
       constexpr int msk = ISM / 8 >= 16 ? 15 : ISM / 8 - 1;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      constexpr int NS = ISM / 32, NH = (NS + 1) / 2;  // steps past IS meet zero operands
+      f32x4 acc[3] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int s = 0; s < ISM / 32; ++s) {  // steps past IS meet zero operands
-        const h8 av = vec_operand(hhl, ISM, 32 * s);
-        const h8 bv = *reinterpret_cast<const h8*>(wd + row * ISM + (((4 * s + kq) ^ (row & msk)) * 8));
-        acc = mfma16(av, bv, acc);
+      for (int s0 = 0; s0 < NS; s0 += NH) {  // the operands of half the steps requested before their MFMAs
+        h8 av[NH], bv[NH];
+#pragma unroll
+        for (int s = s0; s < s0 + NH && s < NS; ++s) {
+          av[s - s0] = vec_operand(hhl, ISM, 32 * s);
+          bv[s - s0] = *reinterpret_cast<const h8*>(wd + row * ISM + (((4 * s + kq) ^ (row & msk)) * 8));
+        }
+#pragma unroll
+        for (int s = s0; s < s0 + NH && s < NS; ++s) acc[s % 3] = mfma16(av[s - s0], bv[s - s0], acc[s % 3]);
       }
-      if (kq == 0) ll_store_buf(a.xd, g * H + jj * RH + row, acc[0] + acc[1] * kLo, tag);
+      const f32x4 r = (acc[0] + acc[1]) + acc[2];
+      if (kq == 0) ll_store_buf(a.xd, g * H + jj * RH + row, r[0] + r[1] * kLo, tag);
     }
     XTRACE(10);
     // the group's next layer: its weight rows stream into registers and LDS while the other group computes (after a

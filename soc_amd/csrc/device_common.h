@@ -126,6 +126,18 @@ __device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const f16* 
   __asm__ volatile("" : "+v"(x0), "+v"(x1));
 }
 
+// The same with the gains g0 = gain[lane], g1 = gain[lane + 64] and the table entries c = cosr[lane], s = sinr[lane]
+// loaded by the caller (so that it can request them early); the same operations in the same order.
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, float g0, float g1, float eps, float c, float s) {
+  const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+  const float scale = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float y0 = x0 * scale * g0;
+  const float y1 = x1 * scale * g1;
+  x0 = fmaf(y0, c, -(y1 * s));
+  x1 = fmaf(y0, s, y1 * c);
+  __asm__ volatile("" : "+v"(x0), "+v"(x1));
+}
+
 // SiLU exactly as the reference writes it: v / (1 + exp(-v)) (Mac/cpu/src/qwen_mlp.cpp:31).
 __device__ __forceinline__ float silu_ref(float v) { return v / (1.0f + expf(-v)); }
 

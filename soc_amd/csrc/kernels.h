@@ -158,6 +158,9 @@ hipError_t launch_decode_persistent(const PersistArgs& a, int nblocks, hipStream
 // 16 blocks per XCD take alternate layers.
 constexpr int kXcdGroups = 8, kXcdBlocks = 32;
 constexpr int kTracePts = 32;  // diagnostic timestamps per block of k_decode_xcd
+// then 128 per-layer slots, then kTracePts timestamps per wave (8 waves per block) of the middle layer
+constexpr int kTraceWaveBase = kXcdGroups * kXcdBlocks * kTracePts + 128;
+constexpr int kTraceTotal = kTraceWaveBase + kXcdGroups * kXcdBlocks * 8 * kTracePts;
 bool xcd_supported(int H, int I, int nq, int nkv, int head_dim, int num_cus);
 int xcd_loc_stride(int G, int I);  // words per per-XCD hand-off region
 hipError_t xcd_blocks_per_cu(int G, int* blocks);

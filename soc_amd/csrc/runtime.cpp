@@ -550,7 +550,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     const char* trace_path = std::getenv("SOC_TRACE_FILE");
     const size_t trace_roles = 2 * (4 + 8 * static_cast<size_t>(m->cfg.num_hidden_layers));
     const size_t xcd_nb = static_cast<size_t>(soc::kXcdGroups) * soc::kXcdBlocks;
-    const size_t trace_n = xcd ? xcd_nb * soc::kTracePts + m->cfg.num_hidden_layers + 4
+    const size_t trace_n = xcd ? static_cast<size_t>(soc::kTraceTotal)
                                : trace_roles + static_cast<size_t>(w.nblocks) * 8;
     if (trace_path != nullptr) {
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
@@ -568,6 +568,13 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       e = hipMemcpy(t.data(), p.trace, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost);
       (void)hipFree(p.trace);
       if (e != hipSuccess) return hip_fail(e, "hipMemcpy trace");
+      if (xcd) {  // the raw timestamps of the last call, for offline analysis
+        FILE* fb = std::fopen((std::string(trace_path) + ".bin").c_str(), "wb");
+        if (fb != nullptr) {
+          (void)std::fwrite(t.data(), sizeof(uint64_t), t.size(), fb);
+          std::fclose(fb);
+        }
+      }
       FILE* f = std::fopen(trace_path, "a");
       if (f != nullptr && xcd) {
         // block (0, 0): layer durations, LM head; then the middle layer's phase points over all blocks
@@ -576,6 +583,10 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
         std::fprintf(f, "xcd block(0,0) layer us:");
         for (int l = 1; l <= L; ++l) std::fprintf(f, " %.2f", (static_cast<double>(t0p[l]) - t0p[l - 1]) * 0.01);
         std::fprintf(f, " | lm head %.2f\n", (static_cast<double>(t0p[L + 1]) - t0p[L]) * 0.01);
+        // the per-block points are wave 0's
+        for (size_t b = 0; b < xcd_nb; ++b)
+          for (int pnt = 0; pnt < soc::kTracePts; ++pnt)
+            t[b * soc::kTracePts + pnt] = t[soc::kTraceWaveBase + (b * 8) * soc::kTracePts + pnt];
         uint64_t tmin = ~0ull;
         for (size_t b = 0; b < xcd_nb; ++b)
           if (t[b * soc::kTracePts] != 0) tmin = std::min(tmin, t[b * soc::kTracePts]);
