@@ -305,6 +305,42 @@ class OracleModel:
         return (toks[:n], logits[:n] if logits is not None else None)
 
 
+class RefCache:
+    """TensorKVCache of the compiled reference (fp32), for cached forwards of a kind="reference" model."""
+
+    def __init__(self, model: OracleModel, max_seq: int):
+        assert model.kind == "reference"
+        self.model = model
+        self.h = ref_lib().ref_cache_create(model.h, max_seq)
+        if not self.h:
+            raise ValueError("ref_cache_create: " + ref_lib().ref_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            ref_lib().ref_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def write(self, layer: int, pos: int, key: np.ndarray, value: np.ndarray) -> None:
+        """TensorKVCache::Write of one position's [nkv][d] keys and values (Mac/cpu/src/kv_cache.cpp:50-78)."""
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        cfg = self.model.cfg
+        if ref_lib().ref_cache_write(self.h, layer, pos, _ptr(k), _ptr(v), cfg.num_key_value_heads, cfg.head_dim) != 0:
+            raise ValueError("ref_cache_write: " + ref_lib().ref_last_error().decode())
+
+    def forward(self, ids, position_offset: int) -> np.ndarray:
+        """QwenCausalLM::ForwardLogitsCached: logits of every row [T][V]."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty((ids.size, self.model.cfg.vocab_size), dtype=np.float32)
+        if ref_lib().ref_forward_logits_cached(self.model.h, self.h, _ptr(ids), ids.size, position_offset,
+                                               _ptr(out)) != 0:
+            raise ValueError("ref_forward_logits_cached: " + ref_lib().ref_last_error().decode())
+        return out
+
+
 class OracleCache:
     """Port-oracle KV cache (fp32) for cached forwards."""
 

@@ -41,7 +41,8 @@ constexpr int HD = 128;
 // Receiver wave: elements i = lane + 64 e (e < MAXE) of a tagged vector, re-read until every one carries `tag`.
 // `addr(i)` gives the source of element i < n. Returns false (wave-uniform) on timeout or a raised error flag.
 template <int MAXE, typename Addr>
-__device__ __forceinline__ bool recv_wait(uint32_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err, int pause) {
+__device__ __forceinline__ bool recv_wait(uint32_t (&v)[MAXE], int n, uint32_t tag, Addr addr, int* err, int pause,
+                                          uint64_t limit) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int e = 0; e < MAXE; ++e) {
@@ -55,7 +56,7 @@ __device__ __forceinline__ bool recv_wait(uint32_t (&v)[MAXE], int n, uint32_t t
 #pragma unroll
     for (int e = 0; e < MAXE; ++e) all = all && tw_tag(v[e]) == tag;
     if (__all(all)) return true;
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > limit || err_raised(err))) {
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
@@ -73,7 +74,7 @@ __device__ __forceinline__ bool recv_wait(uint32_t (&v)[MAXE], int n, uint32_t t
 // Lane l polls the quads q = l + 64 e (elements 4q..4q+3) with one 16-byte load each; n is a multiple of 4.
 template <int MAXQ, bool NORM>
 __device__ __forceinline__ bool recv_vec(const uint32_t* src, int n, uint32_t tag, float* dst, const f16* gain,
-                                         float eps, int* err, int pause) {
+                                         float eps, int* err, int pause, uint64_t limit) {
   const int lane = threadIdx.x & 63;
   const int nq = n / 4;
   f16x4 g[NORM ? MAXQ : 1];
@@ -98,7 +99,7 @@ __device__ __forceinline__ bool recv_vec(const uint32_t* src, int n, uint32_t ta
 #pragma unroll
     for (int e = 0; e < MAXQ; ++e) all = all && tw_quad_ok(v[e], tag);
     if (__all(all)) break;
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(err))) {
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > limit || err_raised(err))) {
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ok = false;
       break;
@@ -282,7 +283,7 @@ __device__ __forceinline__ bool attn_receiver(const Ctx& c, int g, float* qs, fl
                                    const int hidx = i / HD, d = i % HD;
                                    return hidx < G ? q_src + hidx * HD + d : (hidx == G ? k_src + d : v_src + d);
                                  },
-                                 a.err, a.spin_sleep);
+                                 a.err, a.spin_sleep, a.spin_ticks);
     if (ok) {
       // per-head RMSNorm + rotate-half RoPE (qwen_attention.cpp:168-171; rope.cpp:81-84): lane holds dims
       // (lane, lane + 64) of each head; the key and value are rounded to fp16 and appended at `pos`
@@ -488,7 +489,7 @@ __device__ __forceinline__ bool block_recv(const Ctx& c, const uint32_t* src, in
 #pragma unroll
     for (int e = 0; e < MQ; ++e) all = all && tw_quad_ok(v[e], tag);
     if (__all(all)) break;
-    if ((++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err))) {
+    if ((++spins & 63) == 0 && (now_ticks() - t0 > c.a.spin_ticks || err_raised(c.a.err))) {
       __hip_atomic_store(c.a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ok = false;
       break;
@@ -519,10 +520,10 @@ __device__ __forceinline__ bool proj_receiver(const Ctx& c) {
     for (int i = 0; i < 9; ++i) W[i] = ld_global(a.layer_w, static_cast<size_t>(layer) * 9 + i);
     const uint32_t tag = (c.phase0 + static_cast<uint32_t>(layer)) & 3u;
     if (layer == 0) recv_embed<4 * MAXQ_H>(a.embed + static_cast<size_t>(c.token) * H, H, c.xs0, W[0], a.eps);
-    else report(c, recv_vec<MAXQ_H, true>(a.xb, H, (tag - 1u) & 3u, c.xs0, W[0], a.eps, a.err, a.spin_sleep));
+    else report(c, recv_vec<MAXQ_H, true>(a.xb, H, (tag - 1u) & 3u, c.xs0, W[0], a.eps, a.err, a.spin_sleep, a.spin_ticks));
     SOC_SYNC();                                    // P1 input
     if (!block_recv(c, a.attn, a.qd, tag, c.xs1)) return false;  // P3 input
-    report(c, recv_vec<MAXQ_H, true>(a.xa, H, tag, c.xs0, W[1], a.eps, a.err, a.spin_sleep));
+    report(c, recv_vec<MAXQ_H, true>(a.xa, H, tag, c.xs0, W[1], a.eps, a.err, a.spin_sleep, a.spin_ticks));
     SOC_SYNC();                                    // P4 input (receiver alone: its first sight of the data is earliest)
     if (!block_recv(c, a.h, a.I, tag, c.xs1)) return false;      // P5 input
   }
@@ -606,7 +607,7 @@ __device__ __forceinline__ bool proj_compute(const Ctx& c) {
 __device__ __forceinline__ bool lm_receiver(const Ctx& c) {
   const PersistArgs& a = c.a;
   const uint32_t last_tag = (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u;
-  report(c, recv_vec<MAXQ_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err, a.spin_sleep));
+  report(c, recv_vec<MAXQ_H, true>(a.xb, a.H, last_tag, c.xs0, a.final_norm, a.eps, a.err, a.spin_sleep, a.spin_ticks));
   SOC_SYNC();
   return true;
 }
@@ -762,6 +763,11 @@ hipError_t launch_g(const PersistArgs& a, int nblocks, size_t lds, hipStream_t s
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
     attr_lds = lds;
+  }
+  if (a.cooperative) {
+    void* args[] = {const_cast<PersistArgs*>(&a)};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode_persistent<G>), dim3(nblocks), dim3(NT),
+                                      args, static_cast<unsigned>(lds), s);
   }
   hipLaunchKernelGGL(k_decode_persistent<G>, dim3(nblocks), dim3(NT), lds, s, a);
   return hipGetLastError();

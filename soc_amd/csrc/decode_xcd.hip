@@ -238,7 +238,7 @@ __device__ __forceinline__ void wait_failed(const Ctx& c) {
 }
 
 __device__ __forceinline__ bool give_up(const Ctx& c, uint32_t& spins, uint64_t t0) {
-  return (++spins & 63) == 0 && (now_ticks() - t0 > kSpinTicks || err_raised(c.a.err));
+  return (++spins & 63) == 0 && (now_ticks() - t0 > c.a.spin_ticks || err_raised(c.a.err));
 }
 
 // Wave: the quads qi = lane + 64 e < nq of the XCD-local tagged words src[0 .. 4 nq) into dst[4 qi ..] (raw
@@ -1129,6 +1129,11 @@ hipError_t launch_g(const PersistArgs& a, hipStream_t s) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
     attr_lds = lds;
+  }
+  if (a.cooperative) {
+    void* args[] = {const_cast<PersistArgs*>(&a)};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k_decode_xcd<G>), dim3(NX * NBX), dim3(NT), args,
+                                      static_cast<unsigned>(lds), s);
   }
   hipLaunchKernelGGL(k_decode_xcd<G>, dim3(NX * NBX), dim3(NT), lds, s, a);
   return hipGetLastError();

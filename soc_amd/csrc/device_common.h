@@ -19,6 +19,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
+constexpr uint64_t kSpinTicks = 20000000ull;  // default bound of a cross-block wait: 200 ms of the 100 MHz counter
 
 // Global-memory view of a pointer. Pointers read from device memory (per-layer weight tables) are generic to the
 // compiler, which then emits FLAT loads; FLAT loads also count against lgkmcnt, so every later LDS wait of the wave

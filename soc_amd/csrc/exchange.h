@@ -15,8 +15,6 @@
 
 namespace soc {
 
-constexpr uint64_t kSpinTicks = 20000000ull;  // 200 ms of the 100 MHz real-time counter per wait
-
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
 // Tagged exchange word: value rounded to nearest at 21 mantissa bits (relative error <= 2^-22), tag in bits 0..1.

@@ -141,6 +141,9 @@ struct PersistArgs {
   int* err;                   // raised when a wait times out
   uint64_t* trace;            // nullable: phase timestamps (diagnostics)
   int spin_sleep;             // back-off between polling rounds, in units of s_sleep 1 (about 64 clocks)
+  uint64_t spin_ticks;        // bound of every cross-block wait, in ticks of the 100 MHz counter (kSpinTicks)
+  int cooperative;            // launch with hipLaunchCooperativeKernel (the runtime refuses a grid that cannot be
+                              // co-resident instead of leaving its blocks to time out)
   // XCD-partitioned kernel only (k_decode_xcd):
   uint32_t* xo;               // [8][H] tagged partial o_proj outputs of the eight XCDs (cross-XCD)
   uint32_t* xd;               // [8][H] tagged partial down_proj outputs (cross-XCD)

@@ -531,6 +531,12 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
   p.loc_stride = w.loc_stride;
   p.xcd_ctr = w.xcd_ctr;
   if (const char* sl = std::getenv("SOC_SPIN_SLEEP")) p.spin_sleep = std::max(0, std::atoi(sl));
+  // SOC_WAIT_TICKS=<n>: bound of the cross-block waits (tests force the time-out path with a tiny bound; every
+  // block still exits normally, the waits only give up sooner)
+  p.spin_ticks = soc::kSpinTicks;
+  const char* coop = std::getenv("SOC_COOP_LAUNCH");
+  p.cooperative = coop != nullptr && coop[0] == '1';
+  if (const char* wt = std::getenv("SOC_WAIT_TICKS")) p.spin_ticks = std::strtoull(wt, nullptr, 10);
   return p;
 }
 
@@ -546,6 +552,13 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
   const bool xcd = use_xcd(m);
   if (xcd || use_persistent(m)) {
     soc::PersistArgs p = persist_args(m, kv, slot);
+    if (env_flag("SOC_FORCE_WAIT_ERROR")) {
+      // failure-path tests: the error flag as a timed-out wait leaves it, raised before the launches (each block of
+      // each launch then leaves at entry)
+      const int32_t one = 1;
+      if ((e = hipMemcpyAsync(w.err, &one, sizeof(one), hipMemcpyHostToDevice, s)) != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync err");
+    }
     // SOC_TRACE_FILE=<path>: append the last step's per-phase timestamps (diagnostics)
     const char* trace_path = std::getenv("SOC_TRACE_FILE");
     const size_t trace_roles = 2 * (4 + 8 * static_cast<size_t>(m->cfg.num_hidden_layers));
@@ -648,7 +661,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
         m->xcd_off = true;
         return soc::fail(SOC_ERR_HIP, "XCD decode: the launch did not place 32 blocks on each of the 8 XCDs");
       }
-      return soc::fail(SOC_ERR_HIP, "persistent decode: a cross-block wait timed out (grid not co-resident?)");
+      return soc::fail(SOC_ERR_HIP, "one-launch decode: a cross-block wait timed out (grid not co-resident?)");
     }
   } else if (env_flag("SOC_EAGER")) {
     for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_decode(m, kv, slot, nullptr));

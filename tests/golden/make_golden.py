@@ -13,8 +13,23 @@ Fixtures:
                     prompt, generated tokens and every step's full logits row.
   qwen3_0p6b.npz    Qwen3-0.6B architecture, weights N(0, 0.02) seed 1, 32-token prompt (seed 1), 16 greedy tokens.
                     Per step: the 64 largest logits (ids, values), logits at 512 seeded indices, and row statistics.
+  qwen3_0p6b_s2.npz Qwen3-0.6B architecture, tied, weights N(0, 0.05) seed 2, 32-token prompt (seed 2), 16 greedy
+                    tokens, all distinct (the seed-1 model repeats one token), same per-step contents.
+  prefill2048.npz   Qwen3-0.6B (seed 1 weights) prefill of the 2048 uniform-random ids synth_tokens(4, "prefill"):
+                    the last row's 64 largest logits, logits at 512 seeded indices, argmax and row statistics.
+                    Written by this repository's C restatement of the reference (oracle/soc_oracle.cpp) on 8 threads:
+                    the compiled reference needs about an hour for one 2048-token forward on one core. Before it
+                    writes the fixture the script checks, on a 256-token prefill of the same model (all 28 layers),
+                    that the restatement's last-row logits equal the compiled reference's bit for bit.
+  ragged4b.npz      Qwen3-4B architecture (tied, seed 1 weights N(0, 0.02)): one decode step of four of the 16
+                    sequences of the ragged batch (KV lengths synth_int_uniform(5, "ragged.kv_len", 64, 4096),
+                    cache contents N(0, 1) fp16 as soc_kv_fill_synthetic(slot, length, 7) writes them, tokens
+                    synth_tokens(6, "ragged.tokens")): the longest, the shortest, and slots 0 and 1. Per sequence
+                    the slot, length, token, 64 largest logits, logits at 512 seeded indices and argmax, from the
+                    compiled reference.
 
-Usage: python tests/golden/make_golden.py [--skip-0p6b]
+Usage: python tests/golden/make_golden.py [--skip-0p6b] [--only NAME[,NAME...]]
+       (names: dtype, ops, quant, small, 0p6b, 0p6b_s2, prefill2048, ragged4b)
 """
 from __future__ import annotations
 
@@ -29,7 +44,8 @@ ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
 from oracle import oracle as O  # noqa: E402
-from soc_amd import QWEN3_0_6B, QwenConfig, synth_normal_f16, synth_tokens, synth_weights  # noqa: E402
+from soc_amd import (QWEN3_0_6B, QWEN3_4B, QwenConfig, synth_int_uniform, synth_normal_f16,  # noqa: E402
+                     synth_tokens, synth_weights)
 
 OUT = Path(__file__).resolve().parent
 
@@ -131,6 +147,18 @@ def write_small_models() -> None:
         print(name, toks.tolist(), flush=True)
 
 
+def row_summary(logits: np.ndarray, vocab: int) -> dict[str, np.ndarray]:
+    """The parts of full-vocabulary logit rows a fixture keeps: the 64 largest (ids, values), 512 seeded samples,
+    and per-row sum, sum of squares and maximum."""
+    logits = np.atleast_2d(logits)
+    idx = np.sort(np.unique(synth_tokens(1, "fixture.sample", vocab, 600)))[:512].astype(np.int32)
+    top_ids = np.argsort(-logits, axis=1, kind="stable")[:, :64].astype(np.int32)
+    top_vals = np.take_along_axis(logits, top_ids, axis=1)
+    stats = np.stack([logits.astype(np.float64).sum(1), (logits.astype(np.float64) ** 2).sum(1),
+                      logits.max(1).astype(np.float64)], axis=1)
+    return dict(top_ids=top_ids, top_vals=top_vals, sample_idx=idx, sample_vals=logits[:, idx], stats=stats)
+
+
 def write_0p6b() -> None:
     cfg = QWEN3_0_6B
     t0 = time.time()
@@ -138,30 +166,93 @@ def write_0p6b() -> None:
     prompt = synth_tokens(1, "prompt", cfg.vocab_size, 32)
     m = O.OracleModel(cfg, w, "reference")
     toks, logits = m.generate(prompt, 16, want_logits=True)
-    idx = np.sort(np.unique(synth_tokens(1, "fixture.sample", cfg.vocab_size, 600)))[:512].astype(np.int32)
-    top_ids = np.argsort(-logits, axis=1, kind="stable")[:, :64].astype(np.int32)
-    top_vals = np.take_along_axis(logits, top_ids, axis=1)
-    stats = np.stack([logits.astype(np.float64).sum(1), (logits.astype(np.float64) ** 2).sum(1),
-                      logits.max(1).astype(np.float64)], axis=1)
-    np.savez_compressed(OUT / "qwen3_0p6b.npz", weight_seed=np.int64(1), prompt=prompt, tokens=toks, top_ids=top_ids,
-                        top_vals=top_vals, sample_idx=idx, sample_vals=logits[:, idx], stats=stats)
+    np.savez_compressed(OUT / "qwen3_0p6b.npz", weight_seed=np.int64(1), prompt=prompt, tokens=toks,
+                        **row_summary(logits, cfg.vocab_size))
     print("qwen3-0.6b", toks.tolist(), f"{time.time() - t0:.1f}s", flush=True)
+
+
+def write_0p6b_s2() -> None:
+    cfg, seed, sigma = QWEN3_0_6B, 2, 0.05
+    t0 = time.time()
+    w = synth_weights(cfg, seed, sigma)
+    prompt = synth_tokens(seed, "prompt", cfg.vocab_size, 32)
+    m = O.OracleModel(cfg, w, "reference")
+    toks, logits = m.generate(prompt, 16, want_logits=True)
+    assert len(set(toks.tolist())) == len(toks), "the fixture is meant to have distinct greedy tokens"
+    np.savez_compressed(OUT / "qwen3_0p6b_s2.npz", weight_seed=np.int64(seed), sigma=np.float32(sigma), prompt=prompt,
+                        tokens=toks, **row_summary(logits, cfg.vocab_size))
+    print("qwen3-0.6b seed 2", toks.tolist(), f"{time.time() - t0:.1f}s", flush=True)
+
+
+def write_prefill2048() -> None:
+    cfg = QWEN3_0_6B
+    t0 = time.time()
+    w = synth_weights(cfg, 1)
+    ids = synth_tokens(4, "prefill", cfg.vocab_size, 2048)
+    O.set_threads(8)
+    port = O.OracleModel(cfg, w, "port")
+    # pin the restatement at this model's full depth against the compiled reference (256-token prefill, last row)
+    ref = O.OracleModel(cfg, w, "reference")
+    want = ref.forward_logits(ids[:256])[-1]
+    ref.close()
+    cache = O.OracleCache(port, 256)
+    got = cache.forward(ids[:256], 0, 1)[0]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "port and reference differ at 256 tokens"
+    print(f"prefill2048: restatement == reference at 256 tokens ({time.time() - t0:.1f}s)", flush=True)
+    cache = O.OracleCache(port, 2048)
+    row = cache.forward(ids, 0, 1)[0]
+    np.savez_compressed(OUT / "prefill2048.npz", weight_seed=np.int64(1), ids_seed=np.int64(4), n=np.int64(2048),
+                        argmax=np.int32(int(np.argmax(row))), **row_summary(row, cfg.vocab_size))
+    print("prefill2048 argmax", int(np.argmax(row)), f"{time.time() - t0:.1f}s", flush=True)
+
+
+def write_ragged4b() -> None:
+    cfg = QWEN3_4B
+    t0 = time.time()
+    w = synth_weights(cfg, 1)
+    lens = synth_int_uniform(5, "ragged.kv_len", 64, 4096, 16)
+    toks = synth_tokens(6, "ragged.tokens", cfg.vocab_size, 16)
+    slots = sorted({int(np.argmax(lens)), int(np.argmin(lens)), 0, 1})
+    ref = O.OracleModel(cfg, w, "reference")
+    L, nkv, d = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    rows = []
+    for slot in slots:
+        n = int(lens[slot])
+        cache = O.RefCache(ref, n + 1)
+        for layer in range(L):
+            k = np.stack([synth_normal_f16(7, f"kv.{slot}.{layer}.{h}.k", 1.0, n * d).reshape(n, d) for h in range(nkv)],
+                         axis=1)
+            v = np.stack([synth_normal_f16(7, f"kv.{slot}.{layer}.{h}.v", 1.0, n * d).reshape(n, d) for h in range(nkv)],
+                         axis=1)
+            kf = O.f16_to_f32(k)
+            vf = O.f16_to_f32(v)
+            for p in range(n):
+                cache.write(layer, p, kf[p], vf[p])
+        rows.append(cache.forward(toks[slot:slot + 1], n)[0])
+        cache.close()
+        print(f"ragged4b slot {slot} (kv {n}): argmax {int(np.argmax(rows[-1]))} ({time.time() - t0:.1f}s)", flush=True)
+    logits = np.stack(rows)
+    np.savez_compressed(OUT / "ragged4b.npz", weight_seed=np.int64(1), slots=np.array(slots, np.int32),
+                        kv_lens=lens.astype(np.int32), tokens=toks, argmax=np.argmax(logits, axis=1).astype(np.int32),
+                        **row_summary(logits, cfg.vocab_size))
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-0p6b", action="store_true")
+    ap.add_argument("--only", default="", help="comma-separated fixture names")
     args = ap.parse_args()
     O.build(ref=True)
     if not O.ref_available():
         sys.exit("the reference library could not be built (is /root/reference present?)")
     ref = O.ref_lib()
-    write_dtype(ref)
-    write_ops(ref)
-    write_quant(ref)
-    write_small_models()
-    if not args.skip_0p6b:
-        write_0p6b()
+    writers = {"dtype": lambda: write_dtype(ref), "ops": lambda: write_ops(ref), "quant": lambda: write_quant(ref),
+               "small": write_small_models, "0p6b": write_0p6b, "0p6b_s2": write_0p6b_s2,
+               "prefill2048": write_prefill2048, "ragged4b": write_ragged4b}
+    heavy = ["0p6b", "0p6b_s2", "prefill2048", "ragged4b"]
+    names = [n for n in args.only.split(",") if n] or [n for n in writers if not (args.skip_0p6b and n in heavy)]
+    for n in names:
+        writers[n]()
 
 
 if __name__ == "__main__":

@@ -14,19 +14,9 @@ import numpy as np
 import pytest
 
 import soc_amd as S
+from tests.parity import assert_logits_close
 
 pytestmark = pytest.mark.gpu
-
-ATOL, RTOL = 2e-2, 1e-2
-
-
-def assert_logits_close(got, ref, what=""):
-    got = np.asarray(got, np.float32)
-    ref = np.asarray(ref, np.float32)
-    err = float(np.max(np.abs(got - ref)))
-    scale = float(np.max(np.abs(ref)))
-    assert err <= ATOL and err <= RTOL * scale, f"{what}: max abs err {err:.3e}, ref scale {scale:.3e}"
-
 
 def small_cfg(nq=4, nkv=2):
     return S.QwenConfig(vocab_size=2048, hidden_size=256, num_hidden_layers=2, num_attention_heads=nq,
@@ -154,6 +144,48 @@ def test_batch_matches_oracle_mixed_lengths(gpu_ctx, oracle_mod):
             assert_logits_close(lg[i], ref[0], f"row {i} (slot {slot}, {n} cached positions)")
             assert int(nxt[i]) == oracle_mod.sample(ref[0])
             assert kv.length(int(slot)) == n + 1
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_ragged_qwen3_4b_matches_reference(gpu_ctx, golden):
+    """The benchmarked ragged step at its own workload: Qwen3-4B (seed-1 weights), 16 sequences with KV lengths
+    U[64, 4096] (seed 5) of seeded N(0, 1) fp16 contents, one token each (seed 6). The rows of the longest and
+    shortest sequences and of slots 0 and 1 against the compiled reference's cached forward over the same caches;
+    then a second step of all 16 rows, whose checked rows equal single-sequence decode of those slots."""
+    g = golden("ragged4b.npz")
+    cfg = S.QWEN3_4B
+    m = S.Model(gpu_ctx, cfg).synthesize(int(g["weight_seed"]), 0.02)
+    lens = g["kv_lens"].astype(np.int64)
+    n = len(lens)
+    kv = S.KVCache(m, n, int(lens.max()) + 4)
+    try:
+        for slot, ln in enumerate(lens):
+            kv.fill_synthetic(slot, int(ln), 7)
+        slots = np.arange(n, dtype=np.int32)
+        toks = g["tokens"]
+        lg, nxt = S.decode_batch(m, kv, slots, toks)
+        for r, slot in enumerate(g["slots"]):
+            what = f"4B ragged slot {int(slot)} (kv {int(lens[slot])})"
+            assert int(nxt[slot]) == int(g["argmax"][r]), what
+            assert_logits_close(lg[slot][g["top_ids"][r]], g["top_vals"][r], what + " top-64")
+            assert_logits_close(lg[slot][g["sample_idx"]], g["sample_vals"][r], what + " sampled")
+        # a second batch step vs one-sequence decode of the same slots (a second cache with the same contents in
+        # those slots)
+        lg2, nxt2 = S.decode_batch(m, kv, slots, nxt)
+        one = S.KVCache(m, n, int(lens.max()) + 4)
+        try:
+            for slot in g["slots"]:
+                slot = int(slot)
+                one.fill_synthetic(slot, int(lens[slot]), 7)
+                _, t0 = S.decode(m, one, slot, int(toks[slot]))
+                assert t0 == int(nxt[slot])
+                lg1, t1 = S.decode(m, one, slot, t0)
+                assert t1 == int(nxt2[slot])
+                assert_logits_close(lg2[slot], lg1, f"4B ragged slot {slot} batch step 2 vs decode")
+        finally:
+            one.close()
     finally:
         kv.close()
         m.close()
