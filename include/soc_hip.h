@@ -114,6 +114,15 @@ int soc_decode(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, f
  * tokens_out[steps] receives the generated ids. */
 int soc_decode_steps(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, int32_t steps,
                      int32_t* tokens_out);
+/* No counterpart in the reference: for callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc). soc_decode_steps with the same results, its device buffers (exchange state of the
+ * one-launch decode kernel, token ring) taken from a 4 MiB array compiled into the library, one per device, held
+ * until the process ends, instead of hipMalloc'd scratch; it allocates nothing. Needs a model that
+ * soc_model_decode_path reports as 1 or 2 (else SOC_ERR_INVALID); fails with SOC_ERR_CAPACITY when the model's
+ * exchange state plus 4 bytes per step exceed 4 MiB (about 900k steps at Qwen3-0.6B shape). Every call re-initialises
+ * the array; calls that overlap on one device race on it. */
+int soc_decode_steps_noalloc(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, int32_t steps,
+                             int32_t* tokens_out);
 
 /* ---- Ragged multi-sequence decode. The reference decodes one sequence per call (GenerationContext::
  *      DecodeNextToken, Mac/gpu/src/runtime/generation_context.cpp:68-172, one token at pos = len - 1); a batch of n

@@ -132,6 +132,7 @@ def lib() -> C.CDLL:
         "soc_prefill": (C.c_int, [P, P, I32, P, I32, I32, I32, P, C.POINTER(I32)]),
         "soc_decode": (C.c_int, [P, P, I32, I32, P, C.POINTER(I32)]),
         "soc_decode_steps": (C.c_int, [P, P, I32, I32, I32, P]),
+        "soc_decode_steps_noalloc": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_decode_batch": (C.c_int, [P, P, I32, P, P, P, P]),
         "soc_decode_batch_steps": (C.c_int, [P, P, I32, P, P, I32, P]),
         "soc_gemv_f16": (C.c_int, [P, P, P, P, I32, I32]),
@@ -363,6 +364,13 @@ def decode(model: Model, kv: KVCache, slot: int, last_token: int, want_logits: b
 def decode_steps(model: Model, kv: KVCache, slot: int, last_token: int, steps: int) -> np.ndarray:
     out = np.empty(steps, dtype=np.int32)
     check(lib().soc_decode_steps(model.h, kv.h, slot, int(last_token), steps, _ptr(out)))
+    return out
+
+
+def decode_steps_noalloc(model: Model, kv: KVCache, slot: int, last_token: int, steps: int) -> np.ndarray:
+    """decode_steps through soc_decode_steps_noalloc (device buffers from the library's static scratch array)."""
+    out = np.empty(steps, dtype=np.int32)
+    check(lib().soc_decode_steps_noalloc(model.h, kv.h, slot, int(last_token), steps, _ptr(out)))
     return out
 
 

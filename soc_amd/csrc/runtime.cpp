@@ -52,7 +52,31 @@ struct soc_ctx {
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool timing = false;
+  uint32_t* scratch = nullptr;  // device address of this device's copy of `scratch` (soc_decode_steps_noalloc)
 };
+
+// Device memory of soc_decode_steps_noalloc: the exchange state of the one-launch decode kernels and the token ring
+// live here instead of in hipMalloc'd buffers. One copy per device for the whole process; every call re-initialises
+// what it uses, and calls that overlap on one device race on it. Host code never passes `scratch` itself (the host
+// symbol is only a stand-in): it uses the address hipGetSymbolAddress returned for the device, kept in soc_ctx.
+constexpr size_t kNoAllocScratchBytes = size_t{4} << 20;
+static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / 4];
+
+// Fills words [0, n_zero) with zero except the four decode-state words at `state_at` ({token, pos, 1, 1}: the step
+// counters of both one-launch kernels start at 1) and words [ff_at, ff_at + n_ff) with 0xffffffff (tag 3 in every
+// exchange word; the first phase of a step expects tag 0).
+__global__ void k_noalloc_init(uint32_t* base, int n_zero, int state_at, int ff_at, int n_ff, int32_t token,
+                               int32_t pos) {
+  const int stride = gridDim.x * blockDim.x;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += stride) {
+    uint32_t v = 0;
+    if (i == state_at) v = static_cast<uint32_t>(token);
+    else if (i == state_at + 1) v = static_cast<uint32_t>(pos);
+    else if (i == state_at + 2 || i == state_at + 3) v = 1u;
+    base[i] = v;
+  }
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_ff; i += stride) base[ff_at + i] = 0xffffffffu;
+}
 
 namespace {
 
@@ -486,9 +510,8 @@ bool use_persistent(soc_model* m) {
   return per_cu * m->ctx->num_cus >= nb;
 }
 
-soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot) {
+soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot, const DecodeWs& w) {
   const soc_qwen_config& c = m->cfg;
-  DecodeWs& w = m->dws;
   soc::PersistArgs p{};
   p.layer_w = m->d_layer_w;
   p.embed = m->embed;
@@ -551,7 +574,7 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     return hip_fail(e, "hipMemcpyAsync ring");
   const bool xcd = use_xcd(m);
   if (xcd || use_persistent(m)) {
-    soc::PersistArgs p = persist_args(m, kv, slot);
+    soc::PersistArgs p = persist_args(m, kv, slot, w);
     if (env_flag("SOC_FORCE_WAIT_ERROR")) {
       // failure-path tests: the error flag as a timed-out wait leaves it, raised before the launches (each block of
       // each launch then leaves at entry)
@@ -974,6 +997,10 @@ int soc_ctx_create(int device, soc_ctx** out) {
   if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   std::unique_ptr<soc_ctx> c(new soc_ctx());
   c->device = device;
+  // this device's copy of the no-allocation scratch array (the device is current)
+  void* sp = nullptr;
+  if ((e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) != hipSuccess) return hip_fail(e, "hipGetSymbolAddress");
+  c->scratch = static_cast<uint32_t*>(sp);
   if ((e = hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
     return hip_fail(e, "hipDeviceGetAttribute");
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
@@ -1620,6 +1647,91 @@ int soc_decode_steps(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, int32
   hipError_t e = hipMemcpyAsync(tokens_out, m->dws.ring, static_cast<size_t>(steps) * 4, hipMemcpyDeviceToHost, s);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync tokens");
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode steps");
+  kv->len[slot] += steps;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_decode_steps_noalloc(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, int32_t steps,
+                             int32_t* tokens_out) {
+  SOC_API_BEGIN
+  if (m == nullptr || kv == nullptr || (steps > 0 && tokens_out == nullptr))
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
+  if (m->ctx->scratch == nullptr) return soc::fail(SOC_ERR_STATE, "no scratch address for this device");
+  const soc_qwen_config& c = m->cfg;
+  // word layout of the scratch array, regions rounded to 256 bytes: counters and flags, argmax partials (zeroed),
+  // exchange vectors (0xff), token ring
+  auto up = [](size_t n) { return (n + 63) & ~size_t{63}; };
+  const size_t nb = static_cast<size_t>(std::max(m->ctx->num_cus, soc::kXcdGroups * soc::kXcdBlocks));
+  const int G = c.num_attention_heads / c.num_key_value_heads;
+  const size_t H = static_cast<size_t>(c.hidden_size), loc_stride = up(soc::xcd_loc_stride(G, c.intermediate_size));
+  const size_t o_err = 0, o_state = 64, o_ring_pos = 128, o_counter = 192, o_xcd_ctr = 256, o_pv = 320,
+               o_pi = o_pv + up(nb), n_zero = o_pi + up(nb);
+  const size_t o_xa = n_zero, o_xb = o_xa + up(H), o_qkv = o_xb + up(H), o_attn = o_qkv + up(m->qkv_rows),
+               o_h = o_attn + up(m->qd), o_xo = o_h + up(c.intermediate_size), o_xd = o_xo + soc::kXcdGroups * up(H),
+               o_xp = o_xd + soc::kXcdGroups * up(H), o_loc = o_xp + up(H), o_ring = o_loc + soc::kXcdGroups * loc_stride;
+  const size_t need = (o_ring + up(static_cast<size_t>(steps))) * 4;
+  if (need > kNoAllocScratchBytes)
+    return soc::fail(SOC_ERR_CAPACITY, "soc_decode_steps_noalloc: " + std::to_string(steps) + " steps need " +
+                                           std::to_string(need) + " bytes of scratch; the maximum is " +
+                                           std::to_string(kNoAllocScratchBytes) + " (4 bytes per step)");
+  if (kv->len[slot] + steps > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
+  if (steps == 0) return SOC_OK;
+  SOC_TRY(validate_ids(m, &last, 1));
+  const bool xcd = use_xcd(m);
+  if (!xcd && !use_persistent(m))
+    return soc::fail(SOC_ERR_INVALID, "soc_decode_steps_noalloc: this model has no one-launch decode kernel");
+  uint32_t* base = m->ctx->scratch;
+  DecodeWs w;
+  w.err = reinterpret_cast<int*>(base + o_err);
+  w.state = reinterpret_cast<int*>(base + o_state);
+  w.ring_pos = reinterpret_cast<int*>(base + o_ring_pos);
+  w.lm_counter = reinterpret_cast<int*>(base + o_counter);
+  w.xcd_ctr = reinterpret_cast<int*>(base + o_xcd_ctr);
+  w.pv = reinterpret_cast<float*>(base + o_pv);
+  w.pi = reinterpret_cast<int*>(base + o_pi);
+  w.xa = base + o_xa;
+  w.xb = base + o_xb;
+  w.qkv_x = base + o_qkv;
+  w.attn_x = base + o_attn;
+  w.h_x = base + o_h;
+  w.xo = base + o_xo;
+  w.xd = base + o_xd;
+  w.xp = base + o_xp;
+  w.loc = base + o_loc;
+  w.loc_stride = static_cast<int>(loc_stride);
+  w.ring = reinterpret_cast<int*>(base + o_ring);
+  w.nblocks = m->ctx->num_cus;
+  hipStream_t s = m->ctx->stream;
+  // the previous call's contents are stale (any model may have used the array): counters, flags and the decode
+  // state restart, every exchange word carries tag 3; a kernel, not hipMemsetAsync, so a captured call replays it
+  hipLaunchKernelGGL(k_noalloc_init, dim3(64), dim3(256), 0, s, base, static_cast<int>(n_zero),
+                     static_cast<int>(o_state), static_cast<int>(o_xa), static_cast<int>(o_ring - o_xa), last,
+                     kv->len[slot]);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "scratch init launch");
+  const soc::PersistArgs p = persist_args(m, kv, slot, w);
+  for (int i = 0; i < steps; ++i)
+    if ((e = xcd ? soc::launch_decode_xcd(p, s) : soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
+      return hip_fail(e, "one-launch decode launch");
+  int32_t err = 0;
+  if ((e = hipMemcpyAsync(tokens_out, w.ring, static_cast<size_t>(steps) * 4, hipMemcpyDeviceToHost, s)) !=
+      hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync tokens");
+  if ((e = hipMemcpyAsync(&err, w.err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync err");
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode steps (no allocation)");
+  if (err != 0) {
+    if (xcd && err == 2) {
+      m->xcd_off = true;
+      return soc::fail(SOC_ERR_HIP, "XCD decode: the launch did not place 32 blocks on each of the 8 XCDs");
+    }
+    return soc::fail(SOC_ERR_HIP, "one-launch decode: a cross-block wait timed out (grid not co-resident?)");
+  }
   kv->len[slot] += steps;
   return SOC_OK;
   SOC_API_END
