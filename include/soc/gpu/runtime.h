@@ -1,19 +1,28 @@
-// runtime.h - the reference GPU runtime's C++ host interface, kept for callers, on top of the C ABI (soc_hip.h).
+// runtime.h - the reference GPU runtime's C++ host interface, kept for its callers, on top of the C ABI (soc_hip.h).
 //
-// Class and method names, argument meaning and error behaviour follow SongWooYoung/SoC Mac/gpu/include:
-//   MetalContext        -> HipContext            (metal/metal_context.h)
-//   PipelineCache       -> PipelineCache         (kernel/pipeline_cache.h; kernels are compiled ahead of time)
-//   BufferArena         -> BufferArena           (buffer/buffer_arena.h; scratch is owned by the library, the
-//                                                  arena keeps the reference's mark/reset/telemetry surface)
+// Class and method names, signatures, argument meaning and error behaviour follow SongWooYoung/SoC Mac/gpu/include:
+//   MetalContext        -> HipContext            (metal/metal_context.h; kernels are compiled into the library)
+//   MetalBuffer         -> HipBuffer             (buffer/metal_buffer.h; device memory, Write/Read copy)
+//   TensorDesc          -> TensorDesc            (tensor/tensor_desc.h)
+//   DeviceTensor        -> DeviceTensor          (tensor/device_tensor.h)
+//   PipelineCache       -> PipelineCache         (kernel/pipeline_cache.h)
+//   BufferArena         -> BufferArena           (buffer/buffer_arena.h; the forward's scratch is the library's own)
 //   QwenCausalLM        -> QwenCausalLM          (model/qwen_causal_lm.h)
 //   QwenModelLoader     -> QwenModelLoader       (model/qwen_model_loader.h; from named host fp16 tensors)
 //   KVCache             -> KVCache               (runtime/kv_cache.h)
 //   CommandScheduler    -> CommandScheduler      (runtime/command_scheduler.h)
 //   Sampler             -> Sampler               (runtime/sampler.h)
 //   GenerationContext   -> GenerationContext     (runtime/generation_context.h)
-// Token ids and logits cross this interface as host vectors (the reference passes DeviceTensors that it fills from
-// host vectors right before each call). Every method returns bool and fills an optional std::string* error message;
-// nothing throws.
+// MetalContext, MetalBuffer and MetalProfilingSnapshot are also declared under their reference names (aliases at the
+// end of this file), so that reference callers compile unchanged. Every method returns bool (or a null pointer) and
+// fills an optional std::string* error message; nothing throws.
+//
+// Differences a caller can observe (storage is fp16 where the reference stores fp32):
+//   * KVCache keeps fp16 keys/values [kv_head][max_sequence_length][head_dim] per layer; ViewForLayer describes that
+//     (kFloat16, shape {kv_heads, length, head_dim}, strides {max_len * head_dim, head_dim, 1}); AppendPrefill and
+//     AppendDecodeToken take fp32 (as the reference) or fp16 rows [rows][kv_heads * head_dim] and round to fp16.
+//   * CommandScheduler writes the logits of the last r token rows when logits_output has r <= n rows (r = n is the
+//     reference's all-rows output); an invalid (empty) logits_output skips the logits.
 #pragma once
 
 #include <cstddef>
@@ -27,19 +36,106 @@
 
 namespace soc::gpu {
 
+struct HipProfilingSnapshot {  // metal_context.h:19-22
+  double gpu_ms = 0.0;         // GPU time of the forwards run since ResetProfiling (HIP events)
+  std::size_t command_buffer_count = 0;
+};
+
 class HipContext {
  public:
   static std::unique_ptr<HipContext> CreateDefault(int device, std::string* error_message);
+  // The reference's factory (metal_context.h:26-28): the kernel paths are not needed (the kernels are compiled into
+  // the library); device 0.
+  static std::unique_ptr<HipContext> CreateDefault(const std::string& kernel_library_path,
+                                                   const std::string& kernel_source_path,
+                                                   std::string* error_message);
   ~HipContext();
   HipContext(const HipContext&) = delete;
   HipContext& operator=(const HipContext&) = delete;
 
   soc_ctx* handle() const { return ctx_; }
   bool Synchronize(std::string* error_message) const;
+  void ResetProfiling() const { profile_ = {}; }
+  HipProfilingSnapshot GetProfilingSnapshot() const { return profile_; }
+  void AddProfile(double gpu_ms) const {
+    profile_.gpu_ms += gpu_ms;
+    profile_.command_buffer_count += 1;
+  }
 
  private:
   explicit HipContext(soc_ctx* ctx) : ctx_(ctx) {}
   soc_ctx* ctx_ = nullptr;
+  mutable HipProfilingSnapshot profile_;
+};
+
+// Device memory (metal_buffer.h:13-37). Write/Read copy between host memory and the buffer and return when done.
+class HipBuffer {
+ public:
+  static std::shared_ptr<HipBuffer> CreateShared(const HipContext& context, std::size_t size_bytes,
+                                                 const std::string& label, std::string* error_message);
+  // A view of device memory that `owner` keeps alive (the KV cache's layer planes).
+  static std::shared_ptr<HipBuffer> Wrap(const HipContext& context, void* device_ptr, std::size_t size_bytes,
+                                         std::shared_ptr<void> owner);
+  ~HipBuffer();
+  HipBuffer(const HipBuffer&) = delete;
+  HipBuffer& operator=(const HipBuffer&) = delete;
+
+  std::size_t GetSizeBytes() const { return size_; }
+  bool IsHostVisible() const { return false; }
+  bool Write(const void* source, std::size_t size_bytes, std::size_t offset_bytes, std::string* error_message);
+  bool Read(void* destination, std::size_t size_bytes, std::size_t offset_bytes, std::string* error_message) const;
+  const void* GetNativeHandle() const { return ptr_; }  // the device address
+  void* data() const { return ptr_; }
+  soc_ctx* context() const { return ctx_; }
+
+ private:
+  HipBuffer(soc_ctx* ctx, void* ptr, std::size_t size, std::shared_ptr<void> owner)
+      : ctx_(ctx), ptr_(ptr), size_(size), owner_(std::move(owner)) {}
+  soc_ctx* ctx_ = nullptr;
+  void* ptr_ = nullptr;
+  std::size_t size_ = 0;
+  std::shared_ptr<void> owner_;  // null: this buffer owns ptr_
+};
+
+enum class DataType { kFloat16, kFloat32, kInt32 };  // tensor_desc.h:8-12
+std::size_t GetDataTypeSize(DataType data_type);
+
+class TensorDesc {  // tensor_desc.h:14-32
+ public:
+  static TensorDesc CreateContiguous(DataType data_type, const std::vector<std::size_t>& shape);
+  // Element strides given explicitly (views of the KV cache).
+  static TensorDesc CreateStrided(DataType data_type, const std::vector<std::size_t>& shape,
+                                  const std::vector<std::size_t>& strides);
+  DataType GetDataType() const { return data_type_; }
+  const std::vector<std::size_t>& GetShape() const { return shape_; }
+  const std::vector<std::size_t>& GetStrides() const { return strides_; }
+  std::size_t Rank() const { return shape_.size(); }
+  std::size_t ElementCount() const;
+  std::size_t ByteSize() const;  // bytes spanned from element 0 to the last element
+  bool IsContiguous() const { return contiguous_; }
+
+ private:
+  DataType data_type_ = DataType::kFloat32;
+  std::vector<std::size_t> shape_;
+  std::vector<std::size_t> strides_;
+  bool contiguous_ = false;
+};
+
+class DeviceTensor {  // device_tensor.h:11-25
+ public:
+  DeviceTensor() = default;
+  DeviceTensor(std::shared_ptr<HipBuffer> buffer, std::size_t byte_offset, TensorDesc desc)
+      : buffer_(std::move(buffer)), byte_offset_(byte_offset), desc_(std::move(desc)) {}
+  bool IsValid() const;  // a buffer, and the tensor's bytes lie inside it
+  const std::shared_ptr<HipBuffer>& GetBuffer() const { return buffer_; }
+  std::size_t GetByteOffset() const { return byte_offset_; }
+  const TensorDesc& GetDesc() const { return desc_; }
+  void* data() const { return buffer_ ? static_cast<char*>(buffer_->data()) + byte_offset_ : nullptr; }
+
+ private:
+  std::shared_ptr<HipBuffer> buffer_;
+  std::size_t byte_offset_ = 0;
+  TensorDesc desc_;
 };
 
 // Kernels are compiled for gfx950 when the library is built; the cache only keeps the reference's call shape.
@@ -52,24 +148,67 @@ class PipelineCache {
   const HipContext* context_;
 };
 
-// Scratch bookkeeping with the reference's scope API (Mac/gpu/include/buffer/buffer_arena.h:71-80). The forward's
-// device scratch is allocated and reused by the library; the arena records named scope peaks for telemetry.
+// buffer_arena.h:15-80: a bump allocator over one device buffer with marks and per-scope telemetry. The forward
+// passes keep their scratch inside the library, so the arena serves callers' own temporaries.
+using BufferArenaMark = std::size_t;
+
+struct BufferArenaSlice {
+  std::shared_ptr<HipBuffer> buffer;
+  std::size_t offset_bytes = 0;
+  std::size_t size_bytes = 0;
+  bool IsValid() const { return buffer != nullptr && size_bytes > 0; }
+};
+
+struct BufferArenaScopeTelemetry {
+  std::string name;
+  std::size_t invocation_count = 0;
+  std::size_t peak_delta_bytes = 0;
+  std::size_t peak_used_bytes = 0;
+  std::size_t peak_allocation_count = 0;
+};
+
 class BufferArena {
  public:
   static std::unique_ptr<BufferArena> CreateShared(const HipContext& context, std::size_t capacity_bytes,
                                                    const std::string& label, std::string* error_message);
+  bool Allocate(std::size_t size_bytes, std::size_t alignment_bytes, BufferArenaSlice* slice,
+                std::string* error_message);
+  BufferArenaMark GetMark() const { return used_; }
+  bool ResetToMark(BufferArenaMark mark, std::string* error_message);
+  void Reset() { used_ = 0; }
+  void ClearTelemetry();
   std::size_t GetCapacityBytes() const { return capacity_; }
-  std::size_t GetMark() const { return offset_; }
-  void ResetToMark(std::size_t mark) { offset_ = mark; }
-  void Reset() { offset_ = 0; }
-  bool Reserve(std::size_t bytes, std::string* error_message);  // "BufferArena capacity exceeded" on overflow
-  const std::string& label() const { return label_; }
-  std::size_t peak_bytes() const { return peak_; }
+  std::size_t GetUsedBytes() const { return used_; }
+  std::size_t GetPeakUsedBytes() const { return peak_; }
+  const std::vector<BufferArenaScopeTelemetry>& GetTelemetrySnapshot() const { return telemetry_; }
 
  private:
-  BufferArena(std::size_t capacity, std::string label) : capacity_(capacity), label_(std::move(label)) {}
-  std::size_t capacity_ = 0, offset_ = 0, peak_ = 0;
-  std::string label_;
+  struct ActiveScope {
+    std::string name;
+    std::size_t start_used;  // usage when the scope began
+    std::size_t peak_used;
+    std::size_t allocations;
+  };
+  BufferArena(std::shared_ptr<HipBuffer> buffer, std::size_t capacity)
+      : buffer_(std::move(buffer)), capacity_(capacity) {}
+  void BeginScope(const std::string& scope_name);
+  void EndScope();
+  std::shared_ptr<HipBuffer> buffer_;
+  std::size_t capacity_ = 0, used_ = 0, peak_ = 0;
+  std::vector<ActiveScope> active_scopes_;
+  std::vector<BufferArenaScopeTelemetry> telemetry_;
+  friend class BufferArenaMarkGuard;
+};
+
+class BufferArenaMarkGuard {  // buffer_arena.h:71-80: resets the arena to its mark when the scope ends
+ public:
+  explicit BufferArenaMarkGuard(BufferArena* arena, const std::string& scope_name = {});
+  ~BufferArenaMarkGuard();
+
+ private:
+  BufferArena* arena_ = nullptr;
+  BufferArenaMark mark_ = 0;
+  bool has_scope_ = false;
 };
 
 // Mac/gpu/include/model/qwen_causal_lm.h:25-36
@@ -87,6 +226,8 @@ struct QwenCausalLMParams {
   bool tie_word_embeddings = true;
 };
 
+class KVCache;
+
 class QwenCausalLM {
  public:
   QwenCausalLM() = default;
@@ -101,6 +242,12 @@ class QwenCausalLM {
   const QwenCausalLMParams& params() const { return params_; }
   soc_model* handle() const { return model_.get(); }
   bool IsValid() const { return model_ != nullptr; }
+
+  // qwen_causal_lm.cpp:250-268: the forward of token_ids [n] (kInt32) at positions position_offset.., appending
+  // their K/V to kv_cache, logits of the last rows into logits_output [r][vocab] (kFloat32, r <= n).
+  bool ForwardLogitsCached(const HipContext& context, PipelineCache* pipeline_cache, const DeviceTensor& token_ids,
+                           KVCache* kv_cache, const DeviceTensor& logits_output, BufferArena* temporary_arena,
+                           std::size_t position_offset, std::string* error_message) const;
 
  private:
   std::shared_ptr<soc_model> model_;
@@ -122,43 +269,66 @@ class QwenModelLoader {
                               QwenCausalLM* model, std::string* error_message);
 };
 
-// Mac/gpu/include/runtime/kv_cache.h: one sequence, fp16, capacity fixed at creation.
+// kv_cache.h:15-19
+struct KVCacheLayerView {
+  DeviceTensor keys;
+  DeviceTensor values;
+  std::size_t sequence_length = 0;
+};
+
+// kv_cache.h:21-79: one sequence, capacity fixed at creation, a length per layer.
 class KVCache {
  public:
-  static std::unique_ptr<KVCache> CreateShared(const HipContext& context, const QwenCausalLM& model,
+  static std::unique_ptr<KVCache> CreateShared(const HipContext& context, std::size_t layer_count,
+                                               std::size_t key_value_head_count, std::size_t head_dim,
                                                std::size_t max_sequence_length, const std::string& label,
                                                std::string* error_message);
-  ~KVCache();
+  ~KVCache() = default;
   KVCache(const KVCache&) = delete;
   KVCache& operator=(const KVCache&) = delete;
-  std::size_t GetLayerCount() const { return layers_; }
+
+  bool Reserve(std::size_t sequence_length, std::string* error_message);
+  bool AppendPrefill(const HipContext& context, std::size_t layer_index, const DeviceTensor& keys,
+                     const DeviceTensor& values, std::string* error_message);
+  bool AppendDecodeToken(const HipContext& context, std::size_t layer_index, const DeviceTensor& key,
+                         const DeviceTensor& value, std::string* error_message);
+  KVCacheLayerView ViewForLayer(std::size_t layer_index) const;
+  std::size_t GetLayerCount() const { return layer_count_; }
   std::size_t GetKeyValueHeadCount() const { return kv_heads_; }
   std::size_t GetHeadDim() const { return head_dim_; }
   std::size_t GetMaxSequenceLength() const { return capacity_; }
-  std::size_t GetSequenceLength() const;
-  soc_kv* handle() const { return kv_; }
+
+  // Length of layer 0 (every layer after a forward).
+  std::size_t GetSequenceLength() const { return sequence_lengths_.empty() ? 0 : sequence_lengths_[0]; }
+  soc_kv* handle() const { return kv_.get(); }
+  // After a forward that appended `rows` positions to every layer.
+  void OnForward(std::size_t rows);
+  // True when every layer holds the same number of positions (required by a forward).
+  bool LayersAligned() const;
 
  private:
-  KVCache(soc_kv* kv, std::size_t layers, std::size_t kv_heads, std::size_t head_dim, std::size_t capacity)
-      : kv_(kv), layers_(layers), kv_heads_(kv_heads), head_dim_(head_dim), capacity_(capacity) {}
-  soc_kv* kv_ = nullptr;
-  std::size_t layers_, kv_heads_, head_dim_, capacity_;
+  KVCache(const HipContext& context, std::shared_ptr<soc_kv> kv, std::size_t layers, std::size_t kv_heads,
+          std::size_t head_dim, std::size_t capacity)
+      : context_(&context), kv_(std::move(kv)), layer_count_(layers), kv_heads_(kv_heads), head_dim_(head_dim),
+        capacity_(capacity), sequence_lengths_(layers, 0) {}
+  const HipContext* context_;
+  std::shared_ptr<soc_kv> kv_;
+  std::size_t layer_count_, kv_heads_, head_dim_, capacity_;
+  std::vector<std::size_t> sequence_lengths_;
 };
 
-// Mac/gpu/include/runtime/command_scheduler.h:14-35. logits_output (nullable) receives the last row [V].
+// command_scheduler.h:14-35 (both run QwenCausalLM::ForwardLogitsCached).
 class CommandScheduler {
  public:
   bool RunPrefill(const HipContext& context, PipelineCache* pipeline_cache, const QwenCausalLM& model,
-                  const std::vector<int>& token_ids, KVCache* kv_cache, std::vector<float>* logits_output,
-                  BufferArena* temporary_arena, std::size_t position_offset, int* greedy_token,
-                  std::string* error_message) const;
+                  const DeviceTensor& token_ids, KVCache* kv_cache, const DeviceTensor& logits_output,
+                  BufferArena* temporary_arena, std::size_t position_offset, std::string* error_message) const;
   bool RunDecode(const HipContext& context, PipelineCache* pipeline_cache, const QwenCausalLM& model,
-                 const std::vector<int>& token_ids, KVCache* kv_cache, std::vector<float>* logits_output,
-                 BufferArena* temporary_arena, std::size_t position_offset, int* greedy_token,
-                 std::string* error_message) const;
+                 const DeviceTensor& token_ids, KVCache* kv_cache, const DeviceTensor& logits_output,
+                 BufferArena* temporary_arena, std::size_t position_offset, std::string* error_message) const;
 };
 
-// Mac/gpu/include/runtime/sampler.h
+// sampler.h:10-27
 struct SamplerConfig {
   float temperature = 1.0f;
   std::size_t top_k = 1;
@@ -168,16 +338,16 @@ class Sampler {
  public:
   explicit Sampler(SamplerConfig config = {}) : config_(config) {}
   const SamplerConfig& config() const { return config_; }
-  // Mac/gpu/src/runtime/sampler.cpp:14-71 on a host logits row.
-  bool SampleFromLogits(const std::vector<float>& logits_row, int* token_id, std::vector<float>* top_logits,
-                        std::vector<int>* top_token_ids, std::string* error_message) const;
-  bool greedy() const { return config_.top_k <= 1; }
+  // sampler.cpp:14-71: top-k of row `row_index` of logits [rows][vocab] (kFloat32), selected on the device.
+  bool SampleFromLogits(const DeviceTensor& logits, std::size_t row_index, int* token_id,
+                        std::vector<float>* top_logits, std::vector<int>* top_token_ids,
+                        std::string* error_message) const;
 
  private:
   SamplerConfig config_;
 };
 
-struct GenerationStepResult {
+struct GenerationStepResult {  // generation_context.h:17-21
   int token_id = -1;
   std::vector<float> top_logits;
   std::vector<int> top_token_ids;
@@ -202,6 +372,10 @@ class GenerationContext {
   const QwenCausalLM& model() const { return model_; }
 
  private:
+  bool EnsureLogitsBuffer(const HipContext& context, std::string* error_message);
+  bool UploadTokenIds(const HipContext& context, const std::vector<int>& token_ids, DeviceTensor* token_tensor,
+                      std::string* error_message);
+
   QwenCausalLM model_;
   Sampler sampler_;
   CommandScheduler scheduler_;
@@ -209,8 +383,13 @@ class GenerationContext {
   std::unique_ptr<KVCache> kv_cache_;
   std::vector<int> prompt_token_ids_;
   std::vector<int> running_token_ids_;
-  std::vector<float> last_logits_;
-  int prefill_token_ = -1;
+  std::shared_ptr<HipBuffer> logits_buffer_;  // one logits row: generation samples only the last row
+  std::shared_ptr<HipBuffer> token_buffer_;
 };
+
+// The reference's names for the platform classes.
+using MetalContext = HipContext;
+using MetalBuffer = HipBuffer;
+using MetalProfilingSnapshot = HipProfilingSnapshot;
 
 }  // namespace soc::gpu

@@ -32,6 +32,9 @@ enum {
   SOC_ERR_NOMEM = 5      /* device allocation failed (buffer_arena.cpp:59-65 "capacity exceeded" analogue)     */
 };
 
+/* Element types of caller tensors (Mac/gpu/include/tensor/tensor_desc.h DataType kFloat32 / kFloat16). */
+enum { SOC_DTYPE_F32 = 0, SOC_DTYPE_F16 = 1 };
+
 /* Message of the calling thread's last failed call ("" if none). Replaces the `std::string* error_message`
  * out-parameter of every reference GPU entry point (e.g. Mac/gpu/include/runtime/generation_context.h:30-50). */
 const char* soc_last_error(void);
@@ -89,6 +92,11 @@ int soc_model_decode_path(soc_model* model, int32_t* path);
  *      fp16, `num_slots` independent sequences of `capacity` positions each. ---- */
 typedef struct soc_kv soc_kv;
 int soc_kv_create(soc_model* model, int32_t num_slots, int32_t capacity, soc_kv** out);
+/* The same from dimensions alone (KVCache::CreateShared(context, layers, kv_heads, head_dim, max_sequence_length),
+ * kv_cache.h:23-30): the cache is bound to the first model that runs a forward on it, which must have these
+ * dimensions; head_dim must be 128. */
+int soc_kv_create_dims(soc_ctx* ctx, int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t num_slots,
+                       int32_t capacity, soc_kv** out);
 int soc_kv_destroy(soc_kv* kv);
 /* Length (number of cached positions) of one slot; reset sets it to 0 (GenerationContext::Reset). */
 int soc_kv_length(const soc_kv* kv, int32_t slot, int32_t* length);
@@ -100,15 +108,26 @@ int soc_kv_write(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, const flo
 int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t seed);
 /* Read back fp16 K and V of one (slot, layer) as [nkv][length][head_dim] (nullable destinations). */
 int soc_kv_read(const soc_kv* kv, int32_t slot, int32_t layer, uint16_t* keys, uint16_t* values);
+/* Device rows keys/values [rows][kv_heads * head_dim] (SOC_DTYPE_F32 or _F16, device memory) into positions
+ * [pos, pos + rows) of one (slot, layer), stored as fp16 (KVCache::AppendPrefill / AppendDecodeToken,
+ * kv_cache.mm:78-131). The slot length is not changed (soc_kv_set_length); returns when the copy is done. */
+int soc_kv_append(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, int32_t rows, const void* keys,
+                  const void* values, int32_t dtype);
+/* Sets the cached length of a slot (0 <= length <= capacity). */
+int soc_kv_set_length(soc_kv* kv, int32_t slot, int32_t length);
+/* Device addresses of one (slot, layer)'s fp16 key and value planes, [kv_heads][capacity][head_dim] each
+ * (KVCache::ViewForLayer, kv_cache.mm:133-143; nullable outputs). */
+int soc_kv_layer_planes(const soc_kv* kv, int32_t slot, int32_t layer, void** keys, void** values);
 
 /* ---- forward: replaces CommandScheduler::RunPrefill / RunDecode (Mac/gpu/include/runtime/command_scheduler.h:14-35)
  *      -> QwenCausalLM::ForwardLogitsCached (Mac/gpu/src/model/qwen_causal_lm.cpp:250-268) ---- */
 /* Runs `n` tokens of one slot at positions [position_offset, position_offset + n), appending their K/V.
  * position_offset must equal the slot's current length. Writes the fp32 logits of the last `logit_rows` rows
- * (nullable) and the greedy next token from the last row (nullable). */
+ * (nullable; host or device memory) and the greedy next token from the last row (nullable). */
 int soc_prefill(soc_model* model, soc_kv* kv, int32_t slot, const int32_t* token_ids, int32_t n,
                 int32_t position_offset, int32_t logit_rows, float* logits, int32_t* next_token);
-/* One decode step of one slot: feeds `last_token` at position = current length. Logits [V] nullable. */
+/* One decode step of one slot: feeds `last_token` at position = current length. Logits [V] nullable, in host or
+ * device memory. */
 int soc_decode(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, float* logits, int32_t* next_token);
 /* `steps` greedy decode steps of one slot with the token fed back on the device (no host round trip per step).
  * tokens_out[steps] receives the generated ids. */
@@ -135,6 +154,15 @@ int soc_decode_batch(soc_model* model, soc_kv* kv, int32_t n, const int32_t* slo
 /* `steps` greedy steps with each row's token fed back on the device; tokens_out [steps][n]. */
 int soc_decode_batch_steps(soc_model* model, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens,
                            int32_t steps, int32_t* tokens_out);
+
+/* ---- sampler: replaces Sampler::SampleFromLogits (Mac/gpu/src/runtime/sampler.cpp:14-71) ---- */
+/* Top-k sampling of one fp32 logits row in device (or host) memory, with the reference's results: k = top_k clamped
+ * to [1, vocab], temperature <= 0 taken as 1, candidates ordered as std::partial_sort(0..vocab-1, by logit /
+ * temperature, greater first) orders them, ties included; *token_id = the first. top_ids / top_logits (nullable, k
+ * entries) receive the candidates and their raw logits. For k <= 64 the candidates are found on the device and only
+ * they are copied back; larger k, or a row holding NaN, sorts a host copy of the whole row as the reference does. */
+int soc_sample_topk(soc_ctx* ctx, const float* logits_row, int32_t vocab, int32_t top_k, float temperature,
+                    int32_t* token_id, int32_t* top_ids, float* top_logits);
 
 /* ---- op-level entry points on caller device pointers, queued on the context stream (tests, microbenchmarks).
  *      These replace the reference's op wrappers (Mac/gpu/include/op/*.h, static Run(...)). ---- */

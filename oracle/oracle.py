@@ -56,6 +56,7 @@ def port_lib() -> C.CDLL:
             "orc_rope": (None, [P, I64, I64, I64, F64, I64]),
             "orc_gqa": (C.c_int, [P, P, P, I64, I64, I64, I64, I64, I64, C.c_int, P]),
             "orc_sample": (C.c_int, [P, I64, F32, I64]),
+            "orc_sample_topk": (C.c_int, [P, I64, F32, I64, P, P]),
             "orc_mlp_f16": (None, [P, I64, I64, I64, P, P, P, P]),
             "orc_model_create": (P, [I64, I64, I64, I64, I64, I64, I64, F64, F32, C.c_int]),
             "orc_model_destroy": (None, [P]),
@@ -196,6 +197,16 @@ def gqa(q: np.ndarray, k: np.ndarray, v: np.ndarray, prefix: int = 0, causal: bo
 def sample(row: np.ndarray, temperature: float = 1.0, top_k: int = 1) -> int:
     r = np.ascontiguousarray(row, dtype=np.float32)
     return port_lib().orc_sample(_ptr(r), r.size, temperature, top_k)
+
+
+def sample_topk(row: np.ndarray, temperature: float, top_k: int) -> tuple[int, np.ndarray, np.ndarray]:
+    """The reference GPU sampler's result: (token, k candidate ids in its order, their raw logits)."""
+    r = np.ascontiguousarray(row, dtype=np.float32)
+    k = max(1, min(int(top_k), r.size))
+    ids = np.empty(k, np.int32)
+    vals = np.empty(k, np.float32)
+    tok = port_lib().orc_sample_topk(_ptr(r), r.size, temperature, top_k, _ptr(ids), _ptr(vals))
+    return tok, ids, vals
 
 
 def qmm_group(a_f16: np.ndarray, codes: np.ndarray, bits: int, scales_f16: np.ndarray, k: int, n: int,

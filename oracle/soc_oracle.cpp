@@ -233,6 +233,24 @@ int orc_sample(const float* row, int64_t vocab, float temperature, int64_t top_k
   return static_cast<int>(best);
 }
 
+// Mac/gpu/src/runtime/sampler.cpp:44-66: top_k clamped to [1, vocab], a non-positive temperature taken as 1, the
+// same std::partial_sort of candidate ids by logit / temperature; writes the k ids in that order and their raw
+// logits, returns the first id.
+int orc_sample_topk(const float* row, int64_t vocab, float temperature, int64_t top_k, int32_t* ids, float* vals) {
+  if (vocab <= 0) return -1;
+  const int64_t k = std::max<int64_t>(1, std::min<int64_t>(top_k, vocab));
+  const float t = temperature <= 0.0f ? 1.0f : temperature;
+  std::vector<int64_t> cand(static_cast<size_t>(vocab));
+  for (int64_t i = 0; i < vocab; ++i) cand[i] = i;
+  std::partial_sort(cand.begin(), cand.begin() + k, cand.end(),
+                    [row, t](int64_t l, int64_t r) { return row[l] / t > row[r] / t; });
+  for (int64_t r = 0; r < k; ++r) {
+    ids[r] = static_cast<int32_t>(cand[r]);
+    vals[r] = row[cand[r]];
+  }
+  return static_cast<int>(cand[0]);
+}
+
 // Mac/cpu/src/qwen_mlp.cpp:65-74 with ApplySiLU (:20-35) and HadamardProduct (:37-54).
 void orc_mlp_f16(const float* x, int64_t rows, int64_t hidden, int64_t inter, const uint16_t* gate,
                  const uint16_t* up, const uint16_t* down, float* y) {

@@ -15,6 +15,9 @@
  *   orc_linear_f16, orc_rmsnorm, orc_rope, orc_gqa, orc_sample, model forward / generate :
  *       reference KATs (Mac/cpu/test/test_nn_modules.cpp), closed forms, and golden vectors emitted by the
  *       compiled reference sources (oracle/_ref, fixtures under tests/golden/).
+ *   orc_sample_topk : the first id equals orc_sample (pinned above); the ids' values are the k largest of
+ *       logit / temperature in non-increasing order; the order among equal values is std::partial_sort's, the very
+ *       call the reference makes (Mac/gpu/src/runtime/sampler.cpp:50-55).
  *   orc_qmm_group : the group-quantized format is not in the reference; pinned by the closed-form dequant
  *       (exact products), by group size 64 == per-row scale when all scales of a row are equal, and by the int8
  *       per-column reference quantizer (Mac/cpu/header/matrix_ops.h:42-74,308-350) through orc_quant_int8_percol.
@@ -53,6 +56,8 @@ int orc_gqa(const float* q, const float* k, const float* v, int64_t T, int64_t S
 
 /* Mac/cpu/src/sampler.cpp:26-61 on one logits row. Returns the token id (-1 on invalid arguments). */
 int orc_sample(const float* logits_row, int64_t vocab, float temperature, int64_t top_k);
+int orc_sample_topk(const float* logits_row, int64_t vocab, float temperature, int64_t top_k, int32_t* ids,
+                    float* vals);
 
 /* Mac/cpu/src/qwen_mlp.cpp:20-74 with fp16 weights. x [rows][H] -> y [rows][H]. */
 void orc_mlp_f16(const float* x, int64_t rows, int64_t hidden, int64_t inter, const uint16_t* gate,

@@ -133,6 +133,11 @@ def lib() -> C.CDLL:
         "soc_decode": (C.c_int, [P, P, I32, I32, P, C.POINTER(I32)]),
         "soc_decode_steps": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_decode_steps_noalloc": (C.c_int, [P, P, I32, I32, I32, P]),
+        "soc_sample_topk": (C.c_int, [P, P, I32, I32, C.c_float, P, P, P]),
+        "soc_kv_create_dims": (C.c_int, [P, I32, I32, I32, I32, I32, P]),
+        "soc_kv_append": (C.c_int, [P, I32, I32, I32, I32, P, P, I32]),
+        "soc_kv_set_length": (C.c_int, [P, I32, I32]),
+        "soc_kv_layer_planes": (C.c_int, [P, I32, I32, P, P]),
         "soc_decode_batch": (C.c_int, [P, P, I32, P, P, P, P]),
         "soc_decode_batch_steps": (C.c_int, [P, P, I32, P, P, I32, P]),
         "soc_gemv_f16": (C.c_int, [P, P, P, P, I32, I32]),
@@ -372,6 +377,16 @@ def decode_steps_noalloc(model: Model, kv: KVCache, slot: int, last_token: int, 
     out = np.empty(steps, dtype=np.int32)
     check(lib().soc_decode_steps_noalloc(model.h, kv.h, slot, int(last_token), steps, _ptr(out)))
     return out
+
+
+def sample_topk(ctx: Context, row_ptr: int, vocab: int, top_k: int, temperature: float = 1.0):
+    """soc_sample_topk on a device logits row: (token, candidate ids, their raw logits)."""
+    k = max(1, min(int(top_k), int(vocab)))
+    ids = np.empty(k, np.int32)
+    vals = np.empty(k, np.float32)
+    tok = C.c_int32()
+    check(lib().soc_sample_topk(ctx.h, row_ptr, vocab, top_k, temperature, C.byref(tok), _ptr(ids), _ptr(vals)))
+    return tok.value, ids, vals
 
 
 def decode_batch(model: Model, kv: KVCache, slots, tokens, want_logits: bool = True):

@@ -1,5 +1,6 @@
 // host_api.cpp - the reference GPU runtime's C++ classes (include/soc/gpu/runtime.h) implemented on the C ABI.
-// Semantics follow Mac/gpu/src/runtime/generation_context.cpp, command_scheduler.cpp and sampler.cpp.
+// Semantics follow Mac/gpu/src: runtime/generation_context.cpp, command_scheduler.cpp, sampler.cpp, kv_cache.mm,
+// tensor/tensor_desc.cpp, device_tensor.cpp, buffer/buffer_arena.cpp, metal_buffer.mm.
 #include <algorithm>
 #include <cstring>
 #include <numeric>
@@ -42,11 +43,16 @@ std::shared_ptr<soc_model> WrapModel(soc_model* m) {
 
 }  // namespace
 
-// ---- HipContext ----
+// ---- HipContext (metal_context.h) ----
 std::unique_ptr<HipContext> HipContext::CreateDefault(int device, std::string* error_message) {
   soc_ctx* ctx = nullptr;
   if (!Check(soc_ctx_create(device, &ctx), error_message)) return nullptr;
   return std::unique_ptr<HipContext>(new HipContext(ctx));
+}
+
+std::unique_ptr<HipContext> HipContext::CreateDefault(const std::string&, const std::string&,
+                                                      std::string* error_message) {
+  return CreateDefault(0, error_message);
 }
 
 HipContext::~HipContext() { soc_ctx_destroy(ctx_); }
@@ -55,22 +61,157 @@ bool HipContext::Synchronize(std::string* error_message) const {
   return Check(soc_ctx_synchronize(ctx_), error_message);
 }
 
-// ---- BufferArena ----
-std::unique_ptr<BufferArena> BufferArena::CreateShared(const HipContext&, std::size_t capacity_bytes,
-                                                       const std::string& label, std::string* error_message) {
-  if (capacity_bytes == 0) {
-    Fail(error_message, "BufferArena capacity must be positive");
+// ---- HipBuffer (metal_buffer.mm: bounds-checked copies) ----
+std::shared_ptr<HipBuffer> HipBuffer::CreateShared(const HipContext& context, std::size_t size_bytes,
+                                                   const std::string&, std::string* error_message) {
+  void* p = nullptr;
+  if (!Check(soc_buffer_alloc(context.handle(), std::max<std::size_t>(size_bytes, 1), &p), error_message))
     return nullptr;
-  }
-  return std::unique_ptr<BufferArena>(new BufferArena(capacity_bytes, label));
+  return std::shared_ptr<HipBuffer>(new HipBuffer(context.handle(), p, size_bytes, nullptr));
 }
 
-bool BufferArena::Reserve(std::size_t bytes, std::string* error_message) {
-  const std::size_t aligned = (bytes + 255) / 256 * 256;
-  if (offset_ + aligned > capacity_) return Fail(error_message, "BufferArena capacity exceeded");
-  offset_ += aligned;
-  peak_ = std::max(peak_, offset_);
+std::shared_ptr<HipBuffer> HipBuffer::Wrap(const HipContext& context, void* device_ptr, std::size_t size_bytes,
+                                           std::shared_ptr<void> owner) {
+  return std::shared_ptr<HipBuffer>(new HipBuffer(context.handle(), device_ptr, size_bytes, std::move(owner)));
+}
+
+HipBuffer::~HipBuffer() {
+  if (owner_ == nullptr && ptr_ != nullptr) soc_buffer_free(ctx_, ptr_);
+}
+
+bool HipBuffer::Write(const void* source, std::size_t size_bytes, std::size_t offset_bytes,
+                      std::string* error_message) {
+  if (source == nullptr) return Fail(error_message, "Write source must not be null");
+  if (offset_bytes > size_ || size_bytes > size_ - offset_bytes)
+    return Fail(error_message, "Write range exceeds buffer size");
+  if (size_bytes == 0) return true;
+  return Check(soc_buffer_write(ctx_, static_cast<char*>(ptr_) + offset_bytes, source, size_bytes), error_message);
+}
+
+bool HipBuffer::Read(void* destination, std::size_t size_bytes, std::size_t offset_bytes,
+                     std::string* error_message) const {
+  if (destination == nullptr) return Fail(error_message, "Read destination must not be null");
+  if (offset_bytes > size_ || size_bytes > size_ - offset_bytes)
+    return Fail(error_message, "Read range exceeds buffer size");
+  if (size_bytes == 0) return true;
+  return Check(soc_buffer_read(ctx_, destination, static_cast<const char*>(ptr_) + offset_bytes, size_bytes),
+               error_message);
+}
+
+// ---- TensorDesc / DeviceTensor (tensor_desc.cpp, device_tensor.cpp) ----
+std::size_t GetDataTypeSize(DataType data_type) {
+  switch (data_type) {
+    case DataType::kFloat16:
+      return 2;
+    case DataType::kFloat32:
+    case DataType::kInt32:
+      return 4;
+  }
+  return 0;
+}
+
+TensorDesc TensorDesc::CreateContiguous(DataType data_type, const std::vector<std::size_t>& shape) {
+  TensorDesc d;
+  d.data_type_ = data_type;
+  d.shape_ = shape;
+  d.strides_.assign(shape.size(), 1);
+  for (std::size_t i = shape.size(); i-- > 1;) d.strides_[i - 1] = d.strides_[i] * shape[i];  // row-major
+  d.contiguous_ = true;
+  return d;
+}
+
+TensorDesc TensorDesc::CreateStrided(DataType data_type, const std::vector<std::size_t>& shape,
+                                     const std::vector<std::size_t>& strides) {
+  TensorDesc d = CreateContiguous(data_type, shape);
+  if (strides.size() == shape.size() && strides != d.strides_) {
+    d.strides_ = strides;
+    d.contiguous_ = false;
+  }
+  return d;
+}
+
+std::size_t TensorDesc::ElementCount() const {
+  std::size_t n = 1;
+  for (std::size_t s : shape_) n *= s;
+  return n;
+}
+
+std::size_t TensorDesc::ByteSize() const {
+  if (ElementCount() == 0) return 0;
+  std::size_t last = 0;  // element offset of the last element
+  for (std::size_t i = 0; i < shape_.size(); ++i) last += (shape_[i] - 1) * strides_[i];
+  return (last + 1) * GetDataTypeSize(data_type_);
+}
+
+bool DeviceTensor::IsValid() const {
+  return buffer_ != nullptr && byte_offset_ + desc_.ByteSize() <= buffer_->GetSizeBytes();
+}
+
+// ---- BufferArena (buffer_arena.cpp) ----
+std::unique_ptr<BufferArena> BufferArena::CreateShared(const HipContext& context, std::size_t capacity_bytes,
+                                                       const std::string& label, std::string* error_message) {
+  auto buffer = HipBuffer::CreateShared(context, capacity_bytes, label, error_message);
+  if (buffer == nullptr) return nullptr;
+  return std::unique_ptr<BufferArena>(new BufferArena(std::move(buffer), capacity_bytes));
+}
+
+bool BufferArena::Allocate(std::size_t size_bytes, std::size_t alignment_bytes, BufferArenaSlice* slice,
+                           std::string* error_message) {
+  if (slice == nullptr) return Fail(error_message, "Arena allocation slice must not be null");
+  const std::size_t a = std::max<std::size_t>(alignment_bytes, 1);
+  const std::size_t start = (used_ + a - 1) / a * a;
+  if (start + size_bytes > capacity_) return Fail(error_message, "BufferArena capacity exceeded");
+  *slice = BufferArenaSlice{buffer_, start, size_bytes};
+  used_ = start + size_bytes;
+  peak_ = std::max(peak_, used_);
+  for (ActiveScope& sc : active_scopes_) {
+    sc.peak_used = std::max(sc.peak_used, used_);
+    ++sc.allocations;
+  }
   return true;
+}
+
+bool BufferArena::ResetToMark(BufferArenaMark mark, std::string* error_message) {
+  if (mark > used_) return Fail(error_message, "BufferArena mark is ahead of current usage");
+  used_ = mark;
+  return true;
+}
+
+void BufferArena::ClearTelemetry() { telemetry_.clear(); }
+
+void BufferArena::BeginScope(const std::string& scope_name) {
+  if (!scope_name.empty()) active_scopes_.push_back(ActiveScope{scope_name, used_, used_, 0});
+}
+
+void BufferArena::EndScope() {
+  if (active_scopes_.empty()) return;
+  const ActiveScope sc = active_scopes_.back();
+  active_scopes_.pop_back();
+  const std::size_t delta = sc.peak_used - std::min(sc.peak_used, sc.start_used);
+  auto it = std::find_if(telemetry_.begin(), telemetry_.end(),
+                         [&sc](const BufferArenaScopeTelemetry& t) { return t.name == sc.name; });
+  if (it == telemetry_.end()) {
+    telemetry_.push_back(BufferArenaScopeTelemetry{sc.name, 1, delta, sc.peak_used, sc.allocations});
+    return;
+  }
+  it->invocation_count += 1;
+  it->peak_delta_bytes = std::max(it->peak_delta_bytes, delta);
+  it->peak_used_bytes = std::max(it->peak_used_bytes, sc.peak_used);
+  it->peak_allocation_count = std::max(it->peak_allocation_count, sc.allocations);
+}
+
+BufferArenaMarkGuard::BufferArenaMarkGuard(BufferArena* arena, const std::string& scope_name)
+    : arena_(arena), has_scope_(!scope_name.empty()) {
+  if (arena_ == nullptr) return;
+  mark_ = arena_->GetMark();
+  if (has_scope_) arena_->BeginScope(scope_name);
+}
+
+BufferArenaMarkGuard::~BufferArenaMarkGuard() {
+  if (arena_ == nullptr) return;
+  if (has_scope_) arena_->EndScope();
+  std::string ignored;
+  arena_->ResetToMark(mark_, &ignored);
 }
 
 // ---- QwenModelLoader ----
@@ -103,93 +244,199 @@ bool QwenModelLoader::SynthesizeModel(const HipContext& context, const QwenCausa
   return true;
 }
 
-// ---- KVCache ----
-std::unique_ptr<KVCache> KVCache::CreateShared(const HipContext&, const QwenCausalLM& model,
+// ---- KVCache (kv_cache.mm) ----
+std::unique_ptr<KVCache> KVCache::CreateShared(const HipContext& context, std::size_t layer_count,
+                                               std::size_t key_value_head_count, std::size_t head_dim,
                                                std::size_t max_sequence_length, const std::string&,
                                                std::string* error_message) {
-  if (!model.IsValid()) {
-    Fail(error_message, "KVCache requires a loaded model");
+  if (layer_count == 0 || key_value_head_count == 0 || head_dim == 0 || max_sequence_length == 0) {
+    Fail(error_message, "KVCache dimensions must be non-zero");
     return nullptr;
   }
   soc_kv* kv = nullptr;
-  if (!Check(soc_kv_create(model.handle(), 1, static_cast<int32_t>(max_sequence_length), &kv), error_message))
+  if (!Check(soc_kv_create_dims(context.handle(), static_cast<int32_t>(layer_count),
+                                static_cast<int32_t>(key_value_head_count), static_cast<int32_t>(head_dim), 1,
+                                static_cast<int32_t>(max_sequence_length), &kv),
+             error_message))
     return nullptr;
+  std::shared_ptr<soc_kv> holder(kv, [](soc_kv* p) { soc_kv_destroy(p); });
   return std::unique_ptr<KVCache>(
-      new KVCache(kv, model.num_layers(), model.num_key_value_heads(), model.head_dim(), max_sequence_length));
+      new KVCache(context, std::move(holder), layer_count, key_value_head_count, head_dim, max_sequence_length));
 }
 
-KVCache::~KVCache() { soc_kv_destroy(kv_); }
+bool KVCache::Reserve(std::size_t sequence_length, std::string* error_message) {
+  if (sequence_length > capacity_) return Fail(error_message, "KVCache reserve length exceeds max_sequence_length");
+  return true;
+}
 
-std::size_t KVCache::GetSequenceLength() const {
-  int32_t n = 0;
-  soc_kv_length(kv_, 0, &n);
-  return static_cast<std::size_t>(n);
+bool KVCache::AppendPrefill(const HipContext&, std::size_t layer_index, const DeviceTensor& keys,
+                            const DeviceTensor& values, std::string* error_message) {
+  if (layer_index >= layer_count_) return Fail(error_message, "KVCache layer index is out of range");
+  const std::size_t width = kv_heads_ * head_dim_;
+  for (const DeviceTensor* t : {&keys, &values}) {
+    const TensorDesc& d = t->GetDesc();
+    if (!t->IsValid() || d.Rank() != 2 || !d.IsContiguous() ||
+        (d.GetDataType() != DataType::kFloat32 && d.GetDataType() != DataType::kFloat16))
+      return Fail(error_message, "KVCache append expects a valid rank-2 float32 or float16 tensor");
+    if (d.GetShape()[1] != width)
+      return Fail(error_message, "KVCache append tensor hidden size does not match cache configuration");
+  }
+  if (keys.GetDesc().GetShape() != values.GetDesc().GetShape() ||
+      keys.GetDesc().GetDataType() != values.GetDesc().GetDataType())
+    return Fail(error_message, "KVCache key/value append tensors must have matching shapes");
+  const std::size_t rows = keys.GetDesc().GetShape()[0];
+  if (sequence_lengths_[layer_index] + rows > capacity_)
+    return Fail(error_message, "KVCache append would exceed max_sequence_length");
+  const int32_t dtype = keys.GetDesc().GetDataType() == DataType::kFloat16 ? SOC_DTYPE_F16 : SOC_DTYPE_F32;
+  if (!Check(soc_kv_append(kv_.get(), 0, static_cast<int32_t>(layer_index),
+                           static_cast<int32_t>(sequence_lengths_[layer_index]), static_cast<int32_t>(rows),
+                           keys.data(), values.data(), dtype),
+             error_message))
+    return false;
+  sequence_lengths_[layer_index] += rows;
+  // a forward attends over the positions every layer holds
+  const std::size_t common = *std::min_element(sequence_lengths_.begin(), sequence_lengths_.end());
+  return Check(soc_kv_set_length(kv_.get(), 0, static_cast<int32_t>(common)), error_message);
+}
+
+bool KVCache::AppendDecodeToken(const HipContext& context, std::size_t layer_index, const DeviceTensor& key,
+                                const DeviceTensor& value, std::string* error_message) {
+  if (key.GetDesc().Rank() != 2 || value.GetDesc().Rank() != 2 || key.GetDesc().GetShape()[0] != 1 ||
+      value.GetDesc().GetShape()[0] != 1)
+    return Fail(error_message, "KVCache decode append expects single-row key/value tensors");
+  return AppendPrefill(context, layer_index, key, value, error_message);
+}
+
+KVCacheLayerView KVCache::ViewForLayer(std::size_t layer_index) const {
+  if (layer_index >= layer_count_) return {};
+  void* k = nullptr;
+  void* v = nullptr;
+  if (soc_kv_layer_planes(kv_.get(), 0, static_cast<int32_t>(layer_index), &k, &v) != SOC_OK) return {};
+  const std::size_t n = sequence_lengths_[layer_index];
+  const std::size_t bytes = kv_heads_ * capacity_ * head_dim_ * 2;
+  const TensorDesc desc = TensorDesc::CreateStrided(DataType::kFloat16, {kv_heads_, n, head_dim_},
+                                                    {capacity_ * head_dim_, head_dim_, 1});
+  return {DeviceTensor(HipBuffer::Wrap(*context_, k, bytes, kv_), 0, desc),
+          DeviceTensor(HipBuffer::Wrap(*context_, v, bytes, kv_), 0, desc), n};
+}
+
+void KVCache::OnForward(std::size_t rows) {
+  for (std::size_t& n : sequence_lengths_) n += rows;
+}
+
+bool KVCache::LayersAligned() const {
+  return std::all_of(sequence_lengths_.begin(), sequence_lengths_.end(),
+                     [this](std::size_t n) { return n == sequence_lengths_[0]; });
+}
+
+// ---- QwenCausalLM::ForwardLogitsCached (qwen_causal_lm.cpp:250-268) ----
+bool QwenCausalLM::ForwardLogitsCached(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
+                                       KVCache* kv_cache, const DeviceTensor& logits_output, BufferArena*,
+                                       std::size_t position_offset, std::string* error_message) const {
+  if (!IsValid()) return Fail(error_message, "QwenCausalLM is not loaded");
+  if (kv_cache == nullptr) return Fail(error_message, "ForwardLogitsCached requires a KV cache");
+  const TensorDesc& td = token_ids.GetDesc();
+  if (!token_ids.IsValid() || td.GetDataType() != DataType::kInt32 || td.Rank() != 1 || td.GetShape()[0] == 0)
+    return Fail(error_message, "token_ids must be a valid non-empty rank-1 int32 tensor");
+  const std::size_t n = td.GetShape()[0];
+  int32_t rows = 0;
+  float* logits = nullptr;
+  if (logits_output.GetBuffer() != nullptr) {
+    const TensorDesc& ld = logits_output.GetDesc();
+    if (!logits_output.IsValid() || ld.GetDataType() != DataType::kFloat32 || ld.Rank() != 2 ||
+        ld.GetShape()[1] != vocab_size() || ld.GetShape()[0] == 0 || ld.GetShape()[0] > n)
+      return Fail(error_message, "logits_output must be a valid float32 tensor [rows <= token count][vocab]");
+    rows = static_cast<int32_t>(ld.GetShape()[0]);
+    logits = static_cast<float*>(logits_output.data());
+  }
+  if (!kv_cache->LayersAligned())
+    return Fail(error_message, "KV cache layers hold different numbers of positions");
+  if (position_offset != kv_cache->GetSequenceLength())
+    return Fail(error_message, "position_offset must equal the KV cache length");
+  std::vector<int32_t> ids(n);
+  if (!token_ids.GetBuffer()->Read(ids.data(), n * 4, token_ids.GetByteOffset(), error_message)) return false;
+  soc_ctx* ctx = context.handle();
+  if (!Check(soc_ctx_timer_start(ctx), error_message)) return false;
+  int32_t tok = -1;
+  const int rc = n == 1 && rows <= 1
+                     ? soc_decode(model_.get(), kv_cache->handle(), 0, ids[0], logits, &tok)
+                     : soc_prefill(model_.get(), kv_cache->handle(), 0, ids.data(), static_cast<int32_t>(n),
+                                   static_cast<int32_t>(position_offset), rows, logits, &tok);
+  if (!Check(rc, error_message)) return false;
+  float ms = 0.0f;
+  if (soc_ctx_timer_stop(ctx, &ms) == SOC_OK) context.AddProfile(ms);
+  kv_cache->OnForward(n);
+  return true;
 }
 
 // ---- CommandScheduler (command_scheduler.cpp:5-41: both paths are ForwardLogitsCached) ----
-bool CommandScheduler::RunPrefill(const HipContext&, PipelineCache*, const QwenCausalLM& model,
-                                  const std::vector<int>& token_ids, KVCache* kv_cache,
-                                  std::vector<float>* logits_output, BufferArena*, std::size_t position_offset,
-                                  int* greedy_token, std::string* error_message) const {
-  if (kv_cache == nullptr) return Fail(error_message, "CommandScheduler requires a KV cache");
-  if (logits_output != nullptr) logits_output->assign(model.vocab_size(), 0.0f);
-  int32_t tok = -1;
-  const int rc = soc_prefill(model.handle(), kv_cache->handle(), 0, token_ids.data(),
-                             static_cast<int32_t>(token_ids.size()), static_cast<int32_t>(position_offset),
-                             logits_output != nullptr ? 1 : 0, logits_output ? logits_output->data() : nullptr, &tok);
-  if (!Check(rc, error_message)) return false;
-  if (greedy_token) *greedy_token = tok;
-  return true;
+bool CommandScheduler::RunPrefill(const HipContext& context, PipelineCache* pipeline_cache, const QwenCausalLM& model,
+                                  const DeviceTensor& token_ids, KVCache* kv_cache, const DeviceTensor& logits_output,
+                                  BufferArena* temporary_arena, std::size_t position_offset,
+                                  std::string* error_message) const {
+  return model.ForwardLogitsCached(context, pipeline_cache, token_ids, kv_cache, logits_output, temporary_arena,
+                                   position_offset, error_message);
 }
 
-bool CommandScheduler::RunDecode(const HipContext&, PipelineCache*, const QwenCausalLM& model,
-                                 const std::vector<int>& token_ids, KVCache* kv_cache,
-                                 std::vector<float>* logits_output, BufferArena*, std::size_t position_offset,
-                                 int* greedy_token, std::string* error_message) const {
-  if (kv_cache == nullptr) return Fail(error_message, "CommandScheduler requires a KV cache");
-  if (token_ids.size() != 1) return Fail(error_message, "CommandScheduler decode takes exactly one token");
-  if (kv_cache->GetSequenceLength() != position_offset)
-    return Fail(error_message, "CommandScheduler decode position does not match the KV cache length");
-  if (logits_output != nullptr) logits_output->assign(model.vocab_size(), 0.0f);
-  int32_t tok = -1;
-  const int rc = soc_decode(model.handle(), kv_cache->handle(), 0, token_ids[0],
-                            logits_output ? logits_output->data() : nullptr, &tok);
-  if (!Check(rc, error_message)) return false;
-  if (greedy_token) *greedy_token = tok;
-  return true;
+bool CommandScheduler::RunDecode(const HipContext& context, PipelineCache* pipeline_cache, const QwenCausalLM& model,
+                                 const DeviceTensor& token_ids, KVCache* kv_cache, const DeviceTensor& logits_output,
+                                 BufferArena* temporary_arena, std::size_t position_offset,
+                                 std::string* error_message) const {
+  return model.ForwardLogitsCached(context, pipeline_cache, token_ids, kv_cache, logits_output, temporary_arena,
+                                   position_offset, error_message);
 }
 
-// ---- Sampler (Mac/gpu/src/runtime/sampler.cpp:14-71) ----
-bool Sampler::SampleFromLogits(const std::vector<float>& row, int* token_id, std::vector<float>* top_logits,
-                               std::vector<int>* top_token_ids, std::string* error_message) const {
+// ---- Sampler (sampler.cpp:14-71; candidates found on the device by soc_sample_topk) ----
+bool Sampler::SampleFromLogits(const DeviceTensor& logits, std::size_t row_index, int* token_id,
+                               std::vector<float>* top_logits, std::vector<int>* top_token_ids,
+                               std::string* error_message) const {
   if (token_id == nullptr) return Fail(error_message, "Sampler requires a non-null token_id output");
-  if (row.empty()) return Fail(error_message, "Sampler expects a non-empty logits row");
-  const std::size_t vocab = row.size();
-  std::vector<std::size_t> cand(vocab);
-  std::iota(cand.begin(), cand.end(), std::size_t{0});
+  const TensorDesc& d = logits.GetDesc();
+  if (!logits.IsValid() || d.GetDataType() != DataType::kFloat32 || d.Rank() != 2)
+    return Fail(error_message, "Sampler expects a valid rank-2 float32 logits tensor");
+  if (row_index >= d.GetShape()[0]) return Fail(error_message, "Sampler row_index is out of range");
+  const std::size_t vocab = d.GetShape()[1];
   const std::size_t k = std::max<std::size_t>(1, std::min<std::size_t>(config_.top_k, vocab));
-  const float t = config_.temperature <= 0.0f ? 1.0f : config_.temperature;
-  std::partial_sort(cand.begin(), cand.begin() + static_cast<std::ptrdiff_t>(k), cand.end(),
-                    [&row, t](std::size_t l, std::size_t r) { return row[l] / t > row[r] / t; });
-  *token_id = static_cast<int>(cand[0]);
-  if (top_logits) {
-    top_logits->clear();
-    for (std::size_t i = 0; i < k; ++i) top_logits->push_back(row[cand[i]]);
-  }
-  if (top_token_ids) {
-    top_token_ids->clear();
-    for (std::size_t i = 0; i < k; ++i) top_token_ids->push_back(static_cast<int>(cand[i]));
-  }
+  std::vector<int32_t> ids(k);
+  std::vector<float> vals(k);
+  int32_t tok = -1;
+  const float* row = static_cast<const float*>(logits.data()) + row_index * vocab;
+  if (!Check(soc_sample_topk(logits.GetBuffer()->context(), row, static_cast<int32_t>(vocab),
+                             static_cast<int32_t>(k), config_.temperature, &tok, ids.data(), vals.data()),
+             error_message))
+    return false;
+  *token_id = tok;
+  if (top_logits) top_logits->assign(vals.begin(), vals.end());
+  if (top_token_ids) top_token_ids->assign(ids.begin(), ids.end());
   return true;
 }
 
-// ---- GenerationContext (Mac/gpu/src/runtime/generation_context.cpp) ----
+// ---- GenerationContext (generation_context.cpp) ----
 GenerationContext::GenerationContext(QwenCausalLM model, Sampler sampler, CommandScheduler scheduler,
                                      std::size_t max_sequence_length)
     : model_(std::move(model)),
       sampler_(sampler),
       scheduler_(scheduler),
       max_sequence_length_(max_sequence_length) {}
+
+bool GenerationContext::EnsureLogitsBuffer(const HipContext& context, std::string* error_message) {
+  if (logits_buffer_ != nullptr) return true;
+  logits_buffer_ = HipBuffer::CreateShared(context, model_.vocab_size() * 4, "generation_logits", error_message);
+  return logits_buffer_ != nullptr;
+}
+
+bool GenerationContext::UploadTokenIds(const HipContext& context, const std::vector<int>& token_ids,
+                                       DeviceTensor* token_tensor, std::string* error_message) {
+  const std::size_t bytes = token_ids.size() * 4;
+  if (token_buffer_ == nullptr || token_buffer_->GetSizeBytes() < bytes) {
+    token_buffer_ = HipBuffer::CreateShared(context, std::max<std::size_t>(bytes, 256), "generation_tokens",
+                                            error_message);
+    if (token_buffer_ == nullptr) return false;
+  }
+  if (!token_buffer_->Write(token_ids.data(), bytes, 0, error_message)) return false;
+  *token_tensor = DeviceTensor(token_buffer_, 0, TensorDesc::CreateContiguous(DataType::kInt32, {token_ids.size()}));
+  return true;
+}
 
 bool GenerationContext::Prefill(const HipContext& context, PipelineCache* pipeline_cache,
                                 const std::vector<int>& token_ids, BufferArena* temporary_arena,
@@ -198,11 +445,16 @@ bool GenerationContext::Prefill(const HipContext& context, PipelineCache* pipeli
   Reset();
   prompt_token_ids_ = token_ids;
   running_token_ids_ = token_ids;
-  kv_cache_ = KVCache::CreateShared(context, model_, max_sequence_length_, "generation_kv_cache", error_message);
+  kv_cache_ = KVCache::CreateShared(context, model_.num_layers(), model_.num_key_value_heads(), model_.head_dim(),
+                                    max_sequence_length_, "generation_kv_cache", error_message);
   if (kv_cache_ == nullptr) return false;
-  std::vector<float>* logits = sampler_.greedy() ? nullptr : &last_logits_;
-  return scheduler_.RunPrefill(context, pipeline_cache, model_, token_ids, kv_cache_.get(), logits, temporary_arena,
-                               0, &prefill_token_, error_message);
+  if (!EnsureLogitsBuffer(context, error_message)) return false;
+  DeviceTensor tokens;
+  if (!UploadTokenIds(context, token_ids, &tokens, error_message)) return false;
+  // generation samples the last row only: the logits tensor holds that row
+  const DeviceTensor logits(logits_buffer_, 0, TensorDesc::CreateContiguous(DataType::kFloat32, {1, model_.vocab_size()}));
+  return scheduler_.RunPrefill(context, pipeline_cache, model_, tokens, kv_cache_.get(), logits, temporary_arena, 0,
+                               error_message);
 }
 
 bool GenerationContext::DecodeNextToken(const HipContext& context, PipelineCache* pipeline_cache, int last_token_id,
@@ -214,19 +466,16 @@ bool GenerationContext::DecodeNextToken(const HipContext& context, PipelineCache
     return Fail(error_message, "GenerationContext decode requires last_token_id to match the current sequence tail");
   if (running_token_ids_.size() >= max_sequence_length_)
     return Fail(error_message, "GenerationContext sequence length would exceed max_sequence_length");
-  std::vector<float>* logits = sampler_.greedy() ? nullptr : &last_logits_;
-  int greedy = -1;
-  if (!scheduler_.RunDecode(context, pipeline_cache, model_, std::vector<int>{last_token_id}, kv_cache_.get(),
-                            logits, temporary_arena, running_token_ids_.size() - 1, &greedy, error_message))
+  if (!EnsureLogitsBuffer(context, error_message)) return false;
+  DeviceTensor tokens;
+  if (!UploadTokenIds(context, std::vector<int>{last_token_id}, &tokens, error_message)) return false;
+  const DeviceTensor logits(logits_buffer_, 0, TensorDesc::CreateContiguous(DataType::kFloat32, {1, model_.vocab_size()}));
+  if (!scheduler_.RunDecode(context, pipeline_cache, model_, tokens, kv_cache_.get(), logits, temporary_arena,
+                            running_token_ids_.size() - 1, error_message))
     return false;
-  if (sampler_.greedy()) {
-    result->token_id = greedy;
-    result->top_token_ids = {greedy};
-    result->top_logits.clear();
-  } else if (!sampler_.SampleFromLogits(last_logits_, &result->token_id, &result->top_logits,
-                                        &result->top_token_ids, error_message)) {
+  if (!sampler_.SampleFromLogits(logits, 0, &result->token_id, &result->top_logits, &result->top_token_ids,
+                                 error_message))
     return false;
-  }
   running_token_ids_.push_back(result->token_id);
   return true;
 }
@@ -240,17 +489,14 @@ bool GenerationContext::Generate(const HipContext& context, PipelineCache* pipel
   generated_token_ids->clear();
   if (!Prefill(context, pipeline_cache, prompt_token_ids, temporary_arena, error_message)) return false;
   if (max_new_tokens == 0) return true;
-  int first = prefill_token_;
-  if (!sampler_.greedy()) {
-    GenerationStepResult r;
-    if (!sampler_.SampleFromLogits(last_logits_, &r.token_id, &r.top_logits, &r.top_token_ids, error_message))
-      return false;
-    first = r.token_id;
-  }
-  generated_token_ids->push_back(first);
-  running_token_ids_.push_back(first);
-  if (eos_token_id >= 0 && first == eos_token_id) return true;
-  int last = first;
+  GenerationStepResult first;
+  const DeviceTensor logits(logits_buffer_, 0, TensorDesc::CreateContiguous(DataType::kFloat32, {1, model_.vocab_size()}));
+  if (!sampler_.SampleFromLogits(logits, 0, &first.token_id, &first.top_logits, &first.top_token_ids, error_message))
+    return false;
+  generated_token_ids->push_back(first.token_id);
+  running_token_ids_.push_back(first.token_id);
+  if (eos_token_id >= 0 && first.token_id == eos_token_id) return true;
+  int last = first.token_id;
   for (std::size_t step = 1; step < max_new_tokens; ++step) {
     GenerationStepResult r;
     if (!DecodeNextToken(context, pipeline_cache, last, temporary_arena, &r, error_message)) return false;
@@ -265,8 +511,6 @@ void GenerationContext::Reset() {
   kv_cache_.reset();
   prompt_token_ids_.clear();
   running_token_ids_.clear();
-  last_logits_.clear();
-  prefill_token_ = -1;
 }
 
 }  // namespace soc::gpu

@@ -112,6 +112,20 @@ hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s);
 hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, int32_t* pos, const int32_t* start,
                               int32_t* ring, int ring_stride, hipStream_t s);
 
+// K/V rows [rows][nkv * hd] (fp32, or fp16 when `fp16`) into positions pos .. pos + rows - 1 of one (slot, layer)
+// of the cache, whose [nkv][cap][hd] fp16 planes start at kdst / vdst.
+hipError_t launch_kv_append_rows(const void* keys, const void* values, bool fp16, int rows, int nkv, int hd, int cap,
+                                 int pos, f16* kdst, f16* vdst, hipStream_t s);
+
+// ---- sampler: top-k candidates of one logits row (sample.hip) ----
+constexpr int kSampleChunk = 2048, kSampleMaxK = 64;
+// Device workspace bytes for a row of V logits.
+size_t sample_ws_bytes(int V);
+// Finds the candidates that std::partial_sort(top k of row / t) over 0..V-1 moves into its heap, in index order:
+// out[0] = count, out[1] = NaN seen, out[2 .. 2 + max_out) = indices, then max_out raw logits (k <= kSampleMaxK).
+hipError_t launch_sample_topk(const float* row, int V, float t, int k, void* ws, int* out, int max_out,
+                              hipStream_t s);
+
 // ---- persistent batch-1 decode step (one launch per token) ----
 struct PersistArgs {
   const f16* const* layer_w;  // device array [L][9]: in_norm, post_norm, q_norm, k_norm, wqkv, wo, wgate, wup, wdown

@@ -11,6 +11,7 @@
 #include <map>
 #include <memory>
 #include <new>
+#include <numeric>
 #include <string>
 #include <thread>
 #include <vector>
@@ -53,6 +54,9 @@ struct soc_ctx {
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool timing = false;
   uint32_t* scratch = nullptr;  // device address of this device's copy of `scratch` (soc_decode_steps_noalloc)
+  void* sample_ws = nullptr;    // soc_sample_topk: candidate search workspace and its output block
+  size_t sample_ws_bytes = 0;
+  int* sample_out = nullptr;
 };
 
 // Device memory of soc_decode_steps_noalloc: the exchange state of the one-launch decode kernels and the token ring
@@ -158,7 +162,9 @@ struct soc_model {
 };
 
 struct soc_kv {
-  soc_model* model = nullptr;
+  soc_ctx* ctx = nullptr;
+  soc_model* model = nullptr;  // bound by its first forward when created from dimensions alone
+  int layers = 0, nkv = 0, hd = 0;
   int slots = 0, cap = 0;
   f16 *k = nullptr, *v = nullptr;
   long long slot_stride = 0, layer_stride = 0;
@@ -172,6 +178,20 @@ namespace {
 
 int hip_fail(hipError_t e, const char* what) {
   return soc::fail(SOC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// A KV cache serves one model. One created from dimensions alone (soc_kv_create_dims, the reference's
+// KVCache::CreateShared) is bound to the first model that runs a forward on it, if the shapes agree.
+int bind_kv(soc_kv* kv, soc_model* m) {
+  if (kv->model == m) return SOC_OK;
+  if (kv->model != nullptr) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  const soc_qwen_config& c = m->cfg;
+  if (kv->ctx != m->ctx) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another context");
+  if (kv->layers != c.num_hidden_layers || kv->nkv != c.num_key_value_heads || kv->hd != c.head_dim)
+    return soc::fail(SOC_ERR_INVALID, "KV cache dimensions do not match the model (layers, KV heads, head_dim)");
+  if (kv->cap > m->rope_len) return soc::fail(SOC_ERR_CAPACITY, "KV capacity exceeds max_position_embeddings");
+  kv->model = m;
+  return SOC_OK;
 }
 
 int dev_alloc(std::vector<void*>& owner, size_t bytes, void** p) {
@@ -831,7 +851,7 @@ int validate_batch(soc_model* m, soc_kv* kv, int n, const int32_t* slots, const 
                    int* max_len) {
   if (m == nullptr || kv == nullptr || slots == nullptr || tokens == nullptr)
     return soc::fail(SOC_ERR_INVALID, "null argument");
-  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  SOC_TRY(bind_kv(kv, m));
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
   if (n <= 0 || n > kMaxBatchRows) return soc::fail(SOC_ERR_INVALID, "batch size must be in [1, 1024]");
   std::vector<char> seen(kv->slots, 0);
@@ -1018,6 +1038,8 @@ int soc_ctx_destroy(soc_ctx* ctx) {
   (void)hipEventDestroy(ctx->ev0);
   (void)hipEventDestroy(ctx->ev1);
   (void)hipStreamDestroy(ctx->stream);
+  (void)hipFree(ctx->sample_ws);
+  (void)hipFree(ctx->sample_out);
   delete ctx;
   return SOC_OK;
 }
@@ -1254,20 +1276,20 @@ int soc_model_decode_path(soc_model* m, int32_t* path) {
   SOC_API_END
 }
 
-int soc_kv_create(soc_model* m, int32_t slots, int32_t cap, soc_kv** out) {
-  SOC_API_BEGIN
-  if (m == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+namespace {
+int kv_create(soc_ctx* ctx, soc_model* m, int layers, int nkv, int hd, int32_t slots, int32_t cap, soc_kv** out) {
   *out = nullptr;
   if (slots <= 0 || cap <= 0) return soc::fail(SOC_ERR_INVALID, "soc_kv_create: slots and capacity must be positive");
-  if (cap > m->rope_len)
-    return soc::fail(SOC_ERR_CAPACITY, "soc_kv_create: capacity exceeds max_position_embeddings");
   std::unique_ptr<soc_kv> kv(new soc_kv());
+  kv->ctx = ctx;
   kv->model = m;
+  kv->layers = layers;
+  kv->nkv = nkv;
+  kv->hd = hd;
   kv->slots = slots;
   kv->cap = cap;
-  const soc_qwen_config& c = m->cfg;
-  kv->layer_stride = static_cast<long long>(c.num_key_value_heads) * cap * c.head_dim;
-  kv->slot_stride = kv->layer_stride * c.num_hidden_layers;
+  kv->layer_stride = static_cast<long long>(nkv) * cap * hd;
+  kv->slot_stride = kv->layer_stride * layers;
   const size_t bytes = static_cast<size_t>(kv->slot_stride) * slots * 2;
   hipError_t e = hipMalloc(&kv->k, bytes);
   if (e == hipSuccess) e = hipMalloc(&kv->v, bytes);
@@ -1279,12 +1301,35 @@ int soc_kv_create(soc_model* m, int32_t slots, int32_t cap, soc_kv** out) {
   kv->len.assign(slots, 0);
   *out = kv.release();
   return SOC_OK;
+}
+}  // namespace
+
+int soc_kv_create(soc_model* m, int32_t slots, int32_t cap, soc_kv** out) {
+  SOC_API_BEGIN
+  if (m == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (cap > m->rope_len)
+    return soc::fail(SOC_ERR_CAPACITY, "soc_kv_create: capacity exceeds max_position_embeddings");
+  const soc_qwen_config& c = m->cfg;
+  return kv_create(m->ctx, m, c.num_hidden_layers, c.num_key_value_heads, c.head_dim, slots, cap, out);
+  SOC_API_END
+}
+
+int soc_kv_create_dims(soc_ctx* ctx, int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t slots, int32_t cap,
+                       soc_kv** out) {
+  SOC_API_BEGIN
+  if (ctx == nullptr || out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (layers <= 0 || kv_heads <= 0 || head_dim <= 0)
+    return soc::fail(SOC_ERR_INVALID, "KVCache dimensions must be non-zero");  // kv_cache.mm:40-45
+  if (head_dim != 128) return soc::fail(SOC_ERR_INVALID, "soc_kv_create_dims: head_dim must be 128");
+  return kv_create(ctx, nullptr, layers, kv_heads, head_dim, slots, cap, out);
   SOC_API_END
 }
 
 int soc_kv_destroy(soc_kv* kv) {
   if (kv == nullptr) return SOC_OK;
-  (void)hipStreamSynchronize(kv->model->ctx->stream);
+  (void)hipStreamSynchronize(kv->ctx->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second.second);
   for (auto& g : kv->batch_graphs) (void)hipGraphExecDestroy(g.second.second);
   (void)hipFree(kv->k);
@@ -1310,12 +1355,11 @@ int soc_kv_reset(soc_kv* kv, int32_t slot) {
 int soc_kv_write(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, const float* key, const float* value) {
   SOC_API_BEGIN
   if (kv == nullptr || key == nullptr || value == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
-  const soc_qwen_config& c = kv->model->cfg;
-  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= c.num_hidden_layers || pos < 0 || pos >= kv->cap)
+  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= kv->layers || pos < 0 || pos >= kv->cap)
     return soc::fail(SOC_ERR_INVALID, "soc_kv_write: index out of range");  // kv_cache.cpp:51-53
-  const int d = c.head_dim;
+  const int d = kv->hd;
   std::vector<_Float16> kh(d), vh(d);
-  for (int h = 0; h < c.num_key_value_heads; ++h) {
+  for (int h = 0; h < kv->nkv; ++h) {
     for (int i = 0; i < d; ++i) {
       kh[i] = static_cast<_Float16>(key[h * d + i]);
       vh[i] = static_cast<_Float16>(value[h * d + i]);
@@ -1336,8 +1380,7 @@ int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t see
   if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
   if (slot < 0 || slot >= kv->slots || length < 0 || length > kv->cap)
     return soc::fail(SOC_ERR_INVALID, "soc_kv_fill_synthetic: bad slot or length");
-  const soc_qwen_config& c = kv->model->cfg;
-  const int d = c.head_dim, L = c.num_hidden_layers, nkv = c.num_key_value_heads;
+  const int d = kv->hd, L = kv->layers, nkv = kv->nkv;
   const size_t per_head = static_cast<size_t>(length) * d;
   // host image [layer][k|v][head][length][d], generated per (layer, k|v, head) stream on up to 16 threads
   std::vector<uint16_t> buf(static_cast<size_t>(L) * 2 * nkv * per_head);
@@ -1377,13 +1420,12 @@ int soc_kv_fill_synthetic(soc_kv* kv, int32_t slot, int32_t length, uint64_t see
 int soc_kv_read(const soc_kv* kv, int32_t slot, int32_t layer, uint16_t* keys, uint16_t* values) {
   SOC_API_BEGIN
   if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
-  const soc_qwen_config& c = kv->model->cfg;
-  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= c.num_hidden_layers)
+  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= kv->layers)
     return soc::fail(SOC_ERR_INVALID, "soc_kv_read: index out of range");
-  hipError_t e = hipStreamSynchronize(kv->model->ctx->stream);
+  hipError_t e = hipStreamSynchronize(kv->ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-  const int d = c.head_dim, n = kv->len[slot];
-  for (int h = 0; h < c.num_key_value_heads; ++h) {
+  const int d = kv->hd, n = kv->len[slot];
+  for (int h = 0; h < kv->nkv; ++h) {
     const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(layer) * kv->layer_stride +
                        static_cast<size_t>(h) * kv->cap * d;
     if (keys && (e = hipMemcpy(keys + static_cast<size_t>(h) * n * d, kv->k + off, static_cast<size_t>(n) * d * 2,
@@ -1397,11 +1439,49 @@ int soc_kv_read(const soc_kv* kv, int32_t slot, int32_t layer, uint16_t* keys, u
   SOC_API_END
 }
 
+int soc_kv_append(soc_kv* kv, int32_t slot, int32_t layer, int32_t pos, int32_t rows, const void* keys,
+                  const void* values, int32_t dtype) {
+  SOC_API_BEGIN
+  if (kv == nullptr || (rows > 0 && (keys == nullptr || values == nullptr)))
+    return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (layer < 0 || layer >= kv->layers) return soc::fail(SOC_ERR_INVALID, "KVCache layer index is out of range");
+  if (dtype != SOC_DTYPE_F32 && dtype != SOC_DTYPE_F16) return soc::fail(SOC_ERR_INVALID, "dtype must be f32 or f16");
+  if (rows < 0 || pos < 0) return soc::fail(SOC_ERR_INVALID, "rows and pos must be >= 0");
+  if (pos + rows > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "KVCache append would exceed max_sequence_length");
+  if (rows == 0) return SOC_OK;
+  const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(layer) * kv->layer_stride;
+  hipStream_t s = kv->ctx->stream;
+  hipError_t e = soc::launch_kv_append_rows(keys, values, dtype == SOC_DTYPE_F16, rows, kv->nkv, kv->hd, kv->cap, pos,
+                                            kv->k + off, kv->v + off, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);  // the source rows may be released when this returns
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "kv append");
+  SOC_API_END
+}
+
+int soc_kv_set_length(soc_kv* kv, int32_t slot, int32_t length) {
+  if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (length < 0 || length > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "length exceeds the KV capacity");
+  kv->len[slot] = length;
+  return SOC_OK;
+}
+
+int soc_kv_layer_planes(const soc_kv* kv, int32_t slot, int32_t layer, void** keys, void** values) {
+  if (kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null kv");
+  if (slot < 0 || slot >= kv->slots || layer < 0 || layer >= kv->layers)
+    return soc::fail(SOC_ERR_INVALID, "soc_kv_layer_planes: index out of range");
+  const size_t off = static_cast<size_t>(slot) * kv->slot_stride + static_cast<size_t>(layer) * kv->layer_stride;
+  if (keys) *keys = kv->k + off;
+  if (values) *values = kv->v + off;
+  return SOC_OK;
+}
+
 int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off,
                 int32_t logit_rows, float* logits, int32_t* next_token) {
   SOC_API_BEGIN
   if (m == nullptr || kv == nullptr || ids == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
-  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  SOC_TRY(bind_kv(kv, m));
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
   if (n <= 0) return soc::fail(SOC_ERR_INVALID, "prefill requires at least one token");  // generation_context.cpp:22-27
   if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
@@ -1590,8 +1670,8 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     if ((e = prefill_gemm(g,soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
   }
   if (logits != nullptr && logit_rows > 0) {
-    if ((e = hipMemcpyAsync(logits, w.logits, static_cast<size_t>(logit_rows) * c.vocab_size * 4,
-                            hipMemcpyDeviceToHost, s)) != hipSuccess)
+    if ((e = hipMemcpyAsync(logits, w.logits, static_cast<size_t>(logit_rows) * c.vocab_size * 4, hipMemcpyDefault,
+                            s)) != hipSuccess)
       return hip_fail(e, "hipMemcpyAsync logits");
   }
   int32_t tok = 0;
@@ -1607,7 +1687,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
 int soc_decode(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, float* logits, int32_t* next_token) {
   SOC_API_BEGIN
   if (m == nullptr || kv == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
-  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  SOC_TRY(bind_kv(kv, m));
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
   if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
   if (kv->len[slot] + 1 > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
@@ -1617,7 +1697,7 @@ int soc_decode(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, float* logi
   hipStream_t s = m->ctx->stream;
   hipError_t e;
   if (logits != nullptr &&
-      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDeviceToHost,
+      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDefault,
                           s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync logits");
   int32_t tok = 0;
@@ -1634,7 +1714,7 @@ int soc_decode_steps(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, int32
   SOC_API_BEGIN
   if (m == nullptr || kv == nullptr || (steps > 0 && tokens_out == nullptr))
     return soc::fail(SOC_ERR_INVALID, "null argument");
-  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  SOC_TRY(bind_kv(kv, m));
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
   if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
   if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
@@ -1657,7 +1737,7 @@ int soc_decode_steps_noalloc(soc_model* m, soc_kv* kv, int32_t slot, int32_t las
   SOC_API_BEGIN
   if (m == nullptr || kv == nullptr || (steps > 0 && tokens_out == nullptr))
     return soc::fail(SOC_ERR_INVALID, "null argument");
-  if (kv->model != m) return soc::fail(SOC_ERR_INVALID, "KV cache belongs to another model");
+  SOC_TRY(bind_kv(kv, m));
   if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
   if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
   if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
@@ -1751,8 +1831,8 @@ int soc_decode_batch(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, 
   hipStream_t s = m->ctx->stream;
   hipError_t e;
   if (logits != nullptr &&
-      (e = hipMemcpyAsync(logits, m->pws.logits, static_cast<size_t>(n) * m->cfg.vocab_size * 4,
-                          hipMemcpyDeviceToHost, s)) != hipSuccess)
+      (e = hipMemcpyAsync(logits, m->pws.logits, static_cast<size_t>(n) * m->cfg.vocab_size * 4, hipMemcpyDefault,
+                          s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync logits");
   if ((e = hipMemcpyAsync(next_tokens, m->bws.ids, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, s)) !=
       hipSuccess)
@@ -1875,3 +1955,69 @@ int soc_dequant(soc_ctx* ctx, const void* codes, int32_t bits, const void* scale
 }
 
 }  // extern "C"
+
+// ---- sampler (Mac/gpu/src/runtime/sampler.cpp:14-71) ----
+int soc_sample_topk(soc_ctx* ctx, const float* row, int32_t vocab, int32_t top_k, float temperature,
+                    int32_t* token_id, int32_t* top_ids, float* top_logits) {
+  SOC_API_BEGIN
+  if (ctx == nullptr || row == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (token_id == nullptr) return soc::fail(SOC_ERR_INVALID, "Sampler requires a non-null token_id output");
+  if (vocab <= 0) return soc::fail(SOC_ERR_INVALID, "Sampler expects a non-empty logits row");
+  // sampler.cpp:47-48: top_k clamped to [1, vocab]; a non-positive temperature means 1
+  const int k = std::max(1, std::min(top_k, vocab));
+  const float t = temperature <= 0.0f ? 1.0f : temperature;
+  constexpr int kMaxOut = 4096;
+  hipStream_t s = ctx->stream;
+  hipError_t e;
+  std::vector<int32_t> idx;
+  std::vector<float> vals;
+  bool whole_row = k > soc::kSampleMaxK;
+  if (!whole_row) {
+    const size_t need = soc::sample_ws_bytes(vocab);
+    if (ctx->sample_ws_bytes < need) {
+      if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+      (void)hipFree(ctx->sample_ws);
+      ctx->sample_ws = nullptr;
+      ctx->sample_ws_bytes = 0;
+      if ((e = hipMalloc(&ctx->sample_ws, need)) != hipSuccess) return hip_fail(e, "hipMalloc sampler workspace");
+      ctx->sample_ws_bytes = need;
+    }
+    if (ctx->sample_out == nullptr &&
+        (e = hipMalloc(&ctx->sample_out, (2 + 2 * kMaxOut) * sizeof(int))) != hipSuccess)
+      return hip_fail(e, "hipMalloc sampler output");
+    if ((e = soc::launch_sample_topk(row, vocab, t, k, ctx->sample_ws, ctx->sample_out, kMaxOut, s)) != hipSuccess)
+      return hip_fail(e, "sampler launch");
+    std::vector<int32_t> out(2 + 2 * kMaxOut);
+    if ((e = hipMemcpyAsync(out.data(), ctx->sample_out, out.size() * 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync sampler");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "sampler");
+    const int n = out[0];
+    if (out[1] != 0 || n > kMaxOut || n < k) {
+      whole_row = true;  // NaN logits, or more candidates than the output block holds: the reference's full sort
+    } else {
+      idx.assign(out.begin() + 2, out.begin() + 2 + n);
+      vals.resize(n);
+      std::memcpy(vals.data(), out.data() + 2 + kMaxOut, static_cast<size_t>(n) * 4);
+    }
+  }
+  if (whole_row) {
+    vals.resize(vocab);
+    if ((e = hipMemcpyAsync(vals.data(), row, static_cast<size_t>(vocab) * 4, hipMemcpyDefault, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync logits row");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "sampler");
+    idx.resize(vocab);
+    std::iota(idx.begin(), idx.end(), 0);
+  }
+  // the reference's partial sort, over the candidates in index order (the same comparisons on the same heap)
+  std::vector<int32_t> order(idx.size());
+  std::iota(order.begin(), order.end(), 0);
+  std::partial_sort(order.begin(), order.begin() + k, order.end(),
+                    [&vals, t](int32_t l, int32_t r) { return vals[l] / t > vals[r] / t; });
+  *token_id = idx[order[0]];
+  for (int r = 0; r < k; ++r) {
+    if (top_ids) top_ids[r] = idx[order[r]];
+    if (top_logits) top_logits[r] = vals[order[r]];
+  }
+  return SOC_OK;
+  SOC_API_END
+}

@@ -3,6 +3,8 @@
 // head_dim is 128 here (the only head size the kernels take), so the identity model is 128 wide: one-hot embedding
 // rows e_0..e_3, zero projections, unit gains. The residual stream stays e_t, the final RMSNorm scales it to
 // sqrt(128) e_t, and the tied head gives the largest logit to the input token: Generate([1,2], 3) = [2,2,2].
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <map>
 #include <string>
@@ -66,6 +68,26 @@ int main() {
     EXPECT(out == std::vector<int>({2, 2, 2}), "unexpected generated token sequence");
     EXPECT(gen.prompt_token_ids() == prompt, "prompt token ids were not preserved");
     EXPECT(gen.running_token_ids() == std::vector<int>({1, 2, 2, 2, 2}), "running ids do not reflect decoding");
+
+    // the top-k lists of a step (sampler.cpp:56-66): input token 2 gives logits sqrt(128) at id 2 and 0 elsewhere;
+    // the expected order is the reference's std::partial_sort over that row
+    {
+      GenerationStepResult r;
+      EXPECT(gen.DecodeNextToken(*ctx, &cache, 2, arena.get(), &r, &err), err.c_str());
+      std::vector<float> row(4, 0.0f);
+      row[2] = std::sqrt(128.0f);
+      std::vector<int> cand = {0, 1, 2, 3};
+      std::partial_sort(cand.begin(), cand.begin() + top_k, cand.end(),
+                        [&row](int a, int b) { return row[a] / 1.0f > row[b] / 1.0f; });
+      EXPECT(r.token_id == 2, "top-k token");
+      EXPECT(r.top_token_ids.size() == top_k && r.top_logits.size() == top_k, "top-k list sizes");
+      for (std::size_t j = 0; j < top_k && j < r.top_token_ids.size(); ++j) {
+        EXPECT(r.top_token_ids[j] == cand[j], "top-k ids follow the reference's partial sort");
+        EXPECT(std::fabs(r.top_logits[j] - row[cand[j]]) < 1e-3f, "top-k logits");
+      }
+      gen.Reset();
+      EXPECT(gen.Generate(*ctx, &cache, prompt, 3, -1, arena.get(), &out, &err), err.c_str());
+    }
 
     // error paths (generation_context.cpp:67-90): wrong tail token, null result
     GenerationStepResult r;

@@ -37,9 +37,17 @@ def test_library_exports_cpp_host_interface():
     # every out-of-line method declared in runtime.h (those ending in ';' with a parameter list and no body)
     methods = {
         "soc::gpu::HipContext::CreateDefault", "soc::gpu::HipContext::Synchronize",
-        "soc::gpu::BufferArena::CreateShared", "soc::gpu::BufferArena::Reserve",
+        "soc::gpu::HipBuffer::CreateShared", "soc::gpu::HipBuffer::Wrap", "soc::gpu::HipBuffer::Write",
+        "soc::gpu::HipBuffer::Read", "soc::gpu::GetDataTypeSize", "soc::gpu::TensorDesc::CreateContiguous",
+        "soc::gpu::TensorDesc::CreateStrided", "soc::gpu::TensorDesc::ElementCount", "soc::gpu::TensorDesc::ByteSize",
+        "soc::gpu::DeviceTensor::IsValid",
+        "soc::gpu::BufferArena::CreateShared", "soc::gpu::BufferArena::Allocate", "soc::gpu::BufferArena::ResetToMark",
+        "soc::gpu::BufferArena::ClearTelemetry", "soc::gpu::BufferArenaMarkGuard::BufferArenaMarkGuard",
         "soc::gpu::QwenModelLoader::LoadModel", "soc::gpu::QwenModelLoader::SynthesizeModel",
-        "soc::gpu::KVCache::CreateShared", "soc::gpu::KVCache::GetSequenceLength",
+        "soc::gpu::QwenCausalLM::ForwardLogitsCached",
+        "soc::gpu::KVCache::CreateShared", "soc::gpu::KVCache::Reserve", "soc::gpu::KVCache::AppendPrefill",
+        "soc::gpu::KVCache::AppendDecodeToken", "soc::gpu::KVCache::ViewForLayer", "soc::gpu::KVCache::OnForward",
+        "soc::gpu::KVCache::LayersAligned",
         "soc::gpu::CommandScheduler::RunPrefill", "soc::gpu::CommandScheduler::RunDecode",
         "soc::gpu::Sampler::SampleFromLogits", "soc::gpu::GenerationContext::Prefill",
         "soc::gpu::GenerationContext::DecodeNextToken", "soc::gpu::GenerationContext::Generate",

@@ -157,6 +157,27 @@ def test_gqa_matches_float64_softmax(oracle_mod):
             assert np.allclose(o[t, h], w @ v[:vis, g].astype(np.float64), atol=2e-5)
 
 
+def test_sample_topk_restatement(oracle_mod):
+    """The GPU sampler's list: first id == sample() (pinned to the compiled reference), values the k largest of
+    logit / t in order, top_k clamped to [1, vocab], non-positive temperature taken as 1."""
+    rng = np.random.default_rng(5)
+    for trial in range(200):
+        v = int(rng.integers(1, 400))
+        row = rng.integers(-3, 4, v).astype(np.float32) * np.float32(rng.choice([1.0, 0.37]))
+        for k in (0, 1, 2, 5, 50, 1000):
+            for t in (1.0, 0.7, 0.0, -1.0):
+                tok, ids, vals = oracle_mod.sample_topk(row, t, k)
+                kk = max(1, min(k, v))
+                tt = np.float32(t if t > 0 else 1.0)
+                assert ids.size == kk and tok == ids[0]
+                assert tok == oracle_mod.sample(row, float(tt), kk)
+                q = row[ids] / tt
+                assert np.all(q[:-1] >= q[1:])
+                assert np.array_equal(np.sort(row / tt)[::-1][:kk], q)
+                assert np.array_equal(vals, row[ids])
+                assert len(set(ids.tolist())) == kk
+
+
 def test_kat_sampler(oracle_mod):
     # test_nn_modules.cpp:619-628
     assert oracle_mod.sample(np.array([0.1, 3.0, 2.0], np.float32), 1.0, 2) == 1
