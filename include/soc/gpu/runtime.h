@@ -8,7 +8,8 @@
 //   PipelineCache       -> PipelineCache         (kernel/pipeline_cache.h)
 //   BufferArena         -> BufferArena           (buffer/buffer_arena.h; the forward's scratch is the library's own)
 //   QwenCausalLM        -> QwenCausalLM          (model/qwen_causal_lm.h)
-//   QwenModelLoader     -> QwenModelLoader       (model/qwen_model_loader.h; from named host fp16 tensors)
+//   QwenModelLoader     -> QwenModelLoader       (model/qwen_model_loader.h; from a bundle's manifest, or from
+//                                                  named host fp16 tensors)
 //   KVCache             -> KVCache               (runtime/kv_cache.h)
 //   CommandScheduler    -> CommandScheduler      (runtime/command_scheduler.h)
 //   Sampler             -> Sampler               (runtime/sampler.h)
@@ -32,6 +33,7 @@
 #include <string>
 #include <vector>
 
+#include "soc/assets.h"
 #include "soc_hip.h"
 
 namespace soc::gpu {
@@ -264,6 +266,13 @@ class QwenModelLoader {
   static bool LoadModel(const HipContext& context, const QwenCausalLMParams& params,
                         const std::map<std::string, HostTensor>& tensors, QwenCausalLM* model,
                         std::string* error_message);
+  // Mac/gpu/src/model/qwen_model_loader.cpp:100-192 over a manifest (soc/assets.h): validates it and its config
+  // (StartupValidator), reads every weight (float32, float16 or bfloat16 files; kept as fp16) and builds the model;
+  // lm_head.weight only when the embeddings are not tied.
+  static bool LoadModel(const HipContext& context, const soc::ManifestData& manifest, QwenCausalLM* model,
+                        std::string* error_message);
+  static bool LoadModelFromFile(const HipContext& context, const std::string& manifest_path, QwenCausalLM* model,
+                                std::string* error_message);
   // Random-init weights from the seeded generator (norm gains 1.0, the rest N(0, sigma)).
   static bool SynthesizeModel(const HipContext& context, const QwenCausalLMParams& params, uint64_t seed, float sigma,
                               QwenCausalLM* model, std::string* error_message);

@@ -80,6 +80,20 @@ int soc_model_load_tensor(soc_model* model, const char* name, const uint16_t* ho
 int soc_model_synthesize(soc_model* model, uint64_t seed, float sigma);
 /* Validates that every tensor the config needs is present (StartupValidator / loader checks). */
 int soc_model_finalize(soc_model* model);
+/* A model bundle on disk (the reference's export format: manifest.json + one raw tensor file per weight;
+ * Mac/cpu/src/runtime_assets.cpp:138-168, startup_validator.cpp:5-23, qwen3_config.cpp:20-67). Opening parses the
+ * manifest and validates it and its Qwen3 config; it needs no GPU. Messages are the reference loaders'. */
+typedef struct soc_bundle soc_bundle;
+int soc_bundle_open(const char* manifest_path, soc_bundle** out);
+int soc_bundle_close(soc_bundle* bundle);
+/* The config the bundle describes (max_position_embeddings: the config's value, else 32768). */
+int soc_bundle_config(const soc_bundle* bundle, soc_qwen_config* out);
+/* One weight of the model as fp16 bits: float16 as stored, float32 and bfloat16 rounded to nearest even, after the
+ * checks of weight_loader.cpp:17-30 and qwen_model_loader.cpp:17-25 (byte_size, floating dtype, expected shape). */
+int soc_bundle_tensor_f16(const soc_bundle* bundle, const char* name, uint16_t* out, int64_t numel);
+/* Creates, fills and finalizes a model from a bundle (QwenModelLoader::LoadModelFromFile, qwen_model_loader.cpp:
+ * 35-97): every weight of the config's layer count, lm_head.weight only when the embeddings are not tied. */
+int soc_model_load_bundle(soc_ctx* ctx, const char* manifest_path, soc_model** out);
 /* Bytes of weights held on the device. */
 int soc_model_weight_bytes(const soc_model* model, int64_t* bytes);
 /* Which decode implementation soc_decode / soc_decode_steps use on this device: 2 = one kernel launch per token with

@@ -134,6 +134,11 @@ def lib() -> C.CDLL:
         "soc_decode_steps": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_decode_steps_noalloc": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_sample_topk": (C.c_int, [P, P, I32, I32, C.c_float, P, P, P]),
+        "soc_bundle_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "soc_bundle_close": (C.c_int, [P]),
+        "soc_bundle_config": (C.c_int, [P, C.POINTER(QwenConfigC)]),
+        "soc_bundle_tensor_f16": (C.c_int, [P, C.c_char_p, P, I64]),
+        "soc_model_load_bundle": (C.c_int, [P, C.c_char_p, C.POINTER(P)]),
         "soc_kv_create_dims": (C.c_int, [P, I32, I32, I32, I32, I32, P]),
         "soc_kv_append": (C.c_int, [P, I32, I32, I32, I32, P, P, I32]),
         "soc_kv_set_length": (C.c_int, [P, I32, I32]),
@@ -277,6 +282,13 @@ class Model:
         check(lib().soc_model_create(ctx.h, C.byref(c), C.byref(h)))
         self.h = h
 
+    @classmethod
+    def wrap(cls, ctx: Context, cfg: QwenConfig, handle) -> "Model":
+        """A Model around a soc_model the library created (soc_model_load_bundle)."""
+        m = cls.__new__(cls)
+        m.ctx, m.cfg, m.h = ctx, cfg, handle
+        return m
+
     def load(self, weights: dict[str, np.ndarray]) -> "Model":
         for name, arr in weights.items():
             a = np.ascontiguousarray(arr).view(np.uint16)
@@ -377,6 +389,48 @@ def decode_steps_noalloc(model: Model, kv: KVCache, slot: int, last_token: int, 
     out = np.empty(steps, dtype=np.int32)
     check(lib().soc_decode_steps_noalloc(model.h, kv.h, slot, int(last_token), steps, _ptr(out)))
     return out
+
+
+class Bundle:
+    """A model bundle on disk (manifest.json + raw tensor files), opened and validated without a GPU."""
+
+    def __init__(self, manifest_path):
+        self.h = None
+        h = C.c_void_p()
+        check(lib().soc_bundle_open(str(manifest_path).encode(), C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib().soc_bundle_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def config(self) -> QwenConfig:
+        c = QwenConfigC()
+        check(lib().soc_bundle_config(self.h, C.byref(c)))
+        return QwenConfig(c.vocab_size, c.hidden_size, c.num_hidden_layers, c.num_attention_heads,
+                          c.num_key_value_heads, c.intermediate_size, c.head_dim, c.max_position_embeddings,
+                          c.rope_theta, float(c.rms_norm_eps), bool(c.tie_word_embeddings))
+
+    def tensor_f16(self, name: str, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=np.uint16)
+        check(lib().soc_bundle_tensor_f16(self.h, name.encode(), _ptr(out), out.size))
+        return out
+
+
+def load_bundle(ctx: Context, manifest_path) -> "Model":
+    """A finalized model from a bundle (soc_model_load_bundle)."""
+    h = C.c_void_p()
+    check(lib().soc_model_load_bundle(ctx.h, str(manifest_path).encode(), C.byref(h)))
+    b = Bundle(manifest_path)
+    try:
+        cfg = b.config()
+    finally:
+        b.close()
+    return Model.wrap(ctx, cfg, h)
 
 
 def sample_topk(ctx: Context, row_ptr: int, vocab: int, top_k: int, temperature: float = 1.0):

@@ -231,6 +231,49 @@ bool QwenModelLoader::LoadModel(const HipContext& context, const QwenCausalLMPar
   return true;
 }
 
+bool QwenModelLoader::LoadModel(const HipContext& context, const soc::ManifestData& manifest, QwenCausalLM* model,
+                                std::string* error_message) {
+  if (model == nullptr) return Fail(error_message, "QwenModelLoader requires a non-null model output");
+  try {
+    const soc::Qwen3Config c = soc::StartupValidator::ValidateManifest(manifest);
+    QwenCausalLMParams p;
+    p.vocab_size = c.vocab_size;
+    p.hidden_size = c.hidden_size;
+    p.num_hidden_layers = c.num_hidden_layers;
+    p.num_attention_heads = c.num_attention_heads;
+    p.num_key_value_heads = c.num_key_value_heads;
+    p.head_dim = c.head_dim;
+    p.intermediate_size = c.intermediate_size;
+    p.max_position_embeddings = c.max_position_embeddings;
+    p.rope_theta = static_cast<float>(c.rope_theta);
+    p.rms_norm_eps = static_cast<float>(c.rms_norm_eps);
+    p.tie_word_embeddings = c.tie_word_embeddings;
+    const soc_qwen_config cfg = ToConfig(p);
+    soc_model* m = nullptr;
+    if (!Check(soc_model_create(context.handle(), &cfg, &m), error_message)) return false;
+    auto holder = WrapModel(m);
+    for (const auto& [name, shape] : soc::Qwen3TensorShapes(c)) {
+      const std::vector<uint16_t> w = soc::WeightLoader::LoadFloat16(manifest, name, shape);
+      if (!Check(soc_model_load_tensor(m, name.c_str(), w.data(), static_cast<int64_t>(w.size())), error_message))
+        return false;
+    }
+    if (!Check(soc_model_finalize(m), error_message)) return false;
+    *model = QwenCausalLM(std::move(holder), p);
+    return true;
+  } catch (const std::exception& e) {
+    return Fail(error_message, e.what());
+  }
+}
+
+bool QwenModelLoader::LoadModelFromFile(const HipContext& context, const std::string& manifest_path,
+                                        QwenCausalLM* model, std::string* error_message) {
+  try {
+    return LoadModel(context, soc::ManifestLoader::LoadFromFile(manifest_path), model, error_message);
+  } catch (const std::exception& e) {
+    return Fail(error_message, e.what());
+  }
+}
+
 bool QwenModelLoader::SynthesizeModel(const HipContext& context, const QwenCausalLMParams& params, uint64_t seed,
                                       float sigma, QwenCausalLM* model, std::string* error_message) {
   if (model == nullptr) return Fail(error_message, "QwenModelLoader requires a non-null model output");

@@ -6,6 +6,8 @@
 // tests/test_gpu_host_api.py compares with the reference-emitted fixture of the same model.
 //
 // usage: test_harness_sequence OUT vocab hidden layers nq nkv inter tie seed top_k new_tokens id0 id1 ...
+//        test_harness_sequence OUT --bundle MANIFEST top_k new_tokens id0 id1 ...   (model from a bundle on disk,
+//        QwenModelLoader::LoadModelFromFile)
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -37,26 +39,37 @@ int Die(const char* what, const std::string& err) {
 }  // namespace
 
 int main(int argc, char** argv) {
-  if (argc < 13) {
-    std::fprintf(stderr, "usage: %s OUT vocab hidden layers nq nkv inter tie seed top_k new id...\n", argv[0]);
+  const bool from_bundle = argc > 2 && std::string(argv[2]) == "--bundle";
+  if ((from_bundle && argc < 7) || (!from_bundle && argc < 13)) {
+    std::fprintf(stderr, "usage: %s OUT (vocab hidden layers nq nkv inter tie seed | --bundle MANIFEST) top_k new id...\n",
+                 argv[0]);
     return 2;
   }
   QwenCausalLMParams p;
-  p.vocab_size = std::strtoul(argv[2], nullptr, 10);
-  p.hidden_size = std::strtoul(argv[3], nullptr, 10);
-  p.num_hidden_layers = std::strtoul(argv[4], nullptr, 10);
-  p.num_attention_heads = std::strtoul(argv[5], nullptr, 10);
-  p.num_key_value_heads = std::strtoul(argv[6], nullptr, 10);
-  p.head_dim = 128;
-  p.intermediate_size = std::strtoul(argv[7], nullptr, 10);
-  p.max_position_embeddings = 4096;
-  p.tie_word_embeddings = std::atoi(argv[8]) != 0;
-  const uint64_t seed = std::strtoull(argv[9], nullptr, 10);
+  uint64_t seed = 0;
+  std::string manifest_path;
+  int a;  // first of: top_k new_tokens ids...
+  if (from_bundle) {
+    manifest_path = argv[3];
+    a = 4;
+  } else {
+    p.vocab_size = std::strtoul(argv[2], nullptr, 10);
+    p.hidden_size = std::strtoul(argv[3], nullptr, 10);
+    p.num_hidden_layers = std::strtoul(argv[4], nullptr, 10);
+    p.num_attention_heads = std::strtoul(argv[5], nullptr, 10);
+    p.num_key_value_heads = std::strtoul(argv[6], nullptr, 10);
+    p.head_dim = 128;
+    p.intermediate_size = std::strtoul(argv[7], nullptr, 10);
+    p.max_position_embeddings = 4096;
+    p.tie_word_embeddings = std::atoi(argv[8]) != 0;
+    seed = std::strtoull(argv[9], nullptr, 10);
+    a = 10;
+  }
   SamplerConfig sc;
-  sc.top_k = std::strtoul(argv[10], nullptr, 10);
-  const std::size_t max_new_tokens = std::strtoul(argv[11], nullptr, 10);
+  sc.top_k = std::strtoul(argv[a], nullptr, 10);
+  const std::size_t max_new_tokens = std::strtoul(argv[a + 1], nullptr, 10);
   std::vector<int> prompt_token_ids;
-  for (int i = 12; i < argc; ++i) prompt_token_ids.push_back(std::atoi(argv[i]));
+  for (int i = a + 2; i < argc; ++i) prompt_token_ids.push_back(std::atoi(argv[i]));
 
   std::string err;
   auto context_holder = MetalContext::CreateDefault("unused.metallib", "unused.metal", &err);
@@ -66,7 +79,9 @@ int main(int argc, char** argv) {
   auto temporary_arena = BufferArena::CreateShared(context, 1 << 20, "temp", &err);
   if (!temporary_arena) return Die("arena", err);
   QwenCausalLM model;
-  if (!QwenModelLoader::SynthesizeModel(context, p, seed, 0.02f, &model, &err)) return Die("model", err);
+  if (from_bundle ? !QwenModelLoader::LoadModelFromFile(context, manifest_path, &model, &err)
+                  : !QwenModelLoader::SynthesizeModel(context, p, seed, 0.02f, &model, &err))
+    return Die("model", err);
   const CommandScheduler scheduler;
   const Sampler sampler(sc);
 
