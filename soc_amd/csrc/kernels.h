@@ -237,9 +237,14 @@ struct GemmSplitArgs {
 bool gemm_split_supported(const GemmSplitArgs& g);
 hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s);
 
-// Skinny projection of a ragged decode batch: c[M][.] (epi) x[M][K] . [w | w2]^T for 1 <= M <= 16, K % 256 == 0.
-// Rows 0..N0-1 come from w, rows N0..Ntot-1 from w2 (SwiGLU: Ntot = 2 N0, c = silu(gate) * up over N0 outputs;
-// store/residual: Ntot = N0). part: split-K scratch of skinny_part_floats(Ntot, K) floats.
+// Skinny projection of a ragged decode batch: x[M][K] . [w | w2]^T for 1 <= M <= 16 rows, K % 256 == 0, split over
+// K, then an epilogue kernel that adds the splits in order. Rows 0..N0-1 come from w, rows N0..Ntot-1 from w2.
+//   gain set: the input is RMSNorm(x) with that gain: x * gain enters the products, and the row's 1 / rms (from the
+//     sum of squares of x over all K) scales the sums.
+//   EPI_STORE: c = y (Ntot = N0). EPI_RESIDUAL: c += y (Ntot = N0). EPI_SWIGLU: c = silu(gate) * up over N0 outputs
+//   (Ntot = 2 N0, N0 % 64 == 0). EPI_QKV: rows are q | k | v heads of 128; per head RMSNorm (q_gain / k_gain) and
+//   rotate-half RoPE at pos[m] of q and k; q -> q_out [M][nq * 128], k and v -> the fp16 cache of slots[m] at pos[m].
+// part: scratch of skinny_part_floats(Ntot, K) floats.
 struct SkinnyArgs {
   const float* x;
   int ldx;
@@ -249,6 +254,20 @@ struct SkinnyArgs {
   float* part;
   float* c;
   int ldc;
+  const f16* gain;  // nullable: RMSNorm gain of the input
+  float eps;
+  // EPI_QKV
+  float* q_out;
+  f16* kcache;
+  f16* vcache;
+  const f16* q_gain;
+  const f16* k_gain;
+  const float* rope_cos;
+  const float* rope_sin;
+  const int32_t* pos;
+  const int32_t* slots;
+  long long slot_stride, layer_stride;
+  int layer, cap, nq, nkv;
   int KS, Kb;  // set by the launcher
 };
 bool skinny_supported(int M, int K);

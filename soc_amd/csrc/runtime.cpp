@@ -762,23 +762,19 @@ hipError_t split_gemm(const soc::f16* ah, const soc::f16* al, int lda, const soc
 
 // Projections of a ragged decode batch (M = rows of the batch): the skinny MFMA kernel in slabs of 16 rows up to
 // 64 rows (SOC_BATCH_GEMM=tile selects the 128x128-tile GEMM of the prefill path).
-hipError_t batch_gemm(const soc::GemmArgs& g, int epi, float* part, hipStream_t s) {
-  const char* mode = std::getenv("SOC_BATCH_GEMM");
-  const bool tile = mode != nullptr && std::strcmp(mode, "tile") == 0;
-  if (tile || part == nullptr || g.M > 64 || !soc::skinny_supported(1, g.K)) return prefill_gemm(g, epi, s);
-  for (int m0 = 0; m0 < g.M; m0 += 16) {
-    soc::SkinnyArgs a{};
-    a.x = g.a + static_cast<size_t>(m0) * g.lda;
-    a.ldx = g.lda;
-    a.w = g.w;
-    a.w2 = epi == soc::EPI_SWIGLU ? g.w2 : nullptr;
-    a.N0 = g.N;
-    a.Ntot = epi == soc::EPI_SWIGLU ? 2 * g.N : g.N;
-    a.K = g.K;
-    a.M = std::min(16, g.M - m0);
-    a.part = part;
-    a.c = g.c + static_cast<size_t>(m0) * g.ldc;
-    a.ldc = g.ldc;
+// A ragged-batch projection on the skinny kernel, in chunks of 16 rows: `proto` carries the weights, the input
+// RMSNorm gain (or none) and the epilogue's own arguments; rows m0.. of x, c, q_out, pos and slots per chunk.
+hipError_t batch_skinny(const soc::SkinnyArgs& proto, int n, int epi, hipStream_t s) {
+  for (int m0 = 0; m0 < n; m0 += 16) {
+    soc::SkinnyArgs a = proto;
+    a.x = proto.x + static_cast<size_t>(m0) * proto.ldx;
+    a.M = std::min(16, n - m0);
+    if (proto.c != nullptr) a.c = proto.c + static_cast<size_t>(m0) * proto.ldc;
+    if (epi == soc::EPI_QKV) {
+      a.q_out = proto.q_out + static_cast<size_t>(m0) * proto.nq * 128;
+      a.pos = proto.pos + m0;
+      a.slots = proto.slots + m0;
+    }
     const hipError_t e = soc::launch_skinny(a, epi, s);
     if (e != hipSuccess) return e;
   }
@@ -877,57 +873,124 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
   PrefillWs& w = m->pws;
   BatchWs& b = m->bws;
   hipStream_t s = m->ctx->stream;
-  const int H = c.hidden_size;
+  const int H = c.hidden_size, I = c.intermediate_size;
   hipError_t e;
+  // up to 64 rows: the skinny kernels per projection and 16 rows (input RMSNorm and the q/k norm, RoPE and KV append
+  // folded into them); beyond, or with SOC_BATCH_GEMM=tile, the tile GEMMs with separate normalisation and q/k kernels
+  const char* mode = std::getenv("SOC_BATCH_GEMM");
+  const bool fused = w.skpart != nullptr && n <= 64 && !(mode != nullptr && std::strcmp(mode, "tile") == 0);
+  soc::SkinnyArgs sk{};
+  sk.part = w.skpart;
+  sk.eps = c.rms_norm_eps;
   if ((e = soc::launch_embed(b.ids, n, m->embed, H, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
   for (int l = 0; l < c.num_hidden_layers; ++l) {
     const DevLayer& L = m->layers[l];
-    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
-      return hip_fail(e, "rmsnorm");
+    if (fused) {
+      soc::SkinnyArgs a = sk;
+      a.x = w.x;
+      a.ldx = H;
+      a.w = L.wqkv;
+      a.N0 = a.Ntot = m->qkv_rows;
+      a.K = H;
+      a.gain = L.in_norm;
+      a.q_out = w.q;
+      a.kcache = kv->k;
+      a.vcache = kv->v;
+      a.q_gain = L.q_norm;
+      a.k_gain = L.k_norm;
+      a.rope_cos = m->rope_cos;
+      a.rope_sin = m->rope_sin;
+      a.pos = b.pos;
+      a.slots = b.slots;
+      a.slot_stride = kv->slot_stride;
+      a.layer_stride = kv->layer_stride;
+      a.layer = l;
+      a.cap = kv->cap;
+      a.nq = c.num_attention_heads;
+      a.nkv = c.num_key_value_heads;
+      if ((e = batch_skinny(a, n, soc::EPI_QKV, s)) != hipSuccess) return hip_fail(e, "skinny qkv");
+    } else {
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) !=
+          hipSuccess)
+        return hip_fail(e, "rmsnorm");
+      soc::GemmArgs g{};
+      g.a = w.xn;
+      g.lda = H;
+      g.w = L.wqkv;
+      g.c = w.qkv;
+      g.ldc = m->qkv_rows;
+      g.M = n;
+      g.N = m->qkv_rows;
+      g.K = H;
+      if ((e = prefill_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+      soc::QkNormRopeArgs q{};
+      q.qkv = w.qkv;
+      q.ld_qkv = m->qkv_rows;
+      q.q_gain = L.q_norm;
+      q.k_gain = L.k_norm;
+      q.eps = c.rms_norm_eps;
+      q.rope_cos = m->rope_cos;
+      q.rope_sin = m->rope_sin;
+      q.q_out = w.q;
+      q.kcache = kv->k;
+      q.vcache = kv->v;
+      q.slot_stride = kv->slot_stride;
+      q.layer_stride = kv->layer_stride;
+      q.layer = l;
+      q.cap = kv->cap;
+      q.T = n;
+      q.nq = c.num_attention_heads;
+      q.nkv = c.num_key_value_heads;
+      q.pos = b.pos;
+      q.slots = b.slots;
+      if ((e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
+    }
+    soc::AttnArgs at = attn_args(m, kv, l);
+    at.qkv = w.q;
+    at.ld_qkv = m->qd;
+    at.pos = b.pos;
+    at.slot = b.slots;
+    at.out = w.attn;
+    at.ld_out = m->qd;
+    at.part = w.part;
+    at.counters = w.attn_counters;
+    at.B = n;
+    at.max_split = max_split;
+    if ((e = soc::launch_attention(at, 0, s)) != hipSuccess) return hip_fail(e, "attention");
+    if (fused) {
+      soc::SkinnyArgs a = sk;  // o: x += attn . Wo^T
+      a.x = w.attn;
+      a.ldx = m->qd;
+      a.w = L.wo;
+      a.N0 = a.Ntot = H;
+      a.K = m->qd;
+      a.c = w.x;
+      a.ldc = H;
+      if ((e = batch_skinny(a, n, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "skinny o");
+      a = sk;  // gate/up of RMSNorm(x) + SwiGLU
+      a.x = w.x;
+      a.ldx = H;
+      a.w = L.wgate;
+      a.w2 = L.wup;
+      a.N0 = I;
+      a.Ntot = 2 * I;
+      a.K = H;
+      a.gain = L.post_norm;
+      a.c = w.h;
+      a.ldc = I;
+      if ((e = batch_skinny(a, n, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "skinny gate/up");
+      a = sk;  // down: x += h . Wd^T
+      a.x = w.h;
+      a.ldx = I;
+      a.w = L.wdown;
+      a.N0 = a.Ntot = H;
+      a.K = I;
+      a.c = w.x;
+      a.ldc = H;
+      if ((e = batch_skinny(a, n, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "skinny down");
+      continue;
+    }
     soc::GemmArgs g{};
-    g.a = w.xn;
-    g.lda = H;
-    g.w = L.wqkv;
-    g.c = w.qkv;
-    g.ldc = m->qkv_rows;
-    g.M = n;
-    g.N = m->qkv_rows;
-    g.K = H;
-    if ((e = batch_gemm(g, soc::EPI_STORE, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
-    soc::QkNormRopeArgs q{};
-    q.qkv = w.qkv;
-    q.ld_qkv = m->qkv_rows;
-    q.q_gain = L.q_norm;
-    q.k_gain = L.k_norm;
-    q.eps = c.rms_norm_eps;
-    q.rope_cos = m->rope_cos;
-    q.rope_sin = m->rope_sin;
-    q.q_out = w.q;
-    q.kcache = kv->k;
-    q.vcache = kv->v;
-    q.slot_stride = kv->slot_stride;
-    q.layer_stride = kv->layer_stride;
-    q.layer = l;
-    q.cap = kv->cap;
-    q.T = n;
-    q.nq = c.num_attention_heads;
-    q.nkv = c.num_key_value_heads;
-    q.pos = b.pos;
-    q.slots = b.slots;
-    if ((e = soc::launch_qk_norm_rope_append(q, s)) != hipSuccess) return hip_fail(e, "qk norm rope");
-    soc::AttnArgs a = attn_args(m, kv, l);
-    a.qkv = w.q;
-    a.ld_qkv = m->qd;
-    a.pos = b.pos;
-    a.slot = b.slots;
-    a.out = w.attn;
-    a.ld_out = m->qd;
-    a.part = w.part;
-    a.counters = w.attn_counters;
-    a.B = n;
-    a.max_split = max_split;
-    if ((e = soc::launch_attention(a, 0, s)) != hipSuccess) return hip_fail(e, "attention");
-    g = soc::GemmArgs{};
     g.a = w.attn;
     g.lda = m->qd;
     g.w = L.wo;
@@ -936,7 +999,7 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.M = n;
     g.N = H;
     g.K = m->qd;
-    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
     if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
@@ -945,34 +1008,48 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.w = L.wgate;
     g.w2 = L.wup;
     g.c = w.h;
-    g.ldc = c.intermediate_size;
+    g.ldc = I;
     g.M = n;
-    g.N = c.intermediate_size;
+    g.N = I;
     g.K = H;
-    if ((e = batch_gemm(g, soc::EPI_SWIGLU, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    if ((e = prefill_gemm(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
     g = soc::GemmArgs{};
     g.a = w.h;
-    g.lda = c.intermediate_size;
+    g.lda = I;
     g.w = L.wdown;
     g.c = w.x;
     g.ldc = H;
     g.M = n;
     g.N = H;
-    g.K = c.intermediate_size;
-    if ((e = batch_gemm(g, soc::EPI_RESIDUAL, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm down");
+    g.K = I;
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
   }
-  if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
-    return hip_fail(e, "rmsnorm");
-  soc::GemmArgs g{};
-  g.a = w.xn;
-  g.lda = H;
-  g.w = m->lm_head;
-  g.c = w.logits;
-  g.ldc = c.vocab_size;
-  g.M = n;
-  g.N = c.vocab_size;
-  g.K = H;
-  if ((e = batch_gemm(g, soc::EPI_STORE, w.skpart, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+  if (fused) {
+    soc::SkinnyArgs a = sk;  // LM head of RMSNorm(x) with the final gain
+    a.x = w.x;
+    a.ldx = H;
+    a.w = m->lm_head;
+    a.N0 = a.Ntot = c.vocab_size;
+    a.K = H;
+    a.gain = m->final_norm;
+    a.c = w.logits;
+    a.ldc = c.vocab_size;
+    if ((e = batch_skinny(a, n, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "skinny lm head");
+  } else {
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) !=
+        hipSuccess)
+      return hip_fail(e, "rmsnorm");
+    soc::GemmArgs g{};
+    g.a = w.xn;
+    g.lda = H;
+    g.w = m->lm_head;
+    g.c = w.logits;
+    g.ldc = c.vocab_size;
+    g.M = n;
+    g.N = c.vocab_size;
+    g.K = H;
+    if ((e = prefill_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
+  }
   if ((e = soc::launch_argmax_rows(w.logits, c.vocab_size, n, b.ids, b.pos, b.start, ring, ring_stride, s)) !=
       hipSuccess)
     return hip_fail(e, "argmax");

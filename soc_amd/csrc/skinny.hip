@@ -1,5 +1,5 @@
 // skinny.hip - projections of a ragged decode batch: y[M][N] = x[M][K] . W[N][K]^T with M <= 16 rows of fp32
-// activations (one per sequence) and fp16 weights, on MFMA (v_mfma_f32_16x16x32_f16).
+// activations (one per sequence) and fp16 weights, on MFMA (v_mfma_f32_16x16x32_f16), one launch per projection.
 //
 // At M <= 16 the work is a weight stream (2 bytes per weight, 2M flops), so the kernel is built around moving W at
 // HBM rate: every weight is read once, straight into registers, 16 rows x 256 K per wave per chunk with the next
@@ -7,10 +7,13 @@
 // once into hi = f16(x) and lo = f16((x - hi) 2^11) in LDS (about 22 bits of each fp32 value; weights are exact), so
 // the products track the fp32 reference (Mac/cpu/src/linear.cpp:51-84) up to the order of the sums.
 //
-// The grid is (row tiles of 128, K splits): the split count is chosen so that the grid covers the chip even for the
+// The grid is (row tiles, K splits): the split count is chosen so that the grid covers the chip even for the
 // 2560-row projections. Each block writes its partial sums; a second kernel adds the splits in a fixed order (so a
-// row's result never depends on the other rows of the batch or on timing) and applies the epilogue: store,
-// residual add, or SwiGLU of the gate/up halves.
+// row's result never depends on the other rows of the batch or on timing) and applies the epilogue: store, residual
+// add, SwiGLU of the gate/up halves, or the attention input (per-head q/k RMSNorm, RoPE, KV-cache append). An input
+// RMSNorm (rms_norm_module.cpp:56-64) is folded in: the gain multiplies x before the products, the split blocks of
+// row tile 0 write the sums of squares of their K range, and the epilogue scales the finished sums by 1 / rms; so no
+// separate normalisation or q/k kernel runs.
 #include "kernels.h"
 
 #include <cmath>
@@ -25,10 +28,11 @@ typedef _Float16 sk_h8 __attribute__((ext_vector_type(8)));
 }  // namespace
 
 // Split count for a stacked matrix of `rows` rows and depth K (K % 256 == 0): the divisor d of K / 256 (at most
-// SK_MAX_KB of K per block) with the least estimated traffic time: weight bytes over the evenness with which the
-// d * tiles blocks fill the chip's block slots (blocks / slots over its ceiling; 2 blocks per CU when the block's LDS
-// allows, the kernel's registers allow 2) plus the partial sums written and read back (16 rows x 4 bytes x rows x d,
-// twice).
+// SK_MAX_KB of K per block, and at least 512 where K allows: a wave then streams two or more chunks with the next in
+// flight; measured 2 % faster per ragged step at Qwen3-4B than one-chunk splits) with the least estimated traffic
+// time: weight bytes over the evenness with which the d * tiles blocks fill the chip's block slots (blocks / slots
+// over its ceiling; 2 blocks per CU when the block's LDS allows, the kernel's registers allow 2) plus the partial sums
+// written and read back (16 rows x 4 bytes x rows x d, twice).
 int skinny_splits(int rows, int K) {
   const int n256 = K / SK_CHUNK;
   const int tiles = (rows + SK_ROWS - 1) / SK_ROWS;
@@ -36,7 +40,7 @@ int skinny_splits(int rows, int K) {
   double best_cost = 0.0;
   for (int d = 1; d <= n256; ++d) {
     const int kb = K / d;
-    if (n256 % d != 0 || kb > SK_MAX_KB) continue;
+    if (n256 % d != 0 || kb > SK_MAX_KB || (kb < 2 * SK_CHUNK && K >= 2 * SK_CHUNK)) continue;
     const size_t lds = static_cast<size_t>(2) * 16 * (kb + 8) * sizeof(_Float16);
     const int slots = 256 * (2 * lds <= 160 * 1024 ? 2 : 1);
     const double waves = static_cast<double>(tiles) * d / slots;
@@ -52,20 +56,39 @@ int skinny_splits(int rows, int K) {
 
 bool skinny_supported(int M, int K) { return M >= 1 && M <= 16 && K % SK_CHUNK == 0 && K >= SK_CHUNK; }
 
-// grid = (ceil(Ntot / 128), KS), block = 512, dynamic LDS 2 x 16 x (Kb + 8) halves.
+// Rows per tile: 128 (8 waves x 16); SwiGLU tiles hold 64 gate rows (waves 0-3) and the matching 64 up rows
+// (waves 4-7).
+__host__ __device__ inline int skinny_tiles(int epi, int N0, int Ntot) {
+  return epi == EPI_SWIGLU ? (N0 + 63) / 64 : (Ntot + SK_ROWS - 1) / SK_ROWS;
+}
+
+// Scratch: the sums of squares [split][16 rows] (64 words reserved per split), then the partials [split][row][Ntot].
+__host__ __device__ inline float* sk_part(float* base, int KS) { return base + 64 * KS; }
+
+// grid = (tiles, KS), block = 512, dynamic LDS 2 x 16 x (Kb + 8) halves.
+template <int EPI>
 __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
   extern __shared__ _Float16 sk_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int ks = blockIdx.y;
+  const int tile = blockIdx.x, ks = blockIdx.y;
   const int k0 = ks * a.Kb;
   const int ld = a.Kb + 8;
+  const bool norm = a.gain != nullptr;
   _Float16* xh = sk_lds;
   _Float16* xl = sk_lds + 16 * ld;
-  const int r0 = blockIdx.x * SK_ROWS + wid * 16;
-  const bool active = r0 < a.Ntot;
+  // the wave's 16 weight rows (index in the stacked [w | w2] rows) and the limit of its half
+  int r0, lim;
+  if constexpr (EPI == EPI_SWIGLU) {
+    r0 = (wid < 4 ? 0 : a.N0) + tile * 64 + (wid & 3) * 16;
+    lim = wid < 4 ? a.N0 : a.Ntot;
+  } else {
+    r0 = tile * SK_ROWS + wid * 16;
+    lim = a.Ntot;
+  }
+  const bool active = r0 < lim;
   const int rl = lane & 15, kq = lane >> 4;
-  // A operand = W rows r0..r0+15 (lane: row r0 + rl, k = 8 kq + i); rows past Ntot repeat the last row, never stored
-  const int rr = min(r0 + rl, a.Ntot - 1);
+  // A operand = W rows r0..r0+15 (lane: row r0 + rl, k = 8 kq + i); rows past the limit repeat its last row, never stored
+  const int rr = min(r0 + rl, lim - 1);
   const f16* wrow = (rr < a.N0 ? a.w + static_cast<size_t>(rr) * a.K : a.w2 + static_cast<size_t>(rr - a.N0) * a.K) +
                     k0 + kq * 8;
   const int nch = a.Kb / SK_CHUNK;
@@ -77,28 +100,42 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
   // the weight stream does not depend on the activations: start it before staging them
   if (active) load(wa, 0);
 
-  // activations of this K range -> hi/lo fp16 in LDS (rows past M are zero)
-  const int q4 = a.Kb / 4;
-  for (int i = tid; i < 16 * q4; i += 512) {
-    const int m = i / q4, c = (i % q4) * 4;
-    const f32x4 v = m < a.M ? *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(m) * a.ldx + k0 + c)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
-    f16x4 hi, lo;
+  // activations of this K range (times the RMSNorm gain) -> hi/lo fp16 in LDS (rows past M are zero); row m is
+  // staged by the 32 threads 32 m .. 32 m + 31, which also sum its squares (written by the blocks of tile 0)
+  {
+    const int m = tid >> 5, j = tid & 31;
+    float ss = 0.0f;
+    for (int cc = 4 * j; cc < a.Kb; cc += 128) {
+      f32x4 v = m < a.M ? *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(m) * a.ldx + k0 + cc)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (norm) {
+        const f16x4 g = *reinterpret_cast<const f16x4*>(a.gain + k0 + cc);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const _Float16 h = static_cast<_Float16>(v[j]);
-      hi[j] = h;
-      lo[j] = static_cast<_Float16>((v[j] - static_cast<float>(h)) * 2048.0f);
+        for (int e = 0; e < 4; ++e) {
+          ss = fmaf(v[e], v[e], ss);
+          v[e] *= static_cast<float>(g[e]);
+        }
+      }
+      f16x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 h = static_cast<_Float16>(v[e]);
+        hi[e] = h;
+        lo[e] = static_cast<_Float16>((v[e] - static_cast<float>(h)) * 2048.0f);
+      }
+      *reinterpret_cast<f16x4*>(&xh[m * ld + cc]) = hi;
+      *reinterpret_cast<f16x4*>(&xl[m * ld + cc]) = lo;
     }
-    *reinterpret_cast<f16x4*>(&xh[m * ld + c]) = hi;
-    *reinterpret_cast<f16x4*>(&xl[m * ld + c]) = lo;
+    if (norm) {
+      ss = group_sum<32>(ss);
+      if (tile == 0 && j == 0) a.part[64 * ks + m] = ss;
+    }
   }
   __syncthreads();
 
   if (!active) return;  // no barrier follows
   const _Float16* bh = xh + rl * ld + kq * 8;  // B operand = x^T (lane: token rl, k = 8 kq + i)
   const _Float16* bl = xl + rl * ld + kq * 8;
-
   f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accl = {0.f, 0.f, 0.f, 0.f};
   auto mma = [&](const u32x4* src, int c) {
 #pragma unroll
@@ -119,18 +156,13 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
       mma(wb, c + 1);
     }
   }
-  // D: lane holds rows r0 + 4 kq + i (i = 0..3) of token rl
+  // D: lane holds rows row .. row + 3 of token rl (Ntot % 4 == 0 and 16-row alignment: all four or none valid)
   const int row = r0 + 4 * kq;
-  if (row < a.Ntot) {
+  if (row < lim) {
     f32x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = acc[i] + accl[i] * (1.0f / 2048.0f);
-    float* dst = a.part + (static_cast<size_t>(ks) * 16 + rl) * a.Ntot + row;
-    if (row + 3 < a.Ntot) {
-      *reinterpret_cast<f32x4*>(dst) = v;
-    } else {
-      for (int i = 0; row + i < a.Ntot; ++i) dst[i] = v[i];
-    }
+    *reinterpret_cast<f32x4*>(sk_part(a.part, a.KS) + (static_cast<size_t>(ks) * 16 + rl) * a.Ntot + row) = v;
   }
 }
 
@@ -149,17 +181,25 @@ __device__ __forceinline__ float sum_splits(const float* p, size_t stride, int n
   return v;
 }
 
-// One thread per (row m, output n): sum of the KS partials in split order, then the epilogue.
+// 1 / rms of input row m from the splits' sums of squares, in split order (1 without an input RMSNorm).
+__device__ __forceinline__ float sk_rscale(const SkinnyArgs& a, int m) {
+  if (a.gain == nullptr) return 1.0f;
+  const float ss = sum_splits(a.part + m, 64, a.KS);
+  return 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
+}
+
+// Store / residual / SwiGLU: one thread per (row m, output n): the KS partials in split order, then the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
   const int n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
   if (n >= nout) return;
-  const float* p = a.part + static_cast<size_t>(m) * a.Ntot + n;
+  const float s = sk_rscale(a, m);
+  const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + n;
   const size_t split_stride = static_cast<size_t>(16) * a.Ntot;
-  const float v = sum_splits(p, split_stride, a.KS);
+  const float v = s * sum_splits(p, split_stride, a.KS);
   float* dst = a.c + static_cast<size_t>(m) * a.ldc + n;
   if constexpr (EPI == EPI_SWIGLU) {
-    const float u = sum_splits(p + a.N0, split_stride, a.KS);
+    const float u = s * sum_splits(p + a.N0, split_stride, a.KS);
     *dst = silu_ref(v) * u;
   } else if constexpr (EPI == EPI_RESIDUAL) {
     *dst += v;
@@ -168,40 +208,89 @@ __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
   }
 }
 
+// The attention input: one wave per (row m, head h): the head's 128 sums (lane: dims lane, lane + 64), scaled by the
+// input 1 / rms; q and k heads get their RMSNorm and RoPE at pos[m] (qwen_attention.cpp:168-171; rope.cpp:81-84);
+// q -> q_out, k and v -> the fp16 cache of slots[m] at pos[m].
+__global__ __launch_bounds__(64) void k_skinny_epi_qkv(SkinnyArgs a) {
+  const int m = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const float s = sk_rscale(a, m);
+  const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + h * 128;
+  const size_t split_stride = static_cast<size_t>(16) * a.Ntot;
+  float x0 = s * sum_splits(p + lane, split_stride, a.KS);
+  float x1 = s * sum_splits(p + lane + 64, split_stride, a.KS);
+  const int pos = a.pos[m], slot = a.slots[m];
+  const float* cr = a.rope_cos + static_cast<size_t>(pos) * 64;
+  const float* sr = a.rope_sin + static_cast<size_t>(pos) * 64;
+  if (h < a.nq) {
+    norm_rope_pair(x0, x1, a.q_gain, a.eps, cr, sr, lane);
+    float* dst = a.q_out + static_cast<size_t>(m) * a.nq * 128 + h * 128;
+    dst[lane] = x0;
+    dst[lane + 64] = x1;
+  } else {
+    const bool is_k = h < a.nq + a.nkv;
+    const int g = is_k ? h - a.nq : h - a.nq - a.nkv;
+    if (is_k) norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
+    f16* cache = (is_k ? a.kcache : a.vcache) + static_cast<size_t>(slot) * a.slot_stride +
+                 static_cast<size_t>(a.layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * 128 +
+                 static_cast<size_t>(pos) * 128;
+    cache[lane] = static_cast<f16>(x0);
+    cache[lane + 64] = static_cast<f16>(x1);
+  }
+}
+
 hipError_t launch_skinny(const SkinnyArgs& in, int epi, hipStream_t s) {
   SkinnyArgs a = in;
   if (!skinny_supported(a.M, a.K) || a.Ntot <= 0 || a.N0 <= 0 || a.N0 > a.Ntot) return hipErrorInvalidValue;
-  if (epi == EPI_SWIGLU && (a.w2 == nullptr || a.Ntot != 2 * a.N0)) return hipErrorInvalidValue;
+  if (epi == EPI_SWIGLU && (a.w2 == nullptr || a.Ntot != 2 * a.N0 || a.N0 % 64 != 0)) return hipErrorInvalidValue;
   if (epi != EPI_SWIGLU && a.Ntot != a.N0) return hipErrorInvalidValue;
+  if (epi == EPI_QKV && (a.Ntot != (a.nq + 2 * a.nkv) * 128 || a.pos == nullptr || a.slots == nullptr))
+    return hipErrorInvalidValue;
   if (a.ldx % 4 != 0 || a.Ntot % 4 != 0) return hipErrorInvalidValue;
   static const hipError_t configured = skinny_configure();  // allow > 64 KB of dynamic LDS, once per process
   if (configured != hipSuccess) return configured;
   a.KS = skinny_splits(a.Ntot, a.K);
   a.Kb = a.K / a.KS;
   const size_t lds = static_cast<size_t>(2) * 16 * (a.Kb + 8) * sizeof(_Float16);
-  const dim3 grid((a.Ntot + SK_ROWS - 1) / SK_ROWS, a.KS);
-  hipLaunchKernelGGL(k_skinny_part, grid, dim3(512), lds, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const dim3 grid(skinny_tiles(epi, a.N0, a.Ntot), a.KS);
   const int nout = epi == EPI_SWIGLU ? a.N0 : a.Ntot;
   const dim3 g2((nout + 255) / 256, a.M);
   switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL(k_skinny_epi<EPI_STORE>, g2, dim3(256), 0, s, a, nout); break;
-    case EPI_RESIDUAL: hipLaunchKernelGGL(k_skinny_epi<EPI_RESIDUAL>, g2, dim3(256), 0, s, a, nout); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL(k_skinny_epi<EPI_SWIGLU>, g2, dim3(256), 0, s, a, nout); break;
-    default: return hipErrorInvalidValue;
+    case EPI_STORE:
+      hipLaunchKernelGGL(k_skinny_part<EPI_STORE>, grid, dim3(512), lds, s, a);
+      hipLaunchKernelGGL(k_skinny_epi<EPI_STORE>, g2, dim3(256), 0, s, a, nout);
+      break;
+    case EPI_RESIDUAL:
+      hipLaunchKernelGGL(k_skinny_part<EPI_RESIDUAL>, grid, dim3(512), lds, s, a);
+      hipLaunchKernelGGL(k_skinny_epi<EPI_RESIDUAL>, g2, dim3(256), 0, s, a, nout);
+      break;
+    case EPI_SWIGLU:
+      hipLaunchKernelGGL(k_skinny_part<EPI_SWIGLU>, grid, dim3(512), lds, s, a);
+      hipLaunchKernelGGL(k_skinny_epi<EPI_SWIGLU>, g2, dim3(256), 0, s, a, nout);
+      break;
+    case EPI_QKV:
+      hipLaunchKernelGGL(k_skinny_part<EPI_QKV>, grid, dim3(512), lds, s, a);
+      hipLaunchKernelGGL(k_skinny_epi_qkv, dim3(a.M, a.nq + 2 * a.nkv), dim3(64), 0, s, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 size_t skinny_part_floats(int rows, int K) {
-  return static_cast<size_t>(skinny_splits(rows, K)) * 16 * rows;
+  const size_t ks = static_cast<size_t>(skinny_splits(rows, K));
+  return 64 * ks + ks * 16 * rows;  // sums of squares, partials
 }
 
 hipError_t skinny_configure() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_skinny_part),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             static_cast<int>(2 * 16 * (SK_MAX_KB + 8) * sizeof(_Float16)));
+  const int lds = static_cast<int>(2 * 16 * (SK_MAX_KB + 8) * sizeof(_Float16));
+  hipError_t e = hipSuccess;
+  for (const void* f : {reinterpret_cast<const void*>(&k_skinny_part<EPI_STORE>),
+                        reinterpret_cast<const void*>(&k_skinny_part<EPI_RESIDUAL>),
+                        reinterpret_cast<const void*>(&k_skinny_part<EPI_SWIGLU>),
+                        reinterpret_cast<const void*>(&k_skinny_part<EPI_QKV>)})
+    if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  return e;
 }
 
 }  // namespace soc
