@@ -94,6 +94,17 @@ int soc_bundle_tensor_f16(const soc_bundle* bundle, const char* name, uint16_t* 
 /* Creates, fills and finalizes a model from a bundle (QwenModelLoader::LoadModelFromFile, qwen_model_loader.cpp:
  * 35-97): every weight of the config's layer count, lm_head.weight only when the embeddings are not tied. */
 int soc_model_load_bundle(soc_ctx* ctx, const char* manifest_path, soc_model** out);
+/* Group-64 weight packer (the reference's only quantizer, QuantizeMatMulRhs8, Mac/cpu/header/matrix_ops.h:42-74,
+ * applied per 64 weights of a row with the scale kept in fp16): for each row of w [n][k] (fp16 bits, k % 64 == 0) and
+ * group of 64, s = fp16(max |w| / Q) with Q = 127 (bits 8) or 7 (bits 4), code = clamp(round(w / s), -Q, Q) (round
+ * half away from zero; an all-zero group, or one whose scale rounds to 0, gets scale 0 and codes 0). codes: int8
+ * [n][k], or int4 [n][k / 2] two per byte with the even k in the low nibble; scales: fp16 [n][k / 64]. Host only. */
+int soc_quantize_group(const uint16_t* w, int64_t n, int64_t k, int32_t bits, void* codes, uint16_t* scales);
+/* Packs every projection of a finalized model (q/k/v, o, gate/up, down) with soc_quantize_group; afterwards prefill
+ * and decode run those projections as group-quantized matmuls (soc_qmm's kernels) on fp16 activation rows, with
+ * the embedding, norms, attention and LM head unchanged. Quantized models decode on the per-operator path (no
+ * one-launch kernels) and do not support the ragged batch. No counterpart in the reference. */
+int soc_model_quantize(soc_model* model, int32_t bits);
 /* Bytes of weights held on the device. */
 int soc_model_weight_bytes(const soc_model* model, int64_t* bytes);
 /* Which decode implementation soc_decode / soc_decode_steps use on this device: 2 = one kernel launch per token with

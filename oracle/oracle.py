@@ -57,6 +57,8 @@ def port_lib() -> C.CDLL:
             "orc_gqa": (C.c_int, [P, P, P, I64, I64, I64, I64, I64, I64, C.c_int, P]),
             "orc_sample": (C.c_int, [P, I64, F32, I64]),
             "orc_sample_topk": (C.c_int, [P, I64, F32, I64, P, P]),
+            "orc_quantize_group": (C.c_int, [P, I64, I64, C.c_int, P, P]),
+            "orc_model_set_f32": (C.c_int, [P, C.c_char_p, P, I64]),
             "orc_mlp_f16": (None, [P, I64, I64, I64, P, P, P, P]),
             "orc_model_create": (P, [I64, I64, I64, I64, I64, I64, I64, F64, F32, C.c_int]),
             "orc_model_destroy": (None, [P]),
@@ -209,6 +211,18 @@ def sample_topk(row: np.ndarray, temperature: float, top_k: int) -> tuple[int, n
     return tok, ids, vals
 
 
+def quantize_group(w_f16: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """Group-64 quantization of fp16 weight rows [N][K]: (codes int8 [N][K] or packed int4 uint8 [N][K/2],
+    fp16 scale bits [N][K/64])."""
+    w = np.ascontiguousarray(w_f16).view(np.uint16)
+    n, k = w.shape
+    codes = np.zeros((n, k) if bits == 8 else (n, k // 2), np.int8 if bits == 8 else np.uint8)
+    scales = np.zeros((n, k // 64), np.uint16)
+    if port_lib().orc_quantize_group(_ptr(w), n, k, bits, _ptr(codes), _ptr(scales)) != 0:
+        raise ValueError("orc_quantize_group: invalid arguments")
+    return codes, scales
+
+
 def qmm_group(a_f16: np.ndarray, codes: np.ndarray, bits: int, scales_f16: np.ndarray, k: int, n: int,
               group: int = 64) -> np.ndarray:
     a = np.ascontiguousarray(a_f16).view(np.uint16)
@@ -254,8 +268,13 @@ class OracleModel:
     """Qwen3 forward on the CPU. kind="port" (restatement) or "reference" (compiled reference sources)."""
 
     def __init__(self, cfg, weights: dict[str, np.ndarray], kind: str = "port"):
+        """weights: fp16 bits (uint16 / float16) by Hugging Face name; float32 arrays are fp32 projection weights
+        (dequantized group-quantized ones, port only)."""
         self.cfg, self.kind = cfg, kind
-        self._keep = {n: np.ascontiguousarray(w).view(np.uint16) for n, w in weights.items()}
+        self._keep32 = {n: np.ascontiguousarray(w) for n, w in weights.items() if np.asarray(w).dtype == np.float32}
+        self._keep = {n: np.ascontiguousarray(w).view(np.uint16) for n, w in weights.items() if n not in self._keep32}
+        if self._keep32 and kind != "port":
+            raise ValueError("fp32 projection weights are supported by the restatement only")
         args = (cfg.vocab_size, cfg.hidden_size, cfg.num_hidden_layers, cfg.num_attention_heads,
                 cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size, float(cfg.rope_theta),
                 float(cfg.rms_norm_eps), 1 if cfg.tie_word_embeddings else 0)
@@ -267,6 +286,9 @@ class OracleModel:
             for n, a in self._keep.items():
                 if L.orc_model_set(self.h, n.encode(), _ptr(a), a.size) != 0:
                     raise ValueError(f"orc_model_set rejected {n}")
+            for n, a in self._keep32.items():
+                if L.orc_model_set_f32(self.h, n.encode(), _ptr(a), a.size) != 0:
+                    raise ValueError(f"orc_model_set_f32 rejected {n}")
             if L.orc_model_check(self.h) != 0:
                 raise ValueError("oracle model is missing tensors")
         elif kind == "reference":

@@ -111,6 +111,7 @@ void orc_linear_f32(const float* x, int64_t rows, int64_t in_dim, const float* w
   for (int64_t r = 0; r < rows; ++r) {
     const float* xr = x + r * in_dim;
     float* yr = y + r * out_dim;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t o = 0; o < out_dim; ++o) {
       const float* wr = w + o * in_dim;
       float value = 0.0f;
@@ -251,6 +252,45 @@ int orc_sample_topk(const float* row, int64_t vocab, float temperature, int64_t 
   return static_cast<int>(cand[0]);
 }
 
+// Group quantizer (the int8 per-column rule of Mac/cpu/header/matrix_ops.h:42-74 applied per group of 64 along K
+// of each weight row, with the scale stored in fp16): amax = max |w| over the group; a zero group keeps scale 0 and
+// codes 0; else s = fp16(amax / Q) (Q = 127 for 8 bits, 7 for 4 bits; a scale that rounds to 0 is stored as a zero
+// group), code = clamp(round_half_away(w * (1 / s)), -Q, Q). Codes [N][K] int8, or int4 two per byte with the even k
+// in the low nibble; scales [N][K/64] fp16.
+int orc_quantize_group(const uint16_t* w, int64_t N, int64_t K, int bits, void* codes, uint16_t* scales) {
+  if (!w || !codes || !scales || N <= 0 || K <= 0 || K % 64 != 0 || (bits != 8 && bits != 4)) return -1;
+  const int Q = bits == 8 ? 127 : 7;
+  const int64_t G = K / 64;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t g = 0; g < G; ++g) {
+      const uint16_t* src = w + n * K + g * 64;
+      float amax = 0.0f;
+      for (int i = 0; i < 64; ++i) amax = std::max(amax, std::fabs(F16(src[i])));
+      uint16_t s16 = 0;
+      float s = 0.0f;
+      if (amax != 0.0f) {
+        s16 = orc_f32_to_f16(amax / static_cast<float>(Q));
+        s = F16(s16);
+        if (s == 0.0f) s16 = 0;
+      }
+      scales[n * G + g] = s16;
+      const float inv = s != 0.0f ? 1.0f / s : 0.0f;
+      for (int i = 0; i < 64; ++i) {
+        int q = 0;
+        if (s != 0.0f) q = std::clamp(static_cast<int>(std::round(F16(src[i]) * inv)), -Q, Q);
+        const int64_t k = g * 64 + i;
+        if (bits == 8) {
+          static_cast<int8_t*>(codes)[n * K + k] = static_cast<int8_t>(q);
+        } else {
+          uint8_t& byte = static_cast<uint8_t*>(codes)[(n * K + k) / 2];
+          const uint8_t nib = static_cast<uint8_t>(q & 0xF);
+          byte = (k % 2 == 0) ? static_cast<uint8_t>((byte & 0xF0) | nib) : static_cast<uint8_t>((byte & 0x0F) | (nib << 4));
+        }
+      }
+    }
+  return 0;
+}
+
 // Mac/cpu/src/qwen_mlp.cpp:65-74 with ApplySiLU (:20-35) and HadamardProduct (:37-54).
 void orc_mlp_f16(const float* x, int64_t rows, int64_t hidden, int64_t inter, const uint16_t* gate,
                  const uint16_t* up, const uint16_t* down, float* y) {
@@ -282,6 +322,14 @@ struct orc_layer {
   const uint16_t* gate = nullptr;
   const uint16_t* up = nullptr;
   const uint16_t* down = nullptr;
+  // fp32 projections (dequantized group-quantized weights), used instead of the fp16 ones when set
+  const float* qf = nullptr;
+  const float* kf = nullptr;
+  const float* vf = nullptr;
+  const float* of = nullptr;
+  const float* gatef = nullptr;
+  const float* upf = nullptr;
+  const float* downf = nullptr;
 };
 
 struct orc_model {
@@ -368,12 +416,37 @@ int orc_model_set(orc_model* m, const char* name_c, const uint16_t* data, int64_
   return -3;
 }
 
+// fp32 weights for a layer's projections (the reference Linear reads Float32 tensors as they are,
+// Mac/cpu/src/dtype.cpp:165-176): for models whose projections were group-quantized and dequantized.
+int orc_model_set_f32(orc_model* m, const char* name_c, const float* data, int64_t numel) {
+  if (!m || !name_c || !data) return -1;
+  const std::string name(name_c);
+  const int64_t qd = m->nq * m->d, kvd = m->nkv * m->d;
+  auto expect = [&](int64_t n) { return numel == n ? 0 : -2; };
+  const std::string prefix = "model.layers.";
+  if (name.compare(0, prefix.size(), prefix) != 0) return -3;
+  size_t dot = name.find('.', prefix.size());
+  if (dot == std::string::npos) return -3;
+  const int64_t li = std::stoll(name.substr(prefix.size(), dot - prefix.size()));
+  if (li < 0 || li >= m->L) return -3;
+  const std::string suffix = name.substr(dot + 1);
+  orc_layer& l = m->layers[static_cast<size_t>(li)];
+  if (suffix == "self_attn.q_proj.weight") { l.qf = data; return expect(qd * m->H); }
+  if (suffix == "self_attn.k_proj.weight") { l.kf = data; return expect(kvd * m->H); }
+  if (suffix == "self_attn.v_proj.weight") { l.vf = data; return expect(kvd * m->H); }
+  if (suffix == "self_attn.o_proj.weight") { l.of = data; return expect(m->H * qd); }
+  if (suffix == "mlp.gate_proj.weight") { l.gatef = data; return expect(m->I * m->H); }
+  if (suffix == "mlp.up_proj.weight") { l.upf = data; return expect(m->I * m->H); }
+  if (suffix == "mlp.down_proj.weight") { l.downf = data; return expect(m->H * m->I); }
+  return -3;
+}
+
 int orc_model_check(const orc_model* m) {
   if (!m || !m->embed || !m->final_norm) return -1;
   if (!m->tied && !m->lm_head) return -1;
   for (const orc_layer& l : m->layers) {
-    if (!l.input_norm || !l.q || !l.k || !l.v || !l.o || !l.q_norm || !l.k_norm || !l.post_norm || !l.gate ||
-        !l.up || !l.down)
+    if (!l.input_norm || !(l.q || l.qf) || !(l.k || l.kf) || !(l.v || l.vf) || !(l.o || l.of) || !l.q_norm ||
+        !l.k_norm || !l.post_norm || !(l.gate || l.gatef) || !(l.up || l.upf) || !(l.down || l.downf))
       return -1;
   }
   return 0;
@@ -413,15 +486,22 @@ int orc_cache_write(orc_cache* c, int64_t layer, int64_t pos, const float* key, 
 
 namespace {
 
+// A projection with fp16 weights, or fp32 ones when the layer has them.
+void lin(const float* x, int64_t rows, int64_t in_dim, const uint16_t* w16, const float* w32, int64_t out_dim,
+         float* y) {
+  if (w32 != nullptr) orc_linear_f32(x, rows, in_dim, w32, out_dim, y);
+  else orc_linear_f16(x, rows, in_dim, w16, out_dim, y);
+}
+
 // Mac/cpu/src/qwen_attention.cpp:103-140 (uncached) and :142-205 (cached). Returns o_proj output [T][H].
 void attention_forward(const orc_model* m, int64_t li, const float* xn, int64_t T, int64_t pos, orc_cache* cache,
                        float* out) {
   const orc_layer& l = m->layers[static_cast<size_t>(li)];
   const int64_t qd = m->nq * m->d, kvd = m->nkv * m->d;
   std::vector<float> q(static_cast<size_t>(T * qd)), k(static_cast<size_t>(T * kvd)), v(static_cast<size_t>(T * kvd));
-  orc_linear_f16(xn, T, m->H, l.q, qd, q.data());
-  orc_linear_f16(xn, T, m->H, l.k, kvd, k.data());
-  orc_linear_f16(xn, T, m->H, l.v, kvd, v.data());
+  lin(xn, T, m->H, l.q, l.qf, qd, q.data());
+  lin(xn, T, m->H, l.k, l.kf, kvd, k.data());
+  lin(xn, T, m->H, l.v, l.vf, kvd, v.data());
   // q_norm / k_norm over each head's d features (qwen_attention.cpp:168-169), then RoPE (:170-171).
   std::vector<float> qn(q.size()), kn(k.size());
   orc_rmsnorm_f16(q.data(), T * m->nq, m->d, l.q_norm, m->eps, qn.data());
@@ -452,7 +532,7 @@ void attention_forward(const orc_model* m, int64_t li, const float* xn, int64_t 
         }
     orc_gqa(qn.data(), ck.data(), cv.data(), T, S, m->nq, m->nkv, m->d, pos, 1, attn.data());
   }
-  orc_linear_f16(attn.data(), T, qd, l.o, m->H, out);
+  lin(attn.data(), T, qd, l.o, l.of, m->H, out);
 }
 
 // Mac/cpu/src/qwen_block.cpp:63-73 (cached) / :51-61 (uncached): pre-norm residual block.
@@ -464,7 +544,18 @@ void block_forward(const orc_model* m, int64_t li, std::vector<float>& x, int64_
   attention_forward(m, li, xn.data(), T, pos, cache, a.data());
   for (size_t i = 0; i < n; ++i) r[i] = x[i] + a[i];  // AddTensors (qwen_block.cpp:19-34)
   orc_rmsnorm_f16(r.data(), T, m->H, l.post_norm, m->eps, xn.data());
-  orc_mlp_f16(xn.data(), T, m->H, m->I, l.gate, l.up, l.down, mo.data());
+  if (l.gatef == nullptr && l.upf == nullptr && l.downf == nullptr) {
+    orc_mlp_f16(xn.data(), T, m->H, m->I, l.gate, l.up, l.down, mo.data());
+  } else {  // the same steps (qwen_mlp.cpp:65-74) with fp32 projections
+    std::vector<float> g(static_cast<size_t>(T * m->I)), u(g.size());
+    lin(xn.data(), T, m->H, l.gate, l.gatef, m->I, g.data());
+    lin(xn.data(), T, m->H, l.up, l.upf, m->I, u.data());
+    for (size_t i = 0; i < g.size(); ++i) {
+      const float value = g[i];
+      g[i] = value / (1.0f + std::exp(-value)) * u[i];
+    }
+    lin(g.data(), T, m->I, l.down, l.downf, m->H, mo.data());
+  }
   for (size_t i = 0; i < n; ++i) x[i] = r[i] + mo[i];
 }
 

@@ -18,6 +18,9 @@
  *   orc_sample_topk : the first id equals orc_sample (pinned above); the ids' values are the k largest of
  *       logit / temperature in non-increasing order; the order among equal values is std::partial_sort's, the very
  *       call the reference makes (Mac/gpu/src/runtime/sampler.cpp:50-55).
+ *   orc_quantize_group : matrix_ops.h:42-74 per group of 64 with an fp16 scale; pinned where the fp16 scale is exact
+ *       (the int8 codes then equal the reference per-column quantizer's on that group), by the round-trip bound
+ *       |w - code * s| <= s / 2 away from the clamp, and against the library's packer bit for bit.
  *   orc_qmm_group : the group-quantized format is not in the reference; pinned by the closed-form dequant
  *       (exact products), by group size 64 == per-row scale when all scales of a row are equal, and by the int8
  *       per-column reference quantizer (Mac/cpu/header/matrix_ops.h:42-74,308-350) through orc_quant_int8_percol.
@@ -56,6 +59,7 @@ int orc_gqa(const float* q, const float* k, const float* v, int64_t T, int64_t S
 
 /* Mac/cpu/src/sampler.cpp:26-61 on one logits row. Returns the token id (-1 on invalid arguments). */
 int orc_sample(const float* logits_row, int64_t vocab, float temperature, int64_t top_k);
+int orc_quantize_group(const uint16_t* w, int64_t N, int64_t K, int bits, void* codes, uint16_t* scales);
 int orc_sample_topk(const float* logits_row, int64_t vocab, float temperature, int64_t top_k, int32_t* ids,
                     float* vals);
 
@@ -72,6 +76,8 @@ orc_model* orc_model_create(int64_t vocab, int64_t hidden, int64_t layers, int64
 void orc_model_destroy(orc_model* m);
 /* Borrow an fp16 tensor by its Hugging Face name (Mac/cpu/src/qwen_model_loader.cpp:35-93). 0 = ok. */
 int orc_model_set(orc_model* m, const char* name, const uint16_t* data, int64_t numel);
+/* fp32 projection weights (dequantized group-quantized ones) that replace the layer's fp16 projection. */
+int orc_model_set_f32(orc_model* m, const char* name, const float* data, int64_t numel);
 /* 0 when every tensor the config needs is present. */
 int orc_model_check(const orc_model* m);
 

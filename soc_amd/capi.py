@@ -134,6 +134,8 @@ def lib() -> C.CDLL:
         "soc_decode_steps": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_decode_steps_noalloc": (C.c_int, [P, P, I32, I32, I32, P]),
         "soc_sample_topk": (C.c_int, [P, P, I32, I32, C.c_float, P, P, P]),
+        "soc_quantize_group": (C.c_int, [P, I64, I64, I32, P, P]),
+        "soc_model_quantize": (C.c_int, [P, I32]),
         "soc_bundle_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
         "soc_bundle_close": (C.c_int, [P]),
         "soc_bundle_config": (C.c_int, [P, C.POINTER(QwenConfigC)]),
@@ -301,6 +303,11 @@ class Model:
         check(lib().soc_model_finalize(self.h))
         return self
 
+    def quantize(self, bits: int) -> "Model":
+        """Group-64 int8 / int4 projections (soc_model_quantize)."""
+        check(lib().soc_model_quantize(self.h, bits))
+        return self
+
     def weight_bytes(self) -> int:
         v = C.c_int64()
         check(lib().soc_model_weight_bytes(self.h, C.byref(v)))
@@ -431,6 +438,16 @@ def load_bundle(ctx: Context, manifest_path) -> "Model":
     finally:
         b.close()
     return Model.wrap(ctx, cfg, h)
+
+
+def quantize_group(w_f16: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """The library's group-64 packer (soc_quantize_group) on fp16 weight rows [n][k]."""
+    w = np.ascontiguousarray(w_f16).view(np.uint16)
+    n, k = w.shape
+    codes = np.empty((n, k) if bits == 8 else (n, k // 2), np.int8 if bits == 8 else np.uint8)
+    scales = np.empty((n, k // 64), np.uint16)
+    check(lib().soc_quantize_group(_ptr(w), n, k, bits, _ptr(codes), _ptr(scales)))
+    return codes, scales
 
 
 def sample_topk(ctx: Context, row_ptr: int, vocab: int, top_k: int, temperature: float = 1.0):

@@ -117,6 +117,12 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
 hipError_t launch_kv_append_rows(const void* keys, const void* values, bool fp16, int rows, int nkv, int hd, int cap,
                                  int pos, f16* kdst, f16* vdst, hipStream_t s);
 
+// ---- quantized-model forward steps (qpath.hip) ----
+hipError_t launch_f32_to_f16(const float* x, size_t n, f16* y, hipStream_t s);
+hipError_t launch_add_f32(float* x, const float* y, size_t n, hipStream_t s);  // x += y
+// gu [T][2 I] (gate | up) -> h [T][I] = fp16(silu(gate) * up)
+hipError_t launch_swiglu_f16(const float* gu, int T, int I, f16* h, hipStream_t s);
+
 // ---- sampler: top-k candidates of one logits row (sample.hip) ----
 constexpr int kSampleChunk = 2048, kSampleMaxK = 64;
 // Device workspace bytes for a row of V logits.

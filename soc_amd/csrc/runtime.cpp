@@ -88,6 +88,12 @@ struct DevLayer {
   f16 *in_norm, *post_norm, *q_norm, *k_norm, *wqkv, *wo, *wgate, *wup, *wdown;
 };
 
+// Group-quantized copies of a layer's projections (soc_model_quantize): codes and fp16 scales per 64 weights.
+struct QLayer {
+  uint8_t *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;  // gu: gate rows then up rows
+  f16 *qkv_s = nullptr, *o_s = nullptr, *gu_s = nullptr, *down_s = nullptr;
+};
+
 struct TensorSlot {
   f16* ptr;
   int64_t numel;
@@ -111,6 +117,9 @@ struct DecodeWs {
   float* pv = nullptr;
   int *pi = nullptr, *err = nullptr;
   int nblocks = 0;
+  // quantized models: fp16 activation row and fp32 projection output of the per-op decode
+  f16* qx = nullptr;
+  float* qy = nullptr;
   std::vector<void*> allocs;
 };
 
@@ -124,6 +133,9 @@ struct PrefillWs {
   float* skpart = nullptr;  // split-K partials of the skinny batch projections
   // hi/lo fp16 activation pairs of the prefill projections: p = normed input / attention output, q = SwiGLU output
   soc::f16 *ph = nullptr, *pl = nullptr, *qh = nullptr, *ql = nullptr;
+  // quantized models: fp16 activation rows and fp32 projection outputs of one chunk of kQChunk rows
+  soc::f16* qx = nullptr;
+  float* qy = nullptr;
 };
 
 // Per-row state of a ragged decode batch (device arrays of `cap` rows).
@@ -136,6 +148,7 @@ struct BatchWs {
 };
 
 constexpr int kAttnChunk = 256;
+constexpr int kQChunk = 8;  // rows per group-quantized projection call in a quantized model's prefill (k_qmm M <= 8)
 constexpr int kMaxBatchRows = 1024;
 
 }  // namespace
@@ -159,6 +172,9 @@ struct soc_model {
   BatchWs bws;
   bool finalized = false;
   bool xcd_off = false;  // the XCD-partitioned decode step failed its block placement once: not used again
+  int qbits = 0;         // 8 or 4 after soc_model_quantize: the projections run on the group-quantized copies
+  std::vector<QLayer> qlayers;
+  std::vector<void*> qallocs;
 };
 
 struct soc_kv {
@@ -263,6 +279,12 @@ int ensure_decode_ws(soc_model* m, int cap) {
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.state));
   SOC_TRY(dev_alloc_t(w.allocs, cap, &w.ring));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.ring_pos));
+  {
+    const size_t kmax = std::max({c.hidden_size, m->qd, c.intermediate_size});
+    const size_t nmax = std::max({m->qkv_rows, 2 * c.intermediate_size, c.hidden_size});
+    SOC_TRY(dev_alloc_t(w.allocs, kmax, &w.qx));
+    SOC_TRY(dev_alloc_t(w.allocs, nmax, &w.qy));
+  }
   hipError_t e;
   if ((e = hipMemset(w.lm_counter, 0, 64 * sizeof(int))) != hipSuccess) return hip_fail(e, "hipMemset");
   if ((e = hipMemset(w.attn_counters, 0, c.num_key_value_heads * sizeof(int))) != hipSuccess)
@@ -341,6 +363,13 @@ int ensure_prefill_ws(soc_model* m, int rows, int total_len, int logit_rows) {
   SOC_TRY(dev_alloc_t(w.allocs, 1024, &w.lm_idx));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.lm_counter));
   SOC_TRY(dev_alloc_t(w.allocs, 64, &w.token));
+  {
+    const size_t kmax = std::max({c.hidden_size, m->qd, c.intermediate_size});
+    const size_t nmax = std::max({m->qkv_rows, 2 * c.intermediate_size, c.hidden_size});
+    SOC_TRY(dev_alloc_t(w.allocs, kQChunk * kmax, &w.qx));
+    SOC_TRY(dev_alloc_t(w.allocs, kQChunk * nmax, &w.qy));
+    if ((e = hipMemset(w.qx, 0, kQChunk * kmax * sizeof(soc::f16))) != hipSuccess) return hip_fail(e, "hipMemset");
+  }
   if (const size_t sk = skinny_scratch_floats(m)) {
     SOC_TRY(dev_alloc_t(w.allocs, sk, &w.skpart));
     if ((e = soc::skinny_configure()) != hipSuccess) return hip_fail(e, "skinny kernel attributes");
@@ -398,62 +427,130 @@ soc::AttnArgs attn_args(soc_model* m, soc_kv* kv, int layer) {
   return a;
 }
 
+// y[M][N] = x[M][K] . W^T on the model's group-quantized codes (M in 1, 2, 4, 8).
+hipError_t qmm_rows(const soc_model* m, const soc::f16* x, int M, const uint8_t* codes, const soc::f16* scales, int N,
+                    int K, float* y, hipStream_t s) {
+  soc::QmmArgs q{};
+  q.x = x;
+  q.codes = codes;
+  q.scales = scales;
+  q.y = y;
+  q.M = M;
+  q.N = N;
+  q.K = K;
+  return soc::launch_qmm(q, m->qbits, s);
+}
+
+// One layer of a quantized model on T rows x (fp32 [T][H]) whose attention input comes out of `qkv_out` (rows of
+// [T][qkv_rows], M >= T the projection row count): input RMSNorm -> fp16, QKV projection; the caller's attention
+// writes attn (fp32 [T][qd]); then o projection + residual, post RMSNorm -> fp16, gate/up projection, SwiGLU -> fp16,
+// down projection + residual. `attend` enqueues the attention.
+template <typename Attend>
+int enqueue_layer_q(soc_model* m, int l, float* x, int T, int M, soc::f16* qx, float* qy, float* qkv_out,
+                    const float* attn, Attend attend, hipStream_t s) {
+  const soc_qwen_config& c = m->cfg;
+  const DevLayer& L = m->layers[l];
+  const QLayer& Q = m->qlayers[l];
+  const int H = c.hidden_size, I = c.intermediate_size;
+  hipError_t e;
+  if ((e = soc::launch_rmsnorm_rows(x, T, H, L.in_norm, c.rms_norm_eps, nullptr, qx, nullptr, s)) != hipSuccess)
+    return hip_fail(e, "rmsnorm");
+  if ((e = qmm_rows(m, qx, M, Q.qkv, Q.qkv_s, m->qkv_rows, H, qkv_out, s)) != hipSuccess) return hip_fail(e, "qmm qkv");
+  SOC_TRY(attend());
+  if ((e = soc::launch_f32_to_f16(attn, static_cast<size_t>(T) * m->qd, qx, s)) != hipSuccess)
+    return hip_fail(e, "f32 -> f16");
+  if ((e = qmm_rows(m, qx, M, Q.o, Q.o_s, H, m->qd, qy, s)) != hipSuccess) return hip_fail(e, "qmm o");
+  if ((e = soc::launch_add_f32(x, qy, static_cast<size_t>(T) * H, s)) != hipSuccess) return hip_fail(e, "residual");
+  if ((e = soc::launch_rmsnorm_rows(x, T, H, L.post_norm, c.rms_norm_eps, nullptr, qx, nullptr, s)) != hipSuccess)
+    return hip_fail(e, "rmsnorm");
+  if ((e = qmm_rows(m, qx, M, Q.gu, Q.gu_s, 2 * I, H, qy, s)) != hipSuccess) return hip_fail(e, "qmm gate/up");
+  if ((e = soc::launch_swiglu_f16(qy, T, I, qx, s)) != hipSuccess) return hip_fail(e, "swiglu");
+  if ((e = qmm_rows(m, qx, M, Q.down, Q.down_s, H, I, qy, s)) != hipSuccess) return hip_fail(e, "qmm down");
+  if ((e = soc::launch_add_f32(x, qy, static_cast<size_t>(T) * H, s)) != hipSuccess) return hip_fail(e, "residual");
+  return SOC_OK;
+}
+
 // Queues one decode step for `slot` reading {token, pos} from dws.state. Used eagerly and under graph capture.
 int enqueue_decode(soc_model* m, soc_kv* kv, int slot, const int32_t* d_slot) {
   const soc_qwen_config& c = m->cfg;
   DecodeWs& w = m->dws;
   hipStream_t s = m->ctx->stream;
   hipError_t e;
-  if ((e = soc::launch_embed(w.state, 1, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
-  for (int l = 0; l < c.num_hidden_layers; ++l) {
-    const DevLayer& L = m->layers[l];
-    soc::GemvArgs g{};
-    g.x = w.x;
-    g.gain = L.in_norm;
-    g.eps = c.rms_norm_eps;
-    g.w = L.wqkv;
-    g.y = w.qkv;
-    g.N = m->qkv_rows;
-    g.K = c.hidden_size;
-    if ((e = soc::launch_gemv(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemv qkv");
-    soc::AttnArgs a = attn_args(m, kv, l);
-    a.qkv = w.qkv;
-    a.ld_qkv = m->qkv_rows;
-    a.pos = w.state + 1;
-    a.slot = d_slot;
-    a.slot_base = slot;
-    a.pos_base = 0;
-    a.out = w.attn;
-    a.ld_out = m->qd;
-    a.part = w.part;
-    a.counters = w.attn_counters;
-    a.B = 1;
-    a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
-    if ((e = soc::launch_attention(a, 1, s)) != hipSuccess) return hip_fail(e, "attention decode");
-    g = soc::GemvArgs{};
-    g.x = w.attn;
-    g.w = L.wo;
-    g.y = w.x;
-    g.N = c.hidden_size;
-    g.K = m->qd;
-    if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv o");
-    g = soc::GemvArgs{};
-    g.x = w.x;
-    g.gain = L.post_norm;
-    g.eps = c.rms_norm_eps;
-    g.w = L.wgate;
-    g.w2 = L.wup;
-    g.y = w.h;
-    g.N = c.intermediate_size;
-    g.K = c.hidden_size;
-    if ((e = soc::launch_gemv(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemv gate/up");
-    g = soc::GemvArgs{};
-    g.x = w.h;
-    g.w = L.wdown;
-    g.y = w.x;
-    g.N = c.hidden_size;
-    g.K = c.intermediate_size;
-    if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv down");
+  if (m->qbits != 0) {  // quantized model: the same steps with group-quantized projections
+    if ((e = soc::launch_embed(w.state, 1, m->embed, c.hidden_size, w.x, s)) != hipSuccess)
+      return hip_fail(e, "embed");
+    for (int l = 0; l < c.num_hidden_layers; ++l) {
+      auto attend = [&]() -> int {
+        soc::AttnArgs a = attn_args(m, kv, l);
+        a.qkv = w.qkv;
+        a.ld_qkv = m->qkv_rows;
+        a.pos = w.state + 1;
+        a.slot = d_slot;
+        a.slot_base = slot;
+        a.pos_base = 0;
+        a.out = w.attn;
+        a.ld_out = m->qd;
+        a.part = w.part;
+        a.counters = w.attn_counters;
+        a.B = 1;
+        a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+        const hipError_t ea = soc::launch_attention(a, 1, s);
+        return ea == hipSuccess ? SOC_OK : hip_fail(ea, "attention decode");
+      };
+      SOC_TRY(enqueue_layer_q(m, l, w.x, 1, 1, w.qx, w.qy, w.qkv, w.attn, attend, s));
+    }
+  } else {
+    if ((e = soc::launch_embed(w.state, 1, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
+    for (int l = 0; l < c.num_hidden_layers; ++l) {
+      const DevLayer& L = m->layers[l];
+      soc::GemvArgs g{};
+      g.x = w.x;
+      g.gain = L.in_norm;
+      g.eps = c.rms_norm_eps;
+      g.w = L.wqkv;
+      g.y = w.qkv;
+      g.N = m->qkv_rows;
+      g.K = c.hidden_size;
+      if ((e = soc::launch_gemv(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemv qkv");
+      soc::AttnArgs a = attn_args(m, kv, l);
+      a.qkv = w.qkv;
+      a.ld_qkv = m->qkv_rows;
+      a.pos = w.state + 1;
+      a.slot = d_slot;
+      a.slot_base = slot;
+      a.pos_base = 0;
+      a.out = w.attn;
+      a.ld_out = m->qd;
+      a.part = w.part;
+      a.counters = w.attn_counters;
+      a.B = 1;
+      a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+      if ((e = soc::launch_attention(a, 1, s)) != hipSuccess) return hip_fail(e, "attention decode");
+      g = soc::GemvArgs{};
+      g.x = w.attn;
+      g.w = L.wo;
+      g.y = w.x;
+      g.N = c.hidden_size;
+      g.K = m->qd;
+      if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv o");
+      g = soc::GemvArgs{};
+      g.x = w.x;
+      g.gain = L.post_norm;
+      g.eps = c.rms_norm_eps;
+      g.w = L.wgate;
+      g.w2 = L.wup;
+      g.y = w.h;
+      g.N = c.intermediate_size;
+      g.K = c.hidden_size;
+      if ((e = soc::launch_gemv(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemv gate/up");
+      g = soc::GemvArgs{};
+      g.x = w.h;
+      g.w = L.wdown;
+      g.y = w.x;
+      g.N = c.hidden_size;
+      g.K = c.intermediate_size;
+      if ((e = soc::launch_gemv(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemv down");
+    }
   }
   soc::LmHeadArgs h{};
   h.x = w.x;
@@ -506,7 +603,7 @@ int get_decode_graph(soc_model* m, soc_kv* kv, int slot, hipGraphExec_t* out) {
 bool use_xcd(soc_model* m) {
   const char* mode = std::getenv("SOC_DECODE");
   if (mode != nullptr && std::strcmp(mode, "xcd") != 0) return false;
-  if (env_flag("SOC_EAGER") || m->xcd_off) return false;
+  if (env_flag("SOC_EAGER") || m->xcd_off || m->qbits != 0) return false;
   const soc_qwen_config& c = m->cfg;
   if (!soc::xcd_supported(c.hidden_size, c.intermediate_size, c.num_attention_heads, c.num_key_value_heads,
                           c.head_dim, m->ctx->num_cus))
@@ -519,7 +616,7 @@ bool use_xcd(soc_model* m) {
 bool use_persistent(soc_model* m) {
   const char* mode = std::getenv("SOC_DECODE");
   if (mode != nullptr && std::strcmp(mode, "persistent") != 0 && std::strcmp(mode, "xcd") != 0) return false;
-  if (env_flag("SOC_EAGER")) return false;
+  if (env_flag("SOC_EAGER") || m->qbits != 0) return false;
   const soc_qwen_config& c = m->cfg;
   const int nb = m->ctx->num_cus;
   if (!soc::persistent_supported(c.hidden_size, m->qd, c.intermediate_size, m->qkv_rows, c.num_attention_heads,
@@ -1286,6 +1383,7 @@ int soc_model_destroy(soc_model* m) {
   (void)hipFree(m->rope_cos);
   (void)hipFree(m->rope_sin);
   (void)hipFree(m->d_layer_w);
+  free_all(m->qallocs);
   delete m;
   return SOC_OK;
 }
@@ -1334,6 +1432,68 @@ int soc_model_finalize(soc_model* m) {
     if (!kv.second.loaded) return soc::fail(SOC_ERR_INVALID, "missing tensor: " + kv.first);
   m->finalized = true;
   return SOC_OK;
+}
+
+int soc_model_quantize(soc_model* m, int32_t bits) {
+  SOC_API_BEGIN
+  if (m == nullptr) return soc::fail(SOC_ERR_INVALID, "null model");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (m->qbits != 0) return soc::fail(SOC_ERR_STATE, "model is already quantized");
+  if (bits != 8 && bits != 4) return soc::fail(SOC_ERR_INVALID, "soc_model_quantize: bits must be 8 or 4");
+  const soc_qwen_config& c = m->cfg;
+  const int H = c.hidden_size, I = c.intermediate_size, qd = m->qd;
+  for (int k : {H, qd, I})
+    if (k % 64 != 0 || static_cast<size_t>(kQChunk) * k * 2 > 160 * 1024)
+      return soc::fail(SOC_ERR_INVALID, "soc_model_quantize: hidden, q and intermediate sizes must be multiples of 64 "
+                                        "and at most 10240");
+  hipError_t e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  std::vector<QLayer> ql(c.num_hidden_layers);
+  std::vector<void*> allocs;
+  auto fail_free = [&](int rc) {
+    free_all(allocs);
+    return rc;
+  };
+  std::vector<uint16_t> wbuf;
+  std::vector<uint8_t> cbuf;
+  std::vector<uint16_t> sbuf;
+  // reads rows [N][K] of fp16 weights from one or two device tensors, quantizes them, uploads codes and scales
+  auto pack = [&](std::initializer_list<std::pair<const f16*, int>> parts, int K, uint8_t** codes, f16** scales) {
+    int N = 0;
+    for (const auto& p : parts) N += p.second;
+    wbuf.resize(static_cast<size_t>(N) * K);
+    size_t off = 0;
+    for (const auto& p : parts) {
+      const hipError_t ee = hipMemcpy(wbuf.data() + off, p.first, static_cast<size_t>(p.second) * K * 2,
+                                      hipMemcpyDeviceToHost);
+      if (ee != hipSuccess) return hip_fail(ee, "hipMemcpy weights");
+      off += static_cast<size_t>(p.second) * K;
+    }
+    const size_t ncode = static_cast<size_t>(N) * K / (bits == 8 ? 1 : 2), nscale = static_cast<size_t>(N) * K / 64;
+    cbuf.resize(ncode);
+    sbuf.resize(nscale);
+    SOC_TRY(soc_quantize_group(wbuf.data(), N, K, bits, cbuf.data(), sbuf.data()));
+    SOC_TRY(dev_alloc_t(allocs, ncode, codes));
+    SOC_TRY(dev_alloc_t(allocs, nscale, scales));
+    hipError_t ee = hipMemcpy(*codes, cbuf.data(), ncode, hipMemcpyHostToDevice);
+    if (ee == hipSuccess) ee = hipMemcpy(*scales, sbuf.data(), nscale * 2, hipMemcpyHostToDevice);
+    return ee == hipSuccess ? SOC_OK : hip_fail(ee, "hipMemcpy codes");
+  };
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const DevLayer& L = m->layers[l];
+    QLayer& q = ql[l];
+    int rc;
+    if ((rc = pack({{L.wqkv, m->qkv_rows}}, H, &q.qkv, &q.qkv_s)) != SOC_OK) return fail_free(rc);
+    if ((rc = pack({{L.wo, H}}, qd, &q.o, &q.o_s)) != SOC_OK) return fail_free(rc);
+    if ((rc = pack({{L.wgate, I}, {L.wup, I}}, H, &q.gu, &q.gu_s)) != SOC_OK) return fail_free(rc);
+    if ((rc = pack({{L.wdown, H}}, I, &q.down, &q.down_s)) != SOC_OK) return fail_free(rc);
+  }
+  m->qlayers = std::move(ql);
+  m->qallocs = std::move(allocs);
+  m->qbits = bits;
+  ++m->dws_gen;  // captured decode graphs hold the fp16 path: capture again
+  return SOC_OK;
+  SOC_API_END
 }
 
 int soc_model_weight_bytes(const soc_model* m, int64_t* bytes) {
@@ -1554,6 +1714,67 @@ int soc_kv_layer_planes(const soc_kv* kv, int32_t slot, int32_t layer, void** ke
   return SOC_OK;
 }
 
+namespace {
+// The layers of a quantized model's prefill over the n embedded rows in m->pws.x, kQChunk rows at a time (each chunk
+// through every layer, so a chunk's attention sees the keys the earlier chunks appended): group-quantized
+// projections, the prefill q/k-norm + RoPE + append kernel and the split-key attention over the slot's cache.
+int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off) {
+  const soc_qwen_config& c = m->cfg;
+  PrefillWs& w = m->pws;
+  hipStream_t s = m->ctx->stream;
+  const int H = c.hidden_size;
+  for (int c0 = 0; c0 < n; c0 += kQChunk) {
+    const int T = std::min(kQChunk, n - c0);
+    const int M = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8;  // the projection's row count (rows past T unused)
+    float* xr = w.x + static_cast<size_t>(c0) * H;
+    float* qrow = w.q + static_cast<size_t>(c0) * m->qd;
+    float* arow = w.attn + static_cast<size_t>(c0) * m->qd;
+    for (int l = 0; l < c.num_hidden_layers; ++l) {
+      auto attend = [&]() -> int {
+        const DevLayer& L = m->layers[l];
+        soc::QkNormRopeArgs q{};
+        q.qkv = w.qy;
+        q.ld_qkv = m->qkv_rows;
+        q.q_gain = L.q_norm;
+        q.k_gain = L.k_norm;
+        q.eps = c.rms_norm_eps;
+        q.rope_cos = m->rope_cos;
+        q.rope_sin = m->rope_sin;
+        q.q_out = qrow;
+        q.kcache = kv->k;
+        q.vcache = kv->v;
+        q.slot_stride = kv->slot_stride;
+        q.layer_stride = kv->layer_stride;
+        q.slot = slot;
+        q.layer = l;
+        q.cap = kv->cap;
+        q.pos_base = pos_off + c0;
+        q.T = T;
+        q.nq = c.num_attention_heads;
+        q.nkv = c.num_key_value_heads;
+        hipError_t e = soc::launch_qk_norm_rope_append(q, s);
+        if (e != hipSuccess) return hip_fail(e, "qk norm rope");
+        soc::AttnArgs a = attn_args(m, kv, l);
+        a.qkv = qrow;
+        a.ld_qkv = m->qd;
+        a.slot_base = slot;
+        a.pos_base = pos_off + c0;
+        a.out = arow;
+        a.ld_out = m->qd;
+        a.part = w.part;
+        a.counters = w.attn_counters;
+        a.B = T;
+        a.max_split = (pos_off + n + kAttnChunk - 1) / kAttnChunk;
+        e = soc::launch_attention(a, 0, s);
+        return e == hipSuccess ? SOC_OK : hip_fail(e, "attention");
+      };
+      SOC_TRY(enqueue_layer_q(m, l, xr, T, M, w.qx, w.qy, w.qy, arow, attend, s));
+    }
+  }
+  return SOC_OK;
+}
+}  // namespace
+
 int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off,
                 int32_t logit_rows, float* logits, int32_t* next_token) {
   SOC_API_BEGIN
@@ -1575,8 +1796,9 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync ids");
   if ((e = soc::launch_embed(w.ids, n, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
   const int H = c.hidden_size;
+  if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off));
   const bool split = prefill_split_path(m);
-  for (int l = 0; l < c.num_hidden_layers; ++l) {
+  for (int l = 0; m->qbits == 0 && l < c.num_hidden_layers; ++l) {  // fp16 models
     const DevLayer& L = m->layers[l];
     soc::GemmArgs g{};
     bool qkv_fused = false;
@@ -1897,6 +2119,8 @@ int soc_decode_steps_noalloc(soc_model* m, soc_kv* kv, int32_t slot, int32_t las
 int soc_decode_batch(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens, float* logits,
                      int32_t* next_tokens) {
   SOC_API_BEGIN
+  if (m != nullptr && m->qbits != 0)
+    return soc::fail(SOC_ERR_INVALID, "ragged batch decode of a group-quantized model is not supported");
   if (next_tokens == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
   int max_len = 0;
   SOC_TRY(validate_batch(m, kv, n, slots, tokens, 1, &max_len));
@@ -1923,6 +2147,8 @@ int soc_decode_batch(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, 
 int soc_decode_batch_steps(soc_model* m, soc_kv* kv, int32_t n, const int32_t* slots, const int32_t* tokens,
                            int32_t steps, int32_t* tokens_out) {
   SOC_API_BEGIN
+  if (m != nullptr && m->qbits != 0)
+    return soc::fail(SOC_ERR_INVALID, "ragged batch decode of a group-quantized model is not supported");
   if (steps < 0) return soc::fail(SOC_ERR_INVALID, "steps must be >= 0");
   if (steps > 0 && tokens_out == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
   int max_len = 0;
