@@ -114,9 +114,15 @@ struct Qwen3Config {  // qwen3_config.h
   void Validate() const;
 };
 
-class StartupValidator {  // startup_validator.cpp:5-23
+struct TokenizerRuntimeData;  // soc/tokenizer.h
+
+class StartupValidator {  // startup_validator.h:8-17
  public:
-  static Qwen3Config ValidateManifest(const ManifestData& manifest);
+  static Qwen3Config ValidateManifest(const ManifestData& manifest);  // startup_validator.cpp:5-23
+  // The tokenizer runtime's format, chat boundary tokens, BPE model and byte table (startup_validator.cpp:25-72),
+  // and its vocabulary against the model config (:74-100). Defined with the tokenizer.
+  static void ValidateTokenizerRuntime(const TokenizerRuntimeData& tokenizer_runtime);
+  static void ValidateManifestAndTokenizer(const ManifestData& manifest, const TokenizerRuntimeData& tokenizer_runtime);
 };
 
 // Tensor files (weight_loader.cpp:17-30): checks byte_size against dtype and shape and the file against byte_size.

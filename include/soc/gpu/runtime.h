@@ -14,6 +14,9 @@
 //   CommandScheduler    -> CommandScheduler      (runtime/command_scheduler.h)
 //   Sampler             -> Sampler               (runtime/sampler.h)
 //   GenerationContext   -> GenerationContext     (runtime/generation_context.h)
+//   RuntimePipeline     -> RuntimePipeline       (Mac/cpu/header/runtime_pipeline.h; the text-level helpers, with
+//                                                  the bundle's model loaded on the device)
+// The tokenizer runtime and chat template are soc::TokenizerRuntime / soc::Qwen3TemplateBuilder (soc/tokenizer.h).
 // MetalContext, MetalBuffer and MetalProfilingSnapshot are also declared under their reference names (aliases at the
 // end of this file), so that reference callers compile unchanged. Every method returns bool (or a null pointer) and
 // fills an optional std::string* error message; nothing throws.
@@ -34,6 +37,7 @@
 #include <vector>
 
 #include "soc/assets.h"
+#include "soc/tokenizer.h"
 #include "soc_hip.h"
 
 namespace soc::gpu {
@@ -394,6 +398,44 @@ class GenerationContext {
   std::vector<int> running_token_ids_;
   std::shared_ptr<HipBuffer> logits_buffer_;  // one logits row: generation samples only the last row
   std::shared_ptr<HipBuffer> token_buffer_;
+};
+
+// ---- text-level helpers (Mac/cpu/header/runtime_pipeline.h:13-43) ----
+struct RuntimeGenerationOptions {  // runtime_pipeline.h:13-18
+  std::size_t max_new_tokens = 32;
+  SamplerConfig sampler;
+  int eos_token_id = -1;
+  std::size_t max_sequence_length = 256;
+};
+
+struct RuntimePromptOptions {  // runtime_pipeline.h:26-31
+  bool apply_chat_template = false;
+  bool add_generation_prompt = true;
+  bool enable_thinking = true;
+  std::string system_prompt;
+};
+
+// A bundle loaded for generation: its manifest, tokenizer runtime and the model on the device (the reference's
+// RuntimeBundle holds the CPU model; runtime_pipeline.h:20-24).
+struct RuntimeBundle {
+  soc::ManifestData manifest;
+  soc::TokenizerRuntimeData tokenizer_runtime;
+  QwenCausalLM model;
+};
+
+class RuntimePipeline {
+ public:
+  // runtime_pipeline.cpp:35-40: manifest, the tokenizer runtime it names, StartupValidator::
+  // ValidateManifestAndTokenizer, then the weights (QwenModelLoader::LoadModel).
+  static bool LoadBundle(const HipContext& context, const std::string& manifest_path, RuntimeBundle* bundle,
+                         std::string* error_message);
+  // runtime_pipeline.cpp:42-54: max_new_tokens, temperature, top_k, eos_token_id (first entry of a list) and
+  // max_length from the manifest's generation_config, defaults otherwise. Throws std::runtime_error on a value of
+  // the wrong JSON type, as the reference does.
+  static RuntimeGenerationOptions GenerationOptionsFromManifest(const soc::ManifestData& manifest);
+  // runtime_pipeline.cpp:56-70: the prompt itself, or one user turn through the Qwen3 chat template.
+  static std::string PreparePrompt(const soc::TokenizerRuntimeData& tokenizer_runtime, const std::string& prompt,
+                                   const RuntimePromptOptions& options = {});
 };
 
 // The reference's names for the platform classes.

@@ -94,6 +94,30 @@ int soc_bundle_tensor_f16(const soc_bundle* bundle, const char* name, uint16_t* 
 /* Creates, fills and finalizes a model from a bundle (QwenModelLoader::LoadModelFromFile, qwen_model_loader.cpp:
  * 35-97): every weight of the config's layer count, lm_head.weight only when the embeddings are not tied. */
 int soc_model_load_bundle(soc_ctx* ctx, const char* manifest_path, soc_model** out);
+/* The bundle's tokenizer runtime (tokenizer/tokenizer_runtime.json; TokenizerRuntimeLoader and TokenizerRuntime,
+ * Mac/cpu/src/runtime_assets.cpp:170-216, tokenizer_runtime.cpp:8-379) and its Qwen3 chat template
+ * (Qwen3TemplateBuilder, runtime_assets.cpp:218-257). Host only. soc_tokenizer_load reads one runtime file;
+ * soc_tokenizer_load_bundle reads a manifest and the runtime file it names and applies
+ * StartupValidator::ValidateManifestAndTokenizer (startup_validator.cpp:74-100). Text is UTF-8 bytes with an explicit
+ * length. Outputs go to caller buffers of `cap` items; the full size is always stored (*n_ids, *len) and a buffer that
+ * is too small fails with SOC_ERR_INVALID without writing, so a caller can ask with cap 0 first. */
+typedef struct soc_tokenizer soc_tokenizer;
+int soc_tokenizer_load(const char* runtime_path, soc_tokenizer** out);
+int soc_tokenizer_load_bundle(const char* manifest_path, soc_tokenizer** out);
+int soc_tokenizer_destroy(soc_tokenizer* tok);
+/* TokenizerRuntime::Encode (tokenizer_runtime.cpp:54-80). At most 2 * len + 1 ids (one per byte, plus a prefix
+ * space per BPE segment). */
+int soc_tokenizer_encode(const soc_tokenizer* tok, const char* text, int64_t len, int32_t* ids, int64_t cap,
+                         int64_t* n_ids);
+/* TokenizerRuntime::Decode (tokenizer_runtime.cpp:82-96). */
+int soc_tokenizer_decode(const soc_tokenizer* tok, const int32_t* ids, int64_t n, char* text, int64_t cap,
+                         int64_t* len);
+/* TokenizerRuntime::TokenToId (tokenizer_runtime.cpp:98-104). */
+int soc_tokenizer_token_to_id(const soc_tokenizer* tok, const char* token, int64_t len, int32_t* id);
+/* Qwen3TemplateBuilder::BuildPrompt over n_messages (role, content) pairs; system_prompt_override may be NULL. */
+int soc_tokenizer_chat_prompt(const soc_tokenizer* tok, const char* const* roles, const char* const* contents,
+                              int32_t n_messages, int add_generation_prompt, int enable_thinking,
+                              const char* system_prompt_override, char* text, int64_t cap, int64_t* len);
 /* Group-64 weight packer (the reference's only quantizer, QuantizeMatMulRhs8, Mac/cpu/header/matrix_ops.h:42-74,
  * applied per 64 weights of a row with the scale kept in fp16): for each row of w [n][k] (fp16 bits, k % 64 == 0) and
  * group of 64, s = fp16(max |w| / Q) with Q = 127 (bits 8) or 7 (bits 4), code = clamp(round(w / s), -Q, Q) (round
@@ -190,7 +214,7 @@ int soc_sample_topk(soc_ctx* ctx, const float* logits_row, int32_t vocab, int32_
                     int32_t* token_id, int32_t* top_ids, float* top_logits);
 
 /* ---- op-level entry points on caller device pointers, queued on the context stream (tests, microbenchmarks).
- *      These replace the reference's op wrappers (Mac/gpu/include/op/*.h, static Run(...)). ---- */
+ *      These replace the reference's op wrappers (the static Run(...) of the headers under Mac/gpu/include/op/). ---- */
 /* y[N] = W[N][K] . x[K]; W fp16, x fp16, y fp32 (LinearOp/MatMulOp decode mode, matmul_op.mm:143-163). */
 int soc_gemv_f16(soc_ctx* ctx, const void* w, const void* x, float* y, int32_t n, int32_t k);
 /* Group-quantized matmul: y[M][N] = x[M][K] . dequant(codes, scales)^T; bits 8 or 4; group 64 along K. */

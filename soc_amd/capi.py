@@ -141,6 +141,13 @@ def lib() -> C.CDLL:
         "soc_bundle_config": (C.c_int, [P, C.POINTER(QwenConfigC)]),
         "soc_bundle_tensor_f16": (C.c_int, [P, C.c_char_p, P, I64]),
         "soc_model_load_bundle": (C.c_int, [P, C.c_char_p, C.POINTER(P)]),
+        "soc_tokenizer_load": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "soc_tokenizer_load_bundle": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "soc_tokenizer_destroy": (C.c_int, [P]),
+        "soc_tokenizer_encode": (C.c_int, [P, C.c_char_p, I64, P, I64, C.POINTER(I64)]),
+        "soc_tokenizer_decode": (C.c_int, [P, P, I64, P, I64, C.POINTER(I64)]),
+        "soc_tokenizer_token_to_id": (C.c_int, [P, C.c_char_p, I64, C.POINTER(I32)]),
+        "soc_tokenizer_chat_prompt": (C.c_int, [P, P, P, I32, C.c_int, C.c_int, C.c_char_p, P, I64, C.POINTER(I64)]),
         "soc_kv_create_dims": (C.c_int, [P, I32, I32, I32, I32, I32, P]),
         "soc_kv_append": (C.c_int, [P, I32, I32, I32, I32, P, P, I32]),
         "soc_kv_set_length": (C.c_int, [P, I32, I32]),
@@ -438,6 +445,76 @@ def load_bundle(ctx: Context, manifest_path) -> "Model":
     finally:
         b.close()
     return Model.wrap(ctx, cfg, h)
+
+
+class Tokenizer:
+    """The bundle's tokenizer runtime and Qwen3 chat template (soc_tokenizer_*); host only, no GPU needed.
+
+    Tokenizer(runtime_json_path) reads one tokenizer_runtime.json; Tokenizer.from_bundle(manifest_path) reads the file
+    a manifest names and validates the two together. Text is str (UTF-8) or bytes; decode returns bytes, since a
+    token sequence need not end on a character boundary."""
+
+    def __init__(self, runtime_path=None, *, _handle=None):
+        self.h = None
+        if _handle is None:
+            h = C.c_void_p()
+            check(lib().soc_tokenizer_load(str(runtime_path).encode(), C.byref(h)))
+            _handle = h
+        self.h = _handle
+
+    @classmethod
+    def from_bundle(cls, manifest_path) -> "Tokenizer":
+        h = C.c_void_p()
+        check(lib().soc_tokenizer_load_bundle(str(manifest_path).encode(), C.byref(h)))
+        return cls(_handle=h)
+
+    def close(self) -> None:
+        if self.h:
+            lib().soc_tokenizer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, text) -> list[int]:
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        # one id per byte, plus one per BPE segment when a prefix space is added: 2 * len + 1 always suffices
+        out = np.empty(2 * len(b) + 1, np.int32)
+        n = C.c_int64()
+        check(lib().soc_tokenizer_encode(self.h, b, len(b), _ptr(out), out.size, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def decode(self, ids) -> bytes:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        n = C.c_int64()
+        rc = lib().soc_tokenizer_decode(self.h, _ptr(a), a.size, None, 0, C.byref(n))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        buf = C.create_string_buffer(max(1, n.value))
+        check(lib().soc_tokenizer_decode(self.h, _ptr(a), a.size, buf, n.value, C.byref(n)))
+        return buf.raw[: n.value]
+
+    def token_to_id(self, token) -> int:
+        b = token.encode() if isinstance(token, str) else bytes(token)
+        out = C.c_int32()
+        check(lib().soc_tokenizer_token_to_id(self.h, b, len(b), C.byref(out)))
+        return out.value
+
+    def chat_prompt(self, messages, add_generation_prompt=True, enable_thinking=True, system_prompt=None) -> bytes:
+        """Qwen3TemplateBuilder::BuildPrompt over [(role, content), ...]."""
+        enc = [(r.encode(), c.encode()) for r, c in messages]
+        roles = (C.c_char_p * max(1, len(enc)))(*[r for r, _ in enc])
+        contents = (C.c_char_p * max(1, len(enc)))(*[c for _, c in enc])
+        sp = system_prompt.encode() if system_prompt else None
+        n = C.c_int64()
+        args = (self.h, C.cast(roles, C.c_void_p), C.cast(contents, C.c_void_p), len(enc), int(add_generation_prompt),
+                int(enable_thinking), sp)
+        rc = lib().soc_tokenizer_chat_prompt(*args, None, 0, C.byref(n))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        buf = C.create_string_buffer(max(1, n.value))
+        check(lib().soc_tokenizer_chat_prompt(*args, buf, n.value, C.byref(n)))
+        return buf.raw[: n.value]
 
 
 def quantize_group(w_f16: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray]:

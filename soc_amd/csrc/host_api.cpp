@@ -1,6 +1,7 @@
 // host_api.cpp - the reference GPU runtime's C++ classes (include/soc/gpu/runtime.h) implemented on the C ABI.
 // Semantics follow Mac/gpu/src: runtime/generation_context.cpp, command_scheduler.cpp, sampler.cpp, kv_cache.mm,
-// tensor/tensor_desc.cpp, device_tensor.cpp, buffer/buffer_arena.cpp, metal_buffer.mm.
+// tensor/tensor_desc.cpp, device_tensor.cpp, buffer/buffer_arena.cpp, metal_buffer.mm; and the text-level helpers of
+// Mac/cpu/src/runtime_pipeline.cpp.
 #include <algorithm>
 #include <cstring>
 #include <numeric>
@@ -554,6 +555,48 @@ void GenerationContext::Reset() {
   kv_cache_.reset();
   prompt_token_ids_.clear();
   running_token_ids_.clear();
+}
+
+// ---- RuntimePipeline (Mac/cpu/src/runtime_pipeline.cpp) ----
+bool RuntimePipeline::LoadBundle(const HipContext& context, const std::string& manifest_path, RuntimeBundle* bundle,
+                                 std::string* error_message) {
+  if (bundle == nullptr) return Fail(error_message, "RuntimePipeline requires a non-null bundle output");
+  try {
+    RuntimeBundle b;
+    b.manifest = soc::ManifestLoader::LoadFromFile(manifest_path);
+    b.tokenizer_runtime = soc::TokenizerRuntimeLoader::LoadFromFile(b.manifest.tokenizer_runtime_file);
+    soc::StartupValidator::ValidateManifestAndTokenizer(b.manifest, b.tokenizer_runtime);
+    if (!QwenModelLoader::LoadModel(context, b.manifest, &b.model, error_message)) return false;
+    *bundle = std::move(b);
+    return true;
+  } catch (const std::exception& e) {
+    return Fail(error_message, e.what());
+  }
+}
+
+RuntimeGenerationOptions RuntimePipeline::GenerationOptionsFromManifest(const soc::ManifestData& manifest) {
+  RuntimeGenerationOptions o;
+  const soc::JsonValue& g = manifest.generation_config;
+  if (!g.is_object()) return o;
+  if (const soc::JsonValue* v = g.find("max_new_tokens")) o.max_new_tokens = static_cast<std::size_t>(v->as_int64());
+  if (const soc::JsonValue* v = g.find("temperature")) o.sampler.temperature = static_cast<float>(v->as_number());
+  if (const soc::JsonValue* v = g.find("top_k")) o.sampler.top_k = static_cast<std::size_t>(v->as_int64());
+  if (const soc::JsonValue* v = g.find("eos_token_id")) {
+    if (!v->is_array())
+      o.eos_token_id = v->as_int();
+    else if (!v->as_array().empty())
+      o.eos_token_id = v->as_array().front().as_int();  // a list names several; the first one stops generation
+  }
+  if (const soc::JsonValue* v = g.find("max_length")) o.max_sequence_length = static_cast<std::size_t>(v->as_int64());
+  return o;
+}
+
+std::string RuntimePipeline::PreparePrompt(const soc::TokenizerRuntimeData& tokenizer_runtime, const std::string& prompt,
+                                           const RuntimePromptOptions& options) {
+  if (!options.apply_chat_template) return prompt;
+  return soc::Qwen3TemplateBuilder(tokenizer_runtime.template_runtime)
+      .BuildPrompt({soc::ChatMessage{"user", prompt}}, options.add_generation_prompt, options.enable_thinking,
+                   options.system_prompt);
 }
 
 }  // namespace soc::gpu

@@ -47,9 +47,11 @@ def config_dict(cfg, torch_dtype: str = "float16", **extra) -> dict:
 
 def write_bundle(root: Path, config: dict, tensors: dict[str, tuple[np.ndarray, str]], *, export_dtype="float16",
                  manifest_overrides: dict | None = None, byte_size_delta: dict[str, int] | None = None,
-                 truncate: dict[str, int] | None = None, drop: tuple[str, ...] = ()) -> Path:
+                 truncate: dict[str, int] | None = None, drop: tuple[str, ...] = (),
+                 tokenizer_runtime: dict | None = None, generation_config: dict | None = None) -> Path:
     """tensors: name -> (values with their shape, file dtype); manifest_overrides / drop replace or remove top-level
-    manifest keys. Returns the manifest path."""
+    manifest keys; tokenizer_runtime, when given, is written as tokenizer/tokenizer_runtime.json (the file the
+    manifest names). Returns the manifest path."""
     root = Path(root)
     (root / "weights").mkdir(parents=True, exist_ok=True)
     records = []
@@ -66,10 +68,14 @@ def write_bundle(root: Path, config: dict, tensors: dict[str, tuple[np.ndarray, 
     manifest = {"format": "soc.cpp.llm_export", "format_version": 2, "model_id": "test/qwen3",
                 "source_dir": str(root), "export_dtype": export_dtype,
                 "tokenizer_runtime_file": "tokenizer/tokenizer_runtime.json", "config": config,
-                "generation_config": {}, "tensors": records}
+                "generation_config": generation_config or {}, "tensors": records}
     manifest.update(manifest_overrides or {})
     for key in drop:
         del manifest[key]
+    if tokenizer_runtime is not None:
+        (root / "tokenizer").mkdir(exist_ok=True)
+        (root / "tokenizer" / "tokenizer_runtime.json").write_text(
+            json.dumps(tokenizer_runtime, indent=1, ensure_ascii=False), encoding="utf-8")
     path = root / "manifest.json"
     path.write_text(json.dumps(manifest, indent=1))
     return path

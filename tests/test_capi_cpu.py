@@ -52,9 +52,21 @@ def test_library_exports_cpp_host_interface():
         "soc::gpu::Sampler::SampleFromLogits", "soc::gpu::GenerationContext::Prefill",
         "soc::gpu::GenerationContext::DecodeNextToken", "soc::gpu::GenerationContext::Generate",
         "soc::gpu::GenerationContext::Reset", "soc::gpu::GenerationContext::GenerationContext",
+        "soc::gpu::RuntimePipeline::LoadBundle", "soc::gpu::RuntimePipeline::GenerationOptionsFromManifest",
+        "soc::gpu::RuntimePipeline::PreparePrompt",
     }
     for m in methods:
         assert m.split("::")[-1] in text
+        assert m + "(" in out, m
+    # the tokenizer classes of soc/tokenizer.h and the validator of soc/assets.h
+    out = out.replace("[abi:cxx11]", "")
+    tok_text = (ROOT / "include" / "soc" / "tokenizer.h").read_text() + (ROOT / "include" / "soc" / "assets.h").read_text()
+    for m in ("soc::TokenizerRuntimeLoader::LoadFromFile", "soc::TokenizerRuntime::Encode",
+              "soc::TokenizerRuntime::Decode", "soc::TokenizerRuntime::TokenToId", "soc::TokenizerRuntime::IdToToken",
+              "soc::TokenizerRuntime::TokenizerRuntime", "soc::Qwen3TemplateBuilder::BuildPrompt",
+              "soc::StartupValidator::ValidateTokenizerRuntime", "soc::StartupValidator::ValidateManifestAndTokenizer",
+              "soc::StartupValidator::ValidateManifest", "soc::ManifestLoader::LoadFromFile"):
+        assert m.split("::")[-1] in tok_text
         assert m + "(" in out, m
 
 
