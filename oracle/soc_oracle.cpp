@@ -259,6 +259,8 @@ int orc_sample_topk(const float* row, int64_t vocab, float temperature, int64_t 
 // in the low nibble; scales [N][K/64] fp16.
 int orc_quantize_group(const uint16_t* w, int64_t N, int64_t K, int bits, void* codes, uint16_t* scales) {
   if (!w || !codes || !scales || N <= 0 || K <= 0 || K % 64 != 0 || (bits != 8 && bits != 4)) return -1;
+  for (int64_t i = 0; i < N * K; ++i)
+    if ((w[i] & 0x7C00u) == 0x7C00u) return -1;  // inf / NaN: the rule has no scale for them
   const int Q = bits == 8 ? 127 : 7;
   const int64_t G = K / 64;
   for (int64_t n = 0; n < N; ++n)

@@ -1,5 +1,5 @@
 // assets.cpp - JSON, the export manifest, the Qwen3 config and tensor files of a model bundle (include/soc/assets.h),
-// and the C entry points that read a bundle and load it into a model (soc_bundle_*, soc_model_load_bundle).
+// and the C entry points that read a bundle (soc_bundle_*). Host only; soc_model_load_bundle is in model_bundle.cpp.
 // Follows Mac/cpu/src/json_parser.cpp (messages), runtime_assets.cpp:138-168, qwen3_config.cpp:20-67,
 // startup_validator.cpp:5-23, weight_loader.cpp:17-30, qwen_model_loader.cpp:17-93.
 #include <cmath>
@@ -29,8 +29,19 @@ double JsonValue::as_number() const {
   if (type_ != Type::Number) throw std::runtime_error("JSON value is not a number");
   return number_;
 }
-int JsonValue::as_int() const { return static_cast<int>(as_number()); }
-std::int64_t JsonValue::as_int64() const { return static_cast<std::int64_t>(as_number()); }
+// Integers are the number truncated toward zero, as a cast does; a number outside the target range is an error
+// rather than an out-of-range conversion.
+int JsonValue::as_int() const {
+  const double d = as_number();
+  if (!(d > -2147483649.0 && d < 2147483648.0)) throw std::runtime_error("JSON number out of int range");
+  return static_cast<int>(d);
+}
+std::int64_t JsonValue::as_int64() const {
+  const double d = as_number();
+  if (!(d >= -9223372036854775808.0 && d < 9223372036854775808.0))
+    throw std::runtime_error("JSON number out of int64 range");
+  return static_cast<std::int64_t>(d);
+}
 const std::string& JsonValue::as_string() const {
   if (type_ != Type::String) throw std::runtime_error("JSON value is not a string");
   return string_;
@@ -88,8 +99,12 @@ class Reader {
 
   JsonValue Value() {
     const char c = Peek();
-    if (c == '{') return Object();
-    if (c == '[') return ArrayValue();
+    if (c == '{' || c == '[') {
+      if (++depth_ > kMaxDepth) throw std::runtime_error("JSON nesting too deep");
+      JsonValue v = c == '{' ? Object() : ArrayValue();
+      --depth_;
+      return v;
+    }
     if (c == '"') return JsonValue(String());
     if (c == '-' || (c >= '0' && c <= '9')) return Number();
     if (c == 't' || c == 'f' || c == 'n') {
@@ -229,8 +244,10 @@ class Reader {
     }
   }
 
+  static constexpr int kMaxDepth = 256;  // bundle files nest a few levels; bounded recursion keeps the stack safe
   const std::string& t_;
   size_t i_ = 0;
+  int depth_ = 0;
 };
 
 }  // namespace
@@ -476,38 +493,6 @@ int soc_bundle_tensor_f16(const soc_bundle* b, const char* name, uint16_t* out, 
   } catch (const std::exception& e) {
     return soc::fail(SOC_ERR_INVALID, e.what());
   }
-}
-
-int soc_model_load_bundle(soc_ctx* ctx, const char* manifest_path, soc_model** out) {
-  if (ctx == nullptr || manifest_path == nullptr || out == nullptr)
-    return soc::fail(SOC_ERR_INVALID, "null argument");
-  *out = nullptr;
-  soc_bundle* b = nullptr;
-  int rc = soc_bundle_open(manifest_path, &b);
-  if (rc != SOC_OK) return rc;
-  std::unique_ptr<soc_bundle, int (*)(soc_bundle*)> hold(b, soc_bundle_close);
-  soc_qwen_config cfg;
-  soc_bundle_config(b, &cfg);
-  soc_model* m = nullptr;
-  if ((rc = soc_model_create(ctx, &cfg, &m)) != SOC_OK) return rc;
-  try {
-    for (const auto& [name, shape] : soc::Qwen3TensorShapes(b->config)) {
-      const std::vector<uint16_t> v = soc::WeightLoader::LoadFloat16(b->manifest, name, shape);
-      if ((rc = soc_model_load_tensor(m, name.c_str(), v.data(), static_cast<int64_t>(v.size()))) != SOC_OK) {
-        soc_model_destroy(m);
-        return rc;
-      }
-    }
-  } catch (const std::exception& e) {
-    soc_model_destroy(m);
-    return soc::fail(SOC_ERR_INVALID, e.what());
-  }
-  if ((rc = soc_model_finalize(m)) != SOC_OK) {
-    soc_model_destroy(m);
-    return rc;
-  }
-  *out = m;
-  return SOC_OK;
 }
 
 }  // extern "C"

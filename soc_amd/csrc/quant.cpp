@@ -80,6 +80,8 @@ extern "C" int soc_quantize_group(const uint16_t* w, int64_t n, int64_t k, int32
   if (bits != 8 && bits != 4) return soc::fail(SOC_ERR_INVALID, "soc_quantize_group: bits must be 8 or 4");
   if (n <= 0 || k <= 0 || k % 64 != 0)
     return soc::fail(SOC_ERR_INVALID, "soc_quantize_group: k must be a positive multiple of 64");
+  for (int64_t i = 0; i < n * k; ++i)  // inf / NaN have no scale; the reference's rule is undefined for them
+    if ((w[i] & 0x7C00u) == 0x7C00u) return soc::fail(SOC_ERR_INVALID, "soc_quantize_group: weights must be finite");
   uint8_t* c = static_cast<uint8_t*>(codes);
   const unsigned hw = std::thread::hardware_concurrency();
   const int64_t nt = std::min<int64_t>(std::max(1u, std::min(hw, 16u)), n);

@@ -22,18 +22,6 @@
 
 using soc::f16;
 
-// ------------------------------------------------------------------------------------------------------------
-// errors
-// ------------------------------------------------------------------------------------------------------------
-namespace soc {
-static thread_local std::string g_last_error;
-int fail(int code, const std::string& msg) {
-  g_last_error = msg;
-  return code;
-}
-void clear_error() { g_last_error.clear(); }
-}  // namespace soc
-
 #define SOC_API_BEGIN try {
 #define SOC_API_END                                                         \
   }                                                                         \
@@ -1178,7 +1166,6 @@ int upload_batch(soc_model* m, soc_kv* kv, int n, const int32_t* slots, const in
 // ------------------------------------------------------------------------------------------------------------
 extern "C" {
 
-const char* soc_last_error(void) { return soc::g_last_error.c_str(); }
 
 int soc_ctx_create(int device, soc_ctx** out) {
   SOC_API_BEGIN
