@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void k_split_f16(const float* x, size_t n, f16
     const float v = x[i];
     const f16 h = static_cast<f16>(v);
     hi[i] = h;
-    lo[i] = static_cast<f16>((v - static_cast<float>(h)) * 2048.0f);
+    if (lo != nullptr) lo[i] = static_cast<f16>((v - static_cast<float>(h)) * 2048.0f);
   }
 }
 
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
             lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
           }
           *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
-          *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
+          if (a.out_lo != nullptr) *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
         }
       }
   }
@@ -829,7 +829,7 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
                 lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
               }
               *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
-              *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
+              if (a.out_lo != nullptr) *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
             }
           }
       }
@@ -857,7 +857,7 @@ hipError_t launch_attention_prefill_pairs(const AttnArgs& a, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nkv <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;
   if (a.ld_qkv % 4 != 0 || a.ld_out % 4 != 0) return hipErrorInvalidValue;
-  if ((a.out_hi == nullptr) != (a.out_lo == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
+  if ((a.out_lo != nullptr && a.out_hi == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
     return hipErrorInvalidValue;
   if (G == 2) return launch_pairs<2>(a, s);
   if (G == 4) return launch_pairs<4>(a, s);
@@ -870,7 +870,7 @@ hipError_t launch_attention_prefill_mfma(const AttnArgs& a, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.pos != nullptr || a.slot != nullptr || a.B <= 0 || a.nq % a.nkv != 0) return hipErrorInvalidValue;
   if (a.ld_qkv % 4 != 0 || a.ld_out % 4 != 0) return hipErrorInvalidValue;
-  if ((a.out_hi == nullptr) != (a.out_lo == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
+  if ((a.out_lo != nullptr && a.out_hi == nullptr) || (a.out == nullptr && a.out_hi == nullptr))
     return hipErrorInvalidValue;
 #define SOC_FA_CASE(GG)                                                                        \
   if (G == GG) {                                                                               \

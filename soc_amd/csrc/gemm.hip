@@ -264,7 +264,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
 // c ^ (r & 7) (BK = 64): the rows a b128 read phase touches land on different bank groups.
 // BM x BN tile per 4-wave block (2 x 2 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_f16). Tiles are dealt to the
 // eight XCDs as an mx x (8 / mx) grid of rectangles (block b runs on XCD b % 8), mx chosen to minimise the bytes
-// of A and W each XCD's L2 has to fetch. The products and their order match k_gemm_mfma<EPI, true, .> exactly.
+// of A and W each XCD's L2 has to fetch. The products and their order match k_gemm_mfma<EPI, true, .> exactly, or
+// with LO = false (single fp16 activations, no lo part) those of k_gemm_mfma<EPI, false, .>.
 // EPI_SWIGLU with ch/cl set writes silu(g) * u as the hi/lo pair the down projection consumes.
 // ------------------------------------------------------------------------------------------------------------
 namespace {
@@ -299,15 +300,16 @@ __device__ __forceinline__ void block_barrier() {
 }
 }  // namespace
 
-template <int EPI, int BM, int BN, int ST, int MINB, int BK>
+template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO>
 __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int mx) {
   constexpr int MI = BM / 64, NJ = BN / 64;  // 32x32 MFMA tiles per wave
   constexpr int RPI = 1024 / (BK * 2);       // rows per 1 KB wave instruction
   constexpr int CPR = BK / 8;                // 16-byte chunks per row
+  constexpr int AP = LO ? 2 : 1;             // activation parts: hi and lo, or hi alone
   constexpr int AI = BM / RPI / 4, WI = BN / RPI / 4;  // DMA instructions per wave per slice: each A part, W
-  constexpr int IPT = 2 * AI + WI;
+  constexpr int IPT = AP * AI + WI;
   constexpr int KS = BK / 16;  // 16-deep MFMA steps per slice
-  constexpr int STAGE_H = (2 * BM + BN) * BK;
+  constexpr int STAGE_H = (AP * BM + BN) * BK;
   static_assert(EPI != EPI_SWIGLU || NJ == 2, "SwiGLU pairs one gate and one up tile per wave");
   static_assert(KS % 2 == 0 && ST >= 2 && AI >= 1 && WI >= 1, "tile shape");
   extern __shared__ __attribute__((aligned(16))) _Float16 slds[];
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
       const int c = chunk_slot<BK>(r, lane % CPR);
       const size_t off = static_cast<size_t>(min(m0 + r, g.M - 1)) * g.lda + k0 + c * 8;
       __builtin_amdgcn_global_load_lds(g.ah + off, base + rb * BK, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(g.al + off, base + BM * BK + rb * BK, 16, 0, 0);
+      if constexpr (LO) __builtin_amdgcn_global_load_lds(g.al + off, base + BM * BK + rb * BK, 16, 0, 0);
     }
 #pragma unroll
     for (int h = 0; h < WI; ++h) {
@@ -354,7 +356,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
         src = g.w;
       }
       n = min(n, g.N - 1);
-      __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(n) * g.K + k0 + c * 8, base + 2 * BM * BK + rb * BK,
+      __builtin_amdgcn_global_load_lds(src + static_cast<size_t>(n) * g.K + k0 + c * 8, base + AP * BM * BK + rb * BK,
                                        16, 0, 0);
     }
   };
@@ -378,7 +380,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
   auto read = [&](h8 (&fa)[MI][2], h8 (&fb)[NJ], int st, int ks) {
     const _Float16* Ah = slds + st * STAGE_H;
     const _Float16* Al = Ah + BM * BK;
-    const _Float16* Ws = Ah + 2 * BM * BK;
+    const _Float16* Ws = Ah + AP * BM * BK;
     const int c = 2 * ks + (lane >> 5);
 #pragma unroll
     for (int t = 0; t < NJ; ++t) {
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
       const int r = wm * (BM / 2) + i * 32 + (lane & 31);
       const int off = r * BK + chunk_slot<BK>(r, c) * 8;
       fa[i][0] = *reinterpret_cast<const h8*>(Ah + off);
-      fa[i][1] = *reinterpret_cast<const h8*>(Al + off);
+      if constexpr (LO) fa[i][1] = *reinterpret_cast<const h8*>(Al + off);
     }
   };
   auto mma = [&](const h8 (&fa)[MI][2], const h8 (&fb)[NJ]) {
@@ -399,17 +401,18 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
         acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][0], fb[t], acc[i][t], 0, 0, 0);
-        acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][1], fb[t], acc_lo[i][t], 0, 0, 0);
+        if constexpr (LO)
+          acc_lo[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][1], fb[t], acc_lo[i][t], 0, 0, 0);
       }
   };
   // one MFMA, one LDS read, ... then the remaining MFMAs
   auto interleave = [&]() {
 #pragma unroll
-    for (int q = 0; q < 2 * MI + NJ; ++q) {
+    for (int q = 0; q < AP * MI + NJ; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MI * NJ - (2 * MI + NJ), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, AP * MI * NJ - (AP * MI + NJ), 0);
   };
 
 #pragma unroll
@@ -456,7 +459,8 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
         const int ml = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
 #pragma unroll
         for (int t = 0; t < NJ; ++t)
-          xs[ml * LDX + wn * (BN / 2) + t * 32 + (lane & 31)] = acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f);
+          xs[ml * LDX + wn * (BN / 2) + t * 32 + (lane & 31)] =
+              LO ? acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f) : acc[i][t][r];
       }
     __syncthreads();
     const GemmSplitArgs::Qkv& q = g.qkv;
@@ -495,7 +499,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
       if (m >= g.M) continue;
       float v[NJ];
 #pragma unroll
-      for (int t = 0; t < NJ; ++t) v[t] = acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f);
+      for (int t = 0; t < NJ; ++t) v[t] = LO ? acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f) : acc[i][t][r];
       if constexpr (EPI == EPI_SWIGLU) {
         const int n = n0 + wn * 32 + (lane & 31);
         if (n < g.N) {
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
           if (g.ch != nullptr) {
             const _Float16 hi = static_cast<_Float16>(y);
             g.ch[o] = hi;
-            g.cl[o] = static_cast<_Float16>((y - static_cast<float>(hi)) * 2048.0f);
+            if (g.cl != nullptr) g.cl[o] = static_cast<_Float16>((y - static_cast<float>(hi)) * 2048.0f);
           } else {
             g.c[o] = y;
           }
@@ -539,17 +543,18 @@ int xcd_split(int mt, int nt, double abytes, double wbytes) {
   return best;
 }
 
-template <int EPI, int BM, int BN, int ST, int MINB, int BK>
+template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO>
 hipError_t launch_split_cfg(const GemmSplitArgs& g, hipStream_t s) {
+  constexpr int AP = LO ? 2 : 1;
   const int bn = EPI == EPI_SWIGLU ? BN / 2 : BN;
   const int mt = (g.M + BM - 1) / BM, nt = (g.N + bn - 1) / bn;
-  const int mx = xcd_split(mt, nt, 4.0 * g.M * g.K, 2.0 * (EPI == EPI_SWIGLU ? 2 : 1) * g.N * g.K);
-  const size_t lds = static_cast<size_t>(ST) * (2 * BM + BN) * BK * sizeof(_Float16);
+  const int mx = xcd_split(mt, nt, 2.0 * AP * g.M * g.K, 2.0 * (EPI == EPI_SWIGLU ? 2 : 1) * g.N * g.K);
+  const size_t lds = static_cast<size_t>(ST) * (AP * BM + BN) * BK * sizeof(_Float16);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB, BK>),
+      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB, BK>), dim3(mt * nt), dim3(256), lds, s, g, mx);
+  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO>), dim3(mt * nt), dim3(256), lds, s, g, mx);
   return hipGetLastError();
 }
 
@@ -557,7 +562,11 @@ template <int EPI>
 hipError_t launch_split_epi(const GemmSplitArgs& g, hipStream_t s) {
   // 64 x 128 tiles, two blocks per CU: 64-deep slices in a 2-slot ring, or 32-deep ones in a 4-slot ring when K
   // is not a multiple of 64 (measured on the Qwen3-0.6B prefill shapes at 2048 tokens)
-  return g.K % 64 == 0 ? launch_split_cfg<EPI, 64, 128, 2, 2, 64>(g, s) : launch_split_cfg<EPI, 64, 128, 4, 2, 32>(g, s);
+  if (g.al != nullptr)
+    return g.K % 64 == 0 ? launch_split_cfg<EPI, 64, 128, 2, 2, 64, true>(g, s)
+                         : launch_split_cfg<EPI, 64, 128, 4, 2, 32, true>(g, s);
+  return g.K % 64 == 0 ? launch_split_cfg<EPI, 64, 128, 2, 2, 64, false>(g, s)
+                       : launch_split_cfg<EPI, 64, 128, 4, 2, 32, false>(g, s);
 }
 }  // namespace
 
@@ -569,7 +578,7 @@ bool gemm_split_supported(const GemmSplitArgs& g) {
 
 hipError_t launch_gemm_split(const GemmSplitArgs& g, int epi, hipStream_t s) {
   if (!gemm_split_supported(g)) return hipErrorInvalidValue;
-  if (epi == EPI_SWIGLU && (g.w2 == nullptr || (g.ch == nullptr) != (g.cl == nullptr))) return hipErrorInvalidValue;
+  if (epi == EPI_SWIGLU && (g.w2 == nullptr || (g.cl != nullptr && g.ch == nullptr))) return hipErrorInvalidValue;
   if (epi == EPI_QKV && (g.N != (g.qkv.nq + 2 * g.qkv.nkv) * 128 || g.qkv.q_out == nullptr ||
                          g.qkv.kcache == nullptr || g.qkv.vcache == nullptr))
     return hipErrorInvalidValue;

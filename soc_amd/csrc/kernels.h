@@ -213,7 +213,8 @@ hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
 bool gemm_mfma_supported(const GemmArgs& g);
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s);
 // Same products on activations pre-split into hi = f16(a) and lo = f16((a - hi) * 2^11) arrays [M][lda]
-// (lda % 8 == 0, K % 32 == 0, 16-byte aligned). EPI_SWIGLU writes c, or the hi/lo pair ch/cl when set.
+// (lda % 8 == 0, K % 32 == 0, 16-byte aligned); with al = null, on the single fp16 activations ah alone (the
+// products of launch_gemm_mfma with split = false). EPI_SWIGLU writes c, or ch (and cl when set) in the same form.
 struct GemmSplitArgs {
   const f16* ah;
   const f16* al;

@@ -802,30 +802,35 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
   return SOC_OK;
 }
 
-// Prefill projections run on MFMA with hi/lo-split activations when K allows (SOC_PREFILL_GEMM=fma selects the
-// FMA kernel; SOC_PREFILL_SPLIT=0 feeds single fp16 activations to the MFMA).
+// Whether prefill projections see each activation as a hi/lo fp16 pair (the default: 22 significant bits, close to
+// the reference's fp32 activations) or, with SOC_PREFILL_SPLIT=0, as one fp16 value (half the MFMA work; within the
+// logit tolerance at 2048 tokens of the N(0, 0.02) model, but with little margin on models with larger weights).
+bool prefill_hilo() {
+  const char* sp = std::getenv("SOC_PREFILL_SPLIT");
+  return !(sp != nullptr && sp[0] == '0');
+}
+
+// Prefill projections on fp32 activations: MFMA when K allows, on fp16 activations or their hi/lo pairs
+// (prefill_hilo); SOC_PREFILL_GEMM=fma selects the FMA kernel.
 hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
   const char* mode = std::getenv("SOC_PREFILL_GEMM");
   const bool fma = mode != nullptr && std::strcmp(mode, "fma") == 0;
   if (!fma && soc::gemm_mfma_supported(g)) {
-    const char* sp = std::getenv("SOC_PREFILL_SPLIT");
-    const bool split = !(sp != nullptr && sp[0] == '0');
-    return soc::launch_gemm_mfma(g, epi, split, s);
+    return soc::launch_gemm_mfma(g, epi, prefill_hilo(), s);
   }
   return soc::launch_gemm_f32a(g, epi, s);
 }
 
-// The prefill layers use the pre-split-activation GEMM (direct-to-LDS pipeline) on the default MFMA + hi/lo path
-// when the shapes allow; SOC_PREFILL_GEMM=fma, SOC_PREFILL_GEMM=staged (the register-staged MFMA kernel, same
-// products) and SOC_PREFILL_SPLIT=0 keep the fp32-activation kernels.
+// The prefill layers use the GEMM on fp16 activations written by their producers (direct-to-LDS pipeline) when the
+// shapes allow; SOC_PREFILL_GEMM=fma and SOC_PREFILL_GEMM=staged (the register-staged MFMA kernel, same products)
+// keep the fp32-activation kernels.
 bool prefill_split_path(const soc_model* m) {
   const char* mode = std::getenv("SOC_PREFILL_GEMM");
   if (mode != nullptr && (std::strcmp(mode, "fma") == 0 || std::strcmp(mode, "staged") == 0)) return false;
-  const char* sp = std::getenv("SOC_PREFILL_SPLIT");
-  if (sp != nullptr && sp[0] == '0') return false;
   const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
   return H % 32 == 0 && m->qd % 32 == 0 && I % 32 == 0;
 }
+
 
 hipError_t split_gemm(const soc::f16* ah, const soc::f16* al, int lda, const soc::f16* w, const soc::f16* w2,
                       float* c, soc::f16* ch, soc::f16* cl, int ldc, int M, int N, int K, int epi, hipStream_t s) {
@@ -1785,12 +1790,14 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   const int H = c.hidden_size;
   if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off));
   const bool split = prefill_split_path(m);
+  f16* const pl = prefill_hilo() ? w.pl : nullptr;  // lo parts of the activations, or none
+  f16* const ql = prefill_hilo() ? w.ql : nullptr;
   for (int l = 0; m->qbits == 0 && l < c.num_hidden_layers; ++l) {  // fp16 models
     const DevLayer& L = m->layers[l];
     soc::GemmArgs g{};
     bool qkv_fused = false;
     if (split) {
-      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, w.pl, s)) != hipSuccess)
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, pl, s)) != hipSuccess)
         return hip_fail(e, "rmsnorm");
       // QKV projection with the per-head q/k RMSNorm + RoPE, q output and K/V cache append in its epilogue
       // (SOC_PREFILL_QKV=separate: plain projection, then the q/k-norm kernel)
@@ -1798,7 +1805,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
       qkv_fused = qm == nullptr || std::strcmp(qm, "separate") != 0;
       soc::GemmSplitArgs g3{};
       g3.ah = w.ph;
-      g3.al = w.pl;
+      g3.al = pl;
       g3.lda = H;
       g3.w = L.wqkv;
       g3.c = w.qkv;
@@ -1869,7 +1876,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     a.pos_base = pos_off;
     a.out = split ? nullptr : w.attn;
     a.out_hi = split ? w.ph : nullptr;
-    a.out_lo = split ? w.pl : nullptr;
+    a.out_lo = split ? pl : nullptr;
     a.ld_out = m->qd;
     a.part = w.part;
     a.counters = w.attn_counters;
@@ -1878,15 +1885,15 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     if ((e = prefill_attention(a, w.attn, s)) != hipSuccess) return hip_fail(e, "attention prefill");
     const int I = c.intermediate_size;
     if (split) {
-      if ((e = split_gemm(w.ph, w.pl, m->qd, L.wo, nullptr, w.x, nullptr, nullptr, H, n, H, m->qd, soc::EPI_RESIDUAL,
+      if ((e = split_gemm(w.ph, pl, m->qd, L.wo, nullptr, w.x, nullptr, nullptr, H, n, H, m->qd, soc::EPI_RESIDUAL,
                           s)) != hipSuccess)
         return hip_fail(e, "gemm o");
-      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, nullptr, w.ph, w.pl, s)) != hipSuccess)
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, nullptr, w.ph, pl, s)) != hipSuccess)
         return hip_fail(e, "rmsnorm");
-      if ((e = split_gemm(w.ph, w.pl, H, L.wgate, L.wup, nullptr, w.qh, w.ql, I, n, I, H, soc::EPI_SWIGLU, s)) !=
+      if ((e = split_gemm(w.ph, pl, H, L.wgate, L.wup, nullptr, w.qh, ql, I, n, I, H, soc::EPI_SWIGLU, s)) !=
           hipSuccess)
         return hip_fail(e, "gemm gate/up");
-      if ((e = split_gemm(w.qh, w.ql, I, L.wdown, nullptr, w.x, nullptr, nullptr, H, n, H, I, soc::EPI_RESIDUAL, s)) !=
+      if ((e = split_gemm(w.qh, ql, I, L.wdown, nullptr, w.x, nullptr, nullptr, H, n, H, I, soc::EPI_RESIDUAL, s)) !=
           hipSuccess)
         return hip_fail(e, "gemm down");
       continue;
