@@ -7,6 +7,8 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 namespace soc {
 
@@ -226,6 +228,7 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
 // would leave most SIMDs idle.
 namespace {
 typedef _Float16 qh2 __attribute__((ext_vector_type(2)));
+typedef _Float16 sk_qh8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ qh2 as_qh2(uint32_t v) { return __builtin_bit_cast(qh2, v); }
 
@@ -320,6 +323,132 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
         const int row = base + r * RP + sub;
         if (ln == 0 && row < a.N) a.y[static_cast<size_t>(m) * a.N + row] = v;
       }
+  }
+}
+
+// The same product for 2 <= M <= 16 rows on matrix cores (v_mfma_f32_16x16x32_f16, D[token][row] = X . W^T): a
+// block stages the activations once in LDS and its 8 waves then stream 16-row tiles of codes (tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ...), each tile in chunks of eight 16-byte loads per lane with the next chunk (of this or
+// the next tile) in flight. Lane (r, q) = (lane % 16, lane / 16) loads 16 bytes of row r per instruction, 64 bytes
+// of the row across the four q: int8: the 16 codes k = 64 g + 16 q + 0..15 of group g; int4: the 32 codes
+// k = 128 c + 32 q + 0..31 of groups 2c (q < 2) and 2c + 1 (q >= 2), regrouped by one v_permlane32_swap per dword
+// pair so that lane q holds 16 codes of each group at k offset 16 * (0, 2, 1, 3)[q]. The codes unpack exactly to
+// fp16 as in k_qmm and are the MFMA's B operand as they come out; its A operand is the token rows, staged in LDS as
+// fp16 [16][K + 8] in the same k order (int4: within each 8 k, the order 0 4 1 5 2 6 3 7) and read with 16-byte LDS
+// reads (rows M..15 hold zeros, so no lane needs a select). D then holds, per lane, tokens 4 q .. 4 q + 3 of row r,
+// so the lane applies its own row's group scales (loaded with the codes). Each group's codes go to a fresh
+// accumulator whose sum is scaled and added to the result: the product per element is code * scale exactly as in
+// the dequantized weight. Tall matrices only (the LM head): at 151936 x 1024, batch 8, int8 runs at 60 % of HBM
+// bandwidth (the dot-product kernel: 24 %), int4 at 42 % (16 %).
+template <int BITS>
+__global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 qm_lds[];  // activations [16][K + 8]
+  const int K = a.K, G = K / 64, ldx = K + 8;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int rl = lane & 15, kq = lane >> 4;
+  constexpr int LPC = 8;                           // 16-byte code loads per lane per chunk
+  constexpr int GPC = BITS == 8 ? LPC : 2 * LPC;   // scale groups per chunk
+  const int nload = BITS == 8 ? G : G / 2;         // code loads per lane over a row (64 bytes of the row each)
+  const int nchunk = nload / LPC;                  // G % GPC == 0 (checked at launch)
+  const int ntiles = (a.N + 127) / 128;
+  const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+  const int items = my_tiles * nchunk;
+  const size_t rowbytes = BITS == 8 ? static_cast<size_t>(K) : static_cast<size_t>(K) / 2;
+  struct Chunk {
+    u32x4 w[LPC];
+    u32x4 s[GPC / 8];  // the chunk's group scales of the lane's row
+  };
+  auto tile_row = [&](int item) { return (blockIdx.x + (item / nchunk) * gridDim.x) * 128 + wid * 16; };
+  auto load = [&](Chunk& b, int item) {
+    const int c = item % nchunk;
+    const int row = min(tile_row(item) + rl, a.N - 1);
+    const uint8_t* cp = static_cast<const uint8_t*>(a.codes) + row * rowbytes + kq * 16 + static_cast<size_t>(c) * LPC * 64;
+#pragma unroll
+    for (int s = 0; s < LPC; ++s) b.w[s] = load16(cp + s * 64);
+    const f16* sp = a.scales + static_cast<size_t>(row) * G + c * GPC;
+#pragma unroll
+    for (int s = 0; s < GPC / 8; ++s) b.s[s] = load16(sp + 8 * s);
+  };
+  Chunk ba, bb;
+  if (items > 0) load(ba, 0);  // the code stream does not depend on the staging below
+
+  // activations: one 8-k run per thread step (16-byte load, permuted for int4, 16-byte LDS store)
+  for (int i = tid; i < 16 * (K / 8); i += 512) {  // rows M..15 are zeros
+    const int m = i / (K / 8), k8 = i - m * (K / 8);
+    const u32x4 v = m < a.M ? load16(a.x + static_cast<size_t>(m) * K + 8 * k8) : u32x4{0, 0, 0, 0};
+    u32x4 o = v;
+    if constexpr (BITS == 4) {  // halves 0..7 -> 0 4 1 5 2 6 3 7
+      o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+      o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+      o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+      o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+    }
+    *reinterpret_cast<u32x4*>(qm_lds + m * ldx + 8 * k8) = o;
+  }
+  __syncthreads();
+  if (items == 0) return;  // no barrier follows
+
+  const int kb = BITS == 8 ? 16 * kq : 16 * ((kq & 1) * 2 + (kq >> 1));
+  const _Float16* xr = qm_lds + rl * ldx + kb;
+  auto xop = [&](int koff) -> sk_qh8 {  // A operand: 8 activations of the lane's token at k offset koff
+    return *reinterpret_cast<const sk_qh8*>(xr + koff);
+  };
+  auto cop = [](const qh2* p) -> sk_qh8 {
+    return sk_qh8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+  };
+  auto scale_of = [](const Chunk& b, int gl) -> float {  // group gl of the chunk
+    const uint32_t w = b.s[gl >> 3][(gl >> 1) & 3];
+    return static_cast<float>(as_qh2(w)[gl & 1]);
+  };
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto process = [&](Chunk& b, int item) {
+    const int c = item % nchunk;
+#pragma unroll
+    for (int s = 0; s < LPC; ++s) {
+      const int idx = c * LPC + s;  // load index within the row
+      if constexpr (BITS == 8) {    // group idx: k = 64 idx + 16 kq + 0..15
+        qh2 p[8];
+        unpack_codes<8>(b.w[s], p);
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(64 * idx), cop(p), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(64 * idx + 8), cop(p + 4), d, 0, 0, 0);
+        const float sc = scale_of(b, s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sc, acc[i]);
+      } else {  // dwords 0, 1: group 2 idx at k = 128 idx + kb + 0..15; dwords 2, 3: group 2 idx + 1 (k + 64)
+        u32x4 w = b.w[s];
+        const auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        w = u32x4{s02[0], s13[0], s02[1], s13[1]};
+        qh2 p[16];
+        unpack_codes<4>(w, p);
+        f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(128 * idx), cop(p), d0, 0, 0, 0);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(128 * idx + 8), cop(p + 4), d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(128 * idx + 64), cop(p + 8), d1, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop(128 * idx + 72), cop(p + 12), d1, 0, 0, 0);
+        const float s0 = scale_of(b, 2 * s), s1 = scale_of(b, 2 * s + 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d1[i], s1, fmaf(d0[i], s0, acc[i]));
+      }
+    }
+    if (c == nchunk - 1) {  // the tile's row is done: D holds tokens 4 kq + i of row r0 + rl
+      const int row = tile_row(item) + rl;
+      if (row < a.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * kq + i < a.M) a.y[static_cast<size_t>(4 * kq + i) * a.N + row] = acc[i];
+      }
+      acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  for (int it = 0; it < items; it += 2) {
+    if (it + 1 < items) load(bb, it + 1);
+    process(ba, it);
+    if (it + 1 < items) {
+      if (it + 2 < items) load(ba, it + 2);
+      process(bb, it + 1);
+    }
   }
 }
 
@@ -498,7 +627,27 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
   return hipGetLastError();
 }
 
+// K a multiple of 512 (int8) or 1024 (int4): whole chunks of eight 16-byte loads per lane and 16-byte scale loads.
+bool qmm_mfma_supported(const QmmArgs& a, int bits) {
+  const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
+  return a.M >= 2 && a.M <= 16 && a.K % (bits == 8 ? 512 : 1024) == 0 && lds <= 64 * 1024 &&
+         (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.codes) |
+          reinterpret_cast<uintptr_t>(a.scales)) % 16 == 0;
+}
+
 hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
+  const char* mode = std::getenv("SOC_QMM");
+  // matrix cores for tall matrices (the LM head); the dot-product kernel keeps the short ones, where a 128-row
+  // block per 16 waves would leave most of the chip idle (SOC_QMM=mfma / dot force either)
+  const bool force_mfma = mode != nullptr && std::strcmp(mode, "mfma") == 0;
+  const bool force_dot = mode != nullptr && std::strcmp(mode, "dot") == 0;
+  if (qmm_mfma_supported(a, bits) && !force_dot && (force_mfma || a.N >= 16384)) {
+    const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
+    const dim3 grid(std::min((a.N + 127) / 128, 512)), block(512);  // two 16-wave blocks per CU, tiles looped
+    if (bits == 8) hipLaunchKernelGGL(k_qmm_mfma<8>, grid, block, lds, s, a);
+    else hipLaunchKernelGGL(k_qmm_mfma<4>, grid, block, lds, s, a);
+    return hipGetLastError();
+  }
   const int nch = a.K / (bits == 8 ? 16 : 32);  // 16-byte chunks per row
   if (nch < 16) {
     const size_t lds = static_cast<size_t>(a.M) * a.K * sizeof(float);

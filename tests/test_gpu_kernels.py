@@ -78,9 +78,16 @@ def _qmm_inputs(n, k, bits, m):
 
 
 @pytest.mark.parametrize("bits", [8, 4])
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
 @pytest.mark.parametrize("n,k", QMM_SHAPES)
-def test_qmm_matches_oracle(gpu_ctx, oracle_mod, bits, m, n, k):
+@pytest.mark.parametrize("mode", ["auto", "mfma"])
+def test_qmm_matches_oracle(gpu_ctx, oracle_mod, monkeypatch, bits, m, n, k, mode):
+    """auto: the dot-product kernel at m = 1 and for short matrices, the MFMA kernel for tall ones at m >= 2;
+    mfma: the MFMA kernel wherever it applies (m >= 2)."""
+    if mode == "mfma":
+        if m == 1:
+            pytest.skip("the MFMA kernel serves m >= 2")
+        monkeypatch.setenv("SOC_QMM", "mfma")
     ctx = gpu_ctx
     codes, scales, x = _qmm_inputs(n, k, bits, m)
     dc, ds, dx, dy = ctx.upload(codes), ctx.upload(scales), ctx.upload(x), ctx.alloc(m * n * 4)
