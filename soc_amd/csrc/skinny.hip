@@ -170,19 +170,26 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
   }
 }
 
-// Sum of n partials p[0], p[stride], ... in index order, with the loads issued eight at a time.
-__device__ __forceinline__ float sum_splits(const float* p, size_t stride, int n) {
+// Sum of n partials p[0], p[stride], ... in index order. The loads go out W at a time with no branch between them
+// (indices past n re-read the last partial, which is not added), so a split count up to W costs one memory round
+// trip rather than one per partial; W is the smallest of 4, 8, 16 that covers n (at most 16 per round).
+template <int W>
+__device__ __forceinline__ float sum_splits_w(const float* p, size_t stride, int n) {
   float v = 0.0f;
-  int k = 0;
-  for (; k + 8 <= n; k += 8) {
-    float x[8];
+  for (int k = 0; k < n; k += W) {
+    float x[W];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = p[(k + u) * stride];
+    for (int u = 0; u < W; ++u) x[u] = p[static_cast<size_t>(min(k + u, n - 1)) * stride];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v += x[u];
+    for (int u = 0; u < W; ++u)
+      if (k + u < n) v += x[u];
   }
-  for (; k < n; ++k) v += p[k * stride];
   return v;
+}
+__device__ __forceinline__ float sum_splits(const float* p, size_t stride, int n) {
+  if (n <= 4) return sum_splits_w<4>(p, stride, n);
+  if (n <= 8) return sum_splits_w<8>(p, stride, n);
+  return sum_splits_w<16>(p, stride, n);
 }
 
 // 1 / rms of input row m from the splits' sums of squares, in split order (1 without an input RMSNorm).
