@@ -86,39 +86,75 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   const int c0 = s * a.chunk;
   const int n = min(a.chunk, S - c0);
   const int sub = lane & 15, r = lane >> 4;
-  float qreg[G][8];
-#pragma unroll
-  for (int j = 0; j < G; ++j)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qreg[j][i] = qs[j][sub * 8 + i];
 
-  // scores: 16 lanes per key (8 dims each), 4 keys per wave step, 16 keys per block step. The whole chunk's keys
-  // (at most 256, a.chunk <= 256 is checked at launch: 16 per lane) are loaded before any is used, and its values
-  // right after the scores, so each block waits for memory twice instead of once per 64 keys.
-  u32x4 raw[16];
+  // scores on matrix cores: D[row][key] = Q . K^T with v_mfma_f32_16x16x32_f16 over 16-key tiles. The wave's keys
+  // are 64 w .. 64 w + 63 of the chunk; lane (key kl, group kg) = (lane % 16, lane / 16) loads the 16 bytes of dims
+  // 32 t + 8 kg of its key for t = 0..3, the B operand as stored (fp16 keys are exact). The A operand rows are the
+  // G query heads as fp16 hi = f16(q) and, in rows G..2G-1, lo = f16((q - hi) 2^11) (rows 2G..15 zero), so
+  // hi + lo 2^-11 carries about 22 bits of each fp32 query and the score loses nothing a fp32 dot product would keep
+  // beyond the order of its sums. All the chunk's key loads are issued before any is used.
+  static_assert(2 * G <= 16, "hi and lo rows of the query heads fit one 16-row tile");
+  const int kl = lane & 15, kg = lane >> 4;
+  u32x4 raw[16];  // keys: [tile t4][dim step t] -> raw[4 t4 + t]; values: the row layout below
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int p = u * 16 + wid * 4 + r;
-    raw[u] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+  for (int t4 = 0; t4 < 4; ++t4) {
+    const int p = 64 * wid + 16 * t4 + kl;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      raw[4 * t4 + t] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + 32 * t + 8 * kg) : u32x4{0, 0, 0, 0};
+  }
+  f16x8 qa[4];  // A operand: row kl = query head kl (hi) or kl - G (lo), dims 32 t + 8 kg .. + 7
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = 32 * t + 8 * kg + i;
+      float v = 0.0f;
+      if (kl < G) {
+        v = qs[kl][d];
+      } else if (kl < 2 * G) {
+        const float x = qs[kl - G][d];
+        v = (x - static_cast<float>(static_cast<f16>(x))) * 2048.0f;
+      }
+      qa[t][i] = static_cast<f16>(v);
+    }
   }
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int p = u * 16 + wid * 4 + r;
-    if (u * 16 >= n) break;  // block-uniform: no key of this step is in the chunk
-    float kf[8];
-    if (FUSED && c0 + p == qpos) {
+  for (int t4 = 0; t4 < 4; ++t4) {
+    if (64 * wid + 16 * t4 >= n) break;  // wave-uniform: no key of this tile is in the chunk
+    const int p = 64 * wid + 16 * t4 + kl;
+    if (FUSED && c0 + p == qpos) {  // the new key: from this kernel's own normed and roped copy
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = kn[sub * 8 + i];
-    } else {
-      f16x8_to_f32(raw[u], kf);
+      for (int t = 0; t < 4; ++t) {
+        f16x8 kv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kv[i] = static_cast<f16>(kn[32 * t + 8 * kg + i]);
+        raw[4 * t4 + t] = __builtin_bit_cast(u32x4, kv);
+      }
     }
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      float d = 0.0f;
+    for (int t = 0; t < 4; ++t)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[t], __builtin_bit_cast(f16x8, raw[4 * t4 + t]), d, 0, 0, 0);
+    // lane holds D rows 4 kg + i of key p: head j's score is row j + row (G + j) 2^-11
+    if constexpr (G == 8) {
+      f32x4 lo;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d += qreg[j][i] * kf[i];
-      d = group_sum<16>(d);
-      if (sub == 0 && p < n) sc[j][p] = d * a.scale;
+      for (int i = 0; i < 4; ++i) lo[i] = __shfl_xor(d[i], 32, kWave);
+      if (kg < 2 && p < n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[4 * kg + i][p] = (d[i] + lo[i] * (1.0f / 2048.0f)) * a.scale;
+    } else if constexpr (G == 4) {
+      f32x4 lo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lo[i] = __shfl_xor(d[i], 16, kWave);
+      if (kg == 0 && p < n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i][p] = (d[i] + lo[i] * (1.0f / 2048.0f)) * a.scale;
+    } else {
+      if (kg == 0 && p < n)
+#pragma unroll
+        for (int j = 0; j < G; ++j) sc[j][p] = (d[j] + d[G + j] * (1.0f / 2048.0f)) * a.scale;
     }
   }
 #pragma unroll
@@ -219,7 +255,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   __syncthreads();
   if (!last) return;  // the last block reads every partial with device-scope loads
   // combine: every chunk's (m, l) first, all loads in flight at once, then the weighted sums over chunks with the
-  // partial outputs fetched eight chunks at a time (the loads are independent; only their sum is ordered)
+  // partial outputs fetched sixteen chunks at a time (the loads are independent; only their sum is ordered)
   for (int idx = tid; idx < G * nact; idx += 256) {
     const int j = idx / nact, t = idx % nact;
     const float* pj = a.part + ((static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split + t) * stride;
@@ -244,15 +280,14 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split * stride + i;
     const float* ej = cm[j];
     float O = 0.0f;
-    int t = 0;
-    for (; t + 8 <= nact; t += 8) {
-      float v[8];
+    for (int t = 0; t < nact; t += 16) {  // 16 loads in flight per round, no branch between them; sums in order
+      float v[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = ld_dev(p0 + (t + u) * stride);
+      for (int u = 0; u < 16; ++u) v[u] = ld_dev(p0 + min(t + u, nact - 1) * stride);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) O += v[u] * ej[t + u];
+      for (int u = 0; u < 16; ++u)
+        if (t + u < nact) O += v[u] * ej[t + u];
     }
-    for (; t < nact; ++t) O += ld_dev(p0 + t * stride) * ej[t];
     a.out[static_cast<size_t>(b) * a.ld_out + (g * G + j) * HD + i] = O / lstat[j];
   }
   if (tid == 0) st_dev(a.counters + b * a.nkv + g, 0);
