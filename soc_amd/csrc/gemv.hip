@@ -576,42 +576,92 @@ hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t s) {
 
 // One block per logit row: the greedy token (the first index holding the maximum, like the strict `>` scan of
 // Sampler::SampleFromLogits, sampler.cpp:42-48), fed back as the row's next input id at the next position.
-__global__ __launch_bounds__(1024) void k_argmax_rows(const float* logits, int V, int32_t* ids, int32_t* pos,
-                                                      const int32_t* start, int32_t* ring, int ring_stride) {
-  __shared__ float sv[16];
-  __shared__ int si[16];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+// Keeps (v, i) when it beats (bv, bi): larger value, or the same value at a lower index. NaN never wins.
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__device__ __forceinline__ void argmax_wave(float& bv, int& bi) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_take(bv, bi, __shfl_xor(bv, o, kWave), __shfl_xor(bi, o, kWave));
+}
+
+// Grid (C, n): block (c, row) scans logits [c * chunk, (c + 1) * chunk) of its row. With C > 1 each block publishes
+// its candidate, and the last block of the row to arrive (counter per row, reset by that block) picks the winner.
+// Within a thread indices rise, so a strict `>` keeps the lowest index of equal maxima; every merge breaks ties
+// towards the lower index. A row without a finite maximum (all NaN or -inf) yields token 0.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_argmax_rows(const float* logits, int V, int chunk, int32_t* ids,
+                                                     int32_t* pos, const int32_t* start, int32_t* ring,
+                                                     int ring_stride, float* part_val, int32_t* part_idx,
+                                                     int32_t* counters) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ int last;
+  const int c = blockIdx.x, C = gridDim.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const float* x = logits + static_cast<size_t>(row) * V;
+  const int lo = c * chunk, hi = min(V, lo + chunk);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < V; i += 1024) {
-    const float v = x[i];
-    if (v > bv) {  // strided scan: the first (lowest) index of this thread's maxima
-      bv = v;
-      bi = i;
-    }
-  }
+  if (VEC) {  // V and chunk multiples of 4, 16-byte aligned rows: four 16-byte loads in flight per thread
+    for (int i = lo + 4 * tid; i < hi; i += 4 * 1024) {
+      f32x4 v[4];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, kWave);
-    const int oi = __shfl_xor(bi, o, kWave);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
+      for (int u = 0; u < 4; ++u) {
+        const int j = i + 1024 * u;
+        v[u] = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + j)) : f32x4(-INFINITY);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = i + 1024 * u;
+        if (v[u].x > bv) bv = v[u].x, bi = j;
+        if (v[u].y > bv) bv = v[u].y, bi = j + 1;
+        if (v[u].z > bv) bv = v[u].z, bi = j + 2;
+        if (v[u].w > bv) bv = v[u].w, bi = j + 3;
+      }
     }
+  } else {
+    for (int i = lo + tid; i < hi; i += 256)
+      if (x[i] > bv) bv = x[i], bi = i;
   }
+  argmax_wave(bv, bi);
   if (lane == 0) {
     sv[wid] = bv;
     si[wid] = bi;
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < 16; ++w)
-      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
-        bv = sv[w];
-        bi = si[w];
-      }
-    if (bi == 0x7fffffff) bi = 0;  // every logit NaN: token 0
+    for (int w = 1; w < 4; ++w) argmax_take(bv, bi, sv[w], si[w]);
+    if (C > 1) {
+      st_dev(part_val + static_cast<size_t>(row) * C + c, bv);
+      st_dev(part_idx + static_cast<size_t>(row) * C + c, bi);
+      wait_mem();  // the candidate is visible device-wide before it is counted
+      last = atomicAdd(counters + row, 1) == C - 1;
+    } else {
+      last = 1;
+      sv[0] = bv;
+      si[0] = bi;
+    }
+  }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+  if (C > 1) {  // C <= 64: one candidate per lane, device-scope loads
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    if (lane < C) {
+      bv = ld_dev(part_val + static_cast<size_t>(row) * C + lane);
+      bi = ld_dev(part_idx + static_cast<size_t>(row) * C + lane);
+    }
+    argmax_wave(bv, bi);
+  } else {
+    bi = si[0];
+  }
+  if (lane == 0) {
+    if (C > 1) st_dev(counters + row, 0);  // ready for the next step
+    if (bi == 0x7fffffff) bi = 0;
     const int p = pos[row];
     const int k = p - start[row];
     if (k >= 0 && k < ring_stride) ring[static_cast<size_t>(row) * ring_stride + k] = bi;
@@ -620,10 +670,27 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* logits, int V
   }
 }
 
+int argmax_chunks(int V, int n) {
+  // about 512 blocks in all, at most 64 per row and at least 1024 logits per block
+  int C = std::min(kArgmaxMaxChunks, std::max(1, (512 + n - 1) / n));
+  return std::max(1, std::min(C, V / 1024));
+}
+
 hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, int32_t* pos, const int32_t* start,
-                              int32_t* ring, int ring_stride, hipStream_t s) {
+                              int32_t* ring, int ring_stride, float* part_val, int32_t* part_idx, int32_t* counters,
+                              hipStream_t s) {
   if (n <= 0 || V <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_argmax_rows, dim3(n), dim3(1024), 0, s, logits, V, ids, pos, start, ring, ring_stride);
+  const int C = argmax_chunks(V, n);
+  if (C > 1 && (part_val == nullptr || part_idx == nullptr || counters == nullptr)) return hipErrorInvalidValue;
+  const bool vec = V % 4 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0;
+  const int chunk = ((V + C - 1) / C + 3) / 4 * 4;
+  const dim3 grid(C, n), block(256);
+  if (vec)
+    hipLaunchKernelGGL(k_argmax_rows<true>, grid, block, 0, s, logits, V, chunk, ids, pos, start, ring, ring_stride,
+                       part_val, part_idx, counters);
+  else
+    hipLaunchKernelGGL(k_argmax_rows<false>, grid, block, 0, s, logits, V, chunk, ids, pos, start, ring,
+                       ring_stride, part_val, part_idx, counters);
   return hipGetLastError();
 }
 

@@ -109,8 +109,13 @@ hipError_t launch_qk_norm_rope_append(const QkNormRopeArgs& a, hipStream_t s);
 
 // Greedy token of each of n logit rows (lowest index among equal maxima) for a ragged decode batch: writes it as
 // the row's next input id, records it at ring[row * ring_stride + (pos[row] - start[row])] and advances pos[row].
+// Each row is scanned by argmax_chunks(V, n) blocks; with more than one, part_val / part_idx hold
+// [n][kArgmaxMaxChunks] candidates and counters[n] (zero before the first call) count arrivals per row.
+constexpr int kArgmaxMaxChunks = 64;
+int argmax_chunks(int V, int n);
 hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, int32_t* pos, const int32_t* start,
-                              int32_t* ring, int ring_stride, hipStream_t s);
+                              int32_t* ring, int ring_stride, float* part_val, int32_t* part_idx, int32_t* counters,
+                              hipStream_t s);
 
 // K/V rows [rows][nkv * hd] (fp32, or fp16 when `fp16`) into positions pos .. pos + rows - 1 of one (slot, layer)
 // of the cache, whose [nkv][cap][hd] fp16 planes start at kdst / vdst.

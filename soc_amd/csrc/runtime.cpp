@@ -130,6 +130,9 @@ struct PrefillWs {
 struct BatchWs {
   int cap = 0;
   int32_t *ids = nullptr, *pos = nullptr, *start = nullptr, *slots = nullptr, *ring1 = nullptr;
+  // per-row candidates and arrival counters of the split greedy argmax ([cap][kArgmaxMaxChunks], [cap])
+  float* am_val = nullptr;
+  int32_t *am_idx = nullptr, *am_cnt = nullptr;
   std::vector<void*> allocs;
   int32_t* ring = nullptr;  // [rows][steps] tokens of soc_decode_batch_steps
   size_t ring_cap = 0;
@@ -927,6 +930,11 @@ int ensure_batch_ws(soc_model* m, int n) {
   SOC_TRY(dev_alloc_t(b.allocs, n, &b.start));
   SOC_TRY(dev_alloc_t(b.allocs, n, &b.slots));
   SOC_TRY(dev_alloc_t(b.allocs, n, &b.ring1));
+  SOC_TRY(dev_alloc_t(b.allocs, static_cast<size_t>(n) * soc::kArgmaxMaxChunks, &b.am_val));
+  SOC_TRY(dev_alloc_t(b.allocs, static_cast<size_t>(n) * soc::kArgmaxMaxChunks, &b.am_idx));
+  SOC_TRY(dev_alloc_t(b.allocs, n, &b.am_cnt));
+  if ((e = hipMemset(b.am_cnt, 0, static_cast<size_t>(n) * sizeof(int32_t))) != hipSuccess)
+    return hip_fail(e, "hipMemset");
   b.cap = n;
   return SOC_OK;
 }
@@ -1140,8 +1148,8 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
     g.K = H;
     if ((e = prefill_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm lm head");
   }
-  if ((e = soc::launch_argmax_rows(w.logits, c.vocab_size, n, b.ids, b.pos, b.start, ring, ring_stride, s)) !=
-      hipSuccess)
+  if ((e = soc::launch_argmax_rows(w.logits, c.vocab_size, n, b.ids, b.pos, b.start, ring, ring_stride, b.am_val,
+                                   b.am_idx, b.am_cnt, s)) != hipSuccess)
     return hip_fail(e, "argmax");
   return SOC_OK;
 }

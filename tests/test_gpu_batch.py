@@ -191,6 +191,40 @@ def test_ragged_qwen3_4b_matches_reference(gpu_ctx, golden):
         m.close()
 
 
+@pytest.mark.parametrize("pattern", ["repeated_rows", "all_zero"])
+def test_batch_greedy_ties_across_chunks(gpu_ctx, pattern):
+    """Exact ties in the greedy choice: a 65536-token LM head whose rows from 40000 on repeat 8 seeded rows (every
+    maximum recurs ~3000 times, across all the blocks that scan a row), or an all-zero LM head (every logit 0).
+    Each row's token must be the lowest index of its maximum logit: the reference's greedy pick
+    (Mac/cpu/src/sampler.cpp:41-58, a top-1 partial sort, which replaces its candidate only on a strictly greater
+    score)."""
+    cfg = S.QwenConfig(vocab_size=65536, hidden_size=256, num_hidden_layers=2, num_attention_heads=4,
+                       num_key_value_heads=2, intermediate_size=512, tie_word_embeddings=False)
+    w = S.synth_weights(cfg, 36)
+    head = np.zeros((cfg.vocab_size, cfg.hidden_size), np.float16)
+    if pattern == "repeated_rows":
+        rows = w["lm_head.weight"][:8]
+        head[40000:] = rows[np.arange(cfg.vocab_size - 40000) % 8]
+    w["lm_head.weight"] = head
+    m = S.Model(gpu_ctx, cfg).load(w)
+    (kv,), last = _prefilled_caches(m, cfg, 1)
+    try:
+        for n in (5, 1, 3):  # 64 blocks per row for each n
+            slots = np.arange(n, dtype=np.int32)
+            lg, nxt = S.decode_batch(m, kv, slots, last[slots])
+            for i in range(n):
+                want = int(np.argmax(lg[i]))  # numpy: first index of the maximum
+                assert int(nxt[i]) == want, (pattern, n, i)
+                if pattern == "all_zero":
+                    assert want == 0
+                else:
+                    assert want >= 40000 or lg[i].max() == 0.0
+            last[slots] = nxt
+    finally:
+        kv.close()
+        m.close()
+
+
 def test_batch_error_paths(gpu_ctx):
     cfg = small_cfg()
     m = S.Model(gpu_ctx, cfg).load(S.synth_weights(cfg, 35))
