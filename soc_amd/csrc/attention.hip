@@ -21,8 +21,11 @@ constexpr int kMaxCombine = 160;  // key chunks one attention row may be split i
 
 }  // namespace
 
-// grid = (max_split, nkv, B), block = 256 (4 waves). Each block: one KV head g, its G query heads, one batch row,
-// one chunk of keys.
+// grid = (nkv, max_split, B), block = 256 (4 waves). Each block: one KV head g, its G query heads, one batch row,
+// one chunk of keys. The KV head is the fastest grid index: consecutive blocks go to consecutive XCDs (and
+// alternate chunks to alternate shader engines), so with 8 KV heads XCD g serves head g and every XCD gets the same
+// number of chunks however ragged the rows are. (With the chunk index fastest, rows of few chunks would load only
+// the XCDs and shader engines that low chunk indices map to.)
 template <int G, bool FUSED>
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   __shared__ float qs[G][HD];
@@ -33,7 +36,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   __shared__ float cm[G][kMaxCombine], cl[G][kMaxCombine];  // split combine: chunk maxima / weights, sums
   __shared__ int last;
 
-  const int b = blockIdx.z, g = blockIdx.y, s = blockIdx.x;
+  const int b = blockIdx.z, g = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qpos = (a.pos != nullptr ? a.pos[b] : b) + a.pos_base;
   const int S = qpos + 1;
@@ -928,7 +931,7 @@ hipError_t launch_attention(const AttnArgs& a, int fused, hipStream_t s) {
   const int G = a.nq / a.nkv;
   if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;
   if (a.max_split > kMaxCombine) return hipErrorInvalidValue;
-  const dim3 grid(a.max_split, a.nkv, a.B), block(256);
+  const dim3 grid(a.nkv, a.max_split, a.B), block(256);
 #define SOC_ATTN_CASE(GG)                                                                  \
   if (G == GG) {                                                                          \
     if (fused) hipLaunchKernelGGL((k_attention<GG, true>), grid, block, 0, s, a);          \

@@ -660,7 +660,7 @@ __device__ __forceinline__ bool lm_compute(const Ctx& c) {
 // run separate loops with the same sequence of block barriers.
 template <int G>
 __global__ __launch_bounds__(NT) void k_decode_persistent(PersistArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   float* red = lds + 2 * a.xs_cap;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
   const int ng = static_cast<int>(gridDim.x) - a.nkv;

@@ -84,7 +84,7 @@ __device__ __forceinline__ void rows_dot(const f16* __restrict__ W, int row0, in
 // stream, Mac/cpu/src/qwen_block.cpp:70-72). EPI_SWIGLU: y[n] = silu(W.x) * (W2.x) (qwen_mlp.cpp:69-72).
 template <int R, int U, int EPI>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-  extern __shared__ float xs[];
+  extern __shared__ __attribute__((aligned(16))) float xs[];
   __shared__ float red[4];
   stage_x<256>(a.x, a.xh, a.gain, a.eps, a.K, xs, red);
   const int lane = threadIdx.x & (kWave - 1);
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // The last block to finish reduces the per-block winners, writes the token and advances the decode state.
 template <int R, int U>
 __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
-  extern __shared__ float xs[];
+  extern __shared__ __attribute__((aligned(16))) float xs[];
   __shared__ float red[4];
   __shared__ float bv[4];
   __shared__ int bi[4];
@@ -257,7 +257,7 @@ __device__ __forceinline__ void unpack_codes(const u32x4& w, qh2 (&p)[BITS == 8 
 
 template <int BITS, int M, int L, int RR>
 __global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
-  extern __shared__ uint32_t xq[];  // [M][K / 2] fp16 pairs
+  extern __shared__ __attribute__((aligned(16))) uint32_t xq[];  // [M][K / 2] fp16 pairs
   const int K = a.K, KP = K / 2;
   for (int i = threadIdx.x; i < M * KP; i += 256) {
     const int m = i / KP, p = i - m * KP;
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
 // Rows too short for 16 lanes of 16-byte chunks (K < 256 int8 / 512 int4): one lane per 16 k, two rows per wave.
 template <int BITS, int M>
 __global__ __launch_bounds__(256) void k_qmm_short(QmmArgs a) {
-  extern __shared__ float xs[];  // [M][K]
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [M][K]
   for (int m = 0; m < M; ++m)
     for (int i = threadIdx.x; i < a.K; i += 256) xs[m * a.K + i] = static_cast<float>(a.x[static_cast<size_t>(m) * a.K + i]);
   __syncthreads();

@@ -67,8 +67,8 @@ __host__ __device__ inline float* sk_part(float* base, int KS) { return base + 6
 
 // grid = (tiles, KS), block = 512, dynamic LDS 2 x 16 x (Kb + 8) halves.
 template <int EPI>
-__global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
-  extern __shared__ _Float16 sk_lds[];
+__global__ __launch_bounds__(512, 4) void k_skinny_part(SkinnyArgs a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 sk_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int tile = blockIdx.x, ks = blockIdx.y;
   const int k0 = ks * a.Kb;
@@ -101,23 +101,39 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) dst[s] = load16(wrow + c * SK_CHUNK + s * 32);
   };
-  // the weight stream does not depend on the activations: start it before staging them
-  if (active) load(wa, 0);
-
-  // activations of this K range (times the RMSNorm gain) -> hi/lo fp16 in LDS (rows past M are zero); row m is
-  // staged by the 32 threads 32 m .. 32 m + 31, which also sum its squares (written by the blocks of tile 0)
-  {
-    const int m = tid >> 5, j = tid & 31;
-    float ss = 0.0f;
-    for (int cc = 4 * j; cc < a.Kb; cc += 128) {
-      f32x4 v = m < a.M ? *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(m) * a.ldx + k0 + cc)
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
+  // Activations of this K range (times the RMSNorm gain) -> hi/lo fp16 in LDS (rows past M are zero); row m is
+  // staged by the 32 threads 32 m .. 32 m + 31, which also sum its squares (written by the blocks of tile 0). The
+  // first SU runs of each thread are loaded before the first two weight chunks: loads complete in issue order, so
+  // the staging then waits only for its own data while the weight stream stays in flight (a Kb over 128 SU stages
+  // the rest afterwards). All loads are unconditional (rows past M and runs past Kb read in-range data that is not
+  // used; an inactive wave's weight rows are clamped to valid rows), so no branch splits them. The sum of squares
+  // runs in k order.
+  constexpr int SU = 5;
+  const int m = tid >> 5, j = tid & 31;
+  const float* xrow = a.x + static_cast<size_t>(min(m, a.M - 1)) * a.ldx + k0;
+  const f16* grow = (norm ? a.gain : reinterpret_cast<const f16*>(a.x)) + k0;  // (not read without a gain)
+  f32x4 sv[SU];
+  f16x4 sg[SU];
+  auto stage_load = [&](int c0) {  // c0: uniform run base
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int cc = min(c0 + 128 * u + 4 * j, a.Kb - 4);
+      sv[u] = *reinterpret_cast<const f32x4*>(xrow + cc);
+      sg[u] = *reinterpret_cast<const f16x4*>(grow + cc);
+    }
+  };
+  float ss = 0.0f;
+  auto stage_store = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      if (c0 + 128 * u >= a.Kb) break;  // uniform (Kb % 128 == 0)
+      const int cc = c0 + 128 * u + 4 * j;
+      f32x4 v = m < a.M ? sv[u] : f32x4{0.f, 0.f, 0.f, 0.f};
       if (norm) {
-        const f16x4 g = *reinterpret_cast<const f16x4*>(a.gain + k0 + cc);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           ss = fmaf(v[e], v[e], ss);
-          v[e] *= static_cast<float>(g[e]);
+          v[e] *= static_cast<float>(sg[u][e]);
         }
       }
       f16x4 hi, lo;
@@ -130,10 +146,20 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
       *reinterpret_cast<f16x4*>(&xh[m * ld + cc]) = hi;
       *reinterpret_cast<f16x4*>(&xl[m * ld + cc]) = lo;
     }
-    if (norm) {
-      ss = group_sum<32>(ss);
-      if (tile == 0 && j == 0) a.part[64 * ks + m] = ss;
-    }
+  };
+  stage_load(0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order: staging runs, then weights
+  load(wa, 0);
+  load(wb, nch > 1 ? 1 : 0);
+  __builtin_amdgcn_sched_barrier(0);
+  stage_store(0);
+  for (int c0 = 128 * SU; c0 < a.Kb; c0 += 128 * SU) {
+    stage_load(c0);
+    stage_store(c0);
+  }
+  if (norm) {
+    ss = group_sum<32>(ss);
+    if (tile == 0 && j == 0) a.part[64 * ks + m] = ss;
   }
   __syncthreads();
 
@@ -153,7 +179,7 @@ __global__ __launch_bounds__(512) void k_skinny_part(SkinnyArgs a) {
     }
   };
   for (int c = 0; c < nch; c += 2) {
-    if (c + 1 < nch) load(wb, c + 1);
+    if (c > 0 && c + 1 < nch) load(wb, c + 1);  // (chunk 1 went out before the staging)
     mma(wa, c);
     if (c + 1 < nch) {
       if (c + 2 < nch) load(wa, c + 2);
