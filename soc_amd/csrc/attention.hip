@@ -48,8 +48,27 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   f16* kb = a.kcache + head_base;
   f16* vb = a.vcache + head_base;
   const float* row = a.qkv + static_cast<size_t>(b) * a.ld_qkv;
+  const int c0 = s * a.chunk;
+  const int n = min(a.chunk, S - c0);
+
+  // The chunk's keys, as MFMA B operands: the wave's keys are 64 w .. 64 w + 63 of the chunk; lane (key kl, group kg)
+  // = (lane % 16, lane / 16) holds the 16 bytes of dims 32 t + 8 kg of its key for t = 0..3, as stored (fp16 keys are
+  // exact). Keys past the chunk's end load the last key (their scores are never stored), so the loads need no
+  // branch. They are issued before the query is staged; loads complete in issue order, so a wait for the query
+  // (issued first on the plain path) leaves them in flight.
+  const int kl = lane & 15, kg = lane >> 4;
+  u32x4 raw[16];  // keys: [tile t4][dim step t] -> raw[4 t4 + t]; values: the row layout below
+  auto load_keys = [&]() {
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const int p = min(64 * wid + 16 * t4 + kl, n - 1);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) raw[4 * t4 + t] = load16(kb + static_cast<size_t>(c0 + p) * HD + 32 * t + 8 * kg);
+    }
+  };
 
   if constexpr (FUSED) {
+    load_keys();
     const float* cr = a.rope_cos + static_cast<size_t>(qpos) * (HD / 2);
     const float* sr = a.rope_sin + static_cast<size_t>(qpos) * (HD / 2);
     for (int vi = wid; vi < G + 2; vi += 4) {
@@ -82,30 +101,28 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
       }
     }
   } else {
-    for (int i = tid; i < G * HD; i += 256) qs[i / HD][i % HD] = row[(g * G) * HD + i];
+    constexpr int QN = (G * HD + 255) / 256;
+    float qv[QN];
+#pragma unroll
+    for (int u = 0; u < QN; ++u) qv[u] = row[(g * G) * HD + min(tid + 256 * u, G * HD - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    load_keys();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < QN; ++u) {
+      const int i = tid + 256 * u;
+      if (i < G * HD) qs[i / HD][i % HD] = qv[u];
+    }
   }
   __syncthreads();
 
-  const int c0 = s * a.chunk;
-  const int n = min(a.chunk, S - c0);
   const int sub = lane & 15, r = lane >> 4;
 
-  // scores on matrix cores: D[row][key] = Q . K^T with v_mfma_f32_16x16x32_f16 over 16-key tiles. The wave's keys
-  // are 64 w .. 64 w + 63 of the chunk; lane (key kl, group kg) = (lane % 16, lane / 16) loads the 16 bytes of dims
-  // 32 t + 8 kg of its key for t = 0..3, the B operand as stored (fp16 keys are exact). The A operand rows are the
-  // G query heads as fp16 hi = f16(q) and, in rows G..2G-1, lo = f16((q - hi) 2^11) (rows 2G..15 zero), so
-  // hi + lo 2^-11 carries about 22 bits of each fp32 query and the score loses nothing a fp32 dot product would keep
-  // beyond the order of its sums. All the chunk's key loads are issued before any is used.
+  // scores on matrix cores: D[row][key] = Q . K^T with v_mfma_f32_16x16x32_f16 over 16-key tiles, the keys loaded
+  // above as B. The A operand rows are the G query heads as fp16 hi = f16(q) and, in rows G..2G-1,
+  // lo = f16((q - hi) 2^11) (rows 2G..15 zero), so hi + lo 2^-11 carries about 22 bits of each fp32 query and the
+  // score loses nothing a fp32 dot product would keep beyond the order of its sums.
   static_assert(2 * G <= 16, "hi and lo rows of the query heads fit one 16-row tile");
-  const int kl = lane & 15, kg = lane >> 4;
-  u32x4 raw[16];  // keys: [tile t4][dim step t] -> raw[4 t4 + t]; values: the row layout below
-#pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4) {
-    const int p = 64 * wid + 16 * t4 + kl;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      raw[4 * t4 + t] = (p < n) ? load16(kb + static_cast<size_t>(c0 + p) * HD + 32 * t + 8 * kg) : u32x4{0, 0, 0, 0};
-  }
   f16x8 qa[4];  // A operand: row kl = query head kl (hi) or kl - G (lo), dims 32 t + 8 kg .. + 7
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -161,9 +178,9 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int p = u * 16 + wid * 4 + r;
-    raw[u] = (p < n) ? load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8) : u32x4{0, 0, 0, 0};
+  for (int u = 0; u < 16; ++u) {  // values (keys past the chunk's end load the last one, never used)
+    const int p = min(u * 16 + wid * 4 + r, n - 1);
+    raw[u] = load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8);
   }
   __syncthreads();
 
