@@ -196,48 +196,80 @@ __global__ __launch_bounds__(512, 4) void k_skinny_part(SkinnyArgs a) {
   }
 }
 
-// Sum of n partials p[0], p[stride], ... in index order. The loads go out W at a time with no branch between them
-// (indices past n re-read the last partial, which is not added), so a split count up to W costs one memory round
-// trip rather than one per partial; W is the smallest of 4, 8, 16 that covers n (at most 16 per round).
-template <int W>
-__device__ __forceinline__ float sum_splits_w(const float* p, size_t stride, int n) {
-  float v = 0.0f;
-  for (int k = 0; k < n; k += W) {
-    float x[W];
+// Sums, each in split order, of NS streams of n partials (stream i: p[i][0], p[i][st[i]], ...). The loads of all
+// streams go out W per stream at a time with no branch between them (indices past n re-read the last partial, which
+// is not added), so up to W splits cost one memory round trip however many streams; W is the smallest of 4, 8, 16,
+// 32 that covers n (at most 32 per round).
+template <int W, int NS>
+__device__ __forceinline__ void sum_streams_w(const float* const (&p)[NS], const size_t (&st)[NS], int n,
+                                              float (&v)[NS]) {
 #pragma unroll
-    for (int u = 0; u < W; ++u) x[u] = p[static_cast<size_t>(min(k + u, n - 1)) * stride];
+  for (int i = 0; i < NS; ++i) v[i] = 0.0f;
+  for (int k = 0; k < n; k += W) {
+    float x[NS][W];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int u = 0; u < W; ++u) x[i][u] = p[i][static_cast<size_t>(min(k + u, n - 1)) * st[i]];
 #pragma unroll
     for (int u = 0; u < W; ++u)
-      if (k + u < n) v += x[u];
+      if (k + u < n)
+#pragma unroll
+        for (int i = 0; i < NS; ++i) v[i] += x[i][u];
   }
-  return v;
 }
-__device__ __forceinline__ float sum_splits(const float* p, size_t stride, int n) {
-  if (n <= 4) return sum_splits_w<4>(p, stride, n);
-  if (n <= 8) return sum_splits_w<8>(p, stride, n);
-  return sum_splits_w<16>(p, stride, n);
+template <int NS>
+__device__ __forceinline__ void sum_streams(const float* const (&p)[NS], const size_t (&st)[NS], int n,
+                                            float (&v)[NS]) {
+  if (n <= 4) sum_streams_w<4, NS>(p, st, n, v);
+  else if (n <= 8) sum_streams_w<8, NS>(p, st, n, v);
+  else if (n <= 16) sum_streams_w<16, NS>(p, st, n, v);
+  else sum_streams_w<32, NS>(p, st, n, v);
 }
 
-// 1 / rms of input row m from the splits' sums of squares, in split order (1 without an input RMSNorm).
-__device__ __forceinline__ float sk_rscale(const SkinnyArgs& a, int m) {
-  if (a.gain == nullptr) return 1.0f;
-  const float ss = sum_splits(a.part + m, 64, a.KS);
+// 1 / rms of an input row from the sum of its splits' sums of squares.
+__device__ __forceinline__ float sk_rscale(const SkinnyArgs& a, float ss) {
   return 1.0f / sqrtf(ss / static_cast<float>(a.K) + a.eps);
 }
 
-// Store / residual / SwiGLU: one thread per (row m, output n): the KS partials in split order, then the epilogue.
+// Store / residual / SwiGLU: one thread per (row m, output n): the KS partials (and, with an input RMSNorm, the
+// row's sums of squares) summed in split order, loaded together; then the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
   const int n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
   if (n >= nout) return;
-  const float s = sk_rscale(a, m);
   const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + n;
-  const size_t split_stride = static_cast<size_t>(16) * a.Ntot;
-  const float v = s * sum_splits(p, split_stride, a.KS);
+  const size_t ss_stride = 64, split_stride = static_cast<size_t>(16) * a.Ntot;
+  float sc = 1.0f, v, u = 0.0f;
+  if constexpr (EPI == EPI_SWIGLU) {
+    if (a.gain != nullptr) {
+      float r[3];
+      sum_streams<3>({a.part + m, p, p + a.N0}, {ss_stride, split_stride, split_stride}, a.KS, r);
+      sc = sk_rscale(a, r[0]);
+      v = r[1];
+      u = r[2];
+    } else {
+      float r[2];
+      sum_streams<2>({p, p + a.N0}, {split_stride, split_stride}, a.KS, r);
+      v = r[0];
+      u = r[1];
+    }
+  } else {
+    if (a.gain != nullptr) {
+      float r[2];
+      sum_streams<2>({a.part + m, p}, {ss_stride, split_stride}, a.KS, r);
+      sc = sk_rscale(a, r[0]);
+      v = r[1];
+    } else {
+      float r[1];
+      sum_streams<1>({p}, {split_stride}, a.KS, r);
+      v = r[0];
+    }
+  }
+  v *= sc;
   float* dst = a.c + static_cast<size_t>(m) * a.ldc + n;
   if constexpr (EPI == EPI_SWIGLU) {
-    const float u = s * sum_splits(p + a.N0, split_stride, a.KS);
-    *dst = silu_ref(v) * u;
+    *dst = silu_ref(v) * (sc * u);
   } else if constexpr (EPI == EPI_RESIDUAL) {
     *dst += v;
   } else {
@@ -250,11 +282,21 @@ __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
 // q -> q_out, k and v -> the fp16 cache of slots[m] at pos[m].
 __global__ __launch_bounds__(64) void k_skinny_epi_qkv(SkinnyArgs a) {
   const int m = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const float s = sk_rscale(a, m);
   const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + h * 128;
-  const size_t split_stride = static_cast<size_t>(16) * a.Ntot;
-  float x0 = s * sum_splits(p + lane, split_stride, a.KS);
-  float x1 = s * sum_splits(p + lane + 64, split_stride, a.KS);
+  const size_t ss_stride = 64, split_stride = static_cast<size_t>(16) * a.Ntot;
+  float x0, x1;
+  if (a.gain != nullptr) {
+    float r[3];
+    sum_streams<3>({a.part + m, p + lane, p + lane + 64}, {ss_stride, split_stride, split_stride}, a.KS, r);
+    const float sc = sk_rscale(a, r[0]);
+    x0 = sc * r[1];
+    x1 = sc * r[2];
+  } else {
+    float r[2];
+    sum_streams<2>({p + lane, p + lane + 64}, {split_stride, split_stride}, a.KS, r);
+    x0 = r[0];
+    x1 = r[1];
+  }
   const int pos = a.pos[m], slot = a.slots[m];
   const float* cr = a.rope_cos + static_cast<size_t>(pos) * 64;
   const float* sr = a.rope_sin + static_cast<size_t>(pos) * 64;
