@@ -370,12 +370,28 @@ __global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
     for (int s = 0; s < GPC / 8; ++s) b.s[s] = load16(sp + 8 * s);
   };
   Chunk ba, bb;
-  if (items > 0) load(ba, 0);  // the code stream does not depend on the staging below
-
-  // activations: one 8-k run per thread step (16-byte load, permuted for int4, 16-byte LDS store)
-  for (int i = tid; i < 16 * (K / 8); i += 512) {  // rows M..15 are zeros
-    const int m = i / (K / 8), k8 = i - m * (K / 8);
-    const u32x4 v = m < a.M ? load16(a.x + static_cast<size_t>(m) * K + 8 * k8) : u32x4{0, 0, 0, 0};
+  // activations: 8-k runs (16-byte load, permuted for int4, 16-byte LDS store), at most XR per thread (K <= 2040).
+  // The runs are loaded first and the first code chunk after them: loads complete in issue order, so the staging
+  // waits for its own data only and the code stream stays in flight. Rows M..15 are zeros (loaded from row M - 1,
+  // not used); 16 K / 8 is a multiple of 512, so every thread has the same number of runs.
+  constexpr int XR = 8;
+  const int runs = K / 8, nruns = 16 * runs;
+  u32x4 xv[XR];
+#pragma unroll
+  for (int u = 0; u < XR; ++u) {
+    const int i = min(tid + 512 * u, nruns - 1);
+    const int m = i / runs, k8 = i - m * runs;
+    xv[u] = load16(a.x + static_cast<size_t>(min(m, a.M - 1)) * K + 8 * k8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (items > 0) load(ba, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < XR; ++u) {
+    const int i = tid + 512 * u;
+    if (512 * u >= nruns) break;  // uniform
+    const int m = i / runs, k8 = i - m * runs;
+    const u32x4 v = m < a.M ? xv[u] : u32x4{0, 0, 0, 0};
     u32x4 o = v;
     if constexpr (BITS == 4) {  // halves 0..7 -> 0 4 1 5 2 6 3 7
       o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
@@ -694,7 +710,8 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
   return hipGetLastError();
 }
 
-// K a multiple of 512 (int8) or 1024 (int4): whole chunks of eight 16-byte loads per lane and 16-byte scale loads.
+// K a multiple of 512 (int8) or 1024 (int4): whole chunks of eight 16-byte loads per lane and 16-byte scale loads;
+// K <= 2040 (the activations fit 64 KB of LDS; at most eight 8-k runs per thread).
 bool qmm_mfma_supported(const QmmArgs& a, int bits) {
   const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
   return a.M >= 2 && a.M <= 16 && a.K % (bits == 8 ? 512 : 1024) == 0 && lds <= 64 * 1024 &&
