@@ -39,25 +39,27 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, const f16* 
   __syncthreads();
 }
 
-// Dot products of R consecutive rows (starting at row0) with xs; U 512-wide chunks of K are loaded per iteration.
+// Dot products of R consecutive rows (starting at row0) with xs over the 512-wide chunks of K starting at kbase,
+// kbase + cs, kbase + 2 cs, ... (cs = 512: all of K from kbase = 0); U chunks are loaded per iteration.
 template <int R, int U>
-__device__ __forceinline__ void rows_dot(const f16* __restrict__ W, int row0, int N, int K, const float* xs, float* acc) {
+__device__ __forceinline__ void rows_dot(const f16* __restrict__ W, int row0, int N, int K, const float* xs, float* acc,
+                                         int kbase = 0, int cs = 512) {
   const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-  for (int k0 = lane * 8; k0 < K; k0 += 512 * U) {
+  for (int k0 = kbase + lane * 8; k0 < K; k0 += cs * U) {
     u32x4 w[U][R];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, N - 1);
-        const int k = k0 + u * 512;
+        const int k = k0 + u * cs;
         w[u][r] = k < K ? load_stream16(W + static_cast<size_t>(row) * K + k) : u32x4{0, 0, 0, 0};
       }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = k0 + u * 512;
+      const int k = k0 + u * cs;
       if (k < K) {
         float xv[8];
         *reinterpret_cast<f32x4*>(xv) = *reinterpret_cast<const f32x4*>(xs + k);
@@ -108,6 +110,39 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
       *dst = v;
     }
+  }
+}
+
+// The same for matrices with few rows (where a wave per R rows would leave most of the chip idle): block b owns
+// rows R b .. R b + R - 1 and its four waves split K (wave w takes the 512-wide chunks w, w + 4, ...); the four
+// partial sums of a row are added in wave order.
+template <int R, int U, int EPI>
+__global__ __launch_bounds__(256) void k_gemv_ks(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];
+  __shared__ float red[4];
+  __shared__ float part[2][4][R];
+  stage_x<256>(a.x, a.xh, a.gain, a.eps, a.K, xs, red);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * R;
+  float acc[R];
+  rows_dot<R, U>(a.w, row0, a.N, a.K, xs, acc, wid * 512, 4 * 512);
+  if (lane == 0)
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[0][wid][r] = acc[r];
+  if constexpr (EPI == EPI_SWIGLU) {
+    rows_dot<R, U>(a.w2, row0, a.N, a.K, xs, acc, wid * 512, 4 * 512);
+    if (lane == 0)
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[1][wid][r] = acc[r];
+  }
+  __syncthreads();
+  if (threadIdx.x < R && row0 + threadIdx.x < a.N) {
+    const int r = threadIdx.x;
+    float v = part[0][0][r] + part[0][1][r] + part[0][2][r] + part[0][3][r];
+    if constexpr (EPI == EPI_SWIGLU) v = silu_ref(v) * (part[1][0][r] + part[1][1][r] + part[1][2][r] + part[1][3][r]);
+    float* dst = a.y + row0 + r;
+    if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
+    *dst = v;
   }
 }
 
@@ -573,6 +608,21 @@ hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s) {
   constexpr int R = 4, U = 2;
   const size_t lds = static_cast<size_t>(a.K) * sizeof(float);
   const dim3 grid(gemv_grid(a.N, R)), block(256);
+  const char* mode = std::getenv("SOC_GEMV");
+  // fewer than 2048 row groups (waves of the row-per-wave kernel): split K over the waves of a block instead
+  const bool ks = mode != nullptr ? std::strcmp(mode, "ks") == 0
+                                  : (a.N + (epi == EPI_SWIGLU ? 2 : R) - 1) / (epi == EPI_SWIGLU ? 2 : R) < 2048;
+  if (ks) {
+    switch (epi) {
+      case EPI_STORE: hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_STORE>), dim3((a.N + R - 1) / R), block, lds, s, a); break;
+      case EPI_RESIDUAL:
+        hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_RESIDUAL>), dim3((a.N + R - 1) / R), block, lds, s, a);
+        break;
+      case EPI_SWIGLU: hipLaunchKernelGGL((k_gemv_ks<2, U, EPI_SWIGLU>), dim3((a.N + 1) / 2), block, lds, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   switch (epi) {
     case EPI_STORE: hipLaunchKernelGGL((k_gemv<R, U, EPI_STORE>), grid, block, lds, s, a); break;
     case EPI_RESIDUAL: hipLaunchKernelGGL((k_gemv<R, U, EPI_RESIDUAL>), grid, block, lds, s, a); break;

@@ -139,6 +139,19 @@ struct BatchWs {
 };
 
 constexpr int kAttnChunk = 256;
+
+// Keys per attention chunk of single-sequence per-op decode for a cache of `cap` positions: the smallest of 64, 128,
+// 256 that keeps a full cache within 160 chunks (the kernel's combine limit). Smaller chunks give a short context
+// more blocks (at batch 1 every block is one chunk of one KV head). SOC_DECODE_CHUNK overrides (64, 128 or 256).
+int decode_attn_chunk(int cap) {
+  if (const char* e = std::getenv("SOC_DECODE_CHUNK")) {
+    const int v = std::atoi(e);
+    if ((v == 64 || v == 128 || v == 256) && (cap + v - 1) / v <= 160) return v;
+  }
+  for (int c = 64; c < kAttnChunk; c *= 2)
+    if ((cap + c - 1) / c <= 160) return c;
+  return kAttnChunk;
+}
 constexpr int kQChunk = 8;  // rows per group-quantized projection call in a quantized model's prefill (k_qmm M <= 8)
 constexpr int kMaxBatchRows = 1024;
 
@@ -247,7 +260,7 @@ int check_config(const soc_qwen_config& c) {
 
 int ensure_decode_ws(soc_model* m, int cap) {
   DecodeWs& w = m->dws;
-  const int need_split = (cap + kAttnChunk - 1) / kAttnChunk;
+  const int need_split = (cap + decode_attn_chunk(cap) - 1) / decode_attn_chunk(cap);
   if (w.ready && w.max_split >= need_split && w.ring_cap >= cap) return SOC_OK;
   hipError_t se = hipStreamSynchronize(m->ctx->stream);
   if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
@@ -484,7 +497,8 @@ int enqueue_decode(soc_model* m, soc_kv* kv, int slot, const int32_t* d_slot) {
         a.part = w.part;
         a.counters = w.attn_counters;
         a.B = 1;
-        a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+        a.chunk = decode_attn_chunk(kv->cap);
+        a.max_split = (kv->cap + a.chunk - 1) / a.chunk;
         const hipError_t ea = soc::launch_attention(a, 1, s);
         return ea == hipSuccess ? SOC_OK : hip_fail(ea, "attention decode");
       };
@@ -515,7 +529,8 @@ int enqueue_decode(soc_model* m, soc_kv* kv, int slot, const int32_t* d_slot) {
       a.part = w.part;
       a.counters = w.attn_counters;
       a.B = 1;
-      a.max_split = (kv->cap + kAttnChunk - 1) / kAttnChunk;
+      a.chunk = decode_attn_chunk(kv->cap);
+      a.max_split = (kv->cap + a.chunk - 1) / a.chunk;
       if ((e = soc::launch_attention(a, 1, s)) != hipSuccess) return hip_fail(e, "attention decode");
       g = soc::GemvArgs{};
       g.x = w.attn;
