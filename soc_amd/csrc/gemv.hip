@@ -114,32 +114,92 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 }
 
 // The same for matrices with few rows (where a wave per R rows would leave most of the chip idle): block b owns
-// rows R b .. R b + R - 1 and its four waves split K (wave w takes the 512-wide chunks w, w + 4, ...); the four
-// partial sums of a row are added in wave order.
+// rows R b .. R b + R - 1 and its four waves split K (wave w takes the 512-wide chunks w, w + 4, ...). Nothing is
+// staged: a lane loads its own 8 activations (and gains) with the weights, in one round trip, and the RMSNorm scale
+// 1 / rms, which is the same for every product, multiplies the finished sums (the gain multiplies x before the
+// products); the sums of squares and the four partial dot products of a row are added in wave order.
 template <int R, int U, int EPI>
 __global__ __launch_bounds__(256) void k_gemv_ks(GemvArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float xs[];
-  __shared__ float red[4];
   __shared__ float part[2][4][R];
-  stage_x<256>(a.x, a.xh, a.gain, a.eps, a.K, xs, red);
+  __shared__ float ssw[4];
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * R;
-  float acc[R];
-  rows_dot<R, U>(a.w, row0, a.N, a.K, xs, acc, wid * 512, 4 * 512);
-  if (lane == 0)
+  const int row0 = blockIdx.x * R, K = a.K;
+  const bool norm = a.gain != nullptr;
+  float acc[R], acc2[R], ss = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) part[0][wid][r] = acc[r];
-  if constexpr (EPI == EPI_SWIGLU) {
-    rows_dot<R, U>(a.w2, row0, a.N, a.K, xs, acc, wid * 512, 4 * 512);
-    if (lane == 0)
+  for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.0f;
+  for (int kw = wid * 512; kw < K; kw += 2048 * U) {  // the wave's first chunk of this iteration
+    u32x4 w[U][R], w2[U][R];
+    f32x4 xa[U], xb[U];
+    u32x4 gv[U];
 #pragma unroll
-      for (int r = 0; r < R; ++r) part[1][wid][r] = acc[r];
+    for (int u = 0; u < U; ++u) {
+      const int k = min(kw + 2048 * u + lane * 8, K - 8);  // in range; runs past K are loaded and not used
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const size_t off = static_cast<size_t>(min(row0 + r, a.N - 1)) * K + k;
+        w[u][r] = load_stream16(a.w + off);
+        if constexpr (EPI == EPI_SWIGLU) w2[u][r] = load_stream16(a.w2 + off);
+      }
+      if (a.xh != nullptr) {
+        const u32x4 h = load16(a.xh + k);
+        float f[8];
+        f16x8_to_f32(h, f);
+        xa[u] = f32x4{f[0], f[1], f[2], f[3]};
+        xb[u] = f32x4{f[4], f[5], f[6], f[7]};
+      } else {
+        xa[u] = *reinterpret_cast<const f32x4*>(a.x + k);
+        xb[u] = *reinterpret_cast<const f32x4*>(a.x + k + 4);
+      }
+      gv[u] = norm ? load16(a.gain + k) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (kw + 2048 * u + lane * 8 >= K) continue;
+      float xv[8] = {xa[u][0], xa[u][1], xa[u][2], xa[u][3], xb[u][0], xb[u][1], xb[u][2], xb[u][3]};
+      if (norm) {
+        float g[8];
+        f16x8_to_f32(gv[u], g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ss = fmaf(xv[i], xv[i], ss);
+          xv[i] *= g[i];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float wf[8];
+        f16x8_to_f32(w[u][r], wf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r] += xv[i] * wf[i];
+        if constexpr (EPI == EPI_SWIGLU) {
+          f16x8_to_f32(w2[u][r], wf);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc2[r] += xv[i] * wf[i];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = wave_sum(acc[r]);
+    if constexpr (EPI == EPI_SWIGLU) acc2[r] = wave_sum(acc2[r]);
+  }
+  if (norm) ss = wave_sum(ss);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      part[0][wid][r] = acc[r];
+      part[1][wid][r] = acc2[r];
+    }
+    ssw[wid] = ss;
   }
   __syncthreads();
   if (threadIdx.x < R && row0 + threadIdx.x < a.N) {
     const int r = threadIdx.x;
-    float v = part[0][0][r] + part[0][1][r] + part[0][2][r] + part[0][3][r];
-    if constexpr (EPI == EPI_SWIGLU) v = silu_ref(v) * (part[1][0][r] + part[1][1][r] + part[1][2][r] + part[1][3][r]);
+    const float sc = norm ? 1.0f / sqrtf((ssw[0] + ssw[1] + ssw[2] + ssw[3]) / static_cast<float>(K) + a.eps) : 1.0f;
+    float v = sc * (part[0][0][r] + part[0][1][r] + part[0][2][r] + part[0][3][r]);
+    if constexpr (EPI == EPI_SWIGLU) v = silu_ref(v) * (sc * (part[1][0][r] + part[1][1][r] + part[1][2][r] + part[1][3][r]));
     float* dst = a.y + row0 + r;
     if constexpr (EPI == EPI_RESIDUAL) v = *dst + v;
     *dst = v;
@@ -609,16 +669,17 @@ hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s) {
   const size_t lds = static_cast<size_t>(a.K) * sizeof(float);
   const dim3 grid(gemv_grid(a.N, R)), block(256);
   const char* mode = std::getenv("SOC_GEMV");
-  // fewer than 2048 row groups (waves of the row-per-wave kernel): split K over the waves of a block instead
-  const bool ks = mode != nullptr ? std::strcmp(mode, "ks") == 0
-                                  : (a.N + (epi == EPI_SWIGLU ? 2 : R) - 1) / (epi == EPI_SWIGLU ? 2 : R) < 2048;
-  if (ks) {
+  // K split over the waves of a block, no staging, for all but the tallest matrices (SOC_GEMV=ks / rows forces
+  // either); above 16384 row groups the row-per-wave kernel has waves enough to cover its staging
+  const int groups = (a.N + (epi == EPI_SWIGLU ? 2 : R) - 1) / (epi == EPI_SWIGLU ? 2 : R);
+  const bool ks = mode != nullptr ? std::strcmp(mode, "ks") == 0 : groups < 16384;
+  if (ks && a.K % 8 == 0) {
     switch (epi) {
-      case EPI_STORE: hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_STORE>), dim3((a.N + R - 1) / R), block, lds, s, a); break;
+      case EPI_STORE: hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_STORE>), dim3((a.N + R - 1) / R), block, 0, s, a); break;
       case EPI_RESIDUAL:
-        hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_RESIDUAL>), dim3((a.N + R - 1) / R), block, lds, s, a);
+        hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_RESIDUAL>), dim3((a.N + R - 1) / R), block, 0, s, a);
         break;
-      case EPI_SWIGLU: hipLaunchKernelGGL((k_gemv_ks<2, U, EPI_SWIGLU>), dim3((a.N + 1) / 2), block, lds, s, a); break;
+      case EPI_SWIGLU: hipLaunchKernelGGL((k_gemv_ks<2, U, EPI_SWIGLU>), dim3((a.N + 1) / 2), block, 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
