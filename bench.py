@@ -12,6 +12,7 @@ the device. A "step" is one decode token. Also measured in the same run:
   * every decode projection shape (q, k/v, o, gate/up, down, LM head) as an fp16 GEMV at batch 1 and as the
     int8 / int4 group-quantized matmul (group 64, fp16 scales) at batch 1 and 8, in GB/s against 8 TB/s,
   * the Qwen3-4B ragged decode batch (16 sequences, seeded KV lengths in [64, 4096]),
+  * Qwen3-4B greedy decode at batch 1 (per-op kernels replayed as a HIP graph),
   * the reference CPU runtime (compiled reference sources when available, else the oracle restatement), on the
     host, one core, on a bounded sample.
 HBM traffic per launch of the dominant kernel comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
@@ -82,6 +83,24 @@ def bench_prefill(ctx, m, cfg, n: int = 2048):
     ms = ctx.timer_stop()
     kv.close()
     return ms
+
+
+def bench_decode_4b(ctx, steps: int = 64, warmup: int = 8):
+    """Qwen3-4B greedy decode at batch 1 (seed-1 N(0, 0.02) weights) after the same 32-token prompt: the per-op
+    kernels of one token replayed as a HIP graph (the one-launch kernel covers Qwen3-0.6B only)."""
+    cfg = S.QWEN3_4B
+    m = S.Model(ctx, cfg).synthesize(1, 0.02)
+    try:
+        ms, mean_kv, _ = bench_decode(ctx, m, cfg, steps, warmup)
+        path = m.decode_path()
+    finally:
+        m.close()
+    per_tok = ms / steps
+    bpt = decode_bytes_per_token(cfg, mean_kv)
+    gbs = bpt / (per_tok * 1e-3) / 1e9
+    return {"workload": "Qwen3-4B greedy decode, batch 1, 32-token prompt", "decode_path": path, "steps": steps,
+            "ms_per_token": round(per_tok, 4), "tok_s": round(1000.0 / per_tok, 1), "bytes_per_token": int(bpt),
+            "hbm_gbs": round(gbs, 1), "hbm_roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 RAGGED_SEQS, RAGGED_STEPS, RAGGED_MIN, RAGGED_MAX = 16, 64, 64, 4096
@@ -293,6 +312,7 @@ def main() -> None:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-ragged", action="store_true", help="skip the Qwen3-4B ragged decode measurement")
     ap.add_argument("--no-ops", action="store_true", help="skip the GEMV / group-quantized matmul microbenchmarks")
+    ap.add_argument("--no-4b", action="store_true", help="skip the Qwen3-4B batch-1 decode measurement")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -318,6 +338,7 @@ def main() -> None:
     m.close()
     ops_gemv, ops_qmm = (None, None) if args.no_ops else bench_ops(ctx)
     ragged = None if args.no_ragged else bench_ragged(ctx)
+    decode_4b = None if args.no_4b else bench_decode_4b(ctx)
     ctx.close()
 
     if path in ("xcd", "persistent"):
@@ -363,6 +384,7 @@ def main() -> None:
         "gemv_f16_bs1": ops_gemv,
         "qmm_g64": ops_qmm,
         "ragged_4b": ragged,
+        "decode_4b": decode_4b,
         "cpu_baseline": cpu,
         "generated_tokens_head": [int(t) for t in toks[:8]],
     }

@@ -54,8 +54,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   // The chunk's keys, as MFMA B operands: the wave's keys are 64 w .. 64 w + 63 of the chunk; lane (key kl, group kg)
   // = (lane % 16, lane / 16) holds the 16 bytes of dims 32 t + 8 kg of its key for t = 0..3, as stored (fp16 keys are
   // exact). Keys past the chunk's end load the last key (their scores are never stored), so the loads need no
-  // branch. They are issued before the query is staged; loads complete in issue order, so a wait for the query
-  // (issued first on the plain path) leaves them in flight.
+  // branch. They are issued right after the query's own loads; loads complete in issue order, so the staging waits
+  // for the query only and the keys stay in flight.
   const int kl = lane & 15, kg = lane >> 4;
   u32x4 raw[16];  // keys: [tile t4][dim step t] -> raw[4 t4 + t]; values: the row layout below
   auto load_keys = [&]() {
@@ -68,20 +68,36 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   };
 
   if constexpr (FUSED) {
+    // The wave's rows vi = wid, wid + 4, ... of the G query heads, the key head and the value head (rows past G + 1
+    // load row G + 1 again, unused), the q/k gains and the RoPE table row: all requested before the keys, and the
+    // norms computed while the keys are in flight.
+    constexpr int NV = (G + 2 + 3) / 4;
+    float x0v[NV], x1v[NV];
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int vi = min(wid + 4 * t, G + 1);
+      const float* src = vi < G ? row + (g * G + vi) * HD : row + (vi == G ? a.nq : a.nq + a.nkv) * HD + g * HD;
+      x0v[t] = src[lane];
+      x1v[t] = src[lane + 64];
+    }
+    const float qg0 = static_cast<float>(a.q_gain[lane]), qg1 = static_cast<float>(a.q_gain[lane + 64]);
+    const float kg0 = static_cast<float>(a.k_gain[lane]), kg1 = static_cast<float>(a.k_gain[lane + 64]);
+    const float rc = a.rope_cos[static_cast<size_t>(qpos) * (HD / 2) + lane];
+    const float rs = a.rope_sin[static_cast<size_t>(qpos) * (HD / 2) + lane];
+    __builtin_amdgcn_sched_barrier(0);
     load_keys();
-    const float* cr = a.rope_cos + static_cast<size_t>(qpos) * (HD / 2);
-    const float* sr = a.rope_sin + static_cast<size_t>(qpos) * (HD / 2);
-    for (int vi = wid; vi < G + 2; vi += 4) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int vi = wid + 4 * t;
+      if (vi >= G + 2) break;  // wave-uniform
+      float x0 = x0v[t], x1 = x1v[t];
       if (vi < G) {
-        const float* src = row + (g * G + vi) * HD;
-        float x0 = src[lane], x1 = src[lane + 64];
-        norm_rope_pair(x0, x1, a.q_gain, a.eps, cr, sr, lane);
+        norm_rope_pair(x0, x1, qg0, qg1, a.eps, rc, rs);
         qs[vi][lane] = x0;
         qs[vi][lane + 64] = x1;
       } else if (vi == G) {
-        const float* src = row + a.nq * HD + g * HD;
-        float x0 = src[lane], x1 = src[lane + 64];
-        norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
+        norm_rope_pair(x0, x1, kg0, kg1, a.eps, rc, rs);
         const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
         kn[lane] = static_cast<float>(h0);
         kn[lane + 64] = static_cast<float>(h1);
@@ -90,8 +106,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
           kb[static_cast<size_t>(qpos) * HD + lane + 64] = h1;
         }
       } else {
-        const float* src = row + (a.nq + a.nkv) * HD + g * HD;
-        const f16 h0 = static_cast<f16>(src[lane]), h1 = static_cast<f16>(src[lane + 64]);
+        const f16 h0 = static_cast<f16>(x0), h1 = static_cast<f16>(x1);
         vn[lane] = static_cast<float>(h0);
         vn[lane + 64] = static_cast<float>(h1);
         if (s == nact - 1) {
