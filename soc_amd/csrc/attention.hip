@@ -289,8 +289,18 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   }
   __syncthreads();
   if (!last) return;  // the last block reads every partial with device-scope loads
-  // combine: every chunk's (m, l) first, all loads in flight at once, then the weighted sums over chunks with the
-  // partial outputs fetched sixteen chunks at a time (the loads are independent; only their sum is ordered)
+  // combine: the first sixteen chunks' partial outputs of the thread's outputs and every chunk's (m, l) are
+  // requested together (one memory round trip for up to 16 chunks); then the chunk weights, and the weighted sums
+  // over chunks in chunk order (further chunks fetched sixteen at a time, no branch between the loads)
+  constexpr int OPT = (G * HD + 255) / 256;  // outputs per thread
+  float v0[OPT][16];
+#pragma unroll
+  for (int q = 0; q < OPT; ++q) {
+    const int idx = min(tid + 256 * q, G * HD - 1);
+    const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + idx / HD) * a.max_split * stride + idx % HD;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v0[q][u] = ld_dev(p0 + min(u, nact - 1) * stride);
+  }
   for (int idx = tid; idx < G * nact; idx += 256) {
     const int j = idx / nact, t = idx % nact;
     const float* pj = a.part + ((static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split + t) * stride;
@@ -310,12 +320,18 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     lstat[tid] = L;
   }
   __syncthreads();
-  for (int idx = tid; idx < G * HD; idx += 256) {
+#pragma unroll
+  for (int q = 0; q < OPT; ++q) {
+    const int idx = tid + 256 * q;
+    if (idx >= G * HD) break;
     const int j = idx / HD, i = idx % HD;
     const float* p0 = a.part + (static_cast<size_t>(b) * a.nq + g * G + j) * a.max_split * stride + i;
     const float* ej = cm[j];
     float O = 0.0f;
-    for (int t = 0; t < nact; t += 16) {  // 16 loads in flight per round, no branch between them; sums in order
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (u < nact) O += v0[q][u] * ej[u];
+    for (int t = 16; t < nact; t += 16) {
       float v[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] = ld_dev(p0 + min(t + u, nact - 1) * stride);
