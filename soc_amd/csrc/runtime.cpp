@@ -820,21 +820,41 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
   return SOC_OK;
 }
 
-// Whether prefill projections see each activation as a hi/lo fp16 pair (the default: 22 significant bits, close to
-// the reference's fp32 activations) or, with SOC_PREFILL_SPLIT=0, as one fp16 value (half the MFMA work; within the
-// logit tolerance at 2048 tokens of the N(0, 0.02) model, but with little margin on models with larger weights).
-bool prefill_hilo() {
+// Which prefill projections see their activations as hi/lo fp16 pairs (22 significant bits, close to the
+// reference's fp32 activations) rather than as one fp16 value (half the MFMA work, less precision margin): a mask of
+// kSplitQkv | kSplitO | kSplitGateUp | kSplitDown. Default: the QKV projection only — measured on the Qwen3-0.6B
+// fixtures, the pairs on QKV keep most of the precision the pairs on all four give (largest logit error 9.6e-3 vs
+// 6.6e-3 on the N(0, 0.05) model, 1.2e-3 vs 7.7e-4 at 2048 tokens; none: 1.43e-2 / 1.6e-3; tolerance 2e-2) at 84 %
+// of the time (2048 tokens: 6.74 vs 8.06 ms). SOC_PREFILL_SPLIT: "1" / "all" = all four, "0" = none, otherwise a
+// comma list of qkv, o, gateup, down.
+enum { kSplitQkv = 1, kSplitO = 2, kSplitGateUp = 4, kSplitDown = 8, kSplitAll = 15 };
+int prefill_split_mask() {
   const char* sp = std::getenv("SOC_PREFILL_SPLIT");
-  return !(sp != nullptr && sp[0] == '0');
+  if (sp == nullptr) return kSplitQkv;
+  if (sp[0] == '0') return 0;
+  const std::string v(sp);
+  int mask = 0;
+  size_t b = 0;
+  while (b <= v.size()) {
+    const size_t e = std::min(v.find(',', b), v.size());
+    const std::string t = v.substr(b, e - b);
+    if (t == "qkv") mask |= kSplitQkv;
+    if (t == "o") mask |= kSplitO;
+    if (t == "gateup") mask |= kSplitGateUp;
+    if (t == "down") mask |= kSplitDown;
+    if (t == "1" || t == "all") mask |= kSplitAll;
+    b = e + 1;
+  }
+  return mask;
 }
 
-// Prefill projections on fp32 activations: MFMA when K allows, on fp16 activations or their hi/lo pairs
-// (prefill_hilo); SOC_PREFILL_GEMM=fma selects the FMA kernel.
-hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s) {
+// Prefill projections on fp32 activations: MFMA when K allows, on fp16 activations or their hi/lo pairs (hi/lo
+// when prefill_split_mask() has any of the bits `which`); SOC_PREFILL_GEMM=fma selects the FMA kernel.
+hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s, int which = kSplitAll) {
   const char* mode = std::getenv("SOC_PREFILL_GEMM");
   const bool fma = mode != nullptr && std::strcmp(mode, "fma") == 0;
   if (!fma && soc::gemm_mfma_supported(g)) {
-    return soc::launch_gemm_mfma(g, epi, prefill_hilo(), s);
+    return soc::launch_gemm_mfma(g, epi, (prefill_split_mask() & which) != 0, s);
   }
   return soc::launch_gemm_f32a(g, epi, s);
 }
@@ -1813,14 +1833,19 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
   const int H = c.hidden_size;
   if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off));
   const bool split = prefill_split_path(m);
-  f16* const pl = prefill_hilo() ? w.pl : nullptr;  // lo parts of the activations, or none
-  f16* const ql = prefill_hilo() ? w.ql : nullptr;
+  // lo parts of each projection's activations, or none (prefill_split_mask)
+  const int smask = prefill_split_mask();
+  f16* const pl_qkv = (smask & kSplitQkv) ? w.pl : nullptr;
+  f16* const pl_o = (smask & kSplitO) ? w.pl : nullptr;
+  f16* const pl_gu = (smask & kSplitGateUp) ? w.pl : nullptr;
+  f16* const ql = (smask & kSplitDown) ? w.ql : nullptr;
   for (int l = 0; m->qbits == 0 && l < c.num_hidden_layers; ++l) {  // fp16 models
     const DevLayer& L = m->layers[l];
     soc::GemmArgs g{};
     bool qkv_fused = false;
     if (split) {
-      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, pl, s)) != hipSuccess)
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, pl_qkv, s)) !=
+          hipSuccess)
         return hip_fail(e, "rmsnorm");
       // QKV projection with the per-head q/k RMSNorm + RoPE, q output and K/V cache append in its epilogue
       // (SOC_PREFILL_QKV=separate: plain projection, then the q/k-norm kernel)
@@ -1828,7 +1853,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
       qkv_fused = qm == nullptr || std::strcmp(qm, "separate") != 0;
       soc::GemmSplitArgs g3{};
       g3.ah = w.ph;
-      g3.al = pl;
+      g3.al = pl_qkv;
       g3.lda = H;
       g3.w = L.wqkv;
       g3.c = w.qkv;
@@ -1867,7 +1892,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
       g.M = n;
       g.N = m->qkv_rows;
       g.K = H;
-      if ((e = prefill_gemm(g, soc::EPI_STORE, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
+      if ((e = prefill_gemm(g, soc::EPI_STORE, s, kSplitQkv)) != hipSuccess) return hip_fail(e, "gemm qkv");
     }
     soc::QkNormRopeArgs q{};
     q.qkv = w.qkv;
@@ -1899,7 +1924,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     a.pos_base = pos_off;
     a.out = split ? nullptr : w.attn;
     a.out_hi = split ? w.ph : nullptr;
-    a.out_lo = split ? pl : nullptr;
+    a.out_lo = split ? pl_o : nullptr;
     a.ld_out = m->qd;
     a.part = w.part;
     a.counters = w.attn_counters;
@@ -1908,12 +1933,13 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     if ((e = prefill_attention(a, w.attn, s)) != hipSuccess) return hip_fail(e, "attention prefill");
     const int I = c.intermediate_size;
     if (split) {
-      if ((e = split_gemm(w.ph, pl, m->qd, L.wo, nullptr, w.x, nullptr, nullptr, H, n, H, m->qd, soc::EPI_RESIDUAL,
-                          s)) != hipSuccess)
+      if ((e = split_gemm(w.ph, pl_o, m->qd, L.wo, nullptr, w.x, nullptr, nullptr, H, n, H, m->qd,
+                          soc::EPI_RESIDUAL, s)) != hipSuccess)
         return hip_fail(e, "gemm o");
-      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, nullptr, w.ph, pl, s)) != hipSuccess)
+      if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, nullptr, w.ph, pl_gu, s)) !=
+          hipSuccess)
         return hip_fail(e, "rmsnorm");
-      if ((e = split_gemm(w.ph, pl, H, L.wgate, L.wup, nullptr, w.qh, ql, I, n, I, H, soc::EPI_SWIGLU, s)) !=
+      if ((e = split_gemm(w.ph, pl_gu, H, L.wgate, L.wup, nullptr, w.qh, ql, I, n, I, H, soc::EPI_SWIGLU, s)) !=
           hipSuccess)
         return hip_fail(e, "gemm gate/up");
       if ((e = split_gemm(w.qh, ql, I, L.wdown, nullptr, w.x, nullptr, nullptr, H, n, H, I, soc::EPI_RESIDUAL, s)) !=
@@ -1930,7 +1956,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = H;
     g.K = m->qd;
-    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm o");
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s, kSplitO)) != hipSuccess) return hip_fail(e, "gemm o");
     if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.post_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
       return hip_fail(e, "rmsnorm");
     g = soc::GemmArgs{};
@@ -1943,7 +1969,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = I;
     g.K = H;
-    if ((e = prefill_gemm(g, soc::EPI_SWIGLU, s)) != hipSuccess) return hip_fail(e, "gemm gate/up");
+    if ((e = prefill_gemm(g, soc::EPI_SWIGLU, s, kSplitGateUp)) != hipSuccess) return hip_fail(e, "gemm gate/up");
     g = soc::GemmArgs{};
     g.a = w.h;
     g.lda = I;
@@ -1953,7 +1979,7 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     g.M = n;
     g.N = H;
     g.K = I;
-    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s)) != hipSuccess) return hip_fail(e, "gemm down");
+    if ((e = prefill_gemm(g, soc::EPI_RESIDUAL, s, kSplitDown)) != hipSuccess) return hip_fail(e, "gemm down");
   }
   // logits of the last row (with the greedy token), then of the other requested rows
   soc::LmHeadArgs h{};

@@ -118,15 +118,19 @@ def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv
         m.close()
 
 
-@pytest.mark.parametrize("hilo", ["0", "1"])
+@pytest.mark.parametrize("hilo", ["0", "1", "default", "o,down"])
 @pytest.mark.parametrize("n", [150, 300])
 def test_prefill_split_gemm_matches_staged_kernel(gpu_ctx, monkeypatch, n, hilo):
     """The prefill projections on fp16 activations written by their producers (RMSNorm, attention and the SwiGLU
     epilogue; direct-to-LDS pipeline) form the same products in the same order as the register-staged MFMA kernel
-    that converts the fp32 activations itself, both with hi/lo pairs (default) and with single fp16 activations
-    (SOC_PREFILL_SPLIT=0): logits are bit-identical, for a single prefill (row counts off the 64/128-row tiles) and
-    a chunked one. Qwen3-0.6B-wide layers (hidden 1024, 16 q / 8 kv heads, 3072)."""
-    monkeypatch.setenv("SOC_PREFILL_SPLIT", hilo)
+    that converts the fp32 activations itself, with hi/lo pairs on every projection (SOC_PREFILL_SPLIT=1), on none
+    (0), on the QKV projection only (the default) and on another mix: logits are bit-identical, for a single prefill
+    (row counts off the 64/128-row tiles) and a chunked one. Qwen3-0.6B-wide layers (hidden 1024, 16 q / 8 kv heads,
+    3072)."""
+    if hilo == "default":
+        monkeypatch.delenv("SOC_PREFILL_SPLIT", raising=False)
+    else:
+        monkeypatch.setenv("SOC_PREFILL_SPLIT", hilo)
     cfg = S.QwenConfig(vocab_size=512, hidden_size=1024, num_hidden_layers=2, num_attention_heads=16,
                        num_key_value_heads=8, intermediate_size=3072, tie_word_embeddings=True)
     m = _gpu_model(gpu_ctx, cfg, S.synth_weights(cfg, 21))
@@ -341,15 +345,18 @@ def test_one_launch_wait_timeout_recovers(gpu_ctx, mode, monkeypatch):
         m.close()
 
 
-@pytest.mark.parametrize("split", ["1", "0"])
+@pytest.mark.parametrize("split", ["1", "0", "default"])
 def test_prefill_2048_matches_reference(gpu_ctx, golden, split, monkeypatch):
     """The benchmarked prefill: Qwen3-0.6B (seed-1 weights), 2048 uniform-random prompt ids, all 28 layers; last-row
     logits (top 64, 512 sampled ids) and greedy token against the restatement's fixture (pinned bit for bit to the
-    compiled reference at 256 tokens of the same model). split=1 (the default) feeds the projections hi/lo fp16
-    pairs, split=0 single fp16 activations; both errors are printed."""
+    compiled reference at 256 tokens of the same model). split=1 feeds every projection hi/lo fp16 pairs, split=0
+    single fp16 activations, the default hi/lo pairs on the QKV projection only; the errors are printed."""
     g = golden("prefill2048.npz")
     cfg = S.QWEN3_0_6B
-    monkeypatch.setenv("SOC_PREFILL_SPLIT", split)
+    if split == "default":
+        monkeypatch.delenv("SOC_PREFILL_SPLIT", raising=False)
+    else:
+        monkeypatch.setenv("SOC_PREFILL_SPLIT", split)
     m = S.Model(gpu_ctx, cfg).synthesize(int(g["weight_seed"]), 0.02)
     n = int(g["n"])
     kv = S.KVCache(m, 1, n)
