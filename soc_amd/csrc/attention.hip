@@ -11,6 +11,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace soc {
 
@@ -689,7 +690,9 @@ constexpr size_t pairs_lds_bytes() {
 }
 }  // namespace
 
-template <int HB, int R>
+// LOQ / LOP = false: q / p enter as single fp16 values (round to nearest) instead of hi/lo pairs (one MFMA chain
+// fewer each).
+template <int HB, int R, bool LOQ, bool LOP>
 __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) {
   static_assert(HB * R == 8, "8 waves");
   extern __shared__ __attribute__((aligned(16))) _Float16 plds[];
@@ -737,7 +740,7 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
           __asm__ volatile("" : "+v"(v));
           const _Float16 h = static_cast<_Float16>(v);
           qh[ks][i] = h;
-          qlo[ks][i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
+          if constexpr (LOQ) qlo[ks][i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
         }
       }
     }
@@ -801,7 +804,7 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
         for (int ks = 0; ks < 8; ++ks) {
           const fa_h8 ka = *reinterpret_cast<const fa_h8*>(&Ks[ql * HD + ((2 * ks + hb) ^ (ql & 15)) * 8]);
           sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
-          sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sl, 0, 0, 0);
+          if constexpr (LOQ) sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sl, 0, 0, 0);
         }
         // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
         float sv[16];
@@ -844,20 +847,25 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
             const float p0 = sv[k2 * 8 + i], p1 = sv[k2 * 8 + i + 1];
-            const float h0 = __uint_as_float(__float_as_uint(p0) & 0xFFFFE000u);
-            const float h1 = __uint_as_float(__float_as_uint(p1) & 0xFFFFE000u);
-            const auto hv = __builtin_amdgcn_cvt_pkrtz(h0, h1);
-            const auto lv = __builtin_amdgcn_cvt_pkrtz(p0 - h0, p1 - h1);
-            ph8[i] = hv[0];
-            ph8[i + 1] = hv[1];
-            pl8[i] = lv[0];
-            pl8[i + 1] = lv[1];
+            if constexpr (LOP) {
+              const float h0 = __uint_as_float(__float_as_uint(p0) & 0xFFFFE000u);
+              const float h1 = __uint_as_float(__float_as_uint(p1) & 0xFFFFE000u);
+              const auto hv = __builtin_amdgcn_cvt_pkrtz(h0, h1);
+              const auto lv = __builtin_amdgcn_cvt_pkrtz(p0 - h0, p1 - h1);
+              ph8[i] = hv[0];
+              ph8[i + 1] = hv[1];
+              pl8[i] = lv[0];
+              pl8[i + 1] = lv[1];
+            } else {
+              ph8[i] = static_cast<_Float16>(p0);
+              ph8[i + 1] = static_cast<_Float16>(p1);
+            }
           }
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             const fa_h8 va = read_vt(Vt, db, k2);
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph8, o[db], 0, 0, 0);
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl8, o[db], 0, 0, 0);
+            if constexpr (LOP) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl8, o[db], 0, 0, 0);
           }
         }
       }
@@ -925,17 +933,26 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
 }
 
 namespace {
-template <int HB>
-hipError_t launch_pairs(const AttnArgs& a, hipStream_t s) {
+template <int HB, bool LOQ, bool LOP>
+hipError_t launch_pairs_lo(const AttnArgs& a, hipStream_t s) {
   constexpr int R = 8 / HB;
   constexpr size_t lds = pairs_lds_bytes<HB, R>();
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_prefill_pairs<HB, R>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(lds));
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(k_attention_prefill_pairs<HB, R, LOQ, LOP>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(lds));
   if (attr != hipSuccess) return attr;
   const int nqt = (a.B + 31) / 32;
-  hipLaunchKernelGGL((k_attention_prefill_pairs<HB, R>), dim3(((nqt + 1) / 2) * a.nkv), dim3(512), lds, s, a);
+  hipLaunchKernelGGL((k_attention_prefill_pairs<HB, R, LOQ, LOP>), dim3(((nqt + 1) / 2) * a.nkv), dim3(512), lds, s, a);
   return hipGetLastError();
+}
+// SOC_PREFILL_ATTN_SPLIT=0: q and p as single fp16 values; =q: hi/lo for q only; =p: for p only
+template <int HB>
+hipError_t launch_pairs(const AttnArgs& a, hipStream_t s) {
+  const char* e = std::getenv("SOC_PREFILL_ATTN_SPLIT");
+  if (e != nullptr && e[0] == '0') return launch_pairs_lo<HB, false, false>(a, s);
+  if (e != nullptr && e[0] == 'q') return launch_pairs_lo<HB, true, false>(a, s);
+  if (e != nullptr && e[0] == 'p') return launch_pairs_lo<HB, false, true>(a, s);
+  return launch_pairs_lo<HB, true, true>(a, s);
 }
 }  // namespace
 
