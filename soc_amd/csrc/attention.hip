@@ -411,12 +411,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_v(const float* x, int T, i
   const int nv = H / 4;
   const float* xr = x + static_cast<size_t>(t) * H;
   f32x4 v[MAXV];
+  f16x4 gv[MAXV];  // the gains, requested with the row (no second round trip after the reduction)
   float ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < MAXV; ++e) {
-    const int i = lane + 64 * e;
-    v[e] = i < nv ? *reinterpret_cast<const f32x4*>(xr + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int i = min(lane + 64 * e, nv - 1);
+    v[e] = *reinterpret_cast<const f32x4*>(xr + 4 * i);  // pieces past the row reload its last one: zeroed below
+    gv[e] = *reinterpret_cast<const f16x4*>(gain + 4 * i);
   }
+#pragma unroll
+  for (int e = 0; e < MAXV; ++e)
+    if (lane + 64 * e >= nv) v[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int e = 0; e < MAXV; ++e)
 #pragma unroll
@@ -427,10 +432,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_v(const float* x, int T, i
   for (int e = 0; e < MAXV; ++e) {
     const int i = lane + 64 * e;
     if (i >= nv) break;
-    const f16x4 gv = *reinterpret_cast<const f16x4*>(gain + 4 * i);
     f32x4 y;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) y[c] = v[e][c] * scale * static_cast<float>(gv[c]);
+    for (int c = 0; c < 4; ++c) y[c] = v[e][c] * scale * static_cast<float>(gv[e][c]);
     const size_t o = static_cast<size_t>(t) * H + 4 * i;
     if (yf) *reinterpret_cast<f32x4*>(yf + o) = y;
     if (yh) {
