@@ -5,7 +5,7 @@ a C++ host runtime), with the reference's C++ host classes on top of it in inclu
 sources, the in-tree build, and a ctypes binding used by the tests and the benchmark.
 """
 from .capi import (  # noqa: F401
-    QWEN3_0_6B, QWEN3_4B, Bundle, Context, Tokenizer, KVCache, Model, QwenConfig, SocError, decode, decode_batch, decode_batch_steps,
+    QWEN3_0_6B, QWEN3_1_7B, QWEN3_4B, QWEN3_8B, Bundle, Context, Tokenizer, KVCache, Model, QwenConfig, SocError, decode, decode_batch, decode_batch_steps,
     decode_steps, decode_steps_noalloc, dequant, gemv_f16,
     lib, load_bundle, prefill, qmm, quantize_group, sample_topk, synth_codes, synth_int_uniform, synth_normal_f16, synth_tokens, synth_uniform_f16,
     synth_weights, tensor_specs,

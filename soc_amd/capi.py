@@ -61,11 +61,16 @@ class QwenConfig:
         return self.num_key_value_heads * self.head_dim
 
 
-# Qwen3-0.6B and Qwen3-4B shapes (the configs this project measures).
+# Dense Qwen3 shapes within this build's envelope (Hugging Face config.json of each model); 0.6B and 4B are the
+# benchmarked ones.
 QWEN3_0_6B = QwenConfig(vocab_size=151936, hidden_size=1024, num_hidden_layers=28, num_attention_heads=16,
                         num_key_value_heads=8, intermediate_size=3072)
+QWEN3_1_7B = QwenConfig(vocab_size=151936, hidden_size=2048, num_hidden_layers=28, num_attention_heads=16,
+                        num_key_value_heads=8, intermediate_size=6144)
 QWEN3_4B = QwenConfig(vocab_size=151936, hidden_size=2560, num_hidden_layers=36, num_attention_heads=32,
                       num_key_value_heads=8, intermediate_size=9728)
+QWEN3_8B = QwenConfig(vocab_size=151936, hidden_size=4096, num_hidden_layers=36, num_attention_heads=32,
+                      num_key_value_heads=8, intermediate_size=12288, tie_word_embeddings=False)
 
 
 def tensor_specs(cfg: QwenConfig) -> list[tuple[str, tuple[int, ...]]]:
