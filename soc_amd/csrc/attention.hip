@@ -41,7 +41,10 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qpos = (a.pos != nullptr ? a.pos[b] : b) + a.pos_base;
   const int S = qpos + 1;
-  const int nact = (S + a.chunk - 1) / a.chunk;
+  // up to 256 keys one block per (row, KV head) takes them all (no partials and no combine); longer rows use the
+  // caller's chunk (single-sequence decode splits them finer than 256 for more blocks)
+  const int chunk = S <= 256 ? 256 : a.chunk;
+  const int nact = (S + chunk - 1) / chunk;
   if (s >= nact) return;
   const int slot = a.slot != nullptr ? a.slot[b] : a.slot_base;
   const size_t head_base = static_cast<size_t>(slot) * a.slot_stride + static_cast<size_t>(a.layer) * a.layer_stride +
@@ -49,8 +52,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   f16* kb = a.kcache + head_base;
   f16* vb = a.vcache + head_base;
   const float* row = a.qkv + static_cast<size_t>(b) * a.ld_qkv;
-  const int c0 = s * a.chunk;
-  const int n = min(a.chunk, S - c0);
+  const int c0 = s * chunk;
+  const int n = min(chunk, S - c0);
 
   // The chunk's keys, as MFMA B operands: the wave's keys are 64 w .. 64 w + 63 of the chunk; lane (key kl, group kg)
   // = (lane % 16, lane / 16) holds the 16 bytes of dims 32 t + 8 kg of its key for t = 0..3, as stored (fp16 keys are
