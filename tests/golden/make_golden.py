@@ -2,7 +2,7 @@
 
 Runs only where the reference checkout exists: `make -C oracle ref` compiles /root/reference/Mac/cpu/src (the
 13 hot-path files) plus oracle/ref_driver.cpp into oracle/_ref/libsocref.so, and this script drives it. The
-fixtures are data (inputs and outputs); the GPU box and the CPU test suite read them without the reference.
+fixtures are data (inputs and outputs); the GPU tests and the CPU test suite read them without the reference.
 
 Fixtures:
   dtype_f16.npz     Float16ToFloat32 (Mac/cpu/src/dtype.cpp:76-106) of all 65,536 codes, and Float32ToFloat16

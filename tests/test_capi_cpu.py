@@ -76,7 +76,7 @@ def test_calls_without_gpu_fail_cleanly():
 
     h = C.c_void_p()
     rc = S.lib().soc_ctx_create(0, C.byref(h))
-    if rc == capi.SOC_OK:  # a GPU is present (running on the GPU box)
+    if rc == capi.SOC_OK:  # a GPU is present
         S.lib().soc_ctx_destroy(h)
         pytest.skip("GPU present")
     assert rc in (capi.SOC_ERR_HIP, capi.SOC_ERR_INVALID)
