@@ -673,7 +673,10 @@ hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s) {
   // either); above 16384 row groups the row-per-wave kernel has waves enough to cover its staging
   const int groups = (a.N + (epi == EPI_SWIGLU ? 2 : R) - 1) / (epi == EPI_SWIGLU ? 2 : R);
   const bool ks = mode != nullptr ? std::strcmp(mode, "ks") == 0 : groups < 16384;
-  if (ks && a.K % 8 == 0) {
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.xh) |
+                          reinterpret_cast<uintptr_t>(a.gain) | reinterpret_cast<uintptr_t>(a.w) |
+                          reinterpret_cast<uintptr_t>(a.w2);
+  if (ks && a.K % 8 == 0 && align % 16 == 0) {  // 16-byte loads of every operand
     switch (epi) {
       case EPI_STORE: hipLaunchKernelGGL((k_gemv_ks<R, U, EPI_STORE>), dim3((a.N + R - 1) / R), block, 0, s, a); break;
       case EPI_RESIDUAL:
