@@ -315,7 +315,8 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(LmHeadArgs a) {
 // Each lane streams 16-byte chunks of a row's codes (16 int8 or 32 int4 codes; a chunk never crosses a scale
 // group). The codes become exact fp16 pairs without per-code conversions: the biased code (code + 128, or the
 // nibble + 8) is placed in the low mantissa bits of 1024.0 (fp16 0x64xx) by one byte permute (int8) or one
-// mask-or (int4), and one packed fp16 subtract of 1152 (or 1032) leaves the code itself. v_dot2_f32_f16 then
+// mask-xor (int4), and one packed fp16 subtract of 1152 (or 1032) leaves the code itself (int4 nibbles in bits
+// 4..7: one packed fma by 1/16 minus 72, so that half the nibbles need no shift). v_dot2_f32_f16 then
 // accumulates code pairs times fp16 activation pairs in fp32 (products exact), and one fma per chunk applies the
 // group scale. The activations are staged once per block in LDS as fp16 pairs in the order the codes unpack
 // (int4: k and k + 4 of each group of 8). L lanes share a row (64, or 32 / 16 for short rows) and each lane
@@ -339,12 +340,18 @@ __device__ __forceinline__ void unpack_codes(const u32x4& w, qh2 (&p)[BITS == 8 
     }
   } else {
     const qh2 bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const qh2 bias16 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const qh2 sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t u = w[j] ^ 0x88888888u;  // nibble + 8 per nibble
-#pragma unroll
-      for (int i = 0; i < 4; ++i)  // k = 8j + i and 8j + i + 4
-        p[4 * j + i] = as_qh2(((u >> (4 * i)) & 0x000F000Fu) | 0x64006400u) + bias;
+      // k = 8j + i and 8j + i + 4. The mask keeps two nibbles n, the xor adds 8 to them (n ^ 8 = code + 8) and
+      // sets the exponent of 1024 in the same step: nibbles i = 0, 2 land in mantissa bits 0..3 (1024 + n - 1032),
+      // i = 1, 3 in bits 4..7 (1024 + 16 n, times 1/16 minus 72: exact)
+      const uint32_t u = w[j], v = u >> 8;
+      p[4 * j + 0] = as_qh2((u & 0x000F000Fu) ^ 0x64086408u) + bias;
+      p[4 * j + 1] = as_qh2((u & 0x00F000F0u) ^ 0x64806480u) * sixteenth + bias16;
+      p[4 * j + 2] = as_qh2((v & 0x000F000Fu) ^ 0x64086408u) + bias;
+      p[4 * j + 3] = as_qh2((v & 0x00F000F0u) ^ 0x64806480u) * sixteenth + bias16;
     }
   }
 }
