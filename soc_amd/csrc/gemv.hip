@@ -440,8 +440,8 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
 // reads (rows M..15 hold zeros, so no lane needs a select). D then holds, per lane, tokens 4 q .. 4 q + 3 of row r,
 // so the lane applies its own row's group scales (loaded with the codes). Each group's codes go to a fresh
 // accumulator whose sum is scaled and added to the result: the product per element is code * scale exactly as in
-// the dequantized weight. Tall matrices only (the LM head): at 151936 x 1024, batch 8, int8 runs at 60 % of HBM
-// bandwidth (the dot-product kernel: 24 %), int4 at 42 % (16 %).
+// the dequantized weight. Tall matrices only (the LM head): at 151936 x 1024, batch 8, int8 runs at 58 % of HBM
+// bandwidth (the dot-product kernel: 24 %), int4 at 47 % (16 %).
 template <int BITS>
 __global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
   extern __shared__ __attribute__((aligned(16))) _Float16 qm_lds[];  // activations [16][K + 8]
@@ -534,10 +534,11 @@ __global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sc, acc[i]);
       } else {  // dwords 0, 1: group 2 idx at k = 128 idx + kb + 0..15; dwords 2, 3: group 2 idx + 1 (k + 64)
-        u32x4 w = b.w[s];
-        const auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
-        const auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-        w = u32x4{s02[0], s13[0], s02[1], s13[1]};
+        // in place: the chunk's registers are not read again before the next load into them
+        const auto s02 = __builtin_amdgcn_permlane32_swap(b.w[s][0], b.w[s][2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(b.w[s][1], b.w[s][3], false, false);
+        b.w[s] = u32x4{s02[0], s13[0], s02[1], s13[1]};
+        const u32x4 w = b.w[s];
         qh2 p[16];
         unpack_codes<4>(w, p);
         f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
