@@ -428,27 +428,27 @@ __global__ __launch_bounds__(256) void k_qmm(QmmArgs a) {
   }
 }
 
-// The same product for 2 <= M <= 16 rows on matrix cores (v_mfma_f32_16x16x32_f16, D[token][row] = X . W^T): a
-// block stages the activations once in LDS and its 8 waves then stream 16-row tiles of codes (tiles blockIdx.x,
-// blockIdx.x + gridDim.x, ...), each tile in chunks of eight 16-byte loads per lane with the next chunk (of this or
-// the next tile) in flight. Lane (r, q) = (lane % 16, lane / 16) loads 16 bytes of row r per instruction, 64 bytes
-// of the row across the four q: int8: the 16 codes k = 64 g + 16 q + 0..15 of group g; int4: the 32 codes
-// k = 128 c + 32 q + 0..31 of groups 2c (q < 2) and 2c + 1 (q >= 2), regrouped by one v_permlane32_swap per dword
-// pair so that lane q holds 16 codes of each group at k offset 16 * (0, 2, 1, 3)[q]. The codes unpack exactly to
-// fp16 as in k_qmm and are the MFMA's B operand as they come out; its A operand is the token rows, staged in LDS as
-// fp16 [16][K + 8] in the same k order (int4: within each 8 k, the order 0 4 1 5 2 6 3 7) and read with 16-byte LDS
-// reads (rows M..15 hold zeros, so no lane needs a select). D then holds, per lane, tokens 4 q .. 4 q + 3 of row r,
-// so the lane applies its own row's group scales (loaded with the codes). Each group's codes go to a fresh
-// accumulator whose sum is scaled and added to the result: the product per element is code * scale exactly as in
-// the dequantized weight. Tall matrices only (the LM head): at 151936 x 1024, batch 8, int8 runs at 58 % of HBM
-// bandwidth (the dot-product kernel: 24 %), int4 at 47 % (16 %).
+// The same product for 2 <= M <= 16 rows on matrix cores (v_mfma_f32_16x16x32_f16, D[token][row] = X . W^T): a block
+// stages the activations once in LDS and its 8 waves then stream 16-row tiles of codes (tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ...), each tile in chunks of eight (int8) or four (int4) 16-byte loads per lane with the
+// next chunk (of this or the next tile) in flight. Lane (r, q) = (lane % 16, lane / 16) loads 16 bytes of row r per
+// instruction, 64 bytes of the row across the four q: int8: the 16 codes k = 64 g + 16 q + 0..15 of group g; int4:
+// the 32 codes k = 128 c + 32 q + 0..31 of groups 2c (q < 2) and 2c + 1 (q >= 2), regrouped by one v_permlane32_swap
+// per dword pair so that lane q holds 16 codes of each group at k offset 16 * (0, 2, 1, 3)[q]. The codes unpack
+// exactly to fp16 as in k_qmm and are the MFMA's B operand as they come out; its A operand is the token rows, staged
+// in LDS as fp16 [16][K + 8] in the same k order (int4: within each 8 k, the order 0 4 1 5 2 6 3 7) and read with
+// 16-byte LDS reads (rows M..15 hold zeros, so no lane needs a select). D then holds, per lane,
+// tokens 4 q .. 4 q + 3 of row r, so the lane applies its own row's group scales (loaded with the codes). Each
+// group's codes go to a fresh accumulator whose sum is scaled and added to the result: the product per element is
+// code * scale exactly as in the dequantized weight. Tall matrices only (the LM head): at 151936 x 1024, batch 8,
+// int8 runs at 58 % of HBM bandwidth (the dot-product kernel: 24 %), int4 at 52 % (16 %).
 template <int BITS>
 __global__ __launch_bounds__(512, 4) void k_qmm_mfma(QmmArgs a) {
   extern __shared__ __attribute__((aligned(16))) _Float16 qm_lds[];  // activations [16][K + 8]
   const int K = a.K, G = K / 64, ldx = K + 8;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int rl = lane & 15, kq = lane >> 4;
-  constexpr int LPC = 8;                           // 16-byte code loads per lane per chunk
+  constexpr int LPC = BITS == 4 ? 4 : 8;           // 16-byte code loads per lane per chunk
   constexpr int GPC = BITS == 8 ? LPC : 2 * LPC;   // scale groups per chunk
   const int nload = BITS == 8 ? G : G / 2;         // code loads per lane over a row (64 bytes of the row each)
   const int nchunk = nload / LPC;                  // G % GPC == 0 (checked at launch)
@@ -832,8 +832,8 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
   return hipGetLastError();
 }
 
-// K a multiple of 512 (int8) or 1024 (int4): whole chunks of eight 16-byte loads per lane and 16-byte scale loads;
-// K <= 2040 (the activations fit 64 KB of LDS; at most eight 8-k runs per thread).
+// K a multiple of 512 (int8) or 1024 (int4): whole chunks of eight (int8) / four (int4) 16-byte loads per lane and
+// 16-byte scale loads; K <= 2040 (the activations fit 64 KB of LDS; at most eight 8-k runs per thread).
 bool qmm_mfma_supported(const QmmArgs& a, int bits) {
   const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
   return a.M >= 2 && a.M <= 16 && a.K % (bits == 8 ? 512 : 1024) == 0 && lds <= 64 * 1024 &&
@@ -849,7 +849,9 @@ hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
   const bool force_dot = mode != nullptr && std::strcmp(mode, "dot") == 0;
   if (qmm_mfma_supported(a, bits) && !force_dot && (force_mfma || a.N >= 16384)) {
     const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
-    const dim3 grid(std::min((a.N + 127) / 128, 512)), block(512);  // two 16-wave blocks per CU, tiles looped
+    // 8-wave blocks, two resident per CU, tiles looped; int4 (half-size chunks) with 768 blocks, the last third
+    // starting as the first blocks finish: 52 % of HBM bandwidth at 151936 x 1024, batch 8, against 48 % with 512
+    const dim3 grid(std::min((a.N + 127) / 128, bits == 4 ? 768 : 512)), block(512);
     if (bits == 8) hipLaunchKernelGGL(k_qmm_mfma<8>, grid, block, lds, s, a);
     else hipLaunchKernelGGL(k_qmm_mfma<4>, grid, block, lds, s, a);
     return hipGetLastError();
