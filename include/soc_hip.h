@@ -188,7 +188,9 @@ int soc_decode_steps(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_to
  * until the process ends, instead of hipMalloc'd scratch; it allocates nothing. Needs a model that
  * soc_model_decode_path reports as 1 or 2 (else SOC_ERR_INVALID); fails with SOC_ERR_CAPACITY when the model's
  * exchange state plus 4 bytes per step exceed 4 MiB (about 900k steps at Qwen3-0.6B shape). Every call re-initialises
- * the array; calls that overlap on one device race on it. */
+ * the array. Calls on one device are serialised by a per-device flag held from the array's initialisation to the
+ * end of the call: a call made while another one holds it (another thread, another context or model on the same
+ * device) fails at once with SOC_ERR_STATE and touches nothing. */
 int soc_decode_steps_noalloc(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, int32_t steps,
                              int32_t* tokens_out);
 
@@ -205,11 +207,14 @@ int soc_decode_batch_steps(soc_model* model, soc_kv* kv, int32_t n, const int32_
                            int32_t steps, int32_t* tokens_out);
 
 /* ---- sampler: replaces Sampler::SampleFromLogits (Mac/gpu/src/runtime/sampler.cpp:14-71) ---- */
-/* Top-k sampling of one fp32 logits row in device (or host) memory, with the reference's results: k = top_k clamped
- * to [1, vocab], temperature <= 0 taken as 1, candidates ordered as std::partial_sort(0..vocab-1, by logit /
- * temperature, greater first) orders them, ties included; *token_id = the first. top_ids / top_logits (nullable, k
- * entries) receive the candidates and their raw logits. For k <= 64 the candidates are found on the device and only
- * they are copied back; larger k, or a row holding NaN, sorts a host copy of the whole row as the reference does. */
+/* Top-k sampling of one fp32 logits row, with the reference's results: k = top_k clamped to [1, vocab], temperature
+ * <= 0 taken as 1, candidates ordered as std::partial_sort(0..vocab-1, by logit / temperature, greater first) orders
+ * them, ties included; *token_id = the first. top_ids / top_logits (nullable, k entries) receive the candidates and
+ * their raw logits. The row may be in device memory (hipMalloc'd or managed), pinned host memory or pageable host
+ * memory: the pointer is classified with hipPointerGetAttributes first. For k <= 64 and a row a kernel may read
+ * (device or pinned memory, the whole row inside one allocation) the candidates are found on the device and only
+ * they are copied back; larger k, a row holding NaN, or a row in pageable host memory is sorted whole on the host as
+ * the reference does (a kernel never reads pageable host memory). */
 int soc_sample_topk(soc_ctx* ctx, const float* logits_row, int32_t vocab, int32_t top_k, float temperature,
                     int32_t* token_id, int32_t* top_ids, float* top_logits);
 

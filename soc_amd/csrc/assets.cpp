@@ -401,6 +401,10 @@ std::vector<uint16_t> WeightLoader::LoadFloat16(const ManifestData& manifest, co
       float v;
       std::memcpy(&v, &bits, 4);
       out[i] = soc_f64_to_f16_rne(static_cast<double>(v));  // exact in double, one rounding to fp16
+      // the device keeps fp16: a finite weight beyond fp16's range (|w| >= 65520 rounds to inf) is refused rather
+      // than stored as inf; non-finite source values pass through unchanged, as the reference's fp32 copy keeps them
+      if (std::isfinite(v) && (out[i] & 0x7c00u) == 0x7c00u)
+        throw std::runtime_error("tensor value outside the float16 range (|w| >= 65520) in: " + name);
     }
   }
   if (!f) throw std::runtime_error("failed to read tensor file: " + r.file);

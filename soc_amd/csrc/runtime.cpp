@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstdio>
@@ -53,6 +54,12 @@ struct soc_ctx {
 // symbol is only a stand-in): it uses the address hipGetSymbolAddress returned for the device, kept in soc_ctx.
 constexpr size_t kNoAllocScratchBytes = size_t{4} << 20;
 static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / 4];
+
+// One flag per device: set while a soc_decode_steps_noalloc call uses that device's `scratch` (from its
+// initialisation to the synchronisation that ends the call). A call that finds it set fails with SOC_ERR_STATE
+// instead of racing on the array.
+constexpr int kNoAllocMaxDevices = 64;
+static std::atomic<bool> g_noalloc_busy[kNoAllocMaxDevices];
 
 // Fills words [0, n_zero) with zero except the four decode-state words at `state_at` ({token, pos, 1, 1}: the step
 // counters of both one-launch kernels start at 1) and words [ff_at, ff_at + n_ff) with 0xffffffff (tag 3 in every
@@ -198,6 +205,30 @@ namespace {
 
 int hip_fail(hipError_t e, const char* what) {
   return soc::fail(SOC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Where `bytes` bytes at p lie. kDeviceRange: in memory a kernel may read (a hipMalloc'd or managed allocation that
+// holds the whole range, or pinned host memory mapped for the device). kPageable: host memory the device cannot read
+// (a kernel reading it faults on devices without XNACK); HIP reports it as unregistered or fails the query, whose
+// error is cleared here. kOutside: device memory whose allocation ends before p + bytes.
+enum class MemRange { kDeviceRange, kPageable, kOutside };
+MemRange classify_range(const void* p, size_t bytes) {
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return MemRange::kPageable;
+  }
+  if (attr.type == hipMemoryTypeHost && attr.devicePointer != p) return MemRange::kPageable;
+  if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged && attr.type != hipMemoryTypeHost)
+    return MemRange::kPageable;
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
+    (void)hipGetLastError();
+    return MemRange::kOutside;
+  }
+  return static_cast<const char*>(p) + bytes <= static_cast<const char*>(base) + size ? MemRange::kDeviceRange
+                                                                                       : MemRange::kOutside;
 }
 
 // A KV cache serves one model. One created from dimensions alone (soc_kv_create_dims, the reference's
@@ -2107,6 +2138,16 @@ int soc_decode_steps_noalloc(soc_model* m, soc_kv* kv, int32_t slot, int32_t las
   const bool xcd = use_xcd(m);
   if (!xcd && !use_persistent(m))
     return soc::fail(SOC_ERR_INVALID, "soc_decode_steps_noalloc: this model has no one-launch decode kernel");
+  const int dev = m->ctx->device;
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return soc::fail(SOC_ERR_INVALID, "soc_decode_steps_noalloc: device index beyond the supported 64");
+  bool idle = false;
+  if (!g_noalloc_busy[dev].compare_exchange_strong(idle, true))
+    return soc::fail(SOC_ERR_STATE, "soc_decode_steps_noalloc: another call is using this device's scratch array");
+  struct Release {
+    std::atomic<bool>* f;
+    ~Release() { f->store(false); }
+  } release{&g_noalloc_busy[dev]};
   uint32_t* base = m->ctx->scratch;
   DecodeWs w;
   w.err = reinterpret_cast<int*>(base + o_err);
@@ -2317,7 +2358,11 @@ int soc_sample_topk(soc_ctx* ctx, const float* row, int32_t vocab, int32_t top_k
   hipError_t e;
   std::vector<int32_t> idx;
   std::vector<float> vals;
-  bool whole_row = k > soc::kSampleMaxK;
+  // a row in pageable host memory is never handed to a kernel: it is sorted where it lies, as the reference does
+  const MemRange where = classify_range(row, static_cast<size_t>(vocab) * 4);
+  if (where == MemRange::kOutside)
+    return soc::fail(SOC_ERR_INVALID, "Sampler logits row extends past the end of its device allocation");
+  bool whole_row = k > soc::kSampleMaxK || where == MemRange::kPageable;
   if (!whole_row) {
     const size_t need = soc::sample_ws_bytes(vocab);
     if (ctx->sample_ws_bytes < need) {

@@ -55,12 +55,15 @@ def test_model_loader_smoke(tmp_path, oracle_mod, export_dtype):
 def test_dtype_conversions_round_to_nearest_even(tmp_path):
     rng = np.random.default_rng(4)
     vals = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 3,
-                           np.array([65504.0, 65520.0, 1e-8, -0.0, 2.0 ** -24, 3 * 2.0 ** -25], np.float32)])
+                           np.array([65504.0, 65519.0, 1e-8, -0.0, 2.0 ** -24, 3 * 2.0 ** -25], np.float32)])
     n = vals.size
     cfg = S.QwenConfig(vocab_size=n // 2, hidden_size=2, num_hidden_layers=1, num_attention_heads=1,
                        num_key_value_heads=1, intermediate_size=2, head_dim=2, tie_word_embeddings=True)
     for dtype in ("float32", "bfloat16", "float16"):
         t = _loader_tensors("float32")
+        # the largest values stay finite after the source dtype's own rounding (bfloat16 rounds 65504 up to 65536)
+        if dtype == "bfloat16":
+            vals[-6:-4] = 65280.0
         t["model.embed_tokens.weight"] = (vals.reshape(n // 2, 2), dtype)
         with np.errstate(over="ignore"):
             path = write_bundle(tmp_path / dtype, config_dict(cfg), t)
@@ -68,9 +71,30 @@ def test_dtype_conversions_round_to_nearest_even(tmp_path):
         got = b.tensor_f16("model.embed_tokens.weight", (n // 2, 2)).reshape(-1)
         b.close()
         src = vals if dtype != "bfloat16" else (f32_to_bf16_bits(vals).astype(np.uint32) << 16).view(np.float32)
-        with np.errstate(over="ignore"):  # 65520 rounds to inf, as IEEE rounding says
-            want = src.astype(np.float16).view(np.uint16)  # numpy: IEEE round to nearest even
+        want = src.astype(np.float16).view(np.uint16)  # numpy: IEEE round to nearest even
         assert np.array_equal(got, want), dtype
+
+
+def test_weights_beyond_fp16_range_are_refused(tmp_path):
+    """The device keeps fp16: a finite float32 / bfloat16 weight that rounds to inf in fp16 (|w| >= 65520) is an error
+    naming the tensor, while 65504 (fp16's largest finite value) and non-finite source values load as they are."""
+    cfg = S.QwenConfig(vocab_size=4, hidden_size=2, num_hidden_layers=1, num_attention_heads=1,
+                       num_key_value_heads=1, intermediate_size=2, head_dim=2, tie_word_embeddings=True)
+    for dtype, bad in (("float32", 65520.0), ("float32", -1e6), ("bfloat16", 70000.0)):
+        t = _loader_tensors("float32")
+        t["model.embed_tokens.weight"] = (np.array([[1.0, 2.0], [3.0, bad], [0, 0], [0, 0]], np.float32), dtype)
+        path = write_bundle(tmp_path / f"{dtype}_{bad}", config_dict(cfg), t)
+        b = S.Bundle(path)
+        with pytest.raises(S.SocError, match="outside the float16 range.*model.embed_tokens.weight"):
+            b.tensor_f16("model.embed_tokens.weight", (4, 2))
+        b.close()
+    t = _loader_tensors("float32")
+    t["model.embed_tokens.weight"] = (np.array([[65504.0, -65504.0], [np.inf, -np.inf], [0, 0], [0, 0]], np.float32),
+                                      "float32")
+    b = S.Bundle(write_bundle(tmp_path / "edge", config_dict(cfg), t))
+    got = b.tensor_f16("model.embed_tokens.weight", (4, 2)).reshape(-1)
+    b.close()
+    assert got[:4].tolist() == [0x7BFF, 0xFBFF, 0x7C00, 0xFC00]
 
 
 def _expect_error(path, text):

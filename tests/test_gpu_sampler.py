@@ -70,3 +70,30 @@ def test_sample_topk_on_decode_logits(gpu_ctx, oracle_mod):
         gpu_ctx.free(p)
         kv.close()
         m.close()
+
+
+def test_sample_topk_row_in_pageable_host_memory(gpu_ctx, oracle_mod):
+    """A row in pageable host memory (a numpy array) is classified before any launch and sorted on the host: same
+    results as the device search and the reference, for k on both sides of the device limit."""
+    row = np.random.default_rng(11).integers(-6, 7, 151936).astype(np.float32)
+    p = gpu_ctx.upload(row)
+    try:
+        for k in (1, 5, 64, 65):
+            dtok, dids, dvals = S.sample_topk(gpu_ctx, p, row.size, k, 0.9)
+            htok, hids, hvals = S.sample_topk(gpu_ctx, row.ctypes.data, row.size, k, 0.9)
+            rtok, rids, rvals = oracle_mod.sample_topk(row, 0.9, k)
+            assert htok == dtok == rtok
+            assert np.array_equal(hids, rids) and np.array_equal(dids, rids)
+            assert np.array_equal(hvals.view(np.uint32), rvals.view(np.uint32))
+    finally:
+        gpu_ctx.free(p)
+
+
+def test_sample_topk_rejects_row_past_its_allocation(gpu_ctx):
+    """A device row shorter than `vocab` is refused on the host (checked against its allocation's extent)."""
+    p = gpu_ctx.alloc(1000 * 4)
+    try:
+        with pytest.raises(S.SocError, match="past the end of its device allocation"):
+            S.sample_topk(gpu_ctx, p, 1_000_000, 5, 1.0)
+    finally:
+        gpu_ctx.free(p)
