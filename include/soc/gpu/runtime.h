@@ -234,11 +234,53 @@ struct QwenCausalLMParams {
 
 class KVCache;
 
+// The model's weights as device tensors (qwen_attention.h:16-23, qwen_mlp.h:13-17, qwen_block.h:15-20,
+// qwen_causal_lm.h:17-23). A model built from them (the constructor below) copies them into its own fp16 storage; a
+// model from QwenModelLoader reports fp16 views of that storage here.
+struct QwenAttentionWeights {
+  DeviceTensor q_proj_weight;
+  DeviceTensor k_proj_weight;
+  DeviceTensor v_proj_weight;
+  DeviceTensor o_proj_weight;
+  DeviceTensor q_norm_weight;
+  DeviceTensor k_norm_weight;
+};
+
+struct QwenMlpWeights {
+  DeviceTensor gate_proj_weight;
+  DeviceTensor up_proj_weight;
+  DeviceTensor down_proj_weight;
+};
+
+struct QwenBlockWeights {
+  DeviceTensor input_layernorm_weight;
+  QwenAttentionWeights attention;
+  DeviceTensor post_attention_layernorm_weight;
+  QwenMlpWeights mlp;
+};
+
+struct QwenCausalLMWeights {
+  DeviceTensor embed_tokens_weight;
+  std::vector<QwenBlockWeights> blocks;
+  DeviceTensor final_norm_weight;
+  DeviceTensor lm_head_weight;
+  bool tie_word_embeddings = true;
+};
+
+// Mac/gpu/include/model/qwen_causal_lm.h:38-95. Every forward runs the hot-path kernels through soc_forward; token
+// ids and outputs are device tensors, and the ids are never read back to the host.
 class QwenCausalLM {
  public:
   QwenCausalLM() = default;
-  QwenCausalLM(std::shared_ptr<soc_model> model, QwenCausalLMParams params)
-      : model_(std::move(model)), params_(params) {}
+  // qwen_causal_lm.cpp:31-32: a model over the given weights (float32 or float16 device tensors, shapes of
+  // Mac/cpu/src/qwen_model_loader.cpp:57-100; lm_head_weight is used only without tied embeddings). The weights are
+  // converted to fp16 device storage here; the layer count is weights.blocks.size(). A constructor cannot fail in the
+  // reference's interface: a weight of the wrong shape, dtype or memory leaves the model invalid (IsValid() false)
+  // and every forward then fails with the reason.
+  QwenCausalLM(QwenCausalLMWeights weights, QwenCausalLMParams params);
+  // A model over library storage (QwenModelLoader); `weights` holds fp16 views of it.
+  QwenCausalLM(std::shared_ptr<soc_model> model, QwenCausalLMParams params, QwenCausalLMWeights weights = {})
+      : model_(std::move(model)), params_(params), weights_(std::move(weights)) {}
 
   std::size_t num_layers() const { return params_.num_hidden_layers; }
   std::size_t num_key_value_heads() const { return params_.num_key_value_heads; }
@@ -246,18 +288,37 @@ class QwenCausalLM {
   std::size_t vocab_size() const { return params_.vocab_size; }
   std::size_t max_position_embeddings() const { return params_.max_position_embeddings; }
   const QwenCausalLMParams& params() const { return params_; }
+  const QwenCausalLMWeights& weights() const { return weights_; }
   soc_model* handle() const { return model_.get(); }
   bool IsValid() const { return model_ != nullptr; }
 
-  // qwen_causal_lm.cpp:250-268: the forward of token_ids [n] (kInt32) at positions position_offset.., appending
-  // their K/V to kv_cache, logits of the last rows into logits_output [r][vocab] (kFloat32, r <= n).
+  // qwen_causal_lm.cpp:37-129: the uncached forward of token_ids [n] (kInt32) at positions position_offset.. (causal
+  // over the n tokens alone), the final-RMSNorm rows into output [n][hidden_size] (kFloat32).
+  bool ForwardHidden(const HipContext& context, PipelineCache* pipeline_cache, const DeviceTensor& token_ids,
+                     const DeviceTensor& output, BufferArena* temporary_arena, std::size_t position_offset,
+                     std::string* error_message) const;
+  // qwen_causal_lm.cpp:130-229: the same over kv_cache (position_offset must equal its length), appending K/V.
+  bool ForwardHiddenCached(const HipContext& context, PipelineCache* pipeline_cache, const DeviceTensor& token_ids,
+                           KVCache* kv_cache, const DeviceTensor& output, BufferArena* temporary_arena,
+                           std::size_t position_offset, std::string* error_message) const;
+  // qwen_causal_lm.cpp:231-248: uncached logits of the last rows into logits_output [r][vocab] (r <= n; the
+  // reference's all-rows output is r = n).
+  bool ForwardLogits(const HipContext& context, PipelineCache* pipeline_cache, const DeviceTensor& token_ids,
+                     const DeviceTensor& logits_output, BufferArena* temporary_arena, std::size_t position_offset,
+                     std::string* error_message) const;
+  // qwen_causal_lm.cpp:250-268: the cached forward, logits of the last rows into logits_output [r][vocab] (r <= n).
   bool ForwardLogitsCached(const HipContext& context, PipelineCache* pipeline_cache, const DeviceTensor& token_ids,
                            KVCache* kv_cache, const DeviceTensor& logits_output, BufferArena* temporary_arena,
                            std::size_t position_offset, std::string* error_message) const;
 
  private:
+  bool Forward(const HipContext& context, const DeviceTensor& token_ids, KVCache* kv_cache, const DeviceTensor* hidden,
+               const DeviceTensor* logits, std::size_t position_offset, std::string* error_message) const;
+
   std::shared_ptr<soc_model> model_;
   QwenCausalLMParams params_;
+  QwenCausalLMWeights weights_;
+  std::string build_error_;  // why the weights constructor left the model invalid
 };
 
 // Loads a model from named fp16 host tensors (Hugging Face names, Mac/cpu/src/qwen_model_loader.cpp:35-93).
@@ -398,6 +459,7 @@ class GenerationContext {
   std::vector<int> running_token_ids_;
   std::shared_ptr<HipBuffer> logits_buffer_;  // one logits row: generation samples only the last row
   std::shared_ptr<HipBuffer> token_buffer_;
+  std::vector<int> uploaded_ids_;  // source of the last asynchronous token upload, kept until the forward has run
 };
 
 // ---- text-level helpers (Mac/cpu/header/runtime_pipeline.h:13-43) ----
@@ -437,6 +499,12 @@ class RuntimePipeline {
   static std::string PreparePrompt(const soc::TokenizerRuntimeData& tokenizer_runtime, const std::string& prompt,
                                    const RuntimePromptOptions& options = {});
 };
+
+}  // namespace soc::gpu
+
+#include "soc/gpu/ops.h"
+
+namespace soc::gpu {
 
 // The reference's names for the platform classes.
 using MetalContext = HipContext;

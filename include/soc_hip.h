@@ -54,6 +54,9 @@ int soc_buffer_alloc(soc_ctx* ctx, size_t bytes, void** device_ptr);
 int soc_buffer_free(soc_ctx* ctx, void* device_ptr);
 int soc_buffer_write(soc_ctx* ctx, void* device_dst, const void* host_src, size_t bytes);
 int soc_buffer_read(soc_ctx* ctx, void* host_dst, const void* device_src, size_t bytes);
+/* soc_buffer_write queued on the context stream without waiting: host_src must stay unchanged until the stream has
+ * been synchronised (by soc_ctx_synchronize or any call that returns results). */
+int soc_buffer_write_async(soc_ctx* ctx, void* device_dst, const void* host_src, size_t bytes);
 
 /* ---- model: replaces QwenCausalLM + QwenModelLoader (Mac/gpu/include/model/qwen_causal_lm.h:17-95,
  *      Mac/gpu/src/model/qwen_model_loader.cpp:57-192; names/shapes of Mac/cpu/src/qwen_model_loader.cpp:35-93) ---- */
@@ -76,6 +79,14 @@ int soc_model_create(soc_ctx* ctx, const soc_qwen_config* cfg, soc_model** out);
 int soc_model_destroy(soc_model* model);
 /* Upload one fp16 tensor by its Hugging Face name ("model.layers.3.self_attn.q_proj.weight", ...). */
 int soc_model_load_tensor(soc_model* model, const char* name, const uint16_t* host_fp16, int64_t numel);
+/* The same from device memory: `src` holds numel fp32 (SOC_DTYPE_F32, rounded to fp16 to nearest even) or fp16
+ * (SOC_DTYPE_F16) elements of one allocation; the copy is finished when the call returns. Serves the reference's model
+ * constructor from device tensors (QwenCausalLM(QwenCausalLMWeights, QwenCausalLMParams),
+ * Mac/gpu/include/model/qwen_causal_lm.h:40-41). */
+int soc_model_load_tensor_device(soc_model* model, const char* name, const void* src, int32_t dtype, int64_t numel);
+/* The device address (fp16 storage, Hugging Face [out][in] layout) and element count of one named tensor of the model;
+ * the memory belongs to the model. Serves QwenCausalLM::weights() (qwen_causal_lm.h:82) for loaded models. */
+int soc_model_tensor(const soc_model* model, const char* name, void** device_ptr, int64_t* numel);
 /* Fill every tensor with the seeded generator (soc_synth_normal_f16 with `sigma`; norm gains = 1.0). */
 int soc_model_synthesize(soc_model* model, uint64_t seed, float sigma);
 /* Validates that every tensor the config needs is present (StartupValidator / loader checks). */
@@ -175,6 +186,20 @@ int soc_kv_layer_planes(const soc_kv* kv, int32_t slot, int32_t layer, void** ke
  * (nullable; host or device memory) and the greedy next token from the last row (nullable). */
 int soc_prefill(soc_model* model, soc_kv* kv, int32_t slot, const int32_t* token_ids, int32_t n,
                 int32_t position_offset, int32_t logit_rows, float* logits, int32_t* next_token);
+/* The model's forward in every form of QwenCausalLM (Mac/gpu/include/model/qwen_causal_lm.h:47-80,
+ * qwen_causal_lm.cpp:37-268): ForwardHidden / ForwardLogits with kv == NULL, ForwardHiddenCached / ForwardLogitsCached
+ * with a cache. token_ids [n] may be in host or device memory; ids in device memory are checked on the device (an id
+ * outside [0, vocab) fails the call with SOC_ERR_INVALID after it ran, leaving the slot length unchanged) and are never
+ * read back to the host.
+ *   kv == NULL: the uncached forward: causal attention over the n tokens alone, RoPE at positions position_offset ..
+ *     (qwen_attention.cpp:103-140), on a private cache of the model; position_offset + n <= max_position_embeddings.
+ *   kv set: the cached forward of `slot`; position_offset must equal the slot's length; the n tokens' K/V are appended.
+ * hidden [n][hidden_size] (nullable): the final-RMSNorm rows (ForwardHidden*); logits [logit_rows][vocab] (nullable):
+ * the last logit_rows rows (ForwardLogits* with logit_rows = n); next_token (nullable): greedy id of the last row.
+ * Outputs may be host or device memory. One host synchronisation per call; a cached single token without hidden rows
+ * runs the decode path. */
+int soc_forward(soc_model* model, soc_kv* kv, int32_t slot, const int32_t* token_ids, int32_t n,
+                int32_t position_offset, float* hidden, int32_t logit_rows, float* logits, int32_t* next_token);
 /* One decode step of one slot: feeds `last_token` at position = current length. Logits [V] nullable, in host or
  * device memory. */
 int soc_decode(soc_model* model, soc_kv* kv, int32_t slot, int32_t last_token, float* logits, int32_t* next_token);
@@ -222,11 +247,50 @@ int soc_sample_topk(soc_ctx* ctx, const float* logits_row, int32_t vocab, int32_
  *      These replace the reference's op wrappers (the static Run(...) of the headers under Mac/gpu/include/op/). ---- */
 /* y[N] = W[N][K] . x[K]; W fp16, x fp16, y fp32 (LinearOp/MatMulOp decode mode, matmul_op.mm:143-163). */
 int soc_gemv_f16(soc_ctx* ctx, const void* w, const void* x, float* y, int32_t n, int32_t k);
+/* Prefill projection: y[M][N] = x[M][K] . W[N][K]^T; x and W fp16 (16-byte aligned), y fp32; K % 32 == 0. The
+ * prefill GEMM of the model (MFMA 32x32x16, direct-to-LDS tiles; LinearOp / MatMulOp prefill mode, matmul_op.mm). */
+int soc_gemm_f16(soc_ctx* ctx, const void* x, const void* w, float* y, int32_t m, int32_t n, int32_t k);
+/* Causal GQA attention of a prefill chunk (GroupedQueryAttention::ForwardWithPrefix, grouped_query_attention.cpp:
+ * 59-142): q fp32 [rows][nq * 128] (already normed and rotated), keys / values fp16 [nkv][cap][128] (one layer's cache
+ * planes, holding the chunk's own keys), out fp32 [rows][nq * 128]; row t sees keys 0 .. pos_base + t; head_dim must be
+ * 128 and nq / nkv in {1, 2, 4, 8}. */
+int soc_attention_prefill(soc_ctx* ctx, const float* q, const void* keys, const void* values, float* out, int32_t rows,
+                          int32_t pos_base, int32_t nq, int32_t nkv, int32_t head_dim, int32_t cap);
+/* Decode attention of one token over keys 0 .. kv_len - 1 of the same planes (QwenAttention::RunDecode's attention,
+ * Mac/gpu/src/module/qwen_attention.mm): q fp32 [nq * 128], out fp32 [nq * 128]. */
+int soc_attention_decode(soc_ctx* ctx, const float* q, const void* keys, const void* values, float* out,
+                         int32_t kv_len, int32_t nq, int32_t nkv, int32_t head_dim, int32_t cap);
 /* Group-quantized matmul: y[M][N] = x[M][K] . dequant(codes, scales)^T; bits 8 or 4; group 64 along K. */
 int soc_qmm(soc_ctx* ctx, const void* x_f16, const void* codes, int32_t bits, const void* scales_f16, float* y,
             int32_t m, int32_t n, int32_t k);
 /* Dequantize to fp32 [N][K] (bit-exact contract: w = float(code) * float(scale)). */
 int soc_dequant(soc_ctx* ctx, const void* codes, int32_t bits, const void* scales_f16, float* w, int32_t n, int32_t k);
+
+/* ---- the reference's fp32 op kernels (the static Run of the headers under Mac/gpu/include/op/; kernels in
+ *      Mac/gpu/shaders/gpu_kernels.metal:82-289) on caller device pointers, row-major; each validates that every
+ *      operand lies in device memory inside one allocation before launching, and returns when the result is written.
+ *      The C++ classes MatMulOp, LinearOp, RmsNormOp, RopeOp, SoftmaxOp, EmbeddingOp and ElementwiseMulOp
+ *      (include/soc/gpu/ops.h) call these. ---- */
+/* MatMulOp::Run (matmul_op.mm:196-330): out[r][c] = sum_i lhs[r][i] rhs'[i][c] (+ bias[c]) (+ residual[r][c]), then
+ * SiLU when `silu`; rhs' = rhs [inner][cols], or rhs [cols][inner] read transposed when transpose_rhs. bias and
+ * residual nullable; residual may alias out. fp32 operands and accumulation (MFMA 16x16x4 fp32). */
+int soc_op_matmul(soc_ctx* ctx, const float* lhs, const float* rhs, const float* bias, const float* residual,
+                  float* out, int32_t rows, int32_t inner, int32_t cols, int32_t transpose_rhs, int32_t silu);
+/* RmsNormOp::Run: y = x / sqrt(mean(x^2) + eps) * weight per row of n (rms_norm_module.cpp:56-64). */
+int soc_op_rmsnorm(soc_ctx* ctx, const float* x, const float* weight, float* y, int32_t rows, int32_t n, float eps);
+/* RopeOp::Run over [rows][heads * head_dim]: rotate-half of the first rotary_dim dims of each head at position
+ * position_offset + row, angle (position) / theta^(2i / rotary_dim) in double (rope.cpp:72-79); other dims copied.
+ * In place (x == y) allowed. */
+int soc_op_rope(soc_ctx* ctx, const float* x, float* y, int32_t rows, int32_t heads, int32_t head_dim,
+                int32_t rotary_dim, int32_t position_offset, double theta);
+/* SoftmaxOp::Run per row of n: exp(x - max) / sum. */
+int soc_op_softmax(soc_ctx* ctx, const float* x, float* y, int32_t rows, int32_t n);
+/* EmbeddingOp::Run: out[t] = table[ids[t]] (fp32 or fp16 table [vocab][hidden]); an id outside [0, vocab) gives a zero
+ * row, as the reference's kernel (gpu_kernels.metal:104-136). */
+int soc_op_embedding(soc_ctx* ctx, const int32_t* ids, const void* table, int32_t table_dtype, float* out,
+                     int32_t tokens, int32_t hidden, int32_t vocab);
+/* ElementwiseMulOp::Run: y = a * b elementwise over rows * n. */
+int soc_op_mul(soc_ctx* ctx, const float* a, const float* b, float* y, int32_t rows, int32_t n);
 
 /* ---- seeded synthetic data (this project's generator; the reference has none) ---- */
 int soc_synth_normal_f16(uint64_t seed, const char* name, float sigma, int64_t offset, int64_t n, uint16_t* out);

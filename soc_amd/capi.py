@@ -160,6 +160,19 @@ def lib() -> C.CDLL:
         "soc_decode_batch": (C.c_int, [P, P, I32, P, P, P, P]),
         "soc_decode_batch_steps": (C.c_int, [P, P, I32, P, P, I32, P]),
         "soc_gemv_f16": (C.c_int, [P, P, P, P, I32, I32]),
+        "soc_gemm_f16": (C.c_int, [P, P, P, P, I32, I32, I32]),
+        "soc_attention_prefill": (C.c_int, [P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
+        "soc_attention_decode": (C.c_int, [P, P, P, P, P, I32, I32, I32, I32, I32]),
+        "soc_forward": (C.c_int, [P, P, I32, P, I32, I32, P, I32, P, C.POINTER(I32)]),
+        "soc_model_load_tensor_device": (C.c_int, [P, C.c_char_p, P, I32, I64]),
+        "soc_model_tensor": (C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(I64)]),
+        "soc_buffer_write_async": (C.c_int, [P, P, P, C.c_size_t]),
+        "soc_op_matmul": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, I32]),
+        "soc_op_rmsnorm": (C.c_int, [P, P, P, P, I32, I32, F32]),
+        "soc_op_rope": (C.c_int, [P, P, P, I32, I32, I32, I32, I32, C.c_double]),
+        "soc_op_softmax": (C.c_int, [P, P, P, I32, I32]),
+        "soc_op_embedding": (C.c_int, [P, P, P, I32, P, I32, I32, I32]),
+        "soc_op_mul": (C.c_int, [P, P, P, P, I32, I32]),
         "soc_qmm": (C.c_int, [P, P, P, I32, P, P, I32, I32, I32]),
         "soc_dequant": (C.c_int, [P, P, I32, P, P, I32, I32]),
         "soc_synth_normal_f16": (C.c_int, [U64, C.c_char_p, F32, I64, I64, P]),
@@ -576,3 +589,35 @@ def qmm(ctx: Context, x_dev: int, codes_dev: int, bits: int, scales_dev: int, y_
 
 def dequant(ctx: Context, codes_dev: int, bits: int, scales_dev: int, w_dev: int, n: int, k: int) -> None:
     check(lib().soc_dequant(ctx.h, codes_dev, bits, scales_dev, w_dev, n, k))
+
+
+def forward(model: Model, kv: "KVCache | None", slot: int, ids, position_offset: int, want_hidden: bool = False,
+            logit_rows: int = 1, ids_dev: int | None = None):
+    """soc_forward (QwenCausalLM::Forward{Hidden,Logits}[Cached]): kv None = the uncached forward. Token ids from the
+    host array `ids`, or from device memory at ids_dev (len(ids) of them). Returns (hidden [n][H] or None,
+    logits [logit_rows][V] or None, greedy token of the last row)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    n = int(ids.size)
+    hidden = np.empty((n, model.cfg.hidden_size), np.float32) if want_hidden else None
+    logits = np.empty((logit_rows, model.cfg.vocab_size), np.float32) if logit_rows > 0 else None
+    tok = C.c_int32()
+    check(lib().soc_forward(model.h, kv.h if kv is not None else None, slot,
+                            ids_dev if ids_dev is not None else _ptr(ids), n, position_offset,
+                            _ptr(hidden) if hidden is not None else None, logit_rows,
+                            _ptr(logits) if logits is not None else None, C.byref(tok)))
+    return hidden, logits, tok.value
+
+
+def gemm_f16(ctx: Context, x_dev: int, w_dev: int, y_dev: int, m: int, n: int, k: int) -> None:
+    """soc_gemm_f16: y[m][n] = x[m][k] . w[n][k]^T (fp16 operands, fp32 out), the prefill projection GEMM."""
+    check(lib().soc_gemm_f16(ctx.h, x_dev, w_dev, y_dev, m, n, k))
+
+
+def attention_prefill(ctx: Context, q_dev: int, k_dev: int, v_dev: int, out_dev: int, rows: int, pos_base: int,
+                      nq: int, nkv: int, cap: int) -> None:
+    check(lib().soc_attention_prefill(ctx.h, q_dev, k_dev, v_dev, out_dev, rows, pos_base, nq, nkv, 128, cap))
+
+
+def attention_decode(ctx: Context, q_dev: int, k_dev: int, v_dev: int, out_dev: int, kv_len: int, nq: int, nkv: int,
+                     cap: int) -> None:
+    check(lib().soc_attention_decode(ctx.h, q_dev, k_dev, v_dev, out_dev, kv_len, nq, nkv, 128, cap))

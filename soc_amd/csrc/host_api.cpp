@@ -42,6 +42,61 @@ std::shared_ptr<soc_model> WrapModel(soc_model* m) {
   return std::shared_ptr<soc_model>(m, [](soc_model* p) { soc_model_destroy(p); });
 }
 
+struct WeightSlot {
+  std::string name;                // Hugging Face name (Mac/cpu/src/qwen_model_loader.cpp:57-100)
+  DeviceTensor* tensor;            // its place in QwenCausalLMWeights
+  std::vector<std::size_t> shape;  // expected shape
+};
+
+// Every weight of a model of params.num_hidden_layers layers (w.blocks already sized), lm_head only when untied.
+std::vector<WeightSlot> WeightSlots(QwenCausalLMWeights& w, const QwenCausalLMParams& p) {
+  const std::size_t H = p.hidden_size, I = p.intermediate_size, q = p.num_attention_heads * p.head_dim,
+                    kv = p.num_key_value_heads * p.head_dim;
+  std::vector<WeightSlot> out;
+  out.push_back({"model.embed_tokens.weight", &w.embed_tokens_weight, {p.vocab_size, H}});
+  for (std::size_t l = 0; l < w.blocks.size(); ++l) {
+    const std::string n = "model.layers." + std::to_string(l) + ".";
+    QwenBlockWeights& b = w.blocks[l];
+    out.push_back({n + "input_layernorm.weight", &b.input_layernorm_weight, {H}});
+    out.push_back({n + "self_attn.q_proj.weight", &b.attention.q_proj_weight, {q, H}});
+    out.push_back({n + "self_attn.k_proj.weight", &b.attention.k_proj_weight, {kv, H}});
+    out.push_back({n + "self_attn.v_proj.weight", &b.attention.v_proj_weight, {kv, H}});
+    out.push_back({n + "self_attn.o_proj.weight", &b.attention.o_proj_weight, {H, q}});
+    out.push_back({n + "self_attn.q_norm.weight", &b.attention.q_norm_weight, {p.head_dim}});
+    out.push_back({n + "self_attn.k_norm.weight", &b.attention.k_norm_weight, {p.head_dim}});
+    out.push_back({n + "post_attention_layernorm.weight", &b.post_attention_layernorm_weight, {H}});
+    out.push_back({n + "mlp.gate_proj.weight", &b.mlp.gate_proj_weight, {I, H}});
+    out.push_back({n + "mlp.up_proj.weight", &b.mlp.up_proj_weight, {I, H}});
+    out.push_back({n + "mlp.down_proj.weight", &b.mlp.down_proj_weight, {H, I}});
+  }
+  out.push_back({"model.norm.weight", &w.final_norm_weight, {H}});
+  if (!w.tie_word_embeddings) out.push_back({"lm_head.weight", &w.lm_head_weight, {p.vocab_size, H}});
+  return out;
+}
+
+std::string ShapeText(const std::vector<std::size_t>& s) {
+  std::string t = "[";
+  for (std::size_t i = 0; i < s.size(); ++i) t += (i ? ", " : "") + std::to_string(s[i]);
+  return t + "]";
+}
+
+// fp16 views of a loaded model's device storage, kept alive by the model (QwenCausalLM::weights()).
+QwenCausalLMWeights ViewWeights(const HipContext& context, const std::shared_ptr<soc_model>& holder,
+                                const QwenCausalLMParams& p) {
+  QwenCausalLMWeights w;
+  w.blocks.resize(p.num_hidden_layers);
+  w.tie_word_embeddings = p.tie_word_embeddings;
+  for (const WeightSlot& slot : WeightSlots(w, p)) {
+    void* ptr = nullptr;
+    int64_t numel = 0;
+    if (soc_model_tensor(holder.get(), slot.name.c_str(), &ptr, &numel) != SOC_OK) continue;
+    *slot.tensor = DeviceTensor(HipBuffer::Wrap(context, ptr, static_cast<std::size_t>(numel) * 2, holder), 0,
+                                TensorDesc::CreateContiguous(DataType::kFloat16, slot.shape));
+  }
+  if (w.tie_word_embeddings) w.lm_head_weight = w.embed_tokens_weight;
+  return w;
+}
+
 }  // namespace
 
 // ---- HipContext (metal_context.h) ----
@@ -228,7 +283,8 @@ bool QwenModelLoader::LoadModel(const HipContext& context, const QwenCausalLMPar
     if (!Check(soc_model_load_tensor(m, kv.first.c_str(), kv.second.data, kv.second.numel), error_message))
       return false;
   if (!Check(soc_model_finalize(m), error_message)) return false;
-  *model = QwenCausalLM(std::move(holder), params);
+  QwenCausalLMWeights views = ViewWeights(context, holder, params);
+  *model = QwenCausalLM(std::move(holder), params, std::move(views));
   return true;
 }
 
@@ -259,7 +315,8 @@ bool QwenModelLoader::LoadModel(const HipContext& context, const soc::ManifestDa
         return false;
     }
     if (!Check(soc_model_finalize(m), error_message)) return false;
-    *model = QwenCausalLM(std::move(holder), p);
+    QwenCausalLMWeights views = ViewWeights(context, holder, p);
+    *model = QwenCausalLM(std::move(holder), p, std::move(views));
     return true;
   } catch (const std::exception& e) {
     return Fail(error_message, e.what());
@@ -284,7 +341,8 @@ bool QwenModelLoader::SynthesizeModel(const HipContext& context, const QwenCausa
   auto holder = WrapModel(m);
   if (!Check(soc_model_synthesize(m, seed, sigma), error_message)) return false;
   if (!Check(soc_model_finalize(m), error_message)) return false;
-  *model = QwenCausalLM(std::move(holder), params);
+  QwenCausalLMWeights views = ViewWeights(context, holder, params);
+  *model = QwenCausalLM(std::move(holder), params, std::move(views));
   return true;
 }
 
@@ -373,44 +431,131 @@ bool KVCache::LayersAligned() const {
                      [this](std::size_t n) { return n == sequence_lengths_[0]; });
 }
 
-// ---- QwenCausalLM::ForwardLogitsCached (qwen_causal_lm.cpp:250-268) ----
-bool QwenCausalLM::ForwardLogitsCached(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
-                                       KVCache* kv_cache, const DeviceTensor& logits_output, BufferArena*,
-                                       std::size_t position_offset, std::string* error_message) const {
-  if (!IsValid()) return Fail(error_message, "QwenCausalLM is not loaded");
-  if (kv_cache == nullptr) return Fail(error_message, "ForwardLogitsCached requires a KV cache");
+// ---- QwenCausalLM (qwen_causal_lm.cpp) ----
+QwenCausalLM::QwenCausalLM(QwenCausalLMWeights weights, QwenCausalLMParams params)
+    : params_(params), weights_(std::move(weights)) {
+  params_.num_hidden_layers = weights_.blocks.size();  // qwen_causal_lm.cpp:34: the layer count is the blocks'
+  params_.tie_word_embeddings = weights_.tie_word_embeddings;
+  const std::shared_ptr<HipBuffer>& eb = weights_.embed_tokens_weight.GetBuffer();
+  if (eb == nullptr) {
+    build_error_ = "QwenCausalLM weight model.embed_tokens.weight is not a valid device tensor";
+    return;
+  }
+  const soc_qwen_config cfg = ToConfig(params_);
+  soc_model* m = nullptr;
+  if (soc_model_create(eb->context(), &cfg, &m) != SOC_OK) {
+    build_error_ = soc_last_error();
+    return;
+  }
+  std::shared_ptr<soc_model> holder = WrapModel(m);
+  for (const WeightSlot& slot : WeightSlots(weights_, params_)) {
+    const DeviceTensor& t = *slot.tensor;
+    const TensorDesc& d = t.GetDesc();
+    if (!t.IsValid()) {
+      build_error_ = "QwenCausalLM weight " + slot.name + " is not a valid device tensor";
+      return;
+    }
+    if (d.GetDataType() != DataType::kFloat32 && d.GetDataType() != DataType::kFloat16) {
+      build_error_ = "QwenCausalLM weight " + slot.name + " must be float32 or float16";
+      return;
+    }
+    if (!d.IsContiguous() || d.GetShape() != slot.shape) {
+      build_error_ = "QwenCausalLM weight " + slot.name + " has shape " + ShapeText(d.GetShape()) + ", expected " +
+                     ShapeText(slot.shape) + " (contiguous)";
+      return;
+    }
+    const int32_t dtype = d.GetDataType() == DataType::kFloat32 ? SOC_DTYPE_F32 : SOC_DTYPE_F16;
+    if (soc_model_load_tensor_device(m, slot.name.c_str(), t.data(), dtype, static_cast<int64_t>(d.ElementCount())) !=
+        SOC_OK) {
+      build_error_ = soc_last_error();
+      return;
+    }
+  }
+  if (soc_model_finalize(m) != SOC_OK) {
+    build_error_ = soc_last_error();
+    return;
+  }
+  model_ = std::move(holder);
+}
+
+// The forwards: token ids stay on the device (soc_forward checks them there), one host synchronisation per call, and
+// the GPU time of the call is recorded inside it for the context's profiling snapshot.
+bool QwenCausalLM::Forward(const HipContext& context, const DeviceTensor& token_ids, KVCache* kv_cache,
+                           const DeviceTensor* hidden, const DeviceTensor* logits, std::size_t position_offset,
+                           std::string* error_message) const {
+  if (!IsValid())
+    return Fail(error_message, build_error_.empty() ? "QwenCausalLM is not loaded" : build_error_);
   const TensorDesc& td = token_ids.GetDesc();
   if (!token_ids.IsValid() || td.GetDataType() != DataType::kInt32 || td.Rank() != 1 || td.GetShape()[0] == 0)
     return Fail(error_message, "token_ids must be a valid non-empty rank-1 int32 tensor");
   const std::size_t n = td.GetShape()[0];
+  float* hp = nullptr;
+  if (hidden != nullptr) {
+    const TensorDesc& hd = hidden->GetDesc();
+    if (!hidden->IsValid() || hd.GetDataType() != DataType::kFloat32 || hd.Rank() != 2)
+      return Fail(error_message, "QwenCausalLM hidden forward expects rank-1 int32 token ids and rank-2 float32 output");
+    if (hd.GetShape() != std::vector<std::size_t>{n, params_.hidden_size})
+      return Fail(error_message, "QwenCausalLM hidden output shape must be [token_count, hidden_size]");
+    hp = static_cast<float*>(hidden->data());
+  }
   int32_t rows = 0;
-  float* logits = nullptr;
-  if (logits_output.GetBuffer() != nullptr) {
-    const TensorDesc& ld = logits_output.GetDesc();
-    if (!logits_output.IsValid() || ld.GetDataType() != DataType::kFloat32 || ld.Rank() != 2 ||
+  float* lp = nullptr;
+  if (logits != nullptr && logits->GetBuffer() != nullptr) {
+    const TensorDesc& ld = logits->GetDesc();
+    if (!logits->IsValid() || ld.GetDataType() != DataType::kFloat32 || ld.Rank() != 2 ||
         ld.GetShape()[1] != vocab_size() || ld.GetShape()[0] == 0 || ld.GetShape()[0] > n)
       return Fail(error_message, "logits_output must be a valid float32 tensor [rows <= token count][vocab]");
     rows = static_cast<int32_t>(ld.GetShape()[0]);
-    logits = static_cast<float*>(logits_output.data());
+    lp = static_cast<float*>(logits->data());
   }
-  if (!kv_cache->LayersAligned())
-    return Fail(error_message, "KV cache layers hold different numbers of positions");
-  if (position_offset != kv_cache->GetSequenceLength())
-    return Fail(error_message, "position_offset must equal the KV cache length");
-  std::vector<int32_t> ids(n);
-  if (!token_ids.GetBuffer()->Read(ids.data(), n * 4, token_ids.GetByteOffset(), error_message)) return false;
+  if (kv_cache != nullptr) {
+    if (!kv_cache->LayersAligned())
+      return Fail(error_message, "KV cache layers hold different numbers of positions");
+    if (position_offset != kv_cache->GetSequenceLength())
+      return Fail(error_message, "position_offset must equal the KV cache length");
+  }
   soc_ctx* ctx = context.handle();
   if (!Check(soc_ctx_timer_start(ctx), error_message)) return false;
-  int32_t tok = -1;
-  const int rc = n == 1 && rows <= 1
-                     ? soc_decode(model_.get(), kv_cache->handle(), 0, ids[0], logits, &tok)
-                     : soc_prefill(model_.get(), kv_cache->handle(), 0, ids.data(), static_cast<int32_t>(n),
-                                   static_cast<int32_t>(position_offset), rows, logits, &tok);
-  if (!Check(rc, error_message)) return false;
+  const int rc = soc_forward(model_.get(), kv_cache != nullptr ? kv_cache->handle() : nullptr, 0,
+                             static_cast<const int32_t*>(token_ids.data()), static_cast<int32_t>(n),
+                             static_cast<int32_t>(position_offset), hp, rows, lp, nullptr);
+  const std::string err = rc == SOC_OK ? std::string() : soc_last_error();
   float ms = 0.0f;
-  if (soc_ctx_timer_stop(ctx, &ms) == SOC_OK) context.AddProfile(ms);
-  kv_cache->OnForward(n);
+  const bool timed = soc_ctx_timer_stop(ctx, &ms) == SOC_OK;
+  if (rc != SOC_OK) return Fail(error_message, err);
+  if (timed) context.AddProfile(ms);
+  if (kv_cache != nullptr) kv_cache->OnForward(n);
   return true;
+}
+
+bool QwenCausalLM::ForwardHidden(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
+                                 const DeviceTensor& output, BufferArena*, std::size_t position_offset,
+                                 std::string* error_message) const {
+  if (!token_ids.IsValid() || !output.IsValid())
+    return Fail(error_message, "QwenCausalLM hidden forward expects valid tensors");
+  return Forward(context, token_ids, nullptr, &output, nullptr, position_offset, error_message);
+}
+
+bool QwenCausalLM::ForwardHiddenCached(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
+                                       KVCache* kv_cache, const DeviceTensor& output, BufferArena*,
+                                       std::size_t position_offset, std::string* error_message) const {
+  if (kv_cache == nullptr) return Fail(error_message, "QwenCausalLM cached forward requires a KVCache");
+  if (!token_ids.IsValid() || !output.IsValid())
+    return Fail(error_message, "QwenCausalLM cached hidden forward expects valid tensors");
+  return Forward(context, token_ids, kv_cache, &output, nullptr, position_offset, error_message);
+}
+
+bool QwenCausalLM::ForwardLogits(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
+                                 const DeviceTensor& logits_output, BufferArena*, std::size_t position_offset,
+                                 std::string* error_message) const {
+  return Forward(context, token_ids, nullptr, nullptr, &logits_output, position_offset, error_message);
+}
+
+bool QwenCausalLM::ForwardLogitsCached(const HipContext& context, PipelineCache*, const DeviceTensor& token_ids,
+                                       KVCache* kv_cache, const DeviceTensor& logits_output, BufferArena*,
+                                       std::size_t position_offset, std::string* error_message) const {
+  if (kv_cache == nullptr) return Fail(error_message, "ForwardLogitsCached requires a KV cache");
+  return Forward(context, token_ids, kv_cache, nullptr, &logits_output, position_offset, error_message);
 }
 
 // ---- CommandScheduler (command_scheduler.cpp:5-41: both paths are ForwardLogitsCached) ----
@@ -477,7 +622,12 @@ bool GenerationContext::UploadTokenIds(const HipContext& context, const std::vec
                                             error_message);
     if (token_buffer_ == nullptr) return false;
   }
-  if (!token_buffer_->Write(token_ids.data(), bytes, 0, error_message)) return false;
+  // queued without waiting: the forward that reads the ids synchronises the stream before the next upload replaces
+  // uploaded_ids_, the copy's source
+  uploaded_ids_ = token_ids;
+  if (!Check(soc_buffer_write_async(context.handle(), token_buffer_->data(), uploaded_ids_.data(), bytes),
+             error_message))
+    return false;
   *token_tensor = DeviceTensor(token_buffer_, 0, TensorDesc::CreateContiguous(DataType::kInt32, {token_ids.size()}));
   return true;
 }

@@ -122,6 +122,9 @@ hipError_t launch_argmax_rows(const float* logits, int V, int n, int32_t* ids, i
 hipError_t launch_kv_append_rows(const void* keys, const void* values, bool fp16, int rows, int nkv, int hd, int cap,
                                  int pos, f16* kdst, f16* vdst, hipStream_t s);
 
+// Token ids in device memory [n] -> dst [n], ids outside [0, vocab) replaced by 0 with *err set to 1 (ops.hip).
+hipError_t launch_stage_ids(const int32_t* src, int n, int vocab, int32_t* dst, int* err, hipStream_t s);
+
 // ---- quantized-model forward steps (qpath.hip) ----
 hipError_t launch_f32_to_f16(const float* x, size_t n, f16* y, hipStream_t s);
 hipError_t launch_add_f32(float* x, const float* y, size_t n, hipStream_t s);  // x += y

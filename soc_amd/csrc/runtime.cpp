@@ -20,33 +20,13 @@
 #include "kernels.h"
 #include "soc_hip.h"
 #include "status.h"
+#include "capi_internal.h"
 
 using soc::f16;
-
-#define SOC_API_BEGIN try {
-#define SOC_API_END                                                         \
-  }                                                                         \
-  catch (const std::bad_alloc&) {                                           \
-    return soc::fail(SOC_ERR_NOMEM, "host allocation failed");              \
-  }                                                                         \
-  catch (const std::exception& e) {                                         \
-    return soc::fail(SOC_ERR_INVALID, e.what());                            \
-  }
 
 // ------------------------------------------------------------------------------------------------------------
 // objects
 // ------------------------------------------------------------------------------------------------------------
-struct soc_ctx {
-  int device = 0;
-  int num_cus = 0;
-  hipStream_t stream = nullptr;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  bool timing = false;
-  uint32_t* scratch = nullptr;  // device address of this device's copy of `scratch` (soc_decode_steps_noalloc)
-  void* sample_ws = nullptr;    // soc_sample_topk: candidate search workspace and its output block
-  size_t sample_ws_bytes = 0;
-  int* sample_out = nullptr;
-};
 
 // Device memory of soc_decode_steps_noalloc: the exchange state of the one-launch decode kernels and the token ring
 // live here instead of in hipMalloc'd buffers. One copy per device for the whole process; every call re-initialises
@@ -186,6 +166,7 @@ struct soc_model {
   int qbits = 0;         // 8 or 4 after soc_model_quantize: the projections run on the group-quantized copies
   std::vector<QLayer> qlayers;
   std::vector<void*> qallocs;
+  soc_kv* ukv = nullptr;  // private one-slot cache of the uncached forward (soc_forward with kv == NULL)
 };
 
 struct soc_kv {
@@ -207,28 +188,11 @@ int hip_fail(hipError_t e, const char* what) {
   return soc::fail(SOC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Where `bytes` bytes at p lie. kDeviceRange: in memory a kernel may read (a hipMalloc'd or managed allocation that
-// holds the whole range, or pinned host memory mapped for the device). kPageable: host memory the device cannot read
-// (a kernel reading it faults on devices without XNACK); HIP reports it as unregistered or fails the query, whose
-// error is cleared here. kOutside: device memory whose allocation ends before p + bytes.
-enum class MemRange { kDeviceRange, kPageable, kOutside };
-MemRange classify_range(const void* p, size_t bytes) {
-  hipPointerAttribute_t attr{};
-  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
-    (void)hipGetLastError();
-    return MemRange::kPageable;
-  }
-  if (attr.type == hipMemoryTypeHost && attr.devicePointer != p) return MemRange::kPageable;
-  if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged && attr.type != hipMemoryTypeHost)
-    return MemRange::kPageable;
-  void* base = nullptr;
-  size_t size = 0;
-  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess) {
-    (void)hipGetLastError();
-    return MemRange::kOutside;
-  }
-  return static_cast<const char*>(p) + bytes <= static_cast<const char*>(base) + size ? MemRange::kDeviceRange
-                                                                                       : MemRange::kOutside;
+// Records the stop event of soc_ctx_timer_start / _stop on the stream before a forward's final synchronisation, so
+// that reading the timer costs no further round trip.
+void record_timer_stop(soc_ctx* ctx) {
+  if (ctx->timing && !ctx->stop_recorded && hipEventRecord(ctx->ev1, ctx->stream) == hipSuccess)
+    ctx->stop_recorded = true;
 }
 
 // A KV cache serves one model. One created from dimensions alone (soc_kv_create_dims, the reference's
@@ -717,12 +681,36 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot, const DecodeWs
   return p;
 }
 
-int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps) {
+// The status of a one-launch decode whose error word read `err` (0: none).
+int one_launch_status(soc_model* m, bool xcd, int32_t err) {
+  if (err == 0) return SOC_OK;
+  // a bounded wait expired: drop the exchange state so the next call starts clean
+  m->dws.ready = false;
+  if (xcd && err == 2) {
+    m->xcd_off = true;
+    return soc::fail(SOC_ERR_HIP, "XCD decode: the launch did not place 32 blocks on each of the 8 XCDs");
+  }
+  return soc::fail(SOC_ERR_HIP, "one-launch decode: a cross-block wait timed out (grid not co-resident?)");
+}
+
+// `steps` decode steps of one slot from token `last` (host value) or, with dev_last, the id in device memory (staged
+// and checked on the device). With err_out set, the one-launch paths do not synchronise: they queue the read of their
+// error word into *err_out and the caller synchronises, then checks it with one_launch_status (outside a trace run).
+int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps, const int32_t* dev_last = nullptr,
+                     int32_t* err_out = nullptr) {
   DecodeWs& w = m->dws;
   hipStream_t s = m->ctx->stream;
   const int32_t st[2] = {last, kv->len[slot]};
-  hipError_t e = hipMemcpyAsync(w.state, st, sizeof(st), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync state");
+  hipError_t e;
+  if (dev_last == nullptr) {
+    if ((e = hipMemcpyAsync(w.state, st, sizeof(st), hipMemcpyHostToDevice, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync state");
+  } else {
+    if ((e = hipMemcpyAsync(w.state + 1, st + 1, 4, hipMemcpyHostToDevice, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync state");
+    if ((e = soc::launch_stage_ids(dev_last, 1, m->cfg.vocab_size, w.state, m->ctx->id_err, s)) != hipSuccess)
+      return hip_fail(e, "token id staging");
+  }
   const int32_t zero = 0;
   if ((e = hipMemcpyAsync(w.ring_pos, &zero, sizeof(zero), hipMemcpyHostToDevice, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync ring");
@@ -749,9 +737,12 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     for (int i = 0; i < steps; ++i)
       if ((e = xcd ? soc::launch_decode_xcd(p, s) : soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
         return hip_fail(e, "persistent decode launch");
-    int32_t err = 0;
+    int32_t err_local = 0;
+    int32_t& err = err_out != nullptr ? *err_out : err_local;
     if ((e = hipMemcpyAsync(&err, w.err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
       return hip_fail(e, "hipMemcpyAsync err");
+    if (err_out != nullptr && trace_path == nullptr) return SOC_OK;  // the caller synchronises and checks
+    record_timer_stop(m->ctx);
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "persistent decode");
     if (p.trace != nullptr) {
       std::vector<uint64_t> t(trace_n);
@@ -832,13 +823,9 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       }
     }
     if (err != 0) {
-      // a bounded wait expired: drop the exchange state so the next call starts clean
-      m->dws.ready = false;
-      if (xcd && err == 2) {
-        m->xcd_off = true;
-        return soc::fail(SOC_ERR_HIP, "XCD decode: the launch did not place 32 blocks on each of the 8 XCDs");
-      }
-      return soc::fail(SOC_ERR_HIP, "one-launch decode: a cross-block wait timed out (grid not co-resident?)");
+      const int rc = one_launch_status(m, xcd, err);
+      err = 0;  // reported here: the caller does not report it again
+      return rc;
     }
   } else if (env_flag("SOC_EAGER")) {
     for (int i = 0; i < steps; ++i) SOC_TRY(enqueue_decode(m, kv, slot, nullptr));
@@ -1280,6 +1267,9 @@ int soc_ctx_destroy(soc_ctx* ctx) {
   (void)hipStreamDestroy(ctx->stream);
   (void)hipFree(ctx->sample_ws);
   (void)hipFree(ctx->sample_out);
+  (void)hipFree(ctx->op_part);
+  (void)hipFree(ctx->op_counters);
+  (void)hipFree(ctx->id_err);
   delete ctx;
   return SOC_OK;
 }
@@ -1295,17 +1285,21 @@ int soc_ctx_timer_start(soc_ctx* ctx) {
   hipError_t e = hipEventRecord(ctx->ev0, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
   ctx->timing = true;
+  ctx->stop_recorded = false;
   return SOC_OK;
 }
 
 int soc_ctx_timer_stop(soc_ctx* ctx, float* ms) {
   if (ctx == nullptr || ms == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
   if (!ctx->timing) return soc::fail(SOC_ERR_STATE, "soc_ctx_timer_stop without soc_ctx_timer_start");
-  hipError_t e = hipEventRecord(ctx->ev1, ctx->stream);
+  // a forward that ran since the start recorded the stop event before its own synchronisation: then the event has
+  // completed and reading it costs no GPU round trip
+  hipError_t e = ctx->stop_recorded ? hipSuccess : hipEventRecord(ctx->ev1, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
   if ((e = hipEventSynchronize(ctx->ev1)) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
   if ((e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1)) != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
   ctx->timing = false;
+  ctx->stop_recorded = false;
   return SOC_OK;
 }
 
@@ -1332,6 +1326,12 @@ int soc_buffer_write(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   return e == hipSuccess ? SOC_OK : hip_fail(e, "soc_buffer_write");
+}
+
+int soc_buffer_write_async(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (ctx == nullptr || (bytes && (dst == nullptr || src == nullptr))) return soc::fail(SOC_ERR_INVALID, "null argument");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "soc_buffer_write_async");
 }
 
 int soc_buffer_read(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
@@ -1450,6 +1450,7 @@ int soc_model_destroy(soc_model* m) {
   (void)hipFree(m->rope_sin);
   (void)hipFree(m->d_layer_w);
   free_all(m->qallocs);
+  if (m->ukv != nullptr) soc_kv_destroy(m->ukv);
   delete m;
   return SOC_OK;
 }
@@ -1466,6 +1467,17 @@ int soc_model_load_tensor(soc_model* m, const char* name, const uint16_t* host, 
   if (e != hipSuccess) return hip_fail(e, "hipMemcpy weight");
   it->second.loaded = true;
   m->finalized = false;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_model_tensor(const soc_model* m, const char* name, void** device_ptr, int64_t* numel) {
+  SOC_API_BEGIN
+  if (m == nullptr || name == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  auto it = m->tensors.find(name);
+  if (it == m->tensors.end()) return soc::fail(SOC_ERR_INVALID, std::string("unknown tensor name: ") + name);
+  if (device_ptr != nullptr) *device_ptr = it->second.ptr;
+  if (numel != nullptr) *numel = it->second.numel;
   return SOC_OK;
   SOC_API_END
 }
@@ -1784,7 +1796,8 @@ namespace {
 // The layers of a quantized model's prefill over the n embedded rows in m->pws.x, kQChunk rows at a time (each chunk
 // through every layer, so a chunk's attention sees the keys the earlier chunks appended): group-quantized
 // projections, the prefill q/k-norm + RoPE + append kernel and the split-key attention over the slot's cache.
-int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off) {
+int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off, const float* rope_cos,
+                     const float* rope_sin) {
   const soc_qwen_config& c = m->cfg;
   PrefillWs& w = m->pws;
   hipStream_t s = m->ctx->stream;
@@ -1804,8 +1817,8 @@ int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off) {
         q.q_gain = L.q_norm;
         q.k_gain = L.k_norm;
         q.eps = c.rms_norm_eps;
-        q.rope_cos = m->rope_cos;
-        q.rope_sin = m->rope_sin;
+        q.rope_cos = rope_cos;
+        q.rope_sin = rope_sin;
         q.q_out = qrow;
         q.kcache = kv->k;
         q.vcache = kv->v;
@@ -1839,30 +1852,32 @@ int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off) {
   }
   return SOC_OK;
 }
-}  // namespace
 
-int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off,
-                int32_t logit_rows, float* logits, int32_t* next_token) {
-  SOC_API_BEGIN
-  if (m == nullptr || kv == nullptr || ids == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
-  SOC_TRY(bind_kv(kv, m));
-  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
-  if (n <= 0) return soc::fail(SOC_ERR_INVALID, "prefill requires at least one token");  // generation_context.cpp:22-27
-  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
-  if (pos_off != kv->len[slot])
-    return soc::fail(SOC_ERR_STATE, "position_offset must equal the cached length of the slot");
-  if (pos_off + n > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "prefill exceeds KV capacity");
-  if (logit_rows < 0 || logit_rows > n) return soc::fail(SOC_ERR_INVALID, "logit_rows out of range");
-  SOC_TRY(validate_ids(m, ids, n));
+// The forward of n tokens of one slot at positions [pos_off, pos_off + n) (QwenCausalLM::ForwardHiddenCached /
+// ForwardLogitsCached, qwen_causal_lm.cpp:130-268): appends their K/V, writes the final-RMSNorm rows (hidden, [n][H],
+// nullable), the logits of the last logit_rows rows and the greedy token of the last row. ids are host ids already
+// validated, or, with ids_dev, device ids that are staged on the device (an id outside the vocabulary fails the call
+// after the work ran). RoPE uses table rows rope_shift + position: rope_shift = 0 for a cached forward, and the
+// reference's position_offset for an uncached one (run on a private cache from position 0). Nothing past the
+// caller's inputs is changed on failure; on success the caller updates the slot length.
+int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool ids_dev, int32_t n, int32_t pos_off,
+                int32_t rope_shift, float* hidden, int32_t logit_rows, float* logits, int32_t* next_token) {
   SOC_TRY(ensure_prefill_ws(m, n, pos_off + n, logit_rows));
   const soc_qwen_config& c = m->cfg;
   PrefillWs& w = m->pws;
   hipStream_t s = m->ctx->stream;
-  hipError_t e = hipMemcpyAsync(w.ids, ids, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync ids");
+  hipError_t e;
+  if (ids_dev) {
+    if ((e = soc::launch_stage_ids(ids, n, c.vocab_size, w.ids, m->ctx->id_err, s)) != hipSuccess)
+      return hip_fail(e, "token id staging");
+  } else if ((e = hipMemcpyAsync(w.ids, ids, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, s)) != hipSuccess) {
+    return hip_fail(e, "hipMemcpyAsync ids");
+  }
   if ((e = soc::launch_embed(w.ids, n, m->embed, c.hidden_size, w.x, s)) != hipSuccess) return hip_fail(e, "embed");
+  const float* const rope_cos = m->rope_cos + static_cast<size_t>(rope_shift) * (c.head_dim / 2);
+  const float* const rope_sin = m->rope_sin + static_cast<size_t>(rope_shift) * (c.head_dim / 2);
   const int H = c.hidden_size;
-  if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off));
+  if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off, rope_cos, rope_sin));
   const bool split = prefill_split_path(m);
   // lo parts of each projection's activations, or none (prefill_split_mask)
   const int smask = prefill_split_mask();
@@ -1898,8 +1913,8 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
         g3.qkv.vcache = kv->v;
         g3.qkv.q_gain = L.q_norm;
         g3.qkv.k_gain = L.k_norm;
-        g3.qkv.rope_cos = m->rope_cos;
-        g3.qkv.rope_sin = m->rope_sin;
+        g3.qkv.rope_cos = rope_cos;
+        g3.qkv.rope_sin = rope_sin;
         g3.qkv.slot_stride = kv->slot_stride;
         g3.qkv.layer_stride = kv->layer_stride;
         g3.qkv.slot = slot;
@@ -1931,8 +1946,8 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
     q.q_gain = L.q_norm;
     q.k_gain = L.k_norm;
     q.eps = c.rms_norm_eps;
-    q.rope_cos = m->rope_cos;
-    q.rope_sin = m->rope_sin;
+    q.rope_cos = rope_cos;
+    q.rope_sin = rope_sin;
     q.q_out = w.q;
     q.kcache = kv->k;
     q.vcache = kv->v;
@@ -2047,15 +2062,95 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
                             s)) != hipSuccess)
       return hip_fail(e, "hipMemcpyAsync logits");
   }
-  int32_t tok = 0;
+  if (hidden != nullptr) {  // the final RMSNorm of every row (qwen_causal_lm.cpp:117-128)
+    if ((e = soc::launch_rmsnorm_rows(w.x, n, H, m->final_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) !=
+        hipSuccess)
+      return hip_fail(e, "final rmsnorm");
+    if ((e = hipMemcpyAsync(hidden, w.xn, static_cast<size_t>(n) * H * 4, hipMemcpyDefault, s)) != hipSuccess)
+      return hip_fail(e, "hipMemcpyAsync hidden");
+  }
+  int32_t tok = 0, id_err = 0;
   if ((e = hipMemcpyAsync(&tok, w.token, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync token");
+  if (ids_dev && (e = hipMemcpyAsync(&id_err, m->ctx->id_err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync id flag");
+  record_timer_stop(m->ctx);
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "prefill");
-  kv->len[slot] = pos_off + n;
+  if (id_err != 0) {
+    if ((e = hipMemset(m->ctx->id_err, 0, 4)) != hipSuccess) return hip_fail(e, "hipMemset");
+    return soc::fail(SOC_ERR_INVALID, "token id out of range");
+  }
   if (next_token) *next_token = tok;
+  return SOC_OK;
+}
+
+// The context's id-error flag (device words written by the id staging kernel), allocated on first use.
+int ensure_id_flag(soc_ctx* ctx) {
+  if (ctx->id_err != nullptr) return SOC_OK;
+  hipError_t e = hipMalloc(&ctx->id_err, 64);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc id flag");
+  if ((e = hipMemset(ctx->id_err, 0, 64)) != hipSuccess) return hip_fail(e, "hipMemset");
+  return SOC_OK;
+}
+}  // namespace
+
+int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off,
+                int32_t logit_rows, float* logits, int32_t* next_token) {
+  SOC_API_BEGIN
+  if (m == nullptr || kv == nullptr || ids == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  SOC_TRY(bind_kv(kv, m));
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (n <= 0) return soc::fail(SOC_ERR_INVALID, "prefill requires at least one token");  // generation_context.cpp:22-27
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (pos_off != kv->len[slot])
+    return soc::fail(SOC_ERR_STATE, "position_offset must equal the cached length of the slot");
+  if (pos_off + n > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "prefill exceeds KV capacity");
+  if (logit_rows < 0 || logit_rows > n) return soc::fail(SOC_ERR_INVALID, "logit_rows out of range");
+  SOC_TRY(validate_ids(m, ids, n));
+  SOC_TRY(run_prefill(m, kv, slot, ids, false, n, pos_off, 0, nullptr, logit_rows, logits, next_token));
+  kv->len[slot] = pos_off + n;
   return SOC_OK;
   SOC_API_END
 }
+
+namespace {
+// One decode step of one slot (the checks done by the caller): token `last`, or the id at dev_last in device memory;
+// logits [V] nullable (host or device), one synchronisation.
+int decode_one(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, const int32_t* dev_last, float* logits,
+               int32_t* next_token) {
+  SOC_TRY(ensure_decode_ws(m, kv->cap));
+  const bool xcd = use_xcd(m);
+  int32_t err = 0, id_err = 0, tok = 0;
+  SOC_TRY(run_decode_steps(m, kv, slot, last, 1, dev_last, &err));
+  hipStream_t s = m->ctx->stream;
+  hipError_t e;
+  if (logits != nullptr &&
+      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDefault,
+                          s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync logits");
+  if ((e = hipMemcpyAsync(&tok, m->dws.state, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync token");
+  if (dev_last != nullptr && (e = hipMemcpyAsync(&id_err, m->ctx->id_err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync id flag");
+  record_timer_stop(m->ctx);
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode");
+  SOC_TRY(one_launch_status(m, xcd, err));
+  if (id_err != 0) {
+    if ((e = hipMemset(m->ctx->id_err, 0, 4)) != hipSuccess) return hip_fail(e, "hipMemset");
+    return soc::fail(SOC_ERR_INVALID, "token id out of range");
+  }
+  kv->len[slot] += 1;
+  if (next_token) *next_token = tok;
+  return SOC_OK;
+}
+
+// An output of `bytes` bytes that the library copies into with hipMemcpyDefault: host memory, or device memory that
+// holds the whole range.
+int check_output(const char* what, const void* p, size_t bytes) {
+  if (p == nullptr || soc::classify_range(p, bytes) != soc::MemRange::kOutside) return SOC_OK;
+  return soc::fail(SOC_ERR_INVALID, std::string(what) + " extends past the end of its device allocation");
+}
+}  // namespace
 
 int soc_decode(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, float* logits, int32_t* next_token) {
   SOC_API_BEGIN
@@ -2065,20 +2160,80 @@ int soc_decode(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, float* logi
   if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
   if (kv->len[slot] + 1 > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "decode exceeds KV capacity");
   SOC_TRY(validate_ids(m, &last, 1));
-  SOC_TRY(ensure_decode_ws(m, kv->cap));
-  SOC_TRY(run_decode_steps(m, kv, slot, last, 1));
+  SOC_TRY(check_output("decode logits", logits, static_cast<size_t>(m->cfg.vocab_size) * 4));
+  return decode_one(m, kv, slot, last, nullptr, logits, next_token);
+  SOC_API_END
+}
+
+int soc_forward(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int32_t n, int32_t pos_off, float* hidden,
+                int32_t logit_rows, float* logits, int32_t* next_token) {
+  SOC_API_BEGIN
+  if (m == nullptr || ids == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (!m->finalized) return soc::fail(SOC_ERR_STATE, "model is not finalized");
+  if (n <= 0) return soc::fail(SOC_ERR_INVALID, "forward requires at least one token");
+  if (pos_off < 0) return soc::fail(SOC_ERR_INVALID, "position_offset must be >= 0");
+  if (logit_rows < 0 || logit_rows > n) return soc::fail(SOC_ERR_INVALID, "logit_rows out of range");
+  const soc_qwen_config& c = m->cfg;
+  const soc::MemRange where = soc::classify_range(ids, static_cast<size_t>(n) * 4);
+  if (where == soc::MemRange::kOutside)
+    return soc::fail(SOC_ERR_INVALID, "token ids extend past the end of their device allocation");
+  const bool ids_dev = where == soc::MemRange::kDeviceRange;
+  if (ids_dev)
+    SOC_TRY(ensure_id_flag(m->ctx));
+  else
+    SOC_TRY(validate_ids(m, ids, n));
+  SOC_TRY(check_output("hidden output", hidden, static_cast<size_t>(n) * c.hidden_size * 4));
+  SOC_TRY(check_output("logits output", logits, static_cast<size_t>(logit_rows) * c.vocab_size * 4));
+  if (kv == nullptr) {
+    // uncached (qwen_causal_lm.cpp:37-129, 231-248): causal attention over the n tokens alone, RoPE at
+    // position_offset + i; the private cache starts empty and is left empty
+    if (pos_off + n > m->rope_len)
+      return soc::fail(SOC_ERR_CAPACITY, "position_offset + token count exceeds max_position_embeddings");
+    if (m->ukv == nullptr || m->ukv->cap < n) {
+      if (m->ukv != nullptr) {
+        soc_kv_destroy(m->ukv);
+        m->ukv = nullptr;
+      }
+      SOC_TRY(kv_create(m->ctx, m, c.num_hidden_layers, c.num_key_value_heads, c.head_dim, 1, std::max(n, 64),
+                        &m->ukv));
+    }
+    m->ukv->len[0] = 0;
+    return run_prefill(m, m->ukv, 0, ids, ids_dev, n, 0, pos_off, hidden, logit_rows, logits, next_token);
+  }
+  SOC_TRY(bind_kv(kv, m));
+  if (slot < 0 || slot >= kv->slots) return soc::fail(SOC_ERR_INVALID, "slot out of range");
+  if (pos_off != kv->len[slot])
+    return soc::fail(SOC_ERR_STATE, "position_offset must equal the cached length of the slot");
+  if (pos_off + n > kv->cap) return soc::fail(SOC_ERR_CAPACITY, "forward exceeds KV capacity");
+  if (n == 1 && hidden == nullptr)
+    return decode_one(m, kv, slot, ids_dev ? 0 : ids[0], ids_dev ? ids : nullptr, logit_rows > 0 ? logits : nullptr,
+                      next_token);
+  SOC_TRY(run_prefill(m, kv, slot, ids, ids_dev, n, pos_off, 0, hidden, logit_rows, logits, next_token));
+  kv->len[slot] = pos_off + n;
+  return SOC_OK;
+  SOC_API_END
+}
+
+int soc_model_load_tensor_device(soc_model* m, const char* name, const void* src, int32_t dtype, int64_t numel) {
+  SOC_API_BEGIN
+  if (m == nullptr || name == nullptr || src == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
+  if (dtype != SOC_DTYPE_F32 && dtype != SOC_DTYPE_F16)
+    return soc::fail(SOC_ERR_INVALID, "weights must be float32 or float16");
+  auto it = m->tensors.find(name);
+  if (it == m->tensors.end()) return soc::fail(SOC_ERR_INVALID, std::string("unknown tensor name: ") + name);
+  if (it->second.numel != numel)
+    return soc::fail(SOC_ERR_INVALID, std::string("tensor ") + name + " has " + std::to_string(numel) +
+                                          " elements, expected " + std::to_string(it->second.numel));
+  SOC_TRY(soc::check_device_operand(name, src, static_cast<size_t>(numel) * (dtype == SOC_DTYPE_F32 ? 4 : 2)));
   hipStream_t s = m->ctx->stream;
-  hipError_t e;
-  if (logits != nullptr &&
-      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDefault,
-                          s)) != hipSuccess)
-    return hip_fail(e, "hipMemcpyAsync logits");
-  int32_t tok = 0;
-  if ((e = hipMemcpyAsync(&tok, m->dws.state, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
-    return hip_fail(e, "hipMemcpyAsync token");
-  if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode");
-  kv->len[slot] += 1;
-  if (next_token) *next_token = tok;
+  hipError_t e = dtype == SOC_DTYPE_F16
+                     ? hipMemcpyAsync(it->second.ptr, src, static_cast<size_t>(numel) * 2, hipMemcpyDeviceToDevice, s)
+                     : soc::launch_f32_to_f16(static_cast<const float*>(src), static_cast<size_t>(numel),
+                                              it->second.ptr, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "weight copy");
+  it->second.loaded = true;
+  m->finalized = false;
   return SOC_OK;
   SOC_API_END
 }
@@ -2299,6 +2454,147 @@ int soc_decode_batch_steps(soc_model* m, soc_kv* kv, int32_t n, const int32_t* s
 }
 
 // ---- op-level ----
+int soc_gemm_f16(soc_ctx* ctx, const void* x, const void* w, float* y, int32_t m, int32_t n, int32_t k) {
+  SOC_API_BEGIN
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  if (m <= 0 || n <= 0 || k <= 0 || k % 32 != 0)
+    return soc::fail(SOC_ERR_INVALID, "soc_gemm_f16: need m, n > 0 and k a positive multiple of 32");
+  const size_t M = static_cast<size_t>(m), N = static_cast<size_t>(n), K = static_cast<size_t>(k);
+  SOC_TRY(soc::check_device_operand("GEMM activations", x, M * K * 2));
+  SOC_TRY(soc::check_device_operand("GEMM weights", w, N * K * 2));
+  SOC_TRY(soc::check_device_operand("GEMM output", y, M * N * 4));
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 != 0)
+    return soc::fail(SOC_ERR_INVALID, "soc_gemm_f16: activations and weights must be 16-byte aligned");
+  soc::GemmSplitArgs g{};
+  g.ah = static_cast<const f16*>(x);
+  g.lda = k;
+  g.w = static_cast<const f16*>(w);
+  g.c = y;
+  g.ldc = n;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  hipError_t e = soc::launch_gemm_split(g, soc::EPI_STORE, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "gemm");
+  SOC_API_END
+}
+
+namespace {
+// Grows the context's split-key attention scratch to `floats` partial words and `ints` zeroed arrival counters.
+int ensure_op_attention_ws(soc_ctx* ctx, size_t floats, size_t ints) {
+  hipError_t e;
+  if (ctx->op_part_floats < floats) {
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    (void)hipFree(ctx->op_part);
+    ctx->op_part = nullptr;
+    ctx->op_part_floats = 0;
+    if ((e = hipMalloc(&ctx->op_part, floats * 4)) != hipSuccess) return hip_fail(e, "hipMalloc attention scratch");
+    ctx->op_part_floats = floats;
+  }
+  if (ctx->op_counter_ints < ints) {
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    (void)hipFree(ctx->op_counters);
+    ctx->op_counters = nullptr;
+    ctx->op_counter_ints = 0;
+    if ((e = hipMalloc(&ctx->op_counters, ints * 4)) != hipSuccess) return hip_fail(e, "hipMalloc attention counters");
+    // the combining block of each row resets its counter, so the zeros hold from one call to the next
+    if ((e = hipMemset(ctx->op_counters, 0, ints * 4)) != hipSuccess) return hip_fail(e, "hipMemset");
+    ctx->op_counter_ints = ints;
+  }
+  return SOC_OK;
+}
+
+int check_attention_shape(int32_t nq, int32_t nkv, int32_t head_dim, int32_t cap) {
+  if (head_dim != 128) return soc::fail(SOC_ERR_INVALID, "attention: head_dim must be 128");
+  if (nkv <= 0 || nq <= 0 || nq % nkv != 0 || (nq / nkv != 1 && nq / nkv != 2 && nq / nkv != 4 && nq / nkv != 8))
+    return soc::fail(SOC_ERR_INVALID, "attention: query heads per KV head must be 1, 2, 4 or 8");
+  if (cap <= 0) return soc::fail(SOC_ERR_INVALID, "attention: capacity must be positive");
+  return SOC_OK;
+}
+}  // namespace
+
+int soc_attention_prefill(soc_ctx* ctx, const float* q, const void* keys, const void* values, float* out, int32_t rows,
+                          int32_t pos_base, int32_t nq, int32_t nkv, int32_t head_dim, int32_t cap) {
+  SOC_API_BEGIN
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  SOC_TRY(check_attention_shape(nq, nkv, head_dim, cap));
+  if (rows <= 0 || pos_base < 0 || pos_base + rows > cap)
+    return soc::fail(SOC_ERR_INVALID, "attention: need rows > 0 and pos_base + rows <= capacity");
+  const size_t qbytes = static_cast<size_t>(rows) * nq * 128 * 4, kvbytes = static_cast<size_t>(nkv) * cap * 128 * 2;
+  SOC_TRY(soc::check_device_operand("attention queries", q, qbytes));
+  SOC_TRY(soc::check_device_operand("attention keys", keys, kvbytes));
+  SOC_TRY(soc::check_device_operand("attention values", values, kvbytes));
+  SOC_TRY(soc::check_device_operand("attention output", out, qbytes));
+  soc::AttnArgs a{};
+  a.qkv = q;
+  a.ld_qkv = nq * 128;
+  a.kcache = static_cast<f16*>(const_cast<void*>(keys));
+  a.vcache = static_cast<f16*>(const_cast<void*>(values));
+  a.cap = cap;
+  a.pos_base = pos_base;
+  a.out = out;
+  a.ld_out = nq * 128;
+  a.B = rows;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.chunk = kAttnChunk;
+  a.max_split = (pos_base + rows + kAttnChunk - 1) / kAttnChunk;
+  a.scale = 1.0f / std::sqrt(128.0f);  // grouped_query_attention.cpp:81
+  hipError_t e;
+  if (soc::attention_prefill_pairs_supported(nq, nkv)) {
+    e = soc::launch_attention_prefill_pairs(a, ctx->stream);
+  } else if (soc::attention_prefill_mfma_supported(nq, nkv)) {
+    e = soc::launch_attention_prefill_mfma(a, ctx->stream);
+  } else {  // 8 query heads per KV head: the split-key row kernel
+    if (a.max_split > 160) return soc::fail(SOC_ERR_INVALID, "attention: more than 40960 keys");
+    SOC_TRY(ensure_op_attention_ws(ctx, static_cast<size_t>(rows) * nq * a.max_split * 130,
+                                   static_cast<size_t>(rows) * nkv));
+    a.part = ctx->op_part;
+    a.counters = ctx->op_counters;
+    e = soc::launch_attention(a, 0, ctx->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "attention prefill");
+  SOC_API_END
+}
+
+int soc_attention_decode(soc_ctx* ctx, const float* q, const void* keys, const void* values, float* out,
+                         int32_t kv_len, int32_t nq, int32_t nkv, int32_t head_dim, int32_t cap) {
+  SOC_API_BEGIN
+  if (ctx == nullptr) return soc::fail(SOC_ERR_INVALID, "null context");
+  SOC_TRY(check_attention_shape(nq, nkv, head_dim, cap));
+  if (kv_len <= 0 || kv_len > cap) return soc::fail(SOC_ERR_INVALID, "attention: need 0 < kv_len <= capacity");
+  const size_t qbytes = static_cast<size_t>(nq) * 128 * 4, kvbytes = static_cast<size_t>(nkv) * cap * 128 * 2;
+  SOC_TRY(soc::check_device_operand("attention queries", q, qbytes));
+  SOC_TRY(soc::check_device_operand("attention keys", keys, kvbytes));
+  SOC_TRY(soc::check_device_operand("attention values", values, kvbytes));
+  SOC_TRY(soc::check_device_operand("attention output", out, qbytes));
+  soc::AttnArgs a{};
+  a.qkv = q;
+  a.ld_qkv = nq * 128;
+  a.kcache = static_cast<f16*>(const_cast<void*>(keys));
+  a.vcache = static_cast<f16*>(const_cast<void*>(values));
+  a.cap = cap;
+  a.pos_base = kv_len - 1;  // the query sits at the last cached position and sees keys 0 .. kv_len - 1
+  a.out = out;
+  a.ld_out = nq * 128;
+  a.B = 1;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.chunk = decode_attn_chunk(cap);
+  a.max_split = (kv_len + a.chunk - 1) / a.chunk;
+  a.scale = 1.0f / std::sqrt(128.0f);
+  if (a.max_split > 160) return soc::fail(SOC_ERR_INVALID, "attention: too many keys for the capacity's chunk size");
+  SOC_TRY(ensure_op_attention_ws(ctx, static_cast<size_t>(nq) * a.max_split * 130, static_cast<size_t>(nkv)));
+  a.part = ctx->op_part;
+  a.counters = ctx->op_counters;
+  hipError_t e = soc::launch_attention(a, 0, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? SOC_OK : hip_fail(e, "attention decode");
+  SOC_API_END
+}
+
 int soc_gemv_f16(soc_ctx* ctx, const void* w, const void* x, float* y, int32_t n, int32_t k) {
   if (ctx == nullptr || w == nullptr || x == nullptr || y == nullptr) return soc::fail(SOC_ERR_INVALID, "null argument");
   if (n <= 0 || k <= 0 || k % 8 != 0 || k > 16384) return soc::fail(SOC_ERR_INVALID, "soc_gemv_f16: need n > 0, 0 < k <= 16384, k % 8 == 0");
@@ -2359,10 +2655,10 @@ int soc_sample_topk(soc_ctx* ctx, const float* row, int32_t vocab, int32_t top_k
   std::vector<int32_t> idx;
   std::vector<float> vals;
   // a row in pageable host memory is never handed to a kernel: it is sorted where it lies, as the reference does
-  const MemRange where = classify_range(row, static_cast<size_t>(vocab) * 4);
-  if (where == MemRange::kOutside)
+  const soc::MemRange where = soc::classify_range(row, static_cast<size_t>(vocab) * 4);
+  if (where == soc::MemRange::kOutside)
     return soc::fail(SOC_ERR_INVALID, "Sampler logits row extends past the end of its device allocation");
-  bool whole_row = k > soc::kSampleMaxK || where == MemRange::kPageable;
+  bool whole_row = k > soc::kSampleMaxK || where == soc::MemRange::kPageable;
   if (!whole_row) {
     const size_t need = soc::sample_ws_bytes(vocab);
     if (ctx->sample_ws_bytes < need) {

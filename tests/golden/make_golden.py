@@ -60,6 +60,9 @@ SMALL_MODELS = {
     # eight KV heads like every Qwen3 model: decode takes the XCD-partitioned kernel on MI355X
     "tiny_kv8": (QwenConfig(vocab_size=512, hidden_size=256, num_hidden_layers=2, num_attention_heads=16,
                             num_key_value_heads=8, intermediate_size=768, tie_word_embeddings=False), 14, 11, 9),
+    # eight query heads on one KV head: the largest grouping the kernels accept (untied: varied greedy tokens)
+    "tiny_g8": (QwenConfig(vocab_size=384, hidden_size=256, num_hidden_layers=2, num_attention_heads=8,
+                           num_key_value_heads=1, intermediate_size=512, tie_word_embeddings=False), 15, 13, 7),
 }
 
 

@@ -77,3 +77,13 @@ def test_harness_sequence_matches_reference(golden, oracle_mod, tmp_path, name, 
         assert np.array_equal(vals[s].view(np.uint32), rvals.view(np.uint32)), f"step {s}"
     if top_k == 1:
         assert toks == g["tokens"].tolist()
+
+
+def test_qwen_causal_lm_cpp():
+    """The reference generation test's call shape with a model built from device weight tensors
+    (QwenCausalLM(QwenCausalLMWeights, QwenCausalLMParams), weights()), the four forwards, and the op classes."""
+    exe = CPP / "test_qwen_causal_lm"
+    assert exe.exists(), "build it with `python -m soc_amd.build` (build_cpp_tests)"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "test_qwen_causal_lm passed" in r.stdout
