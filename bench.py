@@ -13,8 +13,10 @@ the device. A "step" is one decode token. Also measured in the same run:
     int8 / int4 group-quantized matmul (group 64, fp16 scales) at batch 1 and 8, in GB/s against 8 TB/s,
   * the Qwen3-4B ragged decode batch (16 sequences, seeded KV lengths in [64, 4096]),
   * Qwen3-4B greedy decode at batch 1 (per-op kernels replayed as a HIP graph),
-  * the reference CPU runtime (compiled reference sources when available, else the oracle restatement), on the
-    host, one core, on a bounded sample.
+  * the kept C++ host API (GenerationContext::Generate through soc_amd/apps/soc_generate, a child process) on the
+    headline workload, wall clock,
+  * the reference CPU runtime on this host for every configuration (config 1 in full on the compiled reference, one
+    core; configs 4 and 5 extrapolated from one layer on the bit-identical restatement, all host threads).
 HBM traffic per launch of the dominant kernel comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
 profiles/ (scaled by the same counters over a plain copy of known size), when that summary exists.
 Prints one JSON line.
@@ -117,7 +119,7 @@ def ragged_bytes_per_step(cfg: S.QwenConfig, kv_lens) -> float:
     return weights + gains + len(kv_lens) * 2 * H + kv_pos * float(sum(s + 1 for s in kv_lens))
 
 
-def bench_ragged(ctx):
+def bench_ragged(ctx, steps: int = 64):
     """Qwen3-4B ragged continuous-batch decode: 16 sequences with seeded KV lengths U[64, 4096] (seeded N(0,1) fp16
     cache contents), 64 greedy steps of one token per sequence, each step one replay of the captured batch step."""
     cfg = S.QWEN3_4B
@@ -129,20 +131,20 @@ def bench_ragged(ctx):
             kv.fill_synthetic(slot, int(n), 7)
         slots = np.arange(RAGGED_SEQS, dtype=np.int32)
         toks = S.synth_tokens(6, "ragged.tokens", cfg.vocab_size, RAGGED_SEQS)
-        warm = S.decode_batch_steps(m, kv, slots, toks, RAGGED_STEPS)  # builds and replays the step graph
+        warm = S.decode_batch_steps(m, kv, slots, toks, steps)  # builds and replays the step graph
         start = [kv.length(int(i)) for i in slots]
         ctx.synchronize()
         ctx.timer_start()
-        out = S.decode_batch_steps(m, kv, slots, warm[-1], RAGGED_STEPS)
+        out = S.decode_batch_steps(m, kv, slots, warm[-1], steps)
         ms = ctx.timer_stop()
     finally:
         kv.close()
         m.close()
-    per_step = ms / RAGGED_STEPS
-    mean_bytes = np.mean([ragged_bytes_per_step(cfg, [s + t for s in start]) for t in range(RAGGED_STEPS)])
+    per_step = ms / steps
+    mean_bytes = np.mean([ragged_bytes_per_step(cfg, [s + t for s in start]) for t in range(steps)])
     gbs = mean_bytes / (per_step * 1e-3) / 1e9
     return {"workload": "Qwen3-4B ragged decode, 16 sequences, KV lengths U[64,4096] (seed 5), 64 steps",
-            "kv_lengths": [int(x) for x in lens], "tok_s": round(RAGGED_SEQS * RAGGED_STEPS / (ms * 1e-3), 1),
+            "kv_lengths": [int(x) for x in lens], "tok_s": round(RAGGED_SEQS * steps / (ms * 1e-3), 1),
             "ms_per_step": round(per_step, 4), "bytes_per_step": int(mean_bytes), "hbm_gbs": round(gbs, 1),
             "hbm_roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_head": [int(t) for t in out[0][:4]]}
 
@@ -236,40 +238,199 @@ def bench_ops(ctx, min_bytes: int = 640 << 20):
     return gemv, qmm
 
 
-def cpu_baseline(cfg: S.QwenConfig, budget_s: float = 20.0):
-    """The reference CPU runtime on a bounded sample: single-token cached forwards of the full model."""
+def _progress(msg: str) -> None:
+    """A line on stderr as each stage of the run ends (stdout carries only the result line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _host_threads() -> int:
+    """Host threads this process may use (the box gives one GPU's share of its cores)."""
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except AttributeError:  # pragma: no cover
+        return max(1, min(16, os.cpu_count() or 1))
+
+
+def _oracle_layers(O, cfg: S.QwenConfig, layers: int, seed: int):
+    """The oracle restatement of a model of cfg's shapes cut to `layers` layers (weights as synth_weights writes
+    them for the full model: the seeded generator is counter-based, so a layer's tensors do not depend on the count)."""
+    import dataclasses
+    small = dataclasses.replace(cfg, num_hidden_layers=layers)
+    return O.OracleModel(small, S.synth_weights(small, seed), "port")
+
+
+def cpu_baseline(cfg: S.QwenConfig):
+    """The reference CPU runtime on this host, for each configuration:
+
+    * config 1 (the headline): GenerationSession::Generate of the compiled reference (generation_session.cpp:46-79:
+      the 32-token prompt forwarded twice, uncached for the logits and cached for the KV, then 15 cached decode
+      steps, the calls GenerationSession::Generate makes, in its order) on one core, as the reference runs (no
+      threading anywhere in it); value = 16 tokens / wall time;
+    * config 2: Linear::Forward (linear.cpp:51-84) per Qwen3-0.6B projection shape at batch 1, compiled reference;
+    * config 3: the group-quantized matmul per shape at batch 1 and 8, int8 and int4: the reference has no such
+      kernel, so its restatement (orc_qmm_group), all host threads;
+    * config 4: prefill of 2048 tokens, extrapolated: one and two layers of Qwen3-0.6B timed on the restatement
+      (bit-identical to the reference, all host threads), the layer time x 28 plus the rest;
+    * config 5: one ragged step of the 16 Qwen3-4B sequences, extrapolated: per sequence a single-token cached
+      forward of a one-layer Qwen3-4B over its KV length on the restatement (all host threads), the layer part x 36
+      plus the LM head, summed over the sequences; x 64 steps for the config's run.
+    """
     try:
         from oracle import oracle as O
     except Exception as e:  # pragma: no cover
         return {"value": None, "error": str(e)}
+    threads = _host_threads()
+    out = {"unit": "tok/s", "cpu_model": _cpu_model(), "nproc": os.cpu_count(), "threads_available": threads}
+    # ---- config 1 ----
     kind = "reference" if O.ref_available() else "port"
     O.set_threads(1)
     w = S.synth_weights(cfg, 1)
     om = O.OracleModel(cfg, w, kind)
-    ids = S.synth_tokens(1, "prompt", cfg.vocab_size, 1)
-    times = []
-    t_start = time.time()
-    while len(times) < 5 and (time.time() - t_start) < budget_s:
-        if kind == "reference":
-            lib = O.ref_lib()
-            c = lib.ref_cache_create(om.h, 4)
-            logits = np.empty((1, cfg.vocab_size), np.float32)
-            t0 = time.perf_counter()
-            rc = lib.ref_forward_logits_cached(om.h, c, ids.ctypes.data, 1, 0, logits.ctypes.data)
-            times.append(time.perf_counter() - t0)
-            lib.ref_cache_destroy(c)
-            if rc != 0:
-                return {"value": None, "error": lib.ref_last_error().decode()}
-        else:
-            cache = O.OracleCache(om, 4)
-            t0 = time.perf_counter()
-            cache.forward(ids, 0)
-            times.append(time.perf_counter() - t0)
+    del w
+    prompt = S.synth_tokens(1, "prompt", cfg.vocab_size, PROMPT)
+    # GenerationSession::Generate's calls in its order (generation_session.cpp:46-79): the uncached prompt forward
+    # (its last row gives the first token), the cached prompt forward (fills the KV), then one cached single-token
+    # forward per further token; greedy sampling is the lowest-index argmax (sampler.cpp:42-48)
+    cache = O.RefCache(om, PROMPT + 24) if kind == "reference" else O.OracleCache(om, PROMPT + 24)
+    stages = {}
+    t0 = time.perf_counter()
+    first = om.forward_logits(prompt)[-1]
+    stages["prompt_uncached_s"] = time.perf_counter() - t0
+    _progress(f"cpu config 1: uncached prompt forward {stages['prompt_uncached_s']:.1f} s")
+    t1 = time.perf_counter()
+    cache.forward(prompt, 0)
+    stages["prompt_cached_s"] = time.perf_counter() - t1
+    _progress(f"cpu config 1: cached prompt forward {stages['prompt_cached_s']:.1f} s")
+    toks = [int(np.argmax(first))]
+    t2 = time.perf_counter()
+    for i in range(15):
+        row = cache.forward(np.array([toks[-1]], np.int32), PROMPT + i)[-1]
+        toks.append(int(np.argmax(row)))
+    stages["decode_15_s"] = time.perf_counter() - t2
+    gen_s = time.perf_counter() - t0
+    _progress(f"cpu config 1: 15 decode steps {stages['decode_15_s']:.1f} s")
+    del cache
     om.close()
-    sec = float(np.median(times))
-    return {"value": round(1.0 / sec, 4), "unit": "tok/s", "cores": 1, "kind": kind,
-            "sample": f"{len(times)} single-token cached forwards of the full {cfg.num_hidden_layers}-layer model "
-                      f"(one decode step each; median {sec:.3f} s), 1 host thread of {os.cpu_count()}"}
+    out.update({"value": round(16 / gen_s, 4), "cores": 1, "kind": kind,
+                "sample": f"config 1 in full: Qwen3-0.6B seed-1 weights, 32-token prompt, 16 greedy tokens as "
+                          f"GenerationSession::Generate runs them (prompt forwarded twice, uncached and cached, then "
+                          f"15 cached decode steps), one core: {gen_s:.1f} s",
+                "generate_s": round(gen_s, 2), **{k: round(v, 2) for k, v in stages.items()},
+                "decode_tok_s": round(15 / stages["decode_15_s"], 4), "generated_tokens_head": toks[:4]})
+    # ---- config 2 ----
+    lin = []
+    for name, n, k in OP_SHAPES:
+        x = np.random.default_rng(1).standard_normal((1, k)).astype(np.float32)
+        wt = S.synth_normal_f16(7, f"ops.{name}.w", 0.02, n * k).reshape(n, k)
+        y = np.empty((1, n), np.float32)
+        t0 = time.perf_counter()
+        if kind == "reference":
+            O.ref_lib().ref_linear_f16(x.ctypes.data, 1, k, wt.ctypes.data, n, y.ctypes.data)
+        else:
+            O.linear_f16(x, wt)
+        sec = time.perf_counter() - t0
+        lin.append({"shape": f"{name} {n}x{k}", "ms": round(sec * 1e3, 2), "gbs": round(2 * n * k / sec / 1e9, 2)})
+    out["config2_linear_bs1"] = {"kind": kind, "cores": 1, "rows": lin}
+    # ---- config 3 ----
+    qrows = []
+    O.set_threads(threads)
+    for name, n, k in OP_SHAPES:
+        a = S.synth_normal_f16(7, f"ops.{name}.x", 1.0, 8 * k).reshape(8, k)
+        for bits in (8, 4):
+            codes = S.synth_codes(7, f"ops.{name}.codes{bits}", bits, n * k)
+            scales = S.synth_uniform_f16(7, f"ops.{name}.scales{bits}", 0.005, 0.02, n * (k // 64))
+            for m in (1, 8):
+                t0 = time.perf_counter()
+                O.qmm_group(a[:m], codes, bits, scales, k, n)
+                sec = time.perf_counter() - t0
+                qrows.append({"shape": f"{name} {n}x{k}", "bits": bits, "m": m, "ms": round(sec * 1e3, 2)})
+    out["config3_qmm_g64"] = {"kind": "port (no reference kernel)", "cores": threads, "rows": qrows}
+    _progress("cpu configs 2 and 3 done")
+    # ---- config 4 ----
+    O.set_threads(threads)
+    ids = S.synth_tokens(4, "prefill", cfg.vocab_size, 2048)
+    times = {}
+    for layers in (1, 2):
+        m = _oracle_layers(O, cfg, layers, 1)
+        cache = O.OracleCache(m, 2048)
+        t0 = time.perf_counter()
+        cache.forward(ids, 0)
+        times[layers] = time.perf_counter() - t0
+        del cache
+        m.close()
+    layer_s = times[2] - times[1]
+    total4 = times[1] + (cfg.num_hidden_layers - 1) * layer_s
+    out["config4_prefill_2048"] = {"kind": "port", "cores": threads, "extrapolated": True,
+                                   "one_layer_s": round(layer_s, 3), "prefill_s": round(total4, 2),
+                                   "tok_s": round(2048 / total4, 1),
+                                   "sample": "Qwen3-0.6B with 1 and 2 layers timed (2048-token cached forward, "
+                                             "last-row head); layer = difference, x 28 layers"}
+    _progress(f"cpu config 4: one layer at 2048 tokens {layer_s:.1f} s")
+    # ---- config 5 ----
+    cfg4 = S.QWEN3_4B
+    lens = S.synth_int_uniform(5, "ragged.kv_len", RAGGED_MIN, RAGGED_MAX, RAGGED_SEQS)
+    toks5 = S.synth_tokens(6, "ragged.tokens", cfg4.vocab_size, RAGGED_SEQS)
+    m = _oracle_layers(O, cfg4, 1, 1)
+    rng = np.random.default_rng(7)
+    kvrow = rng.standard_normal((2, cfg4.num_key_value_heads, cfg4.head_dim)).astype(np.float32)
+    step_s = 0.0
+    # the LM head alone (one row through the 151936 x 2560 tied embedding), to split the one-layer forward
+    xh = np.random.default_rng(2).standard_normal((1, cfg4.hidden_size)).astype(np.float32)
+    emb = S.synth_normal_f16(1, "model.embed_tokens.weight", 0.02, cfg4.vocab_size * cfg4.hidden_size)
+    t0 = time.perf_counter()
+    O.linear_f16(xh, emb.reshape(cfg4.vocab_size, cfg4.hidden_size))
+    head_s = time.perf_counter() - t0
+    del emb
+    for i, n in enumerate(lens):
+        cache = O.OracleCache(m, int(n) + 2)
+        for pos in range(int(n)):  # the cache's contents do not change the cost; one row repeated
+            cache.write(0, pos, kvrow[0], kvrow[1])
+        t0 = time.perf_counter()
+        cache.forward(np.array([toks5[i]], np.int32), int(n))
+        t1 = time.perf_counter() - t0
+        del cache
+        step_s += cfg4.num_hidden_layers * max(t1 - head_s, 0.0) + head_s
+    m.close()
+    out["config5_ragged_4b"] = {"kind": "port", "cores": threads, "extrapolated": True,
+                                "step_s": round(step_s, 2), "run_64_steps_s": round(64 * step_s, 1),
+                                "tok_s": round(RAGGED_SEQS / step_s, 3), "lm_head_s": round(head_s, 3),
+                                "sample": "per sequence a single-token cached forward of a 1-layer Qwen3-4B over its "
+                                          "KV length (lengths of the GPU run), minus the LM head, x 36 layers, plus "
+                                          "the head; summed over the 16 sequences"}
+    _progress("cpu config 5 done")
+    O.set_threads(1)
+    return out
+
+
+def bench_cpp_api() -> dict | None:
+    """The kept C++ host API on the headline workload: soc_amd/apps/soc_generate (GenerationContext::Generate over
+    CommandScheduler -> QwenCausalLM::ForwardLogitsCached -> Sampler, Mac/gpu/src/runtime/generation_context.cpp:
+    118-172) with the seed-1 Qwen3-0.6B weights and the same 32-token prompt, 16 new tokens, run as a child process
+    after this one has released the GPU. Reports its wall-clock Generate time and DecodeNextToken latency."""
+    import subprocess
+    exe = ROOT / "soc_amd" / "apps" / "soc_generate"
+    if not exe.exists():
+        return {"error": f"{exe} is not built"}
+    args = [str(exe), "--model", "qwen3-0.6b", "--seed", "1", "--sigma", "0.02", "--prompt-seed", "1",
+            "--prompt-len", str(PROMPT), "--new", "16", "--repeat", "5", "--decode-steps", "64"]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": (r.stderr or r.stdout)[-400:]}
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["workload"] = ("GenerationContext::Generate, Qwen3-0.6B seed-1 weights, 32-token prompt, 16 greedy tokens "
+                       "(wall clock, host synchronisation included)")
+    out.pop("generate_ms", None)
+    return out
 
 
 TRAFFIC_SUMMARY = {"xcd": ROOT / "profiles" / "k_decode_xcd_qwen3_0p6b_traffic.md",
@@ -313,6 +474,9 @@ def main() -> None:
     ap.add_argument("--no-ragged", action="store_true", help="skip the Qwen3-4B ragged decode measurement")
     ap.add_argument("--no-ops", action="store_true", help="skip the GEMV / group-quantized matmul microbenchmarks")
     ap.add_argument("--no-4b", action="store_true", help="skip the Qwen3-4B batch-1 decode measurement")
+    ap.add_argument("--no-cpp-api", action="store_true", help="skip the GenerationContext (C++ API) measurement")
+    ap.add_argument("--ragged-steps", type=int, default=RAGGED_STEPS, help="steps of the ragged run (profiling)")
+    ap.add_argument("--steps-4b", type=int, default=64, help="timed steps of the Qwen3-4B batch-1 decode")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -327,19 +491,29 @@ def main() -> None:
     m = S.Model(ctx, cfg).synthesize(1, 0.02)
     path = m.decode_path()
     ms, mean_kv, toks = bench_decode(ctx, m, cfg, args.steps, args.warmup)
+    _progress(f"decode: {ms / args.steps:.4f} ms per token ({path})")
     ms_per_step = ms / args.steps
     tok_s = 1000.0 / ms_per_step
     bpt = decode_bytes_per_token(cfg, mean_kv)
     step_gbs = bpt / (ms_per_step * 1e-3) / 1e9
 
     prefill_ms = None if args.no_prefill else bench_prefill(ctx, m, cfg, 2048)
+    if prefill_ms is not None:
+        _progress(f"prefill of 2048 tokens: {prefill_ms:.3f} ms")
     us, alg = bench_gemv_kernel(ctx)
     gemv_gbs = alg / (us * 1e-6) / 1e9
     m.close()
     ops_gemv, ops_qmm = (None, None) if args.no_ops else bench_ops(ctx)
-    ragged = None if args.no_ragged else bench_ragged(ctx)
-    decode_4b = None if args.no_4b else bench_decode_4b(ctx)
+    ragged = None if args.no_ragged else bench_ragged(ctx, args.ragged_steps)
+    if ragged is not None:
+        _progress(f"Qwen3-4B ragged step: {ragged['ms_per_step']} ms")
+    decode_4b = None if args.no_4b else bench_decode_4b(ctx, args.steps_4b)
+    if decode_4b is not None:
+        _progress(f"Qwen3-4B decode: {decode_4b['ms_per_token']} ms per token")
     ctx.close()
+    cpp_api = None if args.no_cpp_api else bench_cpp_api()
+    if cpp_api is not None:
+        _progress(f"GenerationContext::Generate: {cpp_api.get('generate_ms_median')} ms for 16 tokens")
 
     if path in ("xcd", "persistent"):
         # one launch per token: the events around the K launches give the average launch duration (the short
@@ -385,6 +559,7 @@ def main() -> None:
         "qmm_g64": ops_qmm,
         "ragged_4b": ragged,
         "decode_4b": decode_4b,
+        "cpp_api_generate": cpp_api,
         "cpu_baseline": cpu,
         "generated_tokens_head": [int(t) for t in toks[:8]],
     }

@@ -71,13 +71,15 @@ def build(verbose: bool = False) -> Path:
 
 
 CPP_TESTS = ROOT / "tests" / "cpp"
+APPS = PKG / "apps"
 
 
 def build_cpp_tests(verbose: bool = False) -> list[Path]:
-    """Host-only C++ programs that drive the C++ host interface (include/soc/gpu/runtime.h) through the library."""
+    """Host-only C++ programs that drive the C++ host interface (include/soc/gpu/runtime.h) through the library: the
+    tests under tests/cpp and the programs under soc_amd/apps (soc_generate: generation through GenerationContext)."""
     outs = []
-    for src in sorted(CPP_TESTS.glob("*.cpp")):
-        exe = src.with_suffix("")
+    for src in sorted(CPP_TESTS.glob("*.cpp")) + sorted(APPS.glob("*.cpp")):
+        exe = src.with_suffix("") if src.parent == CPP_TESTS else src.with_name("soc_" + src.stem)
         cmd = ["g++", "-O2", "-std=c++17", f"-I{ROOT / 'include'}", str(src), f"-L{PKG}", "-lsoc_hip",
                f"-Wl,-rpath,{PKG}", "-o", str(exe)]
         if verbose:

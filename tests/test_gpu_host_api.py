@@ -87,3 +87,20 @@ def test_qwen_causal_lm_cpp():
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "test_qwen_causal_lm passed" in r.stdout
+
+
+def test_generation_context_qwen3_0p6b_matches_reference(golden):
+    """GenerationContext::Generate (generation_context.cpp:118-172) at Qwen3-0.6B shape: the 16 greedy tokens of the
+    compiled reference on the seed-2 N(0, 0.05) model and its 32-token prompt (qwen3_0p6b_s2.npz, 16 distinct
+    tokens), through soc_generate, the program that drives the kept C++ API."""
+    import json
+    g = golden("qwen3_0p6b_s2.npz")
+    exe = CPP.parent.parent / "soc_amd" / "apps" / "soc_generate"
+    assert exe.exists(), "build it with `python -m soc_amd.build` (build_cpp_tests)"
+    args = [str(exe), "--model", "qwen3-0.6b", "--seed", str(int(g["weight_seed"])), "--sigma", str(float(g["sigma"])),
+            "--prompt-seed", str(int(g["weight_seed"])), "--prompt-len", "32", "--new", "16", "--repeat", "1",
+            "--decode-steps", "4"]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["tokens"] == g["tokens"].tolist()
