@@ -33,6 +33,11 @@ struct soc_ctx {
   void* sample_ws = nullptr;    // soc_sample_topk: candidate search workspace and its output block
   size_t sample_ws_bytes = 0;
   int* sample_out = nullptr;
+  int* sample_host = nullptr;   // pinned host copy of the output block (hipHostMalloc)
+  // pinned host words a decode step's readback kernel writes (next token, wait error, token id error), with the
+  // address kernels use for them
+  int32_t* readback = nullptr;
+  int32_t* readback_dev = nullptr;
   // op-level attention (soc_attention_decode): split-key partials and arrival counters, grown on demand
   float* op_part = nullptr;
   size_t op_part_floats = 0;

@@ -124,6 +124,16 @@ hipError_t launch_kv_append_rows(const void* keys, const void* values, bool fp16
 
 // Token ids in device memory [n] -> dst [n], ids outside [0, vocab) replaced by 0 with *err set to 1 (ops.hip).
 hipError_t launch_stage_ids(const int32_t* src, int n, int vocab, int32_t* dst, int* err, hipStream_t s);
+// A decode step's inputs in one launch: state[0] = dev_last ? *dev_last (checked like launch_stage_ids) : host_last,
+// state[1] = pos, *ring = 0 (ops.hip).
+hipError_t launch_decode_prologue(const int32_t* dev_last, int32_t host_last, int32_t pos, int vocab, int32_t* state,
+                                  int32_t* ring, int* err, hipStream_t s);
+// host[0] = state[0], host[1] = *wait_err, host[2] = id_err ? *id_err : 0; host is a device address of pinned host
+// memory (ops.hip).
+hipError_t launch_decode_readback(const int32_t* state, const int32_t* wait_err, const int* id_err, int32_t* host,
+                                  hipStream_t s);
+// dst[0..n) = src[0..n) for n <= 16 words read from the host at launch (the words travel as kernel arguments).
+hipError_t launch_write_words(int32_t* dst, const int32_t* src, int n, hipStream_t s);
 
 // ---- quantized-model forward steps (qpath.hip) ----
 hipError_t launch_f32_to_f16(const float* x, size_t n, f16* y, hipStream_t s);
@@ -133,10 +143,16 @@ hipError_t launch_swiglu_f16(const float* gu, int T, int I, f16* h, hipStream_t 
 
 // ---- sampler: top-k candidates of one logits row (sample.hip) ----
 constexpr int kSampleChunk = 2048, kSampleMaxK = 64;
-// Device workspace bytes for a row of V logits.
+// LDS bound on the prefix lists one block merges: ceil(V / kSampleChunk) * k floats.
+constexpr size_t kSampleTreeBytes = 48 * 1024;
+// Whether a row of V logits at this k is searched on the device (k <= kSampleMaxK and the lists fit).
+bool sample_device_fits(int V, int k);
+// Device workspace bytes for a row of V logits; zero-filled when allocated (its first word is an arrival counter
+// that every k = 1 search leaves at zero).
 size_t sample_ws_bytes(int V);
 // Finds the candidates that std::partial_sort(top k of row / t) over 0..V-1 moves into its heap, in index order:
-// out[0] = count, out[1] = NaN seen, out[2 .. 2 + max_out) = indices, then max_out raw logits (k <= kSampleMaxK).
+// out[0] = count, out[1] = NaN seen, then for j < min(count, max_out): out[2 + 2 j] = index,
+// out[3 + 2 j] = the bits of its raw logit. Requires sample_device_fits(V, k).
 hipError_t launch_sample_topk(const float* row, int V, float t, int k, void* ws, int* out, int max_out,
                               hipStream_t s);
 

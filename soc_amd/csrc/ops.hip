@@ -6,6 +6,7 @@
 // These serve callers of the reference's op API and the op-level tests; the model's forward passes use the fused
 // kernels of the other files.
 #include <cmath>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -211,6 +212,47 @@ __global__ __launch_bounds__(256) void k_stage_ids(const int32_t* __restrict__ s
   }
 }
 
+// A decode step's inputs: state[0] = the token (the host's, or the validated id at dev_last), state[1] = its
+// position, ring position 0.
+__global__ void k_decode_prologue(const int32_t* __restrict__ dev_last, int32_t host_last, int32_t pos, int vocab,
+                                  int32_t* __restrict__ state, int32_t* __restrict__ ring, int* __restrict__ err) {
+  if (threadIdx.x != 0) return;
+  int32_t tok = host_last;
+  if (dev_last != nullptr) {
+    tok = *dev_last;
+    if (tok < 0 || tok >= vocab) {
+      tok = 0;
+      *err = 1;
+    }
+  }
+  state[0] = tok;
+  state[1] = pos;
+  *ring = 0;
+}
+
+// A decode step's results into pinned host words: the next token, the wait error flag, the token id error flag.
+__global__ void k_decode_readback(const int32_t* __restrict__ state, const int32_t* __restrict__ wait_err,
+                                  const int* __restrict__ id_err, int32_t* __restrict__ host) {
+  if (threadIdx.x != 0) return;
+  host[0] = state[0];
+  host[1] = *wait_err;
+  host[2] = id_err != nullptr ? *id_err : 0;
+}
+
+struct Words16 {
+  int32_t w[16];
+};
+
+// dst[0..n) = v.w[0..n), n <= 16, the words travelling in the kernel's arguments.
+__global__ void k_write_words(int32_t* __restrict__ dst, int n, Words16 v) {
+  const int i = threadIdx.x;
+  if (i >= n) return;
+  int32_t x = v.w[0];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) x = i == j ? v.w[j] : x;
+  dst[i] = x;
+}
+
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SOC_OK : fail(SOC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
@@ -227,6 +269,26 @@ constexpr int64_t kMaxElems = int64_t{1} << 31;  // element counts the kernels i
 
 hipError_t launch_stage_ids(const int32_t* src, int n, int vocab, int32_t* dst, int* err, hipStream_t s) {
   hipLaunchKernelGGL(k_stage_ids, dim3(std::min(64, (n + 255) / 256)), dim3(256), 0, s, src, n, vocab, dst, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_prologue(const int32_t* dev_last, int32_t host_last, int32_t pos, int vocab, int32_t* state,
+                                  int32_t* ring, int* err, hipStream_t s) {
+  hipLaunchKernelGGL(k_decode_prologue, dim3(1), dim3(64), 0, s, dev_last, host_last, pos, vocab, state, ring, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_readback(const int32_t* state, const int32_t* wait_err, const int* id_err, int32_t* host,
+                                  hipStream_t s) {
+  hipLaunchKernelGGL(k_decode_readback, dim3(1), dim3(64), 0, s, state, wait_err, id_err, host);
+  return hipGetLastError();
+}
+
+hipError_t launch_write_words(int32_t* dst, const int32_t* src, int n, hipStream_t s) {
+  if (n <= 0 || n > 16) return hipErrorInvalidValue;
+  Words16 v{};
+  std::memcpy(v.w, src, static_cast<size_t>(n) * 4);
+  hipLaunchKernelGGL(k_write_words, dim3(1), dim3(64), 0, s, dst, n, v);
   return hipGetLastError();
 }
 

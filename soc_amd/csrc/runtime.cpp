@@ -694,29 +694,21 @@ int one_launch_status(soc_model* m, bool xcd, int32_t err) {
 }
 
 // `steps` decode steps of one slot from token `last` (host value) or, with dev_last, the id in device memory (staged
-// and checked on the device). With err_out set, the one-launch paths do not synchronise: they queue the read of their
-// error word into *err_out and the caller synchronises, then checks it with one_launch_status (outside a trace run).
+// and checked on the device). With err_out set (and no SOC_TRACE_FILE), the one-launch paths neither read their error
+// word nor synchronise: the caller reads dws.err with its results and checks it with one_launch_status. logits_out
+// (device memory of vocab floats, one-launch paths only) receives the logits in place of dws.logits.
 int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps, const int32_t* dev_last = nullptr,
-                     int32_t* err_out = nullptr) {
+                     int32_t* err_out = nullptr, float* logits_out = nullptr) {
   DecodeWs& w = m->dws;
   hipStream_t s = m->ctx->stream;
-  const int32_t st[2] = {last, kv->len[slot]};
   hipError_t e;
-  if (dev_last == nullptr) {
-    if ((e = hipMemcpyAsync(w.state, st, sizeof(st), hipMemcpyHostToDevice, s)) != hipSuccess)
-      return hip_fail(e, "hipMemcpyAsync state");
-  } else {
-    if ((e = hipMemcpyAsync(w.state + 1, st + 1, 4, hipMemcpyHostToDevice, s)) != hipSuccess)
-      return hip_fail(e, "hipMemcpyAsync state");
-    if ((e = soc::launch_stage_ids(dev_last, 1, m->cfg.vocab_size, w.state, m->ctx->id_err, s)) != hipSuccess)
-      return hip_fail(e, "token id staging");
-  }
-  const int32_t zero = 0;
-  if ((e = hipMemcpyAsync(w.ring_pos, &zero, sizeof(zero), hipMemcpyHostToDevice, s)) != hipSuccess)
-    return hip_fail(e, "hipMemcpyAsync ring");
+  if ((e = soc::launch_decode_prologue(dev_last, last, kv->len[slot], m->cfg.vocab_size, w.state, w.ring_pos,
+                                       m->ctx->id_err, s)) != hipSuccess)
+    return hip_fail(e, "decode prologue");
   const bool xcd = use_xcd(m);
   if (xcd || use_persistent(m)) {
     soc::PersistArgs p = persist_args(m, kv, slot, w);
+    if (logits_out != nullptr) p.logits = logits_out;
     if (env_flag("SOC_FORCE_WAIT_ERROR")) {
       // failure-path tests: the error flag as a timed-out wait leaves it, raised before the launches (each block of
       // each launch then leaves at entry)
@@ -737,11 +729,11 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
     for (int i = 0; i < steps; ++i)
       if ((e = xcd ? soc::launch_decode_xcd(p, s) : soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
         return hip_fail(e, "persistent decode launch");
+    if (err_out != nullptr && trace_path == nullptr) return SOC_OK;  // the caller reads the flag and synchronises
     int32_t err_local = 0;
     int32_t& err = err_out != nullptr ? *err_out : err_local;
     if ((e = hipMemcpyAsync(&err, w.err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
       return hip_fail(e, "hipMemcpyAsync err");
-    if (err_out != nullptr && trace_path == nullptr) return SOC_OK;  // the caller synchronises and checks
     record_timer_stop(m->ctx);
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "persistent decode");
     if (p.trace != nullptr) {
@@ -1267,6 +1259,8 @@ int soc_ctx_destroy(soc_ctx* ctx) {
   (void)hipStreamDestroy(ctx->stream);
   (void)hipFree(ctx->sample_ws);
   (void)hipFree(ctx->sample_out);
+  (void)hipHostFree(ctx->sample_host);
+  (void)hipHostFree(ctx->readback);
   (void)hipFree(ctx->op_part);
   (void)hipFree(ctx->op_counters);
   (void)hipFree(ctx->id_err);
@@ -1330,7 +1324,14 @@ int soc_buffer_write(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 int soc_buffer_write_async(soc_ctx* ctx, void* dst, const void* src, size_t bytes) {
   if (ctx == nullptr || (bytes && (dst == nullptr || src == nullptr))) return soc::fail(SOC_ERR_INVALID, "null argument");
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  hipError_t e;
+  // a few aligned words into device memory travel in a kernel's arguments: no host staging copy, nothing to wait for
+  if (bytes > 0 && bytes <= 64 && bytes % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(src) % 4 == 0 && soc::classify_range(dst, bytes) == soc::MemRange::kDeviceRange)
+    e = soc::launch_write_words(static_cast<int32_t*>(dst), static_cast<const int32_t*>(src),
+                                static_cast<int>(bytes / 4), ctx->stream);
+  else
+    e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
   return e == hipSuccess ? SOC_OK : hip_fail(e, "soc_buffer_write_async");
 }
 
@@ -2116,24 +2117,44 @@ int soc_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, int3
 namespace {
 // One decode step of one slot (the checks done by the caller): token `last`, or the id at dev_last in device memory;
 // logits [V] nullable (host or device), one synchronisation.
+int ensure_readback(soc_ctx* ctx) {
+  if (ctx->readback != nullptr) return SOC_OK;
+  hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&ctx->readback), 64);
+  if (e != hipSuccess) return hip_fail(e, "hipHostMalloc readback words");
+  if ((e = hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->readback_dev), ctx->readback, 0)) != hipSuccess) {
+    (void)hipHostFree(ctx->readback);
+    ctx->readback = nullptr;
+    return hip_fail(e, "hipHostGetDevicePointer");
+  }
+  return SOC_OK;
+}
+
 int decode_one(soc_model* m, soc_kv* kv, int32_t slot, int32_t last, const int32_t* dev_last, float* logits,
                int32_t* next_token) {
   SOC_TRY(ensure_decode_ws(m, kv->cap));
+  SOC_TRY(ensure_readback(m->ctx));
   const bool xcd = use_xcd(m);
-  int32_t err = 0, id_err = 0, tok = 0;
-  SOC_TRY(run_decode_steps(m, kv, slot, last, 1, dev_last, &err));
+  int32_t err = 0;
+  const char* trace_path = std::getenv("SOC_TRACE_FILE");
+  const size_t logit_bytes = static_cast<size_t>(m->cfg.vocab_size) * 4;
+  // device logits are written where the caller wants them by the one-launch kernel itself
+  const bool direct = logits != nullptr && (xcd || use_persistent(m)) &&
+                      soc::classify_range(logits, logit_bytes) == soc::MemRange::kDeviceRange;
+  SOC_TRY(run_decode_steps(m, kv, slot, last, 1, dev_last, &err, direct ? logits : nullptr));
   hipStream_t s = m->ctx->stream;
   hipError_t e;
-  if (logits != nullptr &&
-      (e = hipMemcpyAsync(logits, m->dws.logits, static_cast<size_t>(m->cfg.vocab_size) * 4, hipMemcpyDefault,
-                          s)) != hipSuccess)
+  if (logits != nullptr && !direct &&
+      (e = hipMemcpyAsync(logits, m->dws.logits, logit_bytes, hipMemcpyDefault, s)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync logits");
-  if ((e = hipMemcpyAsync(&tok, m->dws.state, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
-    return hip_fail(e, "hipMemcpyAsync token");
-  if (dev_last != nullptr && (e = hipMemcpyAsync(&id_err, m->ctx->id_err, 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
-    return hip_fail(e, "hipMemcpyAsync id flag");
+  // next token and both error flags in one launch, written straight into pinned host words
+  if ((e = soc::launch_decode_readback(m->dws.state, m->dws.err, dev_last != nullptr ? m->ctx->id_err : nullptr,
+                                       m->ctx->readback_dev, s)) != hipSuccess)
+    return hip_fail(e, "decode readback");
   record_timer_stop(m->ctx);
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "decode");
+  const volatile int32_t* rb = m->ctx->readback;
+  const int32_t tok = rb[0], id_err = rb[2];
+  if (trace_path == nullptr) err = rb[1];  // with a trace, run_decode_steps has read the flag itself
   SOC_TRY(one_launch_status(m, xcd, err));
   if (id_err != 0) {
     if ((e = hipMemset(m->ctx->id_err, 0, 4)) != hipSuccess) return hip_fail(e, "hipMemset");
@@ -2658,7 +2679,7 @@ int soc_sample_topk(soc_ctx* ctx, const float* row, int32_t vocab, int32_t top_k
   const soc::MemRange where = soc::classify_range(row, static_cast<size_t>(vocab) * 4);
   if (where == soc::MemRange::kOutside)
     return soc::fail(SOC_ERR_INVALID, "Sampler logits row extends past the end of its device allocation");
-  bool whole_row = k > soc::kSampleMaxK || where == soc::MemRange::kPageable;
+  bool whole_row = !soc::sample_device_fits(vocab, k) || where == soc::MemRange::kPageable;
   if (!whole_row) {
     const size_t need = soc::sample_ws_bytes(vocab);
     if (ctx->sample_ws_bytes < need) {
@@ -2667,24 +2688,45 @@ int soc_sample_topk(soc_ctx* ctx, const float* row, int32_t vocab, int32_t top_k
       ctx->sample_ws = nullptr;
       ctx->sample_ws_bytes = 0;
       if ((e = hipMalloc(&ctx->sample_ws, need)) != hipSuccess) return hip_fail(e, "hipMalloc sampler workspace");
+      if ((e = hipMemset(ctx->sample_ws, 0, need)) != hipSuccess) {
+        (void)hipFree(ctx->sample_ws);
+        ctx->sample_ws = nullptr;
+        return hip_fail(e, "hipMemset sampler workspace");
+      }
       ctx->sample_ws_bytes = need;
     }
-    if (ctx->sample_out == nullptr &&
-        (e = hipMalloc(&ctx->sample_out, (2 + 2 * kMaxOut) * sizeof(int))) != hipSuccess)
+    constexpr size_t kOutInts = 2 + 2 * static_cast<size_t>(kMaxOut);
+    if (ctx->sample_out == nullptr && (e = hipMalloc(&ctx->sample_out, kOutInts * sizeof(int))) != hipSuccess)
       return hip_fail(e, "hipMalloc sampler output");
+    if (ctx->sample_host == nullptr &&
+        (e = hipHostMalloc(reinterpret_cast<void**>(&ctx->sample_host), kOutInts * sizeof(int))) != hipSuccess)
+      return hip_fail(e, "hipHostMalloc sampler output");
     if ((e = soc::launch_sample_topk(row, vocab, t, k, ctx->sample_ws, ctx->sample_out, kMaxOut, s)) != hipSuccess)
       return hip_fail(e, "sampler launch");
-    std::vector<int32_t> out(2 + 2 * kMaxOut);
-    if ((e = hipMemcpyAsync(out.data(), ctx->sample_out, out.size() * 4, hipMemcpyDeviceToHost, s)) != hipSuccess)
+    // the head of the block first (it holds every candidate of a typical row), the rest only when needed
+    constexpr int kHead = 512;
+    const int* out = ctx->sample_host;
+    if ((e = hipMemcpyAsync(ctx->sample_host, ctx->sample_out, (2 + 2 * kHead) * sizeof(int), hipMemcpyDeviceToHost,
+                            s)) != hipSuccess)
       return hip_fail(e, "hipMemcpyAsync sampler");
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "sampler");
     const int n = out[0];
     if (out[1] != 0 || n > kMaxOut || n < k) {
       whole_row = true;  // NaN logits, or more candidates than the output block holds: the reference's full sort
     } else {
-      idx.assign(out.begin() + 2, out.begin() + 2 + n);
+      if (n > kHead) {
+        if ((e = hipMemcpyAsync(ctx->sample_host + 2 + 2 * kHead, ctx->sample_out + 2 + 2 * kHead,
+                                static_cast<size_t>(n - kHead) * 2 * sizeof(int), hipMemcpyDeviceToHost, s)) !=
+            hipSuccess)
+          return hip_fail(e, "hipMemcpyAsync sampler");
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "sampler");
+      }
+      idx.resize(n);
       vals.resize(n);
-      std::memcpy(vals.data(), out.data() + 2 + kMaxOut, static_cast<size_t>(n) * 4);
+      for (int j = 0; j < n; ++j) {
+        idx[j] = out[2 + 2 * j];
+        std::memcpy(&vals[j], &out[3 + 2 * j], 4);
+      }
     }
   }
   if (whole_row) {

@@ -1,7 +1,8 @@
 """On-device top-k sampling (soc_sample_topk) against the reference GPU sampler's result (oracle sample_topk: the
 same std::partial_sort, Mac/gpu/src/runtime/sampler.cpp:44-66): identical token, candidate ids in the same order
 (ties included) and raw logits, on rows with many ties, at the vocabulary size of Qwen3 and at small sizes, for
-k in {1, 2, 5, 50, 64} (device search) and 65, 300 (host sort of the whole row)."""
+k in {1, 2, 5, 50, 64} (device search) and 65, 300 (host sort of the whole row); rows where every candidate
+enters, where each chunk ascends, and rows longer than the device search takes at k = 64."""
 import numpy as np
 import pytest
 
@@ -15,6 +16,11 @@ def _rows():
     yield "qwen vocab, 9 distinct values", rng.integers(-4, 5, 151936).astype(np.float32)
     yield "qwen vocab, normal", rng.standard_normal(151936).astype(np.float32) * 3
     yield "ascending (every candidate enters)", np.arange(20000, dtype=np.float32)
+    yield "ascending, 3000 candidates (more than the first readback holds)", np.arange(3000, dtype=np.float32)
+    yield "ascending inside each 2048-chunk, descending across chunks", \
+        np.concatenate([np.arange(2048, dtype=np.float32) - 3000 * c for c in range(6)])
+    yield "saw tooth", np.tile(np.arange(300, dtype=np.float32), 40)
+    yield "vocab 250000, normal", rng.standard_normal(250000).astype(np.float32)
     yield "descending", -np.arange(5000, dtype=np.float32)
     yield "all equal", np.zeros(4097, np.float32)
     yield "tiny", np.array([1.0, 5.0, 5.0, 5.0, -np.inf, 5.0, 2.0], np.float32)
@@ -38,16 +44,32 @@ def test_sample_topk_matches_reference(gpu_ctx, oracle_mod, k, temperature):
             assert tok == oracle_mod.sample(row, temperature, k), what
 
 
+def test_sample_topk_row_too_long_for_device_lists(gpu_ctx, oracle_mod):
+    """400000 logits at k = 64: the per-chunk lists one block would merge exceed its LDS bound, so the row is sorted
+    on the host; k = 5 on the same row stays on the device. Both equal the reference."""
+    row = np.random.default_rng(5).standard_normal(400000).astype(np.float32)
+    p = gpu_ctx.upload(row)
+    try:
+        for k in (5, 64):
+            tok, ids, vals = S.sample_topk(gpu_ctx, p, row.size, k, 1.0)
+            rtok, rids, rvals = oracle_mod.sample_topk(row, 1.0, k)
+            assert tok == rtok and np.array_equal(ids, rids)
+            assert np.array_equal(vals.view(np.uint32), rvals.view(np.uint32))
+    finally:
+        gpu_ctx.free(p)
+
+
 def test_sample_topk_row_with_nan_uses_whole_row(gpu_ctx, oracle_mod):
     row = np.random.default_rng(3).standard_normal(10000).astype(np.float32)
     row[[5, 777]] = np.nan
     p = gpu_ctx.upload(row)
     try:
-        tok, ids, vals = S.sample_topk(gpu_ctx, p, row.size, 5, 1.0)
+        for k in (1, 5):
+            tok, ids, vals = S.sample_topk(gpu_ctx, p, row.size, k, 1.0)
+            rtok, rids, _ = oracle_mod.sample_topk(row, 1.0, k)
+            assert tok == rtok and np.array_equal(ids, rids)
     finally:
         gpu_ctx.free(p)
-    rtok, rids, _ = oracle_mod.sample_topk(row, 1.0, 5)
-    assert tok == rtok and np.array_equal(ids, rids)
 
 
 def test_sample_topk_on_decode_logits(gpu_ctx, oracle_mod):
