@@ -280,17 +280,29 @@ __device__ __forceinline__ bool recv_head(const Ctx& c, const uint32_t* src, uin
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, HD * 4, 0x00020000);
+  // two staggered reads in flight (kStaggerLocal); every re-read is unconditional so the in-flight count is fixed
   uint32_t w0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
   uint32_t w1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
+  stagger<kStaggerLocal>();
+  uint32_t u0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
+  uint32_t u1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
   const uint64_t t0 = now_ticks();
   uint32_t spins = 0;
-  while (!__all(tw_tag(w0) == tag && tw_tag(w1) == tag)) {
+  while (true) {
+    if (__all(tw_tag(w0) == tag && tw_tag(w1) == tag)) break;
     if (give_up(c, spins, t0)) {
       wait_failed(c);
       return false;
     }
-    if (tw_tag(w0) != tag) w0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
-    if (tw_tag(w1) != tag) w1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
+    w0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
+    w1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
+    if (__all(tw_tag(u0) == tag && tw_tag(u1) == tag)) {
+      w0 = u0;
+      w1 = u1;
+      break;
+    }
+    u0 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 16);
+    u1 = __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4 + 256, 0, 16);
   }
   x0 = tw_val(w0);
   x1 = tw_val(w1);
@@ -360,14 +372,20 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(base_loc != nullptr ? base_loc : src), 0, H * 4, 0x00020000);
+    // reads are unconditional (a dead lane's words are replaced by the filler after the load)
     u32x4 v[2], bq[2];
+    auto read_all = [&]() {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int qi = (lane >> 3) + 8 * i;
-      const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
-      v[i] = live ? ll_peek_buf4(r, (k * H + 4 * (qb + qi)) * 4) : filler;
-      bq[i] = blive ? ll_peek_buf4(rb, (qb + qi) * 16) : filler;
-    }
+      for (int i = 0; i < 2; ++i) {
+        const int qi = (lane >> 3) + 8 * i;
+        const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
+        const u32x4 tv = ll_peek_buf4(r, (k * H + 4 * (qb + min(qi, nq1 - 1))) * 4);
+        const u32x4 tb = ll_peek_buf4(rb, (qb + min(qi, nq1 - 1)) * 16);
+        v[i] = live ? tv : filler;
+        bq[i] = blive ? tb : filler;
+      }
+    };
+    read_all();
     uint32_t spins = 0;
     while (true) {
       bool all = true;
@@ -378,13 +396,7 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
         wait_failed(c);
         return false;
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int qi = (lane >> 3) + 8 * i;
-        const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
-        if (live && !tw_quad_ok(v[i], tag)) v[i] = ll_peek_buf4(r, (k * H + 4 * (qb + qi)) * 4);
-        if (blive && !tw_quad_ok(bq[i], tag)) bq[i] = ll_peek_buf4(rb, (qb + qi) * 16);
-      }
+      read_all();
     }
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
     float ss = 0.0f;
@@ -422,14 +434,29 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
   // the gains of the lane's quad are requested before the poll: they do not depend on the exchanged words
   const f16x4 g4 = xlive ? ld_global(reinterpret_cast<const f16x4*>(gain), w * per + lane) : f16x4{0, 0, 0, 0};
-  u32x4 v = (xlive || slive) ? ll_peek_buf4(ro, off) : filler;
+  // two staggered reads in flight (kStaggerLocal), unconditional (dead lanes read in range or past the resource's
+  // end, which returns zeros, and take the filler)
+  const bool live = xlive || slive;
+  u32x4 t = ll_peek_buf4(ro, off);
+  u32x4 v = live ? t : filler;
+  stagger<kStaggerLocal>();
+  t = ll_peek_buf4(ro, off);
+  u32x4 v2 = live ? t : filler;
   uint32_t spins = 0;
-  while (!__all(tw_quad_ok(v, tag))) {
+  while (true) {
+    if (__all(tw_quad_ok(v, tag))) break;
     if (give_up(c, spins, t0)) {
       wait_failed(c);
       return false;
     }
-    if (!tw_quad_ok(v, tag)) v = ll_peek_buf4(ro, off);
+    t = ll_peek_buf4(ro, off);
+    v = live ? t : filler;
+    if (__all(tw_quad_ok(v2, tag))) {
+      v = v2;
+      break;
+    }
+    t = ll_peek_buf4(ro, off);
+    v2 = live ? t : filler;
   }
   if (xlive) {
     const int q = w * per + lane;
@@ -918,17 +945,31 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
       const int nq = min(64, IS / 4 - wid * 64);
       const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(loc_h + wid * 256, 0, nq * 16, 0x00020000);
       const u32x4 filler = {tag, tag, tag, tag};
-      u32x4 v = ln < nq ? ll_peek_buf4(r, ln * 16) : filler;
+      // two staggered reads in flight (kStaggerLocal), unconditional (lanes past nq read past the resource's end,
+      // which returns zeros, and take the filler)
+      u32x4 t = ll_peek_buf4(r, ln * 16);
+      u32x4 v = ln < nq ? t : filler;
+      stagger<kStaggerLocal>();
+      t = ll_peek_buf4(r, ln * 16);
+      u32x4 v2 = ln < nq ? t : filler;
       const uint64_t t0 = now_ticks();
       uint32_t spins = 0;
       bool ok = true;
-      while (!__all(tw_quad_ok(v, tag))) {
+      while (true) {
+        if (__all(tw_quad_ok(v, tag))) break;
         if (give_up(c, spins, t0)) {
           wait_failed(c);
           ok = false;
           break;
         }
-        if (!tw_quad_ok(v, tag)) v = ll_peek_buf4(r, ln * 16);
+        t = ll_peek_buf4(r, ln * 16);
+        v = ln < nq ? t : filler;
+        if (__all(tw_quad_ok(v2, tag))) {
+          v = v2;
+          break;
+        }
+        t = ll_peek_buf4(r, ln * 16);
+        v2 = ln < nq ? t : filler;
       }
       if (ok && ln < nq)
         store_hl4(hhl, ISM, 4 * (wid * 64 + ln), f32x4{tw_val(v.x), tw_val(v.y), tw_val(v.z), tw_val(v.w)});

@@ -676,11 +676,10 @@ hipError_t launch_gemv(const GemvArgs& a, int epi, hipStream_t s) {
   constexpr int R = 4, U = 2;
   const size_t lds = static_cast<size_t>(a.K) * sizeof(float);
   const dim3 grid(gemv_grid(a.N, R)), block(256);
-  const char* mode = std::getenv("SOC_GEMV");
-  // K split over the waves of a block, no staging, for all but the tallest matrices (SOC_GEMV=ks / rows forces
-  // either); above 16384 row groups the row-per-wave kernel has waves enough to cover its staging
+  // K split over the waves of a block, no staging, for all but the tallest matrices; above 16384 row groups the
+  // row-per-wave kernel has waves enough to cover its staging
   const int groups = (a.N + (epi == EPI_SWIGLU ? 2 : R) - 1) / (epi == EPI_SWIGLU ? 2 : R);
-  const bool ks = mode != nullptr ? std::strcmp(mode, "ks") == 0 : groups < 16384;
+  const bool ks = groups < 16384;
   const uintptr_t align = reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.xh) |
                           reinterpret_cast<uintptr_t>(a.gain) | reinterpret_cast<uintptr_t>(a.w) |
                           reinterpret_cast<uintptr_t>(a.w2);
@@ -844,10 +843,10 @@ bool qmm_mfma_supported(const QmmArgs& a, int bits) {
 hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
   const char* mode = std::getenv("SOC_QMM");
   // matrix cores for tall matrices (the LM head); the dot-product kernel keeps the short ones, where a 128-row
-  // block per 16 waves would leave most of the chip idle (SOC_QMM=mfma / dot force either)
+  // block per 16 waves would leave most of the chip idle (SOC_QMM=mfma takes the MFMA kernel wherever it applies:
+  // the parity tests run it on the short shapes too)
   const bool force_mfma = mode != nullptr && std::strcmp(mode, "mfma") == 0;
-  const bool force_dot = mode != nullptr && std::strcmp(mode, "dot") == 0;
-  if (qmm_mfma_supported(a, bits) && !force_dot && (force_mfma || a.N >= 16384)) {
+  if (qmm_mfma_supported(a, bits) && (force_mfma || a.N >= 16384)) {
     const size_t lds = static_cast<size_t>(16) * (a.K + 8) * sizeof(f16);
     // 8-wave blocks, two resident per CU, tiles looped; int4 (half-size chunks) with 768 blocks, the last third
     // starting as the first blocks finish: 52 % of HBM bandwidth at 151936 x 1024, batch 8, against 48 % with 512

@@ -232,8 +232,7 @@ struct GemmArgs {
   int ldc;
   int M, N, K;
 };
-hipError_t launch_gemm_f32a(const GemmArgs& g, int epi, hipStream_t s);
-// Same contract on MFMA (fp16 inputs, fp32 accumulation); split = hi/lo fp16 parts of the fp32 activations.
+// MFMA (fp16 inputs, fp32 accumulation); split = hi/lo fp16 parts of the fp32 activations. Requires K % 32 == 0.
 bool gemm_mfma_supported(const GemmArgs& g);
 hipError_t launch_gemm_mfma(const GemmArgs& g, int epi, bool split, hipStream_t s);
 // Same products on activations pre-split into hi = f16(a) and lo = f16((a - hi) * 2^11) arrays [M][lda]

@@ -244,8 +244,8 @@ int check_config(const soc_qwen_config& c) {
   const int G = c.num_attention_heads / c.num_key_value_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return soc::fail(SOC_ERR_INVALID, "qwen config: query heads per KV head must be 1, 2, 4 or 8");
-  if (c.hidden_size % 8 != 0 || c.intermediate_size % 8 != 0)
-    return soc::fail(SOC_ERR_INVALID, "qwen config: hidden and intermediate sizes must be multiples of 8");
+  if (c.hidden_size % 32 != 0 || c.intermediate_size % 32 != 0)
+    return soc::fail(SOC_ERR_INVALID, "qwen config: hidden and intermediate sizes must be multiples of 32");
   if (!(c.rms_norm_eps > 0.0f) || !(c.rope_theta > 0.0))
     return soc::fail(SOC_ERR_INVALID, "qwen config: eps and rope_theta must be positive");
   if (static_cast<size_t>(c.hidden_size) * 4 > 64 * 1024 || static_cast<size_t>(c.intermediate_size) * 4 > 64 * 1024)
@@ -858,25 +858,19 @@ int prefill_split_mask() {
   return mask;
 }
 
-// Prefill projections on fp32 activations: MFMA when K allows, on fp16 activations or their hi/lo pairs (hi/lo
-// when prefill_split_mask() has any of the bits `which`); SOC_PREFILL_GEMM=fma selects the FMA kernel.
+// Prefill projections on fp32 activations, on MFMA (every K the model config admits is a multiple of 32), the
+// activations as fp16 or as hi/lo pairs (hi/lo when prefill_split_mask() has any of the bits `which`).
 hipError_t prefill_gemm(const soc::GemmArgs& g, int epi, hipStream_t s, int which = kSplitAll) {
-  const char* mode = std::getenv("SOC_PREFILL_GEMM");
-  const bool fma = mode != nullptr && std::strcmp(mode, "fma") == 0;
-  if (!fma && soc::gemm_mfma_supported(g)) {
-    return soc::launch_gemm_mfma(g, epi, (prefill_split_mask() & which) != 0, s);
-  }
-  return soc::launch_gemm_f32a(g, epi, s);
+  return soc::launch_gemm_mfma(g, epi, (prefill_split_mask() & which) != 0, s);
 }
 
-// The prefill layers use the GEMM on fp16 activations written by their producers (direct-to-LDS pipeline) when the
-// shapes allow; SOC_PREFILL_GEMM=fma and SOC_PREFILL_GEMM=staged (the register-staged MFMA kernel, same products)
-// keep the fp32-activation kernels.
+// The prefill layers use the GEMM on fp16 activations written by their producers (direct-to-LDS pipeline);
+// SOC_PREFILL_GEMM=staged keeps the register-staged MFMA kernel on fp32 activations (same products: the parity
+// tests compare the two).
 bool prefill_split_path(const soc_model* m) {
+  (void)m;
   const char* mode = std::getenv("SOC_PREFILL_GEMM");
-  if (mode != nullptr && (std::strcmp(mode, "fma") == 0 || std::strcmp(mode, "staged") == 0)) return false;
-  const int H = m->cfg.hidden_size, I = m->cfg.intermediate_size;
-  return H % 32 == 0 && m->qd % 32 == 0 && I % 32 == 0;
+  return !(mode != nullptr && std::strcmp(mode, "staged") == 0);
 }
 
 
@@ -898,8 +892,6 @@ hipError_t split_gemm(const soc::f16* ah, const soc::f16* al, int lda, const soc
   return soc::launch_gemm_split(g, epi, s);
 }
 
-// Projections of a ragged decode batch (M = rows of the batch): the skinny MFMA kernel in slabs of 16 rows up to
-// 64 rows (SOC_BATCH_GEMM=tile selects the 128x128-tile GEMM of the prefill path).
 // A ragged-batch projection on the skinny kernel, in chunks of 16 rows: `proto` carries the weights, the input
 // RMSNorm gain (or none) and the epilogue's own arguments; rows m0.. of x, c, q_out, pos and slots per chunk.
 hipError_t batch_skinny(const soc::SkinnyArgs& proto, int n, int epi, hipStream_t s) {
@@ -1019,9 +1011,8 @@ int enqueue_batch_step(soc_model* m, soc_kv* kv, int n, int max_split, int32_t* 
   const int H = c.hidden_size, I = c.intermediate_size;
   hipError_t e;
   // up to 64 rows: the skinny kernels per projection and 16 rows (input RMSNorm and the q/k norm, RoPE and KV append
-  // folded into them); beyond, or with SOC_BATCH_GEMM=tile, the tile GEMMs with separate normalisation and q/k kernels
-  const char* mode = std::getenv("SOC_BATCH_GEMM");
-  const bool fused = w.skpart != nullptr && n <= 64 && !(mode != nullptr && std::strcmp(mode, "tile") == 0);
+  // folded into them); beyond, the tile GEMMs with separate normalisation and q/k kernels
+  const bool fused = w.skpart != nullptr && n <= 64;
   soc::SkinnyArgs sk{};
   sk.part = w.skpart;
   sk.eps = c.rms_norm_eps;
@@ -1889,15 +1880,12 @@ int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool
   for (int l = 0; m->qbits == 0 && l < c.num_hidden_layers; ++l) {  // fp16 models
     const DevLayer& L = m->layers[l];
     soc::GemmArgs g{};
-    bool qkv_fused = false;
+    const bool qkv_fused = split;  // the staged kernel's QKV is followed by the separate q/k-norm kernel
     if (split) {
       if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, nullptr, w.ph, pl_qkv, s)) !=
           hipSuccess)
         return hip_fail(e, "rmsnorm");
       // QKV projection with the per-head q/k RMSNorm + RoPE, q output and K/V cache append in its epilogue
-      // (SOC_PREFILL_QKV=separate: plain projection, then the q/k-norm kernel)
-      const char* qm = std::getenv("SOC_PREFILL_QKV");
-      qkv_fused = qm == nullptr || std::strcmp(qm, "separate") != 0;
       soc::GemmSplitArgs g3{};
       g3.ah = w.ph;
       g3.al = pl_qkv;
@@ -1908,7 +1896,7 @@ int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool
       g3.M = n;
       g3.N = m->qkv_rows;
       g3.K = H;
-      if (qkv_fused) {
+      {
         g3.qkv.q_out = w.q;
         g3.qkv.kcache = kv->k;
         g3.qkv.vcache = kv->v;
@@ -1926,8 +1914,7 @@ int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool
         g3.qkv.nkv = c.num_key_value_heads;
         g3.qkv.eps = c.rms_norm_eps;
       }
-      if ((e = soc::launch_gemm_split(g3, qkv_fused ? soc::EPI_QKV : soc::EPI_STORE, s)) != hipSuccess)
-        return hip_fail(e, "gemm qkv");
+      if ((e = soc::launch_gemm_split(g3, soc::EPI_QKV, s)) != hipSuccess) return hip_fail(e, "gemm qkv");
     } else {
       if ((e = soc::launch_rmsnorm_rows(w.x, n, H, L.in_norm, c.rms_norm_eps, w.xn, nullptr, nullptr, s)) != hipSuccess)
         return hip_fail(e, "rmsnorm");

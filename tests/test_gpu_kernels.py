@@ -78,15 +78,13 @@ def _qmm_inputs(n, k, bits, m):
 
 
 @pytest.mark.parametrize("bits", [8, 4])
-@pytest.mark.parametrize("m", [1, 2, 4, 8])
 @pytest.mark.parametrize("n,k", QMM_SHAPES)
-@pytest.mark.parametrize("mode", ["auto", "mfma"])
+@pytest.mark.parametrize("mode,m", [("auto", 1), ("auto", 2), ("auto", 4), ("auto", 8),
+                                    ("mfma", 2), ("mfma", 4), ("mfma", 8)])
 def test_qmm_matches_oracle(gpu_ctx, oracle_mod, monkeypatch, bits, m, n, k, mode):
     """auto: the dot-product kernel at m = 1 and for short matrices, the MFMA kernel for tall ones at m >= 2;
-    mfma: the MFMA kernel wherever it applies (m >= 2)."""
+    mfma: the MFMA kernel wherever it applies (it serves m >= 2)."""
     if mode == "mfma":
-        if m == 1:
-            pytest.skip("the MFMA kernel serves m >= 2")
         monkeypatch.setenv("SOC_QMM", "mfma")
     ctx = gpu_ctx
     codes, scales, x = _qmm_inputs(n, k, bits, m)
