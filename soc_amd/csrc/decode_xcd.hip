@@ -185,12 +185,16 @@ struct Lds {
   static_assert(G * NBG * PW * 4 <= NW * KT * HD * 2 && HMAX * 4 <= NW * KT * HD * 2, "VT reuse");
 };
 
+// cross_reduce2's first stage runs on this many waves, wave w's first poll issued w * kStage1Stagger sleep units
+// (64 clocks each) after wave 0's.
+constexpr int kStage1Waves = 4, kStage1Stagger = 8;
+
 struct Ctx {
   const PersistArgs& a;
   int g, j, token, pos;
   uint32_t phase0;  // (step - 1) * L: the tag of layer l is (phase0 + l) & 3
   char* lds;
-  int* flag;
+  int* flag;  // LDS: [0] a wait failed, [1] XCD, [2] rank, [3] last block, [4] cross_reduce2 stage-1 marker
 };
 
 // Attention blocks of the XCD's computing group for S keys (at most 16, whole 32-key tiles each) and keys per block;
@@ -351,81 +355,119 @@ __device__ __forceinline__ void embed_row(const Ctx& c, int w, const f16* embed_
 
 // x = base + sum_k P_k over the eight XCDs' partials P_k (src, [8][H] words), reading each remote partial once per
 // XCD instead of once per block:
-// stage 1 (wave 0 of a block with do1): the block's 1/16 of the elements, quads jj * H/64 ..; base from base_loc
-//   (XCD-local words) or, if null, from xres; x goes to out[0, H) and the block's sum of squares of x to out[H + jj],
-//   as XCD-local words with the same tag;
+// stage 1 (waves 0 .. kStage1Waves - 1 of a block with do1, staggered; the first to see the partials writes, and
+//   marks the call done with `marker`, positive and unique among one launch's calls): the block's 1/16 of the
+//   elements, quads jj * H/64 ..; base from base_loc (XCD-local words) or, if null, from xres; x goes to out[0, H)
+//   and the block's sum of squares of x to out[H + jj], as XCD-local words with the same tag;
 // stage 2 (every wave): all of x and the 16 sums from out; x into xres, the hi/lo rows of x * gain into xhl (or, with
 //   xn32 set, x * gain in fp32 into xn32), red[0..7] = pair sums of the 16 sums (rms_scale adds them in a fixed
 //   order). Every block reads the same words, so x and the norm agree in every block of every XCD. The caller's
 //   barrier publishes xres, xhl / xn32 and red.
 __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool do1, const uint32_t* src,
                                               const uint32_t* base_loc, uint32_t tag, uint32_t* out, const f16* gain,
-                                              float* xres, f16* xhl, float* xn32, float* red, int trace_pt = -1) {
+                                              float* xres, f16* xhl, float* xn32, float* red, int marker,
+                                              int trace_pt = -1) {
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));  // per call: keeps the compiler from hoisting per-lane addresses out of the layers
   const int H = c.a.H;
   const u32x4 filler = {tag, tag, tag, tag};
   const uint64_t t0 = now_ticks();
-  if (w == 0 && do1) {
+  // stage 1 on kStage1Waves waves, the first polls of wave w issued w * kStage1Stagger sleep units after wave 0's:
+  // whichever wave sees the remote partials first writes the block's elements (every wave computes the same bits),
+  // then marks the call done in flag[4] so the others stop polling
+  if (w < kStage1Waves && do1) {
     const int k = lane & 7, nq1 = H / 64, qb = jj * nq1;
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(src), 0, H * NX * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(base_loc != nullptr ? base_loc : src), 0, H * 4, 0x00020000);
-    // reads are unconditional (a dead lane's words are replaced by the filler after the load)
-    u32x4 v[2], bq[2];
-    auto read_all = [&]() {
+    uint32_t spins = 0;
+    // the base first, into registers: from the XCD-local words (written a phase earlier: normally already there) or
+    // from xres, which stage 2 of a faster wave may overwrite while this wave still polls
+    f32x4 bx[2];
+    if (base_loc != nullptr) {
+      u32x4 bq[2];
+      auto read_b = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int qi = (lane >> 3) + 8 * i;
+          const u32x4 tb = ll_peek_buf4(rb, (qb + min(qi, nq1 - 1)) * 16);
+          bq[i] = qi < nq1 && k == 0 ? tb : filler;
+        }
+      };
+      read_b();
+      while (!__all(tw_quad_ok(bq[0], tag) && tw_quad_ok(bq[1], tag))) {
+        if (give_up(c, spins, t0)) {
+          wait_failed(c);
+          return false;
+        }
+        read_b();
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) bx[i] = f32x4{tw_val(bq[i].x), tw_val(bq[i].y), tw_val(bq[i].z), tw_val(bq[i].w)};
+    } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int qi = (lane >> 3) + 8 * i;
-        const bool live = qi < nq1, blive = live && base_loc != nullptr && k == 0;
+        bx[i] = *reinterpret_cast<const f32x4*>(xres + 4 * (qb + min(qi, nq1 - 1)));
+      }
+    }
+    poll_pause(w * kStage1Stagger);
+    // remote partials; reads unconditional (a dead lane's words are replaced by the filler after the load)
+    u32x4 v[2];
+    auto read_v = [&]() {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int qi = (lane >> 3) + 8 * i;
         const u32x4 tv = ll_peek_buf4(r, (k * H + 4 * (qb + min(qi, nq1 - 1))) * 4);
-        const u32x4 tb = ll_peek_buf4(rb, (qb + min(qi, nq1 - 1)) * 16);
-        v[i] = live ? tv : filler;
-        bq[i] = blive ? tb : filler;
+        v[i] = qi < nq1 ? tv : filler;
       }
     };
-    read_all();
-    uint32_t spins = 0;
-    while (true) {
-      bool all = true;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) all = all && tw_quad_ok(v[i], tag) && tw_quad_ok(bq[i], tag);
-      if (__all(all)) break;
+    read_v();
+    bool mine = true;
+    while (!__all(tw_quad_ok(v[0], tag) && tw_quad_ok(v[1], tag))) {
+      if (*reinterpret_cast<volatile int*>(&c.flag[4]) == marker) {  // another wave of the block was first
+        mine = false;
+        break;
+      }
       if (give_up(c, spins, t0)) {
         wait_failed(c);
         return false;
       }
-      read_all();
+      read_v();
     }
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
-    float ss = 0.0f;
+    if (mine) {
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(out, 0, (H + NBG) * 4, 0x00020000);
+      float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int qi = (lane >> 3) + 8 * i, q = qb + qi;
-      const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
-      const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
-      if (qi < nq1 && k == 0) {
-        f32x4 x = base_loc != nullptr ? f32x4{tw_val(bq[i].x), tw_val(bq[i].y), tw_val(bq[i].z), tw_val(bq[i].w)}
-                                      : *reinterpret_cast<const f32x4*>(xres + 4 * q);
-        x[0] += s0;
-        x[1] += s1;
-        x[2] += s2;
-        x[3] += s3;
-        u32x4 wq;
+      for (int i = 0; i < 2; ++i) {
+        const int qi = (lane >> 3) + 8 * i, q = qb + qi;
+        const float s0 = sum8(tw_val(v[i].x)), s1 = sum8(tw_val(v[i].y));
+        const float s2 = sum8(tw_val(v[i].z)), s3 = sum8(tw_val(v[i].w));
+        if (qi < nq1 && k == 0) {
+          f32x4 x = bx[i];
+          x[0] += s0;
+          x[1] += s1;
+          x[2] += s2;
+          x[3] += s3;
+          u32x4 wq;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wq[e] = tw_pack(x[e], tag);
-          const float xr = tw_val(wq[e]);
-          ss += xr * xr;
+          for (int e = 0; e < 4; ++e) {
+            wq[e] = tw_pack(x[e], tag);
+            const float xr = tw_val(wq[e]);
+            ss += xr * xr;
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(wq, ro, q * 16, 0, 0);
         }
-        __builtin_amdgcn_raw_buffer_store_b128(wq, ro, q * 16, 0, 0);
       }
+      ss = wave_sum(ss);
+      if (lane == 0) {
+        ll_store_local(out, H + jj, ss, tag);
+        c.flag[4] = marker;
+      }
+      if (trace_pt >= 0 && c.a.trace != nullptr && lane == 0)
+        c.a.trace[(c.g * NBX + c.j) * kTracePts + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
     }
-    ss = wave_sum(ss);
-    if (lane == 0) ll_store_local(out, H + jj, ss, tag);
-    if (trace_pt >= 0 && c.a.trace != nullptr && threadIdx.x == 0)
-      c.a.trace[(c.g * NBX + c.j) * kTracePts + trace_pt] = now_ticks();  // stage 1 done (diagnostics)
   }
   // stage 2: waves 0..3 take quad w * H/16 + lane of x, wave 4's lanes 0..3 the 16 sums (fewer waves polling L2)
   const int per = H / 16;
@@ -621,7 +663,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     if (layer == 0)
       embed_row(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xhl, red);
     else
-      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red,
+      cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red, 2 * layer + 1,
                     layer == a.L / 2 ? 15 : -1);
     XTRACE(1);
     XSYNC();  // #1
@@ -900,7 +942,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     }
     XTRACE(6);
     // ---- G: x' = x + sum_k O_k, RMSNorm input ----
-    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xhl, nullptr, red,  // x' also for the other group
+    cross_reduce2(c, wid, jj, true, a.xo, nullptr, tag, loc_xg, W[1], xres, xhl, nullptr, red, 2 * layer + 2,  // x' also for the other group
                   layer == a.L / 2 ? 14 : -1);
     XTRACE(7);
     XSYNC();  // #4
@@ -1007,7 +1049,7 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks), in fp32
   // for the LM head
   cross_reduce2(c, wid, jj, pgrp == 0, a.xd, loc_xg, (c.phase0 + static_cast<uint32_t>(a.L) - 1u) & 3u, loc_xa,
-                a.final_norm, xres, xhl, reinterpret_cast<float*>(vtb), red);
+                a.final_norm, xres, xhl, reinterpret_cast<float*>(vtb), red, 2 * a.L + 3);
   XTRACE0(a.L);
   XSYNC();
   return true;
@@ -1077,6 +1119,7 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
     flag[0] = 0;
     flag[1] = xcc;
     flag[2] = rank;
+    flag[4] = 0;  // cross_reduce2's stage-1 marker (its markers are positive)
   }
   __syncthreads();
   const int g = flag[1], j = flag[2];
