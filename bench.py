@@ -4,7 +4,7 @@
 Workload (headline): Qwen3-0.6B architecture, random-init fp16 weights N(0, 0.02) (seed 1), batch 1. A 32-token
 prompt is prefilled (untimed), then W warmup and K timed greedy decode steps run with the sampled token fed back on
 the device. A "step" is one decode token. Also measured in the same run:
-  * prefill of a 2048-token prompt (tok/s),
+  * prefill of a 2048-token prompt (tok/s), on the fp16 model and with its projections group-quantized (int8, int4),
   * the dominant decode kernel: k_decode_xcd (one launch = one whole token, every layer split over the 8 XCDs) or
     k_decode_persistent when the device runs that one, timed with HIP events on the stream it is launched on; the
     fused RMSNorm + QKV GEMV
@@ -85,6 +85,21 @@ def bench_prefill(ctx, m, cfg, n: int = 2048):
     ms = ctx.timer_stop()
     kv.close()
     return ms
+
+
+def bench_prefill_quant(ctx, cfg, n: int = 2048):
+    """Prefill of n tokens on the same model with its projections group-quantized (int8, int4): each layer's codes
+    dequantized to fp16, then the fp16 prefill kernels."""
+    out = {"workload": f"Qwen3-0.6B seed-1 weights, projections group-64 quantized, {n}-token prompt"}
+    for bits in (8, 4):
+        m = S.Model(ctx, cfg).synthesize(1, 0.02).quantize(bits)
+        try:
+            ms = bench_prefill(ctx, m, cfg, n)
+        finally:
+            m.close()
+        out[f"int{bits}_ms"] = round(ms, 3)
+        out[f"int{bits}_tok_s"] = round(n / (ms * 1e-3), 1)
+    return out
 
 
 def bench_decode_4b(ctx, steps: int = 64, warmup: int = 8):
@@ -474,6 +489,7 @@ def main() -> None:
     ap.add_argument("--no-ragged", action="store_true", help="skip the Qwen3-4B ragged decode measurement")
     ap.add_argument("--no-ops", action="store_true", help="skip the GEMV / group-quantized matmul microbenchmarks")
     ap.add_argument("--no-4b", action="store_true", help="skip the Qwen3-4B batch-1 decode measurement")
+    ap.add_argument("--no-quant", action="store_true", help="skip the group-quantized prefill measurement")
     ap.add_argument("--no-cpp-api", action="store_true", help="skip the GenerationContext (C++ API) measurement")
     ap.add_argument("--ragged-steps", type=int, default=RAGGED_STEPS, help="steps of the ragged run (profiling)")
     ap.add_argument("--steps-4b", type=int, default=64, help="timed steps of the Qwen3-4B batch-1 decode")
@@ -503,6 +519,9 @@ def main() -> None:
     us, alg = bench_gemv_kernel(ctx)
     gemv_gbs = alg / (us * 1e-6) / 1e9
     m.close()
+    prefill_q = None if (args.no_prefill or args.no_quant) else bench_prefill_quant(ctx, cfg)
+    if prefill_q is not None:
+        _progress(f"quantized prefill of 2048 tokens: int8 {prefill_q['int8_ms']} ms, int4 {prefill_q['int4_ms']} ms")
     ops_gemv, ops_qmm = (None, None) if args.no_ops else bench_ops(ctx)
     ragged = None if args.no_ragged else bench_ragged(ctx, args.ragged_steps)
     if ragged is not None:
@@ -552,6 +571,7 @@ def main() -> None:
         "decode_hbm_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "prefill_tok_s": None if prefill_ms is None else round(2048 / (prefill_ms * 1e-3), 1),
         "prefill_ms_2048": None if prefill_ms is None else round(prefill_ms, 3),
+        "prefill_quant_2048": prefill_q,
         "roofline": roofline,
         "gemv_qkv_4096x1024": {"avg_launch_us": round(us, 3), "gbs": round(gemv_gbs, 1),
                                "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},

@@ -46,7 +46,7 @@ __device__ __forceinline__ void poll_pause(int n) {
 // Pollers keep two reads of the same words in flight, the second issued about half a read's round trip after the
 // first (s_sleep units of 64 clocks): a word that lands just after one read left is seen by the other half a round
 // trip later instead of a whole one. Loads return in order, so checking the older read waits for it alone.
-constexpr int kStaggerLocal = 4;   // XCD-local words (plain stores, sc1 reads)
+constexpr int kStaggerLocal = 2;   // XCD-local words (plain stores, sc1 reads)
 constexpr int kStaggerRemote = 8;  // words written by other XCDs (sc1 stores)
 template <int N>
 __device__ __forceinline__ void stagger() {

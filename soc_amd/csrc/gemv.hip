@@ -663,6 +663,39 @@ __global__ void k_dequant(const void* codes, const f16* scales, int N, int K, fl
   }
 }
 
+// Dequantize codes to fp16 [N][K], w = f16(float(code) * float(scale)) rounded to nearest: eight consecutive weights
+// of one row (one scale group) per thread and step, a 16-byte store each (K % 64 == 0).
+template <int BITS>
+__global__ __launch_bounds__(256) void k_dequant_f16(const void* codes, const f16* scales, int N, int K, f16* w) {
+  const size_t groups = static_cast<size_t>(N) * (K / 8);
+  for (size_t gi = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; gi < groups;
+       gi += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t idx = gi * 8;
+    const int n = static_cast<int>(idx / K), k = static_cast<int>(idx % K);
+    const float sc = static_cast<float>(scales[static_cast<size_t>(n) * (K / 64) + k / 64]);
+    int32_t c[8];
+    if constexpr (BITS == 8) {
+      const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(codes) + idx);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = static_cast<int8_t>((b.x >> (8 * i)) & 0xffu);
+        c[4 + i] = static_cast<int8_t>((b.y >> (8 * i)) & 0xffu);
+      }
+    } else {
+      const uint32_t b = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(codes) + idx / 2);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int32_t nib = static_cast<int32_t>((b >> (4 * i)) & 0xfu);  // even k in the low nibble
+        c[i] = nib >= 8 ? nib - 16 : nib;
+      }
+    }
+    f16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = static_cast<f16>(static_cast<float>(c[i]) * sc);
+    *reinterpret_cast<f16x8*>(w + idx) = v;
+  }
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // Launchers
 // ------------------------------------------------------------------------------------------------------------
@@ -888,6 +921,16 @@ hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s) {
 #undef SOC_QMM_M
 #undef SOC_QMM_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_dequant_f16(const void* codes, int bits, const f16* scales, int N, int K, f16* w, hipStream_t s) {
+  if (N <= 0 || K <= 0 || K % 64 != 0) return hipErrorInvalidValue;
+  const size_t groups = static_cast<size_t>(N) * (K / 8);
+  const dim3 grid(static_cast<unsigned>(std::min<size_t>((groups + 255) / 256, 4096))), block(256);
+  if (bits == 8) hipLaunchKernelGGL((k_dequant_f16<8>), grid, block, 0, s, codes, scales, N, K, w);
+  else if (bits == 4) hipLaunchKernelGGL((k_dequant_f16<4>), grid, block, 0, s, codes, scales, N, K, w);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_dequant(const void* codes, int bits, const f16* scales, int N, int K, float* w, hipStream_t s) {

@@ -50,6 +50,8 @@ struct QmmArgs {
 };
 hipError_t launch_qmm(const QmmArgs& a, int bits, hipStream_t s);
 hipError_t launch_dequant(const void* codes, int bits, const f16* scales, int N, int K, float* w, hipStream_t s);
+// The same weights rounded to fp16 (nearest) [N][K], for the prefill GEMMs of a quantized model (K % 64 == 0).
+hipError_t launch_dequant_f16(const void* codes, int bits, const f16* scales, int N, int K, f16* w, hipStream_t s);
 
 // ---- attention ----
 struct AttnArgs {

@@ -166,6 +166,7 @@ struct soc_model {
   int qbits = 0;         // 8 or 4 after soc_model_quantize: the projections run on the group-quantized copies
   std::vector<QLayer> qlayers;
   std::vector<void*> qallocs;
+  f16* qdeq = nullptr;    // quantized models: one layer's projections dequantized to fp16 for prefill GEMMs
   soc_kv* ukv = nullptr;  // private one-slot cache of the uncached forward (soc_forward with kv == NULL)
 };
 
@@ -1442,6 +1443,7 @@ int soc_model_destroy(soc_model* m) {
   (void)hipFree(m->rope_sin);
   (void)hipFree(m->d_layer_w);
   free_all(m->qallocs);
+  (void)hipFree(m->qdeq);
   if (m->ukv != nullptr) soc_kv_destroy(m->ukv);
   delete m;
   return SOC_OK;
@@ -1788,6 +1790,41 @@ namespace {
 // The layers of a quantized model's prefill over the n embedded rows in m->pws.x, kQChunk rows at a time (each chunk
 // through every layer, so a chunk's attention sees the keys the earlier chunks appended): group-quantized
 // projections, the prefill q/k-norm + RoPE + append kernel and the split-key attention over the slot's cache.
+// Layer l of a quantized model with its projections dequantized to fp16 (rounded to nearest) in m->qdeq, for the
+// prefill GEMMs of more than kQChunk rows: the norms are the model's own, the weight pointers the scratch's. The
+// scratch holds one layer; stream order keeps a layer's GEMMs ahead of the next layer's dequantization.
+int dequant_layer(soc_model* m, int l, DevLayer* out) {
+  const soc_qwen_config& c = m->cfg;
+  const size_t H = c.hidden_size, I = c.intermediate_size, qd = m->qd, qkv = m->qkv_rows;
+  const size_t n_qkv = qkv * H, n_o = H * qd, n_gu = 2 * I * H, n_down = H * I;
+  hipError_t e;
+  if (m->qdeq == nullptr &&
+      (e = hipMalloc(&m->qdeq, (n_qkv + n_o + n_gu + n_down) * sizeof(f16))) != hipSuccess)
+    return hip_fail(e, "hipMalloc dequantized layer");
+  const QLayer& q = m->qlayers[l];
+  f16* const wqkv = m->qdeq;
+  f16* const wo = wqkv + n_qkv;
+  f16* const wgu = wo + n_o;
+  f16* const wdown = wgu + n_gu;
+  hipStream_t s = m->ctx->stream;
+  const int b = m->qbits;
+  if ((e = soc::launch_dequant_f16(q.qkv, b, q.qkv_s, static_cast<int>(qkv), static_cast<int>(H), wqkv, s)) !=
+          hipSuccess ||
+      (e = soc::launch_dequant_f16(q.o, b, q.o_s, static_cast<int>(H), static_cast<int>(qd), wo, s)) != hipSuccess ||
+      (e = soc::launch_dequant_f16(q.gu, b, q.gu_s, static_cast<int>(2 * I), static_cast<int>(H), wgu, s)) !=
+          hipSuccess ||
+      (e = soc::launch_dequant_f16(q.down, b, q.down_s, static_cast<int>(H), static_cast<int>(I), wdown, s)) !=
+          hipSuccess)
+    return hip_fail(e, "dequantize layer");
+  *out = m->layers[l];
+  out->wqkv = wqkv;
+  out->wo = wo;
+  out->wgate = wgu;
+  out->wup = wgu + I * H;
+  out->wdown = wdown;
+  return SOC_OK;
+}
+
 int prefill_layers_q(soc_model* m, soc_kv* kv, int slot, int n, int pos_off, const float* rope_cos,
                      const float* rope_sin) {
   const soc_qwen_config& c = m->cfg;
@@ -1869,7 +1906,10 @@ int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool
   const float* const rope_cos = m->rope_cos + static_cast<size_t>(rope_shift) * (c.head_dim / 2);
   const float* const rope_sin = m->rope_sin + static_cast<size_t>(rope_shift) * (c.head_dim / 2);
   const int H = c.hidden_size;
-  if (m->qbits != 0) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off, rope_cos, rope_sin));
+  // a quantized model's prompt of up to kQChunk rows streams the codes once through the group-quantized kernels;
+  // longer prompts run the fp16 layers on each layer's projections dequantized to fp16
+  const bool qchunks = m->qbits != 0 && n <= kQChunk;
+  if (qchunks) SOC_TRY(prefill_layers_q(m, kv, slot, n, pos_off, rope_cos, rope_sin));
   const bool split = prefill_split_path(m);
   // lo parts of each projection's activations, or none (prefill_split_mask)
   const int smask = prefill_split_mask();
@@ -1877,8 +1917,10 @@ int run_prefill(soc_model* m, soc_kv* kv, int32_t slot, const int32_t* ids, bool
   f16* const pl_o = (smask & kSplitO) ? w.pl : nullptr;
   f16* const pl_gu = (smask & kSplitGateUp) ? w.pl : nullptr;
   f16* const ql = (smask & kSplitDown) ? w.ql : nullptr;
-  for (int l = 0; m->qbits == 0 && l < c.num_hidden_layers; ++l) {  // fp16 models
-    const DevLayer& L = m->layers[l];
+  for (int l = 0; !qchunks && l < c.num_hidden_layers; ++l) {
+    DevLayer deq;
+    if (m->qbits != 0) SOC_TRY(dequant_layer(m, l, &deq));
+    const DevLayer& L = m->qbits != 0 ? deq : m->layers[l];
     soc::GemmArgs g{};
     const bool qkv_fused = split;  // the staged kernel's QKV is followed by the separate q/k-norm kernel
     if (split) {
