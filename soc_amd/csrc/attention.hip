@@ -670,30 +670,48 @@ __global__ __launch_bounds__(256, 2) void k_attention_prefill_mfma(AttnArgs a) {
 // and tile nqt - 1 - j, one after the other, so every block sees about the same number of visible keys. Its 8 waves
 // are HB query heads (the whole group of the KV head) x R = 8 / HB key residues: key tile kt goes to the waves of
 // residue kt % R, and each step stages R tiles. At the end of a query tile the R partial (max, sum, weighted values)
-// of each row are merged through LDS.
+// of each row are merged through LDS: every wave owns 4 / R of the four 32-dimension blocks of its head's output and
+// combines them from the other residues' partials, in residue order.
+// The query rows (fp32) go global -> LDS with global_load_lds_dwordx4 together with the first key tiles, and when the
+// merge area fits in the key/value ring the rows of the block's second query tile are requested while the first
+// tile's keys are processed, so neither waits on a load of its own.
 // Per tile a wave does what k_attention_prefill_mfma does (S^T = K . Q^T on MFMA, one query per lane, P^T straight
 // from registers into O^T = V^T . P^T with V^T stored key-swizzled), with three changes:
-//  * q is pre-multiplied by scale * log2(e) before its hi/lo split, so a score is sh + sl 2^-11;
+//  * q is pre-multiplied by scale * log2(e) before its hi/lo split (lo = f16(q - hi), not rescaled), and both parts
+//    accumulate into the same scores;
 //  * the running max is lazy: it moves only when a score exceeds it by more than 8 (log2 units), so p <= 2^8 and
 //    the 64 accumulators are rescaled rarely; the result is the same softmax (every partial keeps its own max and
 //    the merge rescales exactly);
 //  * p = hi + lo with hi = p with its low 13 mantissa bits cleared (exact in fp16 for p >= 2^-14) and lo = p - hi.
-// K and V tiles go global -> LDS row-major with global_load_lds_dwordx4 (32 rows x 256 B; 16-byte chunk c of row r
-// at slot c ^ (r & 15) for K, c ^ 2 (r & 7) for V) and V^T operands come out of LDS through the transposing read
-// ds_read_b64_tr_b16 (in each 16-lane group, lane j names 8 bytes = 4 dims of one key, and lane i receives dim i
-// of 4 consecutive keys), so no register staging or transposed stores are needed. Keys past the chunk's last row
-// read the last key and are masked (p = 0 against finite values).
+// K and V tiles go global -> LDS row-major with buffer_load_dwordx4 ... lds (32 rows x 256 B; 16-byte chunk c of
+// row r at slot c ^ (r & 15) for K, c ^ 2 (r & 7) for V) and V^T operands come out of LDS through the transposing
+// read ds_read_b64_tr_b16 (in each 16-lane group, lane j names 8 bytes = 4 dims of one key, and lane i receives dim
+// i of 4 consecutive keys), so no register staging or transposed stores are needed. Keys past the chunk's last row
+// read as zero (the buffer range ends there) and are masked (p = 0).
 // grid = ceil(ceil(B / 32) / 2) * nkv blocks (block b: KV head b % nkv, so with 8 KV heads each XCD's L2 holds one
-// head), block = 512, dynamic LDS = max(staging, merge).
+// head), block = 512, dynamic LDS = [key/value ring | query rows], with the merge area over the ring (and past it
+// when it does not fit, in which case the query rows are not prefetched).
 // ------------------------------------------------------------------------------------------------------------
 namespace {
 constexpr int FP_KD = FA_KT * HD;     // K or V tile in halves (row-major, swizzled)
 typedef __fp16 fp_hv4 __attribute__((__vector_size__(4 * sizeof(__fp16))));  // operand type of the transposing read
+typedef __attribute__((address_space(3))) void pa_lds_void;
 template <int HB, int R>
-constexpr size_t pairs_lds_bytes() {
-  const size_t staging = static_cast<size_t>(2) * R * 2 * FP_KD * sizeof(_Float16);
-  const size_t merge = static_cast<size_t>(HB) * (R - 1) * 66 * 64 * sizeof(float);
-  return staging > merge ? staging : merge;
+struct PairsLds {
+  static constexpr size_t ring = static_cast<size_t>(2) * R * 2 * FP_KD * sizeof(_Float16);  // [2][R] K, [2][R] V
+  static constexpr size_t qrows = static_cast<size_t>(HB) * 32 * HD * sizeof(float);     // [HB][32 rows][128]
+  // per head: the o blocks a wave does not own ([4 blocks][R - 1 writers][16][64 lanes]), then (max, sum) per
+  // residue ([R][2][64])
+  static constexpr size_t merge = static_cast<size_t>(HB) * (4 * (R - 1) * 16 + 2 * R) * 64 * sizeof(float);
+  static constexpr bool prefetch_q = merge <= ring;
+  static constexpr size_t bytes = ring + qrows > merge ? ring + qrows : merge;
+};
+// a barrier with no fence: global loads and stores stay in flight across it; the signal fences keep the compiler
+// from moving LDS accesses across it
+__device__ __forceinline__ void block_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 }  // namespace
 
@@ -705,7 +723,9 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
   extern __shared__ __attribute__((aligned(16))) _Float16 plds[];
   _Float16* Ksb = plds;                  // [2][R][FP_KD]
   _Float16* Vb = plds + 2 * R * FP_KD;   // [2][R][FP_KD]
-  float* xs = reinterpret_cast<float*>(plds);  // merge area [HB][R - 1][66][64], after the key loop
+  float* xs = reinterpret_cast<float*>(plds);  // merge area, after the key loop
+  float* qs = reinterpret_cast<float*>(plds + 4 * R * FP_KD);  // query rows [HB][32][32 chunks of 4]
+  using Lds = PairsLds<HB, R>;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int hh = wid % HB, res = wid / HB;
   const int g = static_cast<int>(blockIdx.x % a.nkv);
@@ -718,6 +738,27 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
   const f16* kb = a.kcache + head_base;
   const f16* vb = a.vcache + head_base;
   const float scale2 = a.scale * 1.4426950408889634f;
+  // byte offsets of this lane's 16-byte chunk in a K / V tile: row 4 w + lane / 16, chunk slot lane % 16 holding
+  // chunk (lane % 16) ^ (row % 16) of K and (lane % 16) ^ 2 (row % 8) of V
+  const int krow = 4 * wid + (lane >> 4);
+  const int koff = (krow * HD + (((lane & 15) ^ (krow & 15)) * 8)) * 2;
+  const int voff = (krow * HD + (((lane & 15) ^ (2 * (krow & 7))) * 8)) * 2;
+  // the rows of query tile qt for the block's HB heads -> qs; 16-byte chunk c of row r at slot c ^ r (conflict-free
+  // reads of one chunk index by 32 rows). Instruction n of wave w fills rows 2 (w NI + n) and 2 (w NI + n) + 1.
+  auto load_q = [&](int qt) {
+    constexpr int NI = HB * 32 / 2 / 8;
+    int ln = lane;
+    __asm__ volatile("" : "+v"(ln));  // addresses computed here, not kept in registers across the key loop
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+      const int rr = 2 * (wid * NI + n) + (ln >> 5);
+      const int h = rr / 32, r = rr % 32;
+      const int c = (ln & 31) ^ r;
+      const int tq = min(qt * 32 + r, a.B - 1);
+      __builtin_amdgcn_global_load_lds(a.qkv + static_cast<size_t>(tq) * a.ld_qkv + (g * HB + h) * HD + c * 4,
+                                       qs + (wid * NI + n) * 256, 16, 0, 0);
+    }
+  };
 
   for (int ph = 0; ph < 2; ++ph) {
     if (ph == 1 && nqt - 1 - j == j) break;  // odd tile count: the middle tile has no partner
@@ -731,14 +772,37 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
     const int nsteps = (ntiles + R - 1) / R;
     const int wave_min_pos = a.pos_base + t0;
 
+    // K and V tiles of a step: wave w writes rows 4w..4w+3 of tile p through a buffer resource that starts at the
+    // tile's first key and ends after key `last`, so rows past it read as zero (masked: p = 0) and the lane's byte
+    // offset is the same for every tile (no per-step address arithmetic on the vector ALUs)
+    auto load_step = [&](int step, int buf) {
+#pragma unroll
+      for (int p = 0; p < R; ++p) {
+        const int key0 = (R * step + p) * FA_KT;
+        const int nrec = max(0, last + 1 - key0) * HD * 2;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(kb) + static_cast<size_t>(key0) * HD, 0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(vb) + static_cast<size_t>(key0) * HD, 0, nrec, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pa_lds_void*)(Ksb + (buf * R + p) * FP_KD + 4 * wid * HD), 16,
+                                                 koff, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pa_lds_void*)(Vb + (buf * R + p) * FP_KD + 4 * wid * HD), 16,
+                                                 voff, 0, 0, 0);
+      }
+    };
+    if (ph == 0 || !Lds::prefetch_q) load_q(qt);
+    load_step(0, 0);
+    __syncthreads();  // also waits for the tiles and the query rows (vmcnt)
+
     // Q^T operand (lane holds q[t][16 ks + 8 hb + i]) of q * scale * log2(e)
     fa_h8 qh[8], qlo[8];
     {
-      const float* qrow = a.qkv + static_cast<size_t>(tq) * a.ld_qkv + head * HD;
+      const float* qrow = qs + (hh * 32 + ql) * HD;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + ks * 16 + hb * 8 + 4);
+        const int c0 = 4 * ks + 2 * hb;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(qrow + (c0 ^ ql) * 4);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(qrow + ((c0 + 1) ^ ql) * 4);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float v = (i < 4 ? v0[i] : v1[i - 4]) * scale2;
@@ -747,23 +811,14 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
           __asm__ volatile("" : "+v"(v));
           const _Float16 h = static_cast<_Float16>(v);
           qh[ks][i] = h;
-          if constexpr (LOQ) qlo[ks][i] = static_cast<_Float16>((v - static_cast<float>(h)) * 2048.0f);
+          if constexpr (LOQ) qlo[ks][i] = static_cast<_Float16>(v - static_cast<float>(h));
         }
       }
     }
-    auto load_step = [&](int step, int buf) {
-      const int r = 4 * wid + (lane >> 4);
-#pragma unroll
-      for (int p = 0; p < R; ++p) {  // K and V: wave w writes rows 4w..4w+3 of tile p
-        const int key = min((R * step + p) * FA_KT + r, last);
-        const int ck = (lane & 15) ^ (r & 15);
-        const int cv = (lane & 15) ^ (2 * (r & 7));
-        __builtin_amdgcn_global_load_lds(kb + static_cast<size_t>(key) * HD + ck * 8,
-                                         Ksb + (buf * R + p) * FP_KD + 4 * wid * HD, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb + static_cast<size_t>(key) * HD + cv * 8,
-                                         Vb + (buf * R + p) * FP_KD + 4 * wid * HD, 16, 0, 0);
-      }
-    };
+    if (Lds::prefetch_q && ph == 0 && nqt - 1 - j != j) {
+      block_barrier();  // every wave has read its query rows: the partner tile's rows go to the same place
+      load_q(nqt - 1 - j);
+    }
     // A operand of O^T = V^T . P^T for dims db*32.. and the 16-key step k2: lane (dim l % 32, hb) needs keys
     // hb*4 + 0..3 and 8 + hb*4 + 0..3 of the step (the key order of the P^T operand); 16-lane group grp covers dims
     // (grp & 1) * 16.. and keys (grp >> 1) * 4..
@@ -792,8 +847,6 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
       for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
     float m = -INFINITY, l = 0.0f;
 
-    load_step(0, 0);
-    __syncthreads();  // also waits for the tiles (vmcnt)
     for (int step = 0; step < nsteps; ++step) {
       const int buf = step & 1;
       if (step + 1 < nsteps) load_step(step + 1, buf ^ 1);
@@ -801,17 +854,14 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
       if (kt < ntiles) {
         const _Float16* Ks = Ksb + (buf * R + res) * FP_KD;
         const _Float16* Vt = Vb + (buf * R + res) * FP_KD;
-        f32x16 sh, sl;
+        f32x16 sh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sh[r] = 0.0f;
-          sl[r] = 0.0f;
-        }
+        for (int r = 0; r < 16; ++r) sh[r] = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
           const fa_h8 ka = *reinterpret_cast<const fa_h8*>(&Ks[ql * HD + ((2 * ks + hb) ^ (ql & 15)) * 8]);
           sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
-          if constexpr (LOQ) sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sl, 0, 0, 0);
+          if constexpr (LOQ) sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sh, 0, 0, 0);
         }
         // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
         float sv[16];
@@ -819,15 +869,14 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
         if (kt * FA_KT + FA_KT - 1 <= wave_min_pos) {  // every key of the tile is visible to every row
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            sv[r] = sh[r] + sl[r] * (1.0f / 2048.0f);
+            sv[r] = sh[r];
             mt = fmaxf(mt, sv[r]);
           }
         } else {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kt * FA_KT + (r >> 2) * 8 + hb * 4 + (r & 3);
-            const float v = sh[r] + sl[r] * (1.0f / 2048.0f);
-            sv[r] = key <= qpos ? v : -INFINITY;
+            sv[r] = key <= qpos ? sh[r] : -INFINITY;
             mt = fmaxf(mt, sv[r]);
           }
         }
@@ -879,71 +928,86 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
       __syncthreads();
     }
 
-    // merge the R residues of each (head, row): residues 1..R-1 park (m, l, o) in LDS
+    // merge the R residues of each (head, row): wave (hh, res) owns the output blocks db with db % R == res and
+    // parks the other blocks and its (max, sum) for their owners; each owner adds the partials in residue order
     const float lt = l + __shfl_xor(l, 32);
-    if (res > 0) {
-      float* dst = xs + (hh * (R - 1) + res - 1) * 66 * 64 + lane;
-      dst[0] = m;
-      dst[64] = lt;
+    float* mls = xs + HB * 4 * (R - 1) * 16 * 64;  // [HB][R][max, sum][64]
+    mls[(hh * R + res) * 2 * 64 + lane] = m;
+    mls[((hh * R + res) * 2 + 1) * 64 + lane] = lt;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db) {
+      const int own = db % R;
+      if (own != res) {
+        float* dst = xs + ((hh * 4 + db) * (R - 1) + (res < own ? res : res - 1)) * 16 * 64 + lane;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dst[(2 + db * 16 + r) * 64] = o[db][r];
+        for (int r = 0; r < 16; ++r) dst[r * 64] = o[db][r];
+      }
     }
     __syncthreads();
-    if (res == 0) {
-      const float* part = xs + hh * (R - 1) * 66 * 64 + lane;
-      float M = m;
+    {
+      float mr[R], lr[R];
 #pragma unroll
-      for (int q = 0; q < R - 1; ++q) M = fmaxf(M, part[q * 66 * 64]);
-      const float ca = __builtin_amdgcn_exp2f(m - M);  // m is finite: key 0 is in residue 0's first tile
-      float cq[R - 1];
-      float L = lt * ca;
-#pragma unroll
-      for (int q = 0; q < R - 1; ++q) {
-        const float mq = part[q * 66 * 64];
-        cq[q] = mq == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mq - M);
-        L += part[q * 66 * 64 + 64] * cq[q];
+      for (int q = 0; q < R; ++q) {
+        mr[q] = q == res ? m : mls[(hh * R + q) * 2 * 64 + lane];
+        lr[q] = q == res ? lt : mls[((hh * R + q) * 2 + 1) * 64 + lane];
       }
-      if (t < a.B) {
+      float M = mr[0];
+#pragma unroll
+      for (int q = 1; q < R; ++q) M = fmaxf(M, mr[q]);
+      float cq[R];
+      cq[0] = __builtin_amdgcn_exp2f(mr[0] - M);  // residue 0's max is finite: key 0 is in its first tile
+#pragma unroll
+      for (int q = 1; q < R; ++q) cq[q] = mr[q] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr[q] - M);
+      float L = lr[0] * cq[0];
+#pragma unroll
+      for (int q = 1; q < R; ++q) L += lr[q] * cq[q];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        if (db % R != res || t >= a.B) continue;
         const size_t row = static_cast<size_t>(t) * a.ld_out + head * HD;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int r4 = 0; r4 < 4; ++r4) {
+          f32x4 v;
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            f32x4 v;
+          for (int i = 0; i < 4; ++i) {
+            const int r = r4 * 4 + i;
+            float x[R];
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+              x[q] = q == res ? o[db][r] : xs[(((hh * 4 + db) * (R - 1) + (q < res ? q : q - 1)) * 16 + r) * 64 + lane];
+            float acc = x[0] * cq[0];
+#pragma unroll
+            for (int q = 1; q < R; ++q) acc += x[q] * cq[q];
+            v[i] = acc / L;
+          }
+          const size_t off = row + db * 32 + r4 * 8 + hb * 4;
+          if (a.out != nullptr) *reinterpret_cast<f32x4*>(a.out + off) = v;
+          if (a.out_hi != nullptr) {  // the hi/lo activation pair of the o projection
+            f16x4 hi, lo;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int r = r4 * 4 + i;
-              float acc = o[db][r] * ca;
-#pragma unroll
-              for (int q = 0; q < R - 1; ++q) acc += part[q * 66 * 64 + (2 + db * 16 + r) * 64] * cq[q];
-              v[i] = acc / L;
+              hi[i] = static_cast<f16>(v[i]);
+              lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
             }
-            const size_t off = row + db * 32 + r4 * 8 + hb * 4;
-            if (a.out != nullptr) *reinterpret_cast<f32x4*>(a.out + off) = v;
-            if (a.out_hi != nullptr) {  // the hi/lo activation pair of the o projection
-              f16x4 hi, lo;
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                hi[i] = static_cast<f16>(v[i]);
-                lo[i] = static_cast<f16>((v[i] - static_cast<float>(hi[i])) * 2048.0f);
-              }
-              *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
-              if (a.out_lo != nullptr) *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
-            }
+            *reinterpret_cast<f16x4*>(a.out_hi + off) = hi;
+            if (a.out_lo != nullptr) *reinterpret_cast<f16x4*>(a.out_lo + off) = lo;
           }
+        }
       }
     }
-    __syncthreads();  // the merge area is the next query tile's staging area
+    // the merge area is the next query tile's staging area: every wave's reads of it have returned (the output
+    // stores may still be in flight)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    block_barrier();
   }
 }
+
 
 namespace {
 template <int HB, bool LOQ, bool LOP>
 hipError_t launch_pairs_lo(const AttnArgs& a, hipStream_t s) {
   constexpr int R = 8 / HB;
-  constexpr size_t lds = pairs_lds_bytes<HB, R>();
+  constexpr size_t lds = PairsLds<HB, R>::bytes;
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(k_attention_prefill_pairs<HB, R, LOQ, LOP>), hipFuncAttributeMaxDynamicSharedMemorySize,
       static_cast<int>(lds));
