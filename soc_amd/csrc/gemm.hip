@@ -184,7 +184,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
 // read from LDS while the current step's MFMAs run (two register sets used in turn), one read issued after each
 // MFMA. Rows are BK halves with the 16-byte chunk c of row r stored at slot c ^ ((r >> 1) & 3) (BK = 32) or
 // c ^ (r & 7) (BK = 64): the rows a b128 read phase touches land on different bank groups.
-// BM x BN tile per 4-wave block (2 x 2 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_f16). Tiles are dealt to the
+// BM x BN tile per block of NWM x NWN waves (each a (BM/NWM) x (BN/NWN) part, v_mfma_f32_32x32x16_f16; every
+// configuration accumulates the same 16-deep MFMA steps in the same K order). Tiles are dealt to the
 // eight XCDs as an mx x (8 / mx) grid of rectangles (block b runs on XCD b % 8), mx chosen to minimise the bytes
 // of A and W each XCD's L2 has to fetch. The products and their order match k_gemm_mfma<EPI, true, .> exactly, or
 // with LO = false (single fp16 activations, no lo part) those of k_gemm_mfma<EPI, false, .>.
@@ -222,21 +223,24 @@ __device__ __forceinline__ void block_barrier() {
 }
 }  // namespace
 
-template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO>
-__global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int mx) {
-  constexpr int MI = BM / 64, NJ = BN / 64;  // 32x32 MFMA tiles per wave
-  constexpr int RPI = 1024 / (BK * 2);       // rows per 1 KB wave instruction
-  constexpr int CPR = BK / 8;                // 16-byte chunks per row
-  constexpr int AP = LO ? 2 : 1;             // activation parts: hi and lo, or hi alone
-  constexpr int AI = BM / RPI / 4, WI = BN / RPI / 4;  // DMA instructions per wave per slice: each A part, W
+template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN, MINB) void k_gemm_split(GemmSplitArgs g, int mx) {
+  constexpr int NW = NWM * NWN;                    // waves: NWM x NWN, each a WTM x WTN part of the tile
+  constexpr int WTM = BM / NWM, WTN = BN / NWN;
+  constexpr int MI = WTM / 32, NJ = WTN / 32;      // 32x32 MFMA tiles per wave
+  constexpr int RPI = 1024 / (BK * 2);             // rows per 1 KB wave instruction
+  constexpr int CPR = BK / 8;                      // 16-byte chunks per row
+  constexpr int AP = LO ? 2 : 1;                   // activation parts: hi and lo, or hi alone
+  constexpr int AI = BM / RPI / NW, WI = BN / RPI / NW;  // DMA instructions per wave per slice: each A part, W
   constexpr int IPT = AP * AI + WI;
   constexpr int KS = BK / 16;  // 16-deep MFMA steps per slice
   constexpr int STAGE_H = (AP * BM + BN) * BK;
-  static_assert(EPI != EPI_SWIGLU || NJ == 2, "SwiGLU pairs one gate and one up tile per wave");
+  static_assert(EPI != EPI_SWIGLU || NJ % 2 == 0, "SwiGLU pairs gate and up tiles within a wave");
   static_assert(KS % 2 == 0 && ST >= 2 && AI >= 1 && WI >= 1, "tile shape");
+  static_assert(AI * RPI * NW == BM && WI * RPI * NW == BN && MI >= 1 && NJ >= 1, "tile shape");
   extern __shared__ __attribute__((aligned(16))) _Float16 slds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid / NWN, wn = wid % NWN;
   const int mt = (g.M + BM - 1) / BM, nt = gridDim.x / mt;
   int mtile, ntile;
   if (mx > 0) {  // XCD rectangle (b % 8) of (mt / mx) x (nt / nx) tiles, walked along N
@@ -293,10 +297,12 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
         acc[i][j][r] = 0.0f;
         acc_lo[i][j][r] = 0.0f;
       }
-  // W rows of the wave's 32-column tiles: plain wn*(BN/2) + t*32; SwiGLU: gate wn*32, up BN/2 + wn*32
+  // W rows of the wave's 32-column tiles: plain wn*WTN + t*32; SwiGLU: gate rows wn*WTN/2 + t*32 (t < NJ/2), the
+  // matching up rows BN/2 + the same
   int brow[NJ];
 #pragma unroll
-  for (int t = 0; t < NJ; ++t) brow[t] = EPI == EPI_SWIGLU ? t * (BN / 2) + wn * 32 : wn * (BN / 2) + t * 32;
+  for (int t = 0; t < NJ; ++t)
+    brow[t] = EPI == EPI_SWIGLU ? (t / (NJ / 2)) * (BN / 2) + wn * (WTN / 2) + (t % (NJ / 2)) * 32 : wn * WTN + t * 32;
 
   h8 a0[MI][2], b0[NJ], a1[MI][2], b1[NJ];  // the two operand sets
   auto read = [&](h8 (&fa)[MI][2], h8 (&fb)[NJ], int st, int ks) {
@@ -311,7 +317,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      const int r = wm * (BM / 2) + i * 32 + (lane & 31);
+      const int r = wm * WTM + i * 32 + (lane & 31);
       const int off = r * BK + chunk_slot<BK>(r, c) * 8;
       fa[i][0] = *reinterpret_cast<const h8*>(Ah + off);
       if constexpr (LO) fa[i][1] = *reinterpret_cast<const h8*>(Al + off);
@@ -371,9 +377,10 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
   }
   // epilogue: lane holds D[m][n] for n = lane % 32, m = (r / 4) * 8 + (lane / 32) * 4 + r % 4
   if constexpr (EPI == EPI_QKV) {
-    // the tile's 128 columns are one head: park the tile in LDS, then each wave takes BM / 4 of its rows with lane l
+    // the tile's 128 columns are one head: park the tile in LDS, then each wave takes BM / NW of its rows with lane l
     // holding dims (l, l + 64), as the q/k-norm kernel does, so q, k and v come out bit-identical to it
     static_assert(BN == 128, "one 128-dim head per tile");
+    static_assert(static_cast<size_t>(BM) * (BN + 1) * 4 <= static_cast<size_t>(ST) * STAGE_H * 2, "park area");
     constexpr int LDX = BN + 1;
     float* xs = reinterpret_cast<float*>(slds);
     __syncthreads();  // every wave's MFMA operand reads of the ring are done
@@ -381,17 +388,17 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int ml = wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int ml = wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
 #pragma unroll
         for (int t = 0; t < NJ; ++t)
-          xs[ml * LDX + wn * (BN / 2) + t * 32 + (lane & 31)] =
+          xs[ml * LDX + wn * WTN + t * 32 + (lane & 31)] =
               LO ? acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f) : acc[i][t][r];
       }
     __syncthreads();
     const GemmSplitArgs::Qkv& q = g.qkv;
     const int head = n0 / BN;  // q heads, then k heads, then v heads
-    for (int rr = 0; rr < BM / 4; ++rr) {
-      const int ml = wid * (BM / 4) + rr, m = m0 + ml;
+    for (int rr = 0; rr < BM / NW; ++rr) {
+      const int ml = wid * (BM / NW) + rr, m = m0 + ml;
       if (m >= g.M) break;  // wave-uniform
       float x0 = xs[ml * LDX + lane], x1 = xs[ml * LDX + lane + 64];
       const int pos = q.pos_base + m;
@@ -420,28 +427,31 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_split(GemmSplitArgs g, int m
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
       if (m >= g.M) continue;
       float v[NJ];
 #pragma unroll
       for (int t = 0; t < NJ; ++t) v[t] = LO ? acc[i][t][r] + acc_lo[i][t][r] * (1.0f / 2048.0f) : acc[i][t][r];
       if constexpr (EPI == EPI_SWIGLU) {
-        const int n = n0 + wn * 32 + (lane & 31);
-        if (n < g.N) {
-          const float y = silu_ref(v[0]) * v[1];
-          const size_t o = static_cast<size_t>(m) * g.ldc + n;
-          if (g.ch != nullptr) {
-            const _Float16 hi = static_cast<_Float16>(y);
-            g.ch[o] = hi;
-            if (g.cl != nullptr) g.cl[o] = static_cast<_Float16>((y - static_cast<float>(hi)) * 2048.0f);
-          } else {
-            g.c[o] = y;
+#pragma unroll
+        for (int t = 0; t < NJ / 2; ++t) {
+          const int n = n0 + wn * (WTN / 2) + t * 32 + (lane & 31);
+          if (n < g.N) {
+            const float y = silu_ref(v[t]) * v[t + NJ / 2];
+            const size_t o = static_cast<size_t>(m) * g.ldc + n;
+            if (g.ch != nullptr) {
+              const _Float16 hi = static_cast<_Float16>(y);
+              g.ch[o] = hi;
+              if (g.cl != nullptr) g.cl[o] = static_cast<_Float16>((y - static_cast<float>(hi)) * 2048.0f);
+            } else {
+              g.c[o] = y;
+            }
           }
         }
       } else {
 #pragma unroll
         for (int t = 0; t < NJ; ++t) {
-          const int n = n0 + wn * (BN / 2) + t * 32 + (lane & 31);
+          const int n = n0 + wn * WTN + t * 32 + (lane & 31);
           if (n < g.N) {
             float* dst = g.c + static_cast<size_t>(m) * g.ldc + n;
             *dst = EPI == EPI_RESIDUAL ? *dst + v[t] : v[t];
@@ -468,7 +478,7 @@ int xcd_split(int mt, int nt, double abytes, double wbytes) {
   return best;
 }
 
-template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO>
+template <int EPI, int BM, int BN, int ST, int MINB, int BK, bool LO, int NWM = 2, int NWN = 2>
 hipError_t launch_split_cfg(const GemmSplitArgs& g, hipStream_t s) {
   constexpr int AP = LO ? 2 : 1;
   const int bn = EPI == EPI_SWIGLU ? BN / 2 : BN;
@@ -476,24 +486,41 @@ hipError_t launch_split_cfg(const GemmSplitArgs& g, hipStream_t s) {
   const int mx = xcd_split(mt, nt, 2.0 * AP * g.M * g.K, 2.0 * (EPI == EPI_SWIGLU ? 2 : 1) * g.N * g.K);
   const size_t lds = static_cast<size_t>(ST) * (AP * BM + BN) * BK * sizeof(_Float16);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO>),
+      reinterpret_cast<const void*>(k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO, NWM, NWN>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO>), dim3(mt * nt), dim3(256), lds, s, g, mx);
+  hipLaunchKernelGGL((k_gemm_split<EPI, BM, BN, ST, MINB, BK, LO, NWM, NWN>), dim3(mt * nt), dim3(64 * NWM * NWN), lds, s,
+                     g, mx);
   return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t launch_split_epi(const GemmSplitArgs& g, hipStream_t s) {
+  // 128-row tiles on 8 waves when they still give every CU its blocks (long prompts; measured on the Qwen3-0.6B
+  // prefill at 2048 tokens): a block's 8 waves share twice the rows of A and W per LDS slice, and two such blocks per
+  // CU keep 16 waves resident. QKV (hi/lo activations): 128 x 128 tiles, 32-deep slices in a 3-slot ring (56 -> 53
+  // us); gate/up: 128 x 128 (64 gate and 64 up rows), 64-deep slices in a 2-slot ring (44 -> 39.5 us); o/down
+  // (N <= 1024, one block per CU): 128 x 64, a 4-slot ring (29 -> 28 us).
+  const int mt128 = (g.M + 127) / 128;
+  if constexpr (EPI == EPI_QKV) {
+    if (g.al != nullptr && mt128 * (g.N / 128) >= 512) return launch_split_cfg<EPI, 128, 128, 3, 2, 32, true, 4, 2>(g, s);
+  }
+  if constexpr (EPI == EPI_SWIGLU) {
+    if (g.al == nullptr && g.K % 64 == 0 && mt128 * ((g.N + 63) / 64) >= 512)
+      return launch_split_cfg<EPI, 128, 128, 2, 2, 64, false, 4, 2>(g, s);
+  }
   // 64 x 128 tiles, two blocks per CU: 64-deep slices in a 2-slot ring, or 32-deep ones in a 4-slot ring when K
   // is not a multiple of 64 (measured on the Qwen3-0.6B prefill shapes at 2048 tokens). The residual projections
   // of <= 1024 columns (o and down) would get one 64 x 128 tile per CU; 64 x 64 tiles, up to three blocks per CU,
   // give them twice the blocks (2048 tokens: 8.29 -> 7.97 ms per prefill); on single fp16 activations a 3-slot ring
   // fits three blocks per CU and hides more of the load latency (6.92 -> 6.69 ms)
   if constexpr (EPI == EPI_RESIDUAL) {
-    if (g.K % 64 == 0 && g.N <= 1024)
+    if (g.K % 64 == 0 && g.N <= 1024) {
+      if (g.al == nullptr && mt128 * ((g.N + 63) / 64) >= 256)
+        return launch_split_cfg<EPI, 128, 64, 4, 1, 64, false, 4, 2>(g, s);
       return g.al != nullptr ? launch_split_cfg<EPI, 64, 64, 2, 3, 64, true>(g, s)
                              : launch_split_cfg<EPI, 64, 64, 3, 3, 64, false>(g, s);
+    }
   }
   if (g.al != nullptr)
     return g.K % 64 == 0 ? launch_split_cfg<EPI, 64, 128, 2, 2, 64, true>(g, s)

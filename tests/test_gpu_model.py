@@ -119,14 +119,15 @@ def test_prefill_mfma_attention_matches_row_kernel(gpu_ctx, monkeypatch, nq, nkv
 
 
 @pytest.mark.parametrize("hilo", ["0", "1", "default", "o,down"])
-@pytest.mark.parametrize("n", [150, 300])
+@pytest.mark.parametrize("n", [150, 300, 2000])
 def test_prefill_split_gemm_matches_staged_kernel(gpu_ctx, monkeypatch, n, hilo):
     """The prefill projections on fp16 activations written by their producers (RMSNorm, attention and the SwiGLU
     epilogue; direct-to-LDS pipeline) form the same products in the same order as the register-staged MFMA kernel
     that converts the fp32 activations itself, with hi/lo pairs on every projection (SOC_PREFILL_SPLIT=1), on none
     (0), on the QKV projection only (the default) and on another mix: logits are bit-identical, for a single prefill
     (row counts off the 64/128-row tiles) and a chunked one. Qwen3-0.6B-wide layers (hidden 1024, 16 q / 8 kv heads,
-    3072)."""
+    3072). At 2000 rows the projections take the 128-row, 8-wave tile configurations (the 77-row chunk the small
+    ones)."""
     if hilo == "default":
         monkeypatch.delenv("SOC_PREFILL_SPLIT", raising=False)
     else:
