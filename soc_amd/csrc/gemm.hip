@@ -182,8 +182,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
 // so ST slices are in flight while a slice's last 16-deep step runs; before that barrier a wave waits only for its
 // own loads of slice kt + 1 (vmcnt) and for its LDS reads (lgkmcnt). The MFMA operands of the next 16-deep step are
 // read from LDS while the current step's MFMAs run (two register sets used in turn), one read issued after each
-// MFMA. Rows are BK halves with the 16-byte chunk c of row r stored at slot c ^ ((r >> 1) & 3) (BK = 32) or
-// c ^ (r & 7) (BK = 64): the rows a b128 read phase touches land on different bank groups.
+// MFMA. Rows are BK halves with the 16-byte chunk c of row r stored at slot c ^ ((r >> 2) & 3) (BK = 32) or
+// c ^ ((r >> 1) & 7) (BK = 64): the 16 rows a b128 read phase touches land on different bank groups.
 // BM x BN tile per block of NWM x NWN waves (each a (BM/NWM) x (BN/NWN) part, v_mfma_f32_32x32x16_f16; every
 // configuration accumulates the same 16-deep MFMA steps in the same K order). Tiles are dealt to the
 // eight XCDs as an mx x (8 / mx) grid of rectangles (block b runs on XCD b % 8), mx chosen to minimise the bytes
@@ -192,10 +192,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(GemmArgs g) {
 // EPI_SWIGLU with ch/cl set writes silu(g) * u as the hi/lo pair the down projection consumes.
 // ------------------------------------------------------------------------------------------------------------
 namespace {
+// LDS has 64 banks of 4 bytes, and a 16-byte read serves 16 lanes per cycle: the 16 rows one read phase touches
+// (lanes 0-15, 16-31, ...) must hit 16 different 16-byte bank groups. A 64-half row is half a bank row, so rows r and
+// r + 1 sit in different halves and the slot must differ between rows of equal parity: c ^ ((r >> 1) & 7). A
+// 32-half row is a quarter: c ^ ((r >> 2) & 3).
 template <int BK>
 __device__ __forceinline__ int chunk_slot(int r, int c) {
-  if constexpr (BK == 32) return c ^ ((r >> 1) & 3);
-  else return c ^ (r & 7);
+  if constexpr (BK == 32) return c ^ ((r >> 2) & 3);
+  else return c ^ ((r >> 1) & 7);
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -397,31 +401,66 @@ __global__ __launch_bounds__(64 * NWM * NWN, MINB) void k_gemm_split(GemmSplitAr
     __syncthreads();
     const GemmSplitArgs::Qkv& q = g.qkv;
     const int head = n0 / BN;  // q heads, then k heads, then v heads
-    for (int rr = 0; rr < BM / NW; ++rr) {
-      const int ml = wid * (BM / NW) + rr, m = m0 + ml;
-      if (m >= g.M) break;  // wave-uniform
-      float x0 = xs[ml * LDX + lane], x1 = xs[ml * LDX + lane + 64];
-      const int pos = q.pos_base + m;
-      if (head < q.nq + q.nkv) {
-        const float* cr = q.rope_cos + static_cast<size_t>(pos) * 64;
-        const float* sr = q.rope_sin + static_cast<size_t>(pos) * 64;
-        norm_rope_pair(x0, x1, head < q.nq ? q.q_gain : q.k_gain, q.eps, cr, sr, lane);
+    const bool rope = head < q.nq + q.nkv;
+    // every load of the wave's BM / NW rows (values from LDS, the head's gains, the rows' RoPE table entries) is
+    // issued before the first store, so none of them waits behind a store it might alias
+    constexpr int RW = BM / NW;
+    float x0[RW], x1[RW], cr[RW], sr[RW];
+    float g0 = 1.0f, g1 = 1.0f;
+    if (rope) {
+      const f16* gn = head < q.nq ? q.q_gain : q.k_gain;
+      g0 = static_cast<float>(ld_global(gn, lane));
+      g1 = static_cast<float>(ld_global(gn, lane + 64));
+    }
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int ml = wid * RW + rr;
+      x0[rr] = xs[ml * LDX + lane];
+      x1[rr] = xs[ml * LDX + lane + 64];
+      cr[rr] = sr[rr] = 0.0f;
+      if (rope) {
+        const int pos = q.pos_base + min(m0 + ml, g.M - 1);
+        cr[rr] = q.rope_cos[static_cast<size_t>(pos) * 64 + lane];
+        sr[rr] = q.rope_sin[static_cast<size_t>(pos) * 64 + lane];
       }
+    }
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int m = m0 + wid * RW + rr;
+      if (m >= g.M) break;  // wave-uniform
+      const int pos = q.pos_base + m;
+      if (rope) norm_rope_pair(x0[rr], x1[rr], g0, g1, q.eps, cr[rr], sr[rr]);
       if (head < q.nq) {
         float* dst = q.q_out + static_cast<size_t>(m) * q.nq * 128 + head * 128;
-        dst[lane] = x0;
-        dst[lane + 64] = x1;
+        dst[lane] = x0[rr];
+        dst[lane + 64] = x1[rr];
       } else {
         const bool is_k = head < q.nq + q.nkv;
         const int kvh = is_k ? head - q.nq : head - q.nq - q.nkv;
         const size_t base = static_cast<size_t>(q.slot) * q.slot_stride + static_cast<size_t>(q.layer) * q.layer_stride +
                             (static_cast<size_t>(kvh) * q.cap + pos) * 128;
         f16* cache = is_k ? q.kcache : q.vcache;
-        cache[base + lane] = static_cast<f16>(x0);
-        cache[base + lane + 64] = static_cast<f16>(x1);
+        cache[base + lane] = static_cast<f16>(x0[rr]);
+        cache[base + lane + 64] = static_cast<f16>(x1[rr]);
       }
     }
     return;
+  }
+  // residual: every element of the wave's part of C is read before the first store (otherwise each read waits
+  // behind the store before it, which the compiler cannot prove does not alias it)
+  float res[EPI == EPI_RESIDUAL ? MI : 1][EPI == EPI_RESIDUAL ? NJ : 1][16];
+  if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = min(m0 + wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), g.M - 1);
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) {
+          const int n = min(n0 + wn * WTN + t * 32 + (lane & 31), g.N - 1);
+          res[i][t][r] = g.c[static_cast<size_t>(m) * g.ldc + n];
+        }
+      }
   }
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -452,10 +491,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, MINB) void k_gemm_split(GemmSplitAr
 #pragma unroll
         for (int t = 0; t < NJ; ++t) {
           const int n = n0 + wn * WTN + t * 32 + (lane & 31);
-          if (n < g.N) {
-            float* dst = g.c + static_cast<size_t>(m) * g.ldc + n;
-            *dst = EPI == EPI_RESIDUAL ? *dst + v[t] : v[t];
-          }
+          if (n < g.N) g.c[static_cast<size_t>(m) * g.ldc + n] = EPI == EPI_RESIDUAL ? res[i][t][r] + v[t] : v[t];
         }
       }
     }
