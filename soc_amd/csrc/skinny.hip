@@ -240,6 +240,10 @@ __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
   if (n >= nout) return;
   const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + n;
   const size_t ss_stride = 64, split_stride = static_cast<size_t>(16) * a.Ntot;
+  float* dst = a.c + static_cast<size_t>(m) * a.ldc + n;
+  // the residual is requested with the partials (read after them it would cost a second memory round trip)
+  float prev = 0.0f;
+  if constexpr (EPI == EPI_RESIDUAL) prev = *dst;
   float sc = 1.0f, v, u = 0.0f;
   if constexpr (EPI == EPI_SWIGLU) {
     if (a.gain != nullptr) {
@@ -267,11 +271,10 @@ __global__ __launch_bounds__(256) void k_skinny_epi(SkinnyArgs a, int nout) {
     }
   }
   v *= sc;
-  float* dst = a.c + static_cast<size_t>(m) * a.ldc + n;
   if constexpr (EPI == EPI_SWIGLU) {
     *dst = silu_ref(v) * (sc * u);
   } else if constexpr (EPI == EPI_RESIDUAL) {
-    *dst += v;
+    *dst = prev + v;
   } else {
     *dst = v;
   }
@@ -284,6 +287,18 @@ __global__ __launch_bounds__(64) void k_skinny_epi_qkv(SkinnyArgs a) {
   const int m = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   const float* p = sk_part(a.part, a.KS) + static_cast<size_t>(m) * a.Ntot + h * 128;
   const size_t ss_stride = 64, split_stride = static_cast<size_t>(16) * a.Ntot;
+  // the row's position and slot, the head's gains and the RoPE entries at pos go out before the partials: the
+  // table entries wait only for pos, and their round trip overlaps the partials'
+  const int pos = a.pos[m], slot = a.slots[m];
+  const bool normed = h < a.nq + a.nkv;
+  float g0 = 1.0f, g1 = 1.0f, c = 0.0f, sn = 0.0f;
+  if (normed) {
+    const f16* gn = h < a.nq ? a.q_gain : a.k_gain;
+    g0 = static_cast<float>(ld_global(gn, lane));
+    g1 = static_cast<float>(ld_global(gn, lane + 64));
+    c = a.rope_cos[static_cast<size_t>(pos) * 64 + lane];
+    sn = a.rope_sin[static_cast<size_t>(pos) * 64 + lane];
+  }
   float x0, x1;
   if (a.gain != nullptr) {
     float r[3];
@@ -297,18 +312,14 @@ __global__ __launch_bounds__(64) void k_skinny_epi_qkv(SkinnyArgs a) {
     x0 = r[0];
     x1 = r[1];
   }
-  const int pos = a.pos[m], slot = a.slots[m];
-  const float* cr = a.rope_cos + static_cast<size_t>(pos) * 64;
-  const float* sr = a.rope_sin + static_cast<size_t>(pos) * 64;
+  if (normed) norm_rope_pair(x0, x1, g0, g1, a.eps, c, sn);
   if (h < a.nq) {
-    norm_rope_pair(x0, x1, a.q_gain, a.eps, cr, sr, lane);
     float* dst = a.q_out + static_cast<size_t>(m) * a.nq * 128 + h * 128;
     dst[lane] = x0;
     dst[lane + 64] = x1;
   } else {
-    const bool is_k = h < a.nq + a.nkv;
+    const bool is_k = normed;
     const int g = is_k ? h - a.nq : h - a.nq - a.nkv;
-    if (is_k) norm_rope_pair(x0, x1, a.k_gain, a.eps, cr, sr, lane);
     f16* cache = (is_k ? a.kcache : a.vcache) + static_cast<size_t>(slot) * a.slot_stride +
                  static_cast<size_t>(a.layer) * a.layer_stride + static_cast<size_t>(g) * a.cap * 128 +
                  static_cast<size_t>(pos) * 128;
