@@ -4,7 +4,8 @@
 Workload (headline): Qwen3-0.6B architecture, random-init fp16 weights N(0, 0.02) (seed 1), batch 1. A 32-token
 prompt is prefilled (untimed), then W warmup and K timed greedy decode steps run with the sampled token fed back on
 the device. A "step" is one decode token. Also measured in the same run:
-  * prefill of a 2048-token prompt (tok/s), on the fp16 model and with its projections group-quantized (int8, int4),
+  * prefill of a 2048-token prompt (tok/s, and its algorithmic FLOP/s against the 2.5 PFLOP/s dense fp16 peak in
+    "prefill_roofline"), on the fp16 model and with its projections group-quantized (int8, int4),
   * the dominant decode kernel: k_decode_xcd (one launch = one whole token, every layer split over the 8 XCDs) or
     k_decode_persistent when the device runs that one, timed with HIP events on the stream it is launched on; the
     fused RMSNorm + QKV GEMV
@@ -70,6 +71,19 @@ def bench_decode(ctx, m, cfg, steps: int, warmup: int):
     mean_kv = start_len + (steps - 1) / 2.0
     kv.close()
     return ms, mean_kv, toks
+
+
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def prefill_flop(cfg, n: int) -> float:
+    """Algorithmic FLOP of an n-token prefill: the projections (2 per weight per row), causal attention (q.k and p.v
+    over the keys each row sees: 4 d flops per (head, row, visible key)) and the last row's LM head."""
+    H, I, d = cfg.hidden_size, cfg.intermediate_size, 128
+    qd, kvd = cfg.num_attention_heads * d, cfg.num_key_value_heads * d
+    proj = 2.0 * n * (H * (qd + 2 * kvd) + qd * H + 2 * H * I + I * H)
+    attn = 4.0 * d * cfg.num_attention_heads * n * (n + 1) / 2
+    return cfg.num_hidden_layers * (proj + attn) + 2.0 * H * cfg.vocab_size
 
 
 def bench_prefill(ctx, m, cfg, n: int = 2048):
@@ -572,6 +586,12 @@ def main() -> None:
         "prefill_tok_s": None if prefill_ms is None else round(2048 / (prefill_ms * 1e-3), 1),
         "prefill_ms_2048": None if prefill_ms is None else round(prefill_ms, 3),
         "prefill_quant_2048": prefill_q,
+        "prefill_roofline": None if prefill_ms is None else {
+            "workload": "2048-token prefill, Qwen3-0.6B: 28 layers (projections, causal attention, norms) and the "
+                        "last row's LM head", "bound": "mfma",
+            "achieved": round(prefill_flop(cfg, 2048) / (prefill_ms * 1e-3) / 1e12, 1), "peak": FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(prefill_flop(cfg, 2048) / (prefill_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+            "alg_flop": prefill_flop(cfg, 2048)},
         "roofline": roofline,
         "gemv_qkv_4096x1024": {"avg_launch_us": round(us, 3), "gbs": round(gemv_gbs, 1),
                                "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
