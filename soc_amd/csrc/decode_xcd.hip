@@ -860,16 +860,25 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
         // output t (head t / 128, dim t % 128): the waves' partials rescaled to the block max, in wave order
         for (int t = tid; t < G * HD; t += NT) {
           const int h = t / HD, d = t % HD;
-          float M = kNoKeys;
+          float M = kNoKeys, mw[NW];
 #pragma unroll
-          for (int w = 0; w < NW; ++w)
-            M = fmaxf(M, reinterpret_cast<const float*>(vtb + w * KT * HD * 2)[G * HD + h]);
+          for (int w = 0; w < NW; ++w) {
+            mw[w] = reinterpret_cast<const float*>(vtb + w * KT * HD * 2)[G * HD + h];
+            M = fmaxf(M, mw[w]);
+          }
           if (!allkeys) M = tw_val(tw_pack(M, 0u));  // as the exchange word will carry it
+          // the weight of wave w's partial, exp2(max_w - M) (0 for a wave without keys), is the same for every dim
+          // of the head: lane w computes it once and the wave reads it back per w (G * HD is a multiple of 64, so
+          // every thread of a wave is here with the same head)
+          float ml = mw[0];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) ml = (lane & (NW - 1)) == w ? mw[w] : ml;
+          const float fl = __builtin_amdgcn_exp2f(ml - M);
           float O = 0.0f, Lw = 0.0f;
 #pragma unroll
           for (int w = 0; w < NW; ++w) {
             const float* gw = reinterpret_cast<const float*>(vtb + w * KT * HD * 2);
-            const float f = __builtin_amdgcn_exp2f(gw[G * HD + h] - M);  // 0 for a wave without keys
+            const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), w));
             Lw += gw[G * HD + G + h] * f;
             O += gw[h * HD + d] * f;
           }
