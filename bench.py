@@ -466,16 +466,21 @@ TRAFFIC_SUMMARY = {"xcd": ROOT / "profiles" / "k_decode_xcd_qwen3_0p6b_traffic.m
                    "persistent": ROOT / "profiles" / "k_decode_persistent_qwen3_0p6b_traffic.md"}
 
 
-def measured_traffic(path: Path):
-    """HBM bytes per launch of a one-launch decode kernel from its committed rocprofv3 counter summary
-    (line `traffic_bytes_per_launch: <int>`), or None when no summary exists."""
+def measured_traffic(path: Path, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes of a one-launch decode kernel from its committed rocprofv3 counter summary (line `<key>: <int>`;
+    the XCD kernel's summary gives them per decode token), or None when no summary exists."""
     try:
         for line in path.read_text().splitlines():
-            if line.strip().startswith("traffic_bytes_per_launch:"):
+            if line.strip().startswith(key + ":"):
                 return int(line.split(":", 1)[1].strip())
     except OSError:
         return None
     return None
+
+
+# Decode tokens per launch of k_decode_xcd (kXcdStepsPerLaunch in soc_amd/csrc/runtime.cpp): soc_decode_steps runs
+# up to this many steps in one launch.
+XCD_TOKENS_PER_LAUNCH = 64
 
 
 def copy_calibrate(mib: int = 1024) -> None:
@@ -548,11 +553,20 @@ def main() -> None:
     if cpp_api is not None:
         _progress(f"GenerationContext::Generate: {cpp_api.get('generate_ms_median')} ms for 16 tokens")
 
-    if path in ("xcd", "persistent"):
-        # one launch per token: the events around the K launches give the average launch duration (the short
-        # gaps between back-to-back launches included)
-        kname = "k_decode_xcd" if path == "xcd" else "k_decode_persistent"
-        roofline = {"kernel": f"{kname} (whole decode token: 28 layers + LM head + argmax)",
+    if path == "xcd":
+        # the timed steps run as ceil(K / XCD_TOKENS_PER_LAUNCH) launches: the events around them give the average
+        # launch duration (the short gaps between launches included) and tpl tokens per launch on average
+        tpl = args.steps / -(-args.steps // XCD_TOKENS_PER_LAUNCH)
+        per_tok = measured_traffic(TRAFFIC_SUMMARY[path], "traffic_bytes_per_token")
+        roofline = {"kernel": f"k_decode_xcd ({tpl:g} decode tokens per launch, each 28 layers + LM head + greedy "
+                              "token)",
+                    "bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": round(per_tok * tpl) if per_tok is not None else None, "tokens_per_launch": tpl,
+                    "avg_launch_us": round(ms_per_step * 1e3 * tpl, 3), "alg_bytes_per_launch": round(bpt * tpl)}
+    elif path == "persistent":
+        # one launch per token
+        roofline = {"kernel": "k_decode_persistent (whole decode token: 28 layers + LM head + argmax)",
                     "bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(TRAFFIC_SUMMARY[path]),
                     "avg_launch_us": round(ms_per_step * 1e3, 3), "alg_bytes_per_launch": int(bpt)}

@@ -1,5 +1,9 @@
-// decode_xcd.hip - one-launch decode step for batch 1 with every layer partitioned over the eight XCDs of MI355X, the
-// layers alternating between two groups of blocks, and every dot product of a layer on the matrix cores.
+// decode_xcd.hip - one-launch decode for batch 1 with every layer partitioned over the eight XCDs of MI355X, the
+// layers alternating between two groups of blocks, and every dot product of a layer on the matrix cores. One launch
+// runs a.steps decode steps: the blocks stay resident from token to token, the last block to finish a step's LM head
+// hands the greedy token to the next step through one device word, and with an even layer count group 0, which has
+// nothing to compute during the last layer, streams the next step's first layer then (instead of every step starting
+// with a whole layer's rows to load).
 //
 // Block (g, j): XCD g, read from the XCC_ID hardware register, and rank j < 32 among the blocks of this launch that
 // arrived on it. Group p = j / 16 computes the layers l with l % 2 == p while the other group streams the weight rows
@@ -193,6 +197,9 @@ struct Ctx {
   const PersistArgs& a;
   int g, j, token, pos;
   uint32_t phase0;  // (step - 1) * L: the tag of layer l is (phase0 + l) & 3
+  uint32_t step;    // this step's number (state[3] when it started; steps count from 1)
+  uint32_t step1;   // the launch's first step
+  int ring1;        // ring slot of the launch's first token
   char* lds;
   int* flag;  // LDS: [0] a wait failed, [1] XCD, [2] rank, [3] last block, [4] cross_reduce2 stage-1 marker
 };
@@ -520,14 +527,170 @@ __device__ __forceinline__ bool cross_reduce2(const Ctx& c, int w, int jj, bool 
   return true;
 }
 
-// The layers l % 2 == p of one decode step for a block of group p, then the final hidden state (all blocks).
+// LM head rows of block b = 32 g + j on all 512 threads, best (value, index) per 32-lane slot into bv/bi. The logits
+// are RMSNorm(x) . W = (x * gain) . W * scale.
 template <int G>
-__device__ __forceinline__ bool run_layers(const Ctx& c) {
+__device__ __forceinline__ void lm_head(const Ctx& c) {
+  using T = Tiling<G>;
+  using LD = Lds<G>;
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x, slot = tid / T::TPR_LM;
+  const bool lead = (tid % T::TPR_LM) == 0;
+  const float* xn = reinterpret_cast<const float*>(c.lds + LD::VT);
+  const float scale = rms_scale(reinterpret_cast<const float*>(c.lds + LD::RED), a.H, a.eps);
+  const int b = c.g * NBX + c.j;
+  const int rv = (a.V + NX * NBX - 1) / (NX * NBX);
+  const int v0 = b * rv, v1 = min(a.V, v0 + rv);
+  constexpr int STEP = NT / T::TPR_LM;
+  Slice<T::TPR_LM, T::CPT_LM> f0, f1;
+  auto rowp = [&](int r) { return r < v1 ? a.lm_head + static_cast<size_t>(r) * a.H : nullptr; };
+  slice_load(f0, rowp(v0 + slot), a.H);
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  auto consume = [&](const Slice<T::TPR_LM, T::CPT_LM>& f, int r0) {
+    const float out = slice_dot(f, xn, a.H) * scale;
+    const int row = r0 + slot;
+    if (row < v1) {
+      if (lead && a.logits != nullptr) a.logits[row] = out;
+      if (out > best) {  // a slot's rows ascend: strict > keeps the lowest index
+        best = out;
+        best_i = row;
+      }
+    }
+  };
+  for (int r0 = v0; r0 < v1; r0 += 2 * STEP) {
+    slice_load(f1, rowp(r0 + STEP + slot), a.H);
+    consume(f0, r0);
+    slice_load(f0, rowp(r0 + 2 * STEP + slot), a.H);
+    consume(f1, r0 + STEP);
+  }
+  float* bv = reinterpret_cast<float*>(c.lds + LD::BV);
+  int* bi = reinterpret_cast<int*>(c.lds + LD::BI);
+  if (lead) {
+    bv[slot] = best;
+    bi[slot] = best_i;
+  }
+}
+
+// Greedy token of the step (sampler.cpp:26-61 with top_k = 1): every block's best (value, index) over its LM-head
+// rows is published and counted; the last block to arrive picks the best (lowest index on ties) and writes it to the
+// ring. Within a launch the next step learns its token from one 64-bit word {step, token} (state[8..9]), written and
+// read with device scope and no fence: nothing else the last block writes is read before the launch ends. The
+// arrival counter only grows during a launch (a step's last block sees a multiple of the block count); the launch's
+// last step resets it and writes the state the next launch starts from.
+template <int G>
+__device__ __forceinline__ void finish_step(const Ctx& c) {
+  using LD = Lds<G>;
+  const PersistArgs& a = c.a;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  float* bv = reinterpret_cast<float*>(c.lds + LD::BV);
+  int* bi = reinterpret_cast<int*>(c.lds + LD::BI);
+  const int b = c.g * NBX + c.j, nb = NX * NBX;
+  __syncthreads();
+  if (tid == 0) {
+    float v = bv[0];
+    int i = bi[0];
+    for (int w = 1; w < NT / Tiling<G>::TPR_LM; ++w)
+      if (bv[w] > v || (bv[w] == v && bi[w] < i)) {
+        v = bv[w];
+        i = bi[w];
+      }
+    st_dev(a.part_val + b, v);
+    st_dev(a.part_idx + b, i);
+    wait_mem();  // the block's candidate is visible device-wide before it is counted
+    const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c.flag[3] = (done + 1) % nb == 0;
+  }
+  __syncthreads();
+  if (c.flag[3] == 0) return;
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int q = tid; q < nb; q += NT) {
+    const float pv = ld_dev(a.part_val + q);
+    const int pi = ld_dev(a.part_idx + q);
+    if (pv > v || (pv == v && pi < i)) {
+      v = pv;
+      i = pi;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(i, off, kWave);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    bv[wid] = v;
+    bi[wid] = i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < NT / 64; ++w)
+      if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
+        bv[0] = bv[w];
+        bi[0] = bi[w];
+      }
+    const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
+    const int k = static_cast<int>(c.step - c.step1);  // the step's index in this launch
+    if (a.ring != nullptr) __hip_atomic_store(a.ring + c.ring1 + k, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k + 1 < a.steps) {
+      const uint64_t word = (static_cast<uint64_t>(c.step + 1u) << 32) | static_cast<uint32_t>(tok);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(a.state + 8), word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {  // the launch's last step: the next launch's start
+      a.state[0] = tok;
+      a.state[1] = c.pos + 1;
+      a.state[3] = static_cast<int>(c.step + 1u);
+      if (a.ring != nullptr) *a.ring_pos = c.ring1 + a.steps;
+      for (int x = 0; x < NX; ++x) a.xcd_ctr[((c.step + 1u) & 1u) * NX + x] = 0;  // the next launch's arrivals
+      __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Start of the launch's next step: thread 0 waits (bounded) for the previous step's word {step, token}; every thread
+// takes the token from LDS; the position advances by one.
+template <int G>
+__device__ __forceinline__ bool next_step(Ctx& c) {
+  const PersistArgs& a = c.a;
+  const uint32_t want = c.step + 1u;
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = now_ticks();
+    uint32_t spins = 0;
+    uint64_t w;
+    while (true) {
+      w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.state + 8), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (static_cast<uint32_t>(w >> 32) == want) break;
+      if (give_up(c, spins, t0)) {
+        wait_failed(c);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    c.flag[5] = static_cast<int>(static_cast<uint32_t>(w));
+    c.flag[4] = 0;  // cross_reduce2's stage-1 marker
+  }
+  __syncthreads();
+  if (c.flag[0] != 0) return false;
+  c.token = __builtin_amdgcn_readfirstlane(c.flag[5]);  // uniform: scalar registers
+  c.pos += 1;
+  c.step = want;
+  c.phase0 += static_cast<uint32_t>(a.L);
+  return true;
+}
+
+// The a.steps decode steps of one launch: per step, the layers l % 2 == p for a block of group p, the final hidden
+// state (all blocks), the LM head and the greedy token.
+template <int G>
+__device__ __forceinline__ bool run_steps(Ctx& c) {
   using T = Tiling<G>;
   using LD = Lds<G>;
   const PersistArgs& a = c.a;
   const int tid = threadIdx.x, wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
-  const int g = c.g, pgrp = c.j / NBG, jj = c.j % NBG, pos = c.pos, S = pos + 1;
+  const int g = c.g, pgrp = c.j / NBG, jj = c.j % NBG;
   uint64_t* const trw =
       a.trace != nullptr ? a.trace + kTraceWaveBase + ((g * NBX + c.j) * NW + wid) * kTracePts : nullptr;
   const int H = a.H, I = a.I, qd = a.qd;
@@ -558,13 +721,6 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   uint32_t* loc_xa = loc_h + ((IS + 63) & ~63);               // [H + 16]: x after the attention-input reduction
   uint32_t* loc_xg = loc_xa + HMAX + 64;                      // [H + 16]: x' after the o_proj reduction
   constexpr int PST = T::GT * 16;                             // partial-sum row stride of a wave
-  // attention: up to KALL keys every block takes all keys; beyond that block jj < na takes keys [k0, k1) and the
-  // blocks' partials are exchanged
-  const bool allkeys = S <= KALL;
-  int na, chunk;
-  attn_split(S, na, chunk);
-  const int k0 = allkeys ? 0 : (jj < na ? min(S, jj * chunk) : S);
-  const int k1 = allkeys ? S : (jj < na ? min(S, k0 + chunk) : S);
   int lane = tid & 63, rl = lane & 15, kq = lane >> 4;
   // this block's local q/k/v row lr of the XCD's (G + 2) * 128 (q heads, key, value) as a row of the fused matrix
   auto qkv_row = [&](int lr) {
@@ -618,7 +774,25 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
   // the hi/lo rows of x and h are zero past H and IS (the fixed-length MFMA steps read them)
   for (int i = tid; i < 2 * HMAX; i += NT) xhl[i] = static_cast<f16>(0.0f);
   for (int i = tid; i < 2 * ISM; i += NT) hhl[i] = static_cast<f16>(0.0f);
+  // With an even layer count the last layer is group 1's, and group 0, idle during it, streams the next step's first
+  // layer then; otherwise each group streams its first layer when the step starts.
+  const bool pre0 = a.L % 2 == 0;
   if (pgrp < a.L) stream(pgrp);
+
+  for (int k = 0; k < a.steps; ++k) {
+  if (k > 0) {
+    // the next token: the previous step's last block releases the step count after the token and the position
+    if (!next_step<G>(c)) return false;
+    if (pgrp < a.L && !(pre0 && pgrp == 0)) stream(pgrp);
+  }
+  const int pos = c.pos, S = pos + 1;
+  // attention: up to KALL keys every block takes all keys; beyond that block jj < na takes keys [k0, k1) and the
+  // blocks' partials are exchanged
+  const bool allkeys = S <= KALL;
+  int na, chunk;
+  attn_split(S, na, chunk);
+  const int k0 = allkeys ? 0 : (jj < na ? min(S, jj * chunk) : S);
+  const int k1 = allkeys ? S : (jj < na ? min(S, k0 + chunk) : S);
 
   for (int layer = pgrp; layer < a.L; layer += 2) {
     const f16* W[4];  // in_norm, post_norm, q_norm, k_norm
@@ -818,19 +992,23 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
         // dims 16 dt + 4 (rl & 3): chunk 2 dt + (rl & 3) / 2 stored at slot (2 dt + (rl & 3) / 2) ^ 2 (row & 7), i.e.
         // byte 32 ((dt ^ (rl / 4)) ^ 4 half) + 16 ((rl & 3) / 2) + 8 (rl & 1) of the row
         const int vbase = (8 * kq + (rl >> 2)) * HD * 2 + ((rl & 3) >> 1) * 16 + (rl & 1) * 8, vsw = (rl >> 2) * 32;
-        hv4 vr[HD / 16][2];
+        // in two halves of the head's dims (fewer registers at the kernel's peak)
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt)
+        for (int d0 = 0; d0 < HD / 16; d0 += HD / 32) {
+          hv4 vr[HD / 32][2];
 #pragma unroll
-          for (int half = 0; half < 2; ++half)
-            vr[dt][half] = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) hv4*)(
-                (__attribute__((address_space(3))) char*)(vt) + vbase + half * 4 * HD * 2 +
-                ((32 * dt) ^ vsw ^ (128 * half))));
+          for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt) {
-          const f16x4 w0 = __builtin_bit_cast(f16x4, vr[dt][0]), w1 = __builtin_bit_cast(f16x4, vr[dt][1]);
-          const h8 vb = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-          o[dt] = mfma16(pa, vb, o[dt]);
+            for (int half = 0; half < 2; ++half)
+              vr[dt][half] = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) hv4*)(
+                  (__attribute__((address_space(3))) char*)(vt) + vbase + half * 4 * HD * 2 +
+                  ((32 * (d0 + dt)) ^ vsw ^ (128 * half))));
+#pragma unroll
+          for (int dt = 0; dt < HD / 32; ++dt) {
+            const f16x4 w0 = __builtin_bit_cast(f16x4, vr[dt][0]), w1 = __builtin_bit_cast(f16x4, vr[dt][1]);
+            const h8 vb = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            o[d0 + dt] = mfma16(pa, vb, o[d0 + dt]);
+          }
         }
         if (t == kb / KT + wr) XTRACEW(20);
       }
@@ -1053,6 +1231,9 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
     if (layer + 2 < a.L) {
       XSYNC();
       stream(layer + 2);
+    } else if (pre0 && pgrp == 0 && k + 1 < a.steps) {
+      XSYNC();
+      stream(0);  // the next step's first layer, while group 1 computes the last one
     }
   }
   // final hidden state x = x' + sum_k D_k of the last layer, RMSNorm input with the final gain (all blocks), in fp32
@@ -1061,52 +1242,11 @@ __device__ __forceinline__ bool run_layers(const Ctx& c) {
                 a.final_norm, xres, xhl, reinterpret_cast<float*>(vtb), red, 2 * a.L + 3);
   XTRACE0(a.L);
   XSYNC();
+  lm_head<G>(c);
+  XTRACE0(a.L + 1);
+  finish_step<G>(c);
+  }
   return true;
-}
-
-// LM head rows of block b = 32 g + j on all 512 threads, best (value, index) per 32-lane slot into bv/bi. The logits
-// are RMSNorm(x) . W = (x * gain) . W * scale.
-template <int G>
-__device__ __forceinline__ void lm_head(const Ctx& c) {
-  using T = Tiling<G>;
-  using LD = Lds<G>;
-  const PersistArgs& a = c.a;
-  const int tid = threadIdx.x, slot = tid / T::TPR_LM;
-  const bool lead = (tid % T::TPR_LM) == 0;
-  const float* xn = reinterpret_cast<const float*>(c.lds + LD::VT);
-  const float scale = rms_scale(reinterpret_cast<const float*>(c.lds + LD::RED), a.H, a.eps);
-  const int b = c.g * NBX + c.j;
-  const int rv = (a.V + NX * NBX - 1) / (NX * NBX);
-  const int v0 = b * rv, v1 = min(a.V, v0 + rv);
-  constexpr int STEP = NT / T::TPR_LM;
-  Slice<T::TPR_LM, T::CPT_LM> f0, f1;
-  auto rowp = [&](int r) { return r < v1 ? a.lm_head + static_cast<size_t>(r) * a.H : nullptr; };
-  slice_load(f0, rowp(v0 + slot), a.H);
-  float best = -INFINITY;
-  int best_i = 0x7fffffff;
-  auto consume = [&](const Slice<T::TPR_LM, T::CPT_LM>& f, int r0) {
-    const float out = slice_dot(f, xn, a.H) * scale;
-    const int row = r0 + slot;
-    if (row < v1) {
-      if (lead && a.logits != nullptr) a.logits[row] = out;
-      if (out > best) {  // a slot's rows ascend: strict > keeps the lowest index
-        best = out;
-        best_i = row;
-      }
-    }
-  };
-  for (int r0 = v0; r0 < v1; r0 += 2 * STEP) {
-    slice_load(f1, rowp(r0 + STEP + slot), a.H);
-    consume(f0, r0);
-    slice_load(f0, rowp(r0 + 2 * STEP + slot), a.H);
-    consume(f1, r0 + STEP);
-  }
-  float* bv = reinterpret_cast<float*>(c.lds + LD::BV);
-  int* bi = reinterpret_cast<int*>(c.lds + LD::BI);
-  if (lead) {
-    bv[slot] = best;
-    bi[slot] = best_i;
-  }
 }
 
 }  // namespace
@@ -1137,75 +1277,11 @@ __global__ __launch_bounds__(NT) void k_decode_xcd(PersistArgs a) {
     if (tid == 0) __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  Ctx c{a, g, j, a.state[0], a.state[1], (step - 1u) * static_cast<uint32_t>(a.L), lds, flag};
-  if (!run_layers<G>(c)) return;
-  lm_head<G>(c);
-  XTRACE0(a.L + 1);
-
-  // ---- greedy argmax over the blocks' candidates (sampler.cpp:26-61 with top_k = 1) ----
-  float* bv = reinterpret_cast<float*>(lds + LD::BV);
-  int* bi = reinterpret_cast<int*>(lds + LD::BI);
-  const int b = g * NBX + j, nb = NX * NBX;
-  __syncthreads();
-  if (tid == 0) {
-    float v = bv[0];
-    int i = bi[0];
-    for (int w = 1; w < NT / Tiling<G>::TPR_LM; ++w)
-      if (bv[w] > v || (bv[w] == v && bi[w] < i)) {
-        v = bv[w];
-        i = bi[w];
-      }
-    st_dev(a.part_val + b, v);
-    st_dev(a.part_idx + b, i);
-    wait_mem();  // the block's candidate is visible device-wide before it is counted
-    const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag[3] = (done == nb - 1);
-  }
-  __syncthreads();
-  if (flag[3] == 0) return;
-  float v = -INFINITY;
-  int i = 0x7fffffff;
-  for (int q = tid; q < nb; q += NT) {
-    const float pv = ld_dev(a.part_val + q);
-    const int pi = ld_dev(a.part_idx + q);
-    if (pv > v || (pv == v && pi < i)) {
-      v = pv;
-      i = pi;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(v, off, kWave);
-    const int oi = __shfl_xor(i, off, kWave);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
-  }
-  __syncthreads();
-  if (lane == 0) {
-    bv[wid] = v;
-    bi[wid] = i;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < NT / 64; ++w)
-      if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
-        bv[0] = bv[w];
-        bi[0] = bi[w];
-      }
-    const int tok = bi[0] == 0x7fffffff ? 0 : bi[0];
-    a.state[0] = tok;
-    a.state[1] = c.pos + 1;
-    a.state[3] = static_cast<int>(step + 1u);
-    if (a.ring != nullptr) {
-      a.ring[*a.ring_pos] = tok;
-      *a.ring_pos += 1;
-    }
-    for (int k = 0; k < NX; ++k) a.xcd_ctr[((step + 1u) & 1u) * NX + k] = 0;  // the next step's arrival counters
-    __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  Ctx c{a, g, j, a.state[0], a.state[1], (step - 1u) * static_cast<uint32_t>(a.L), step, step,
+        a.ring != nullptr ? *a.ring_pos : 0, lds, flag};
+  run_steps<G>(c);
 }
+
 #undef XSYNC
 #undef XTRACE
 #undef XTRACE0

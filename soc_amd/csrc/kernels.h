@@ -197,6 +197,8 @@ struct PersistArgs {
   uint32_t* loc;              // [8][loc_stride] per-XCD hand-off regions (q/k/v, attention partials, h)
   int loc_stride;             // words per region
   int* xcd_ctr;               // [2][8] arrivals per XCD, by step parity (zero; the next step's pair is reset)
+  int steps;                  // decode steps one launch of k_decode_xcd runs (>= 1; the token of each is released to
+                              // the next through state[3])
 };
 bool persistent_supported(int H, int qd, int I, int qkv_rows, int nq, int nkv, int nblocks);
 size_t persistent_lds_bytes(const PersistArgs& a, int G);

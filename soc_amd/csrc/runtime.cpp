@@ -126,6 +126,9 @@ struct BatchWs {
 };
 
 constexpr int kAttnChunk = 256;
+// Decode steps per launch of the XCD-partitioned one-launch kernel (its blocks stay resident from step to step: the
+// next token's first layer streams while the last layer of the current one runs).
+constexpr int kXcdStepsPerLaunch = 64;
 
 // Keys per attention chunk of single-sequence per-op decode for a cache of `cap` positions: the smallest of 64, 128,
 // 256 that keeps a full cache within 160 chunks (the kernel's combine limit). Smaller chunks give a short context
@@ -672,6 +675,7 @@ soc::PersistArgs persist_args(soc_model* m, soc_kv* kv, int slot, const DecodeWs
   p.loc = w.loc;
   p.loc_stride = w.loc_stride;
   p.xcd_ctr = w.xcd_ctr;
+  p.steps = 1;
   if (const char* sl = std::getenv("SOC_SPIN_SLEEP")) p.spin_sleep = std::max(0, std::atoi(sl));
   // SOC_WAIT_TICKS=<n>: bound of the cross-block waits (tests force the time-out path with a tiny bound; every
   // block still exits normally, the waits only give up sooner)
@@ -727,9 +731,16 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
       if ((e = hipMemset(p.trace, 0, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
     }
-    for (int i = 0; i < steps; ++i)
-      if ((e = xcd ? soc::launch_decode_xcd(p, s) : soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
-        return hip_fail(e, "persistent decode launch");
+    if (xcd) {  // k_decode_xcd runs up to kXcdStepsPerLaunch steps per launch, releasing each token on the device
+      for (int i = 0; i < steps; i += kXcdStepsPerLaunch) {
+        p.steps = std::min(kXcdStepsPerLaunch, steps - i);
+        if ((e = soc::launch_decode_xcd(p, s)) != hipSuccess) return hip_fail(e, "one-launch decode");
+      }
+    } else {
+      for (int i = 0; i < steps; ++i)
+        if ((e = soc::launch_decode_persistent(p, w.nblocks, s)) != hipSuccess)
+          return hip_fail(e, "persistent decode launch");
+    }
     if (err_out != nullptr && trace_path == nullptr) return SOC_OK;  // the caller reads the flag and synchronises
     int32_t err_local = 0;
     int32_t& err = err_out != nullptr ? *err_out : err_local;
