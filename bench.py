@@ -480,7 +480,7 @@ def measured_traffic(path: Path, key: str = "traffic_bytes_per_launch"):
 
 # Decode tokens per launch of k_decode_xcd (kXcdStepsPerLaunch in soc_amd/csrc/runtime.cpp): soc_decode_steps runs
 # up to this many steps in one launch.
-XCD_TOKENS_PER_LAUNCH = 64
+XCD_TOKENS_PER_LAUNCH = 128
 
 
 def copy_calibrate(mib: int = 1024) -> None:

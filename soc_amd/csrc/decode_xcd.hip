@@ -331,9 +331,25 @@ __device__ __forceinline__ float sum8(float v) {
 
 // Wave w < 8 of the block: its eighth of x = embedding row (layer 0, embedding.cpp:51-77), into xres, the hi/lo
 // rows of x * gain into xhl and its partial sum of x^2 into red[w] (the RMSNorm of rms_norm_module.cpp:56-64 is
-// completed by rms_scale). The wave owns the element quads w * H / 32 .. + H / 32.
-__device__ __forceinline__ void embed_row(const Ctx& c, int w, const f16* embed_row, const f16* gain, float* xres,
-                                          f16* xhl, float* red) {
+// completed by rms_scale). The wave owns the element quads w * H / 32 .. + H / 32. embed_fetch requests the quads and
+// gains, embed_finish consumes them (the first layer's first key tile is requested in between).
+struct EmbedFetch {
+  f16x4 e[HMAX / 256], g[HMAX / 256];
+};
+__device__ __forceinline__ void embed_fetch(const Ctx& c, int w, const f16* embed_row, const f16* gain, EmbedFetch& f) {
+  constexpr int NI = HMAX / 256;
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const int H = c.a.H, ni = H / 256, q0 = w * (H / 32);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int q = i < ni ? q0 + i * 8 + (lane >> 3) : q0;  // quads past the slice re-read its first (unused)
+    f.e[i] = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
+    f.g[i] = ld_global(reinterpret_cast<const f16x4*>(gain), q);
+  }
+}
+__device__ __forceinline__ void embed_finish(const Ctx& c, int w, const EmbedFetch& f, float* xres, f16* xhl,
+                                             float* red) {
   constexpr int NI = HMAX / 256;
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));
@@ -343,13 +359,11 @@ __device__ __forceinline__ void embed_row(const Ctx& c, int w, const f16* embed_
   for (int i = 0; i < NI; ++i) {
     const int q = q0 + i * 8 + (lane >> 3);
     if (i < ni && (lane & 7) == 0) {
-      const f16x4 e4 = ld_global(reinterpret_cast<const f16x4*>(embed_row), q);
-      const f16x4 g4 = ld_global(reinterpret_cast<const f16x4*>(gain), q);
       f32x4 x, y;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[e] = static_cast<float>(e4[e]);
-        y[e] = x[e] * static_cast<float>(g4[e]);
+        x[e] = static_cast<float>(f.e[i][e]);
+        y[e] = x[e] * static_cast<float>(f.g[i][e]);
         ss += x[e] * x[e];
       }
       *reinterpret_cast<f32x4*>(xres + 4 * q) = x;
@@ -831,14 +845,19 @@ __device__ __forceinline__ bool run_steps(Ctx& c) {
                                                  (p0 + row) * HD * 2 + ((rl ^ (2 * (row & 7))) * 16), 0, 0, 0);
       }
     };
-    const bool early = layer > 0 && (kb / KT + wr) * KT < ke;
-    if (early) load_tile(kb / KT + wr);
-    // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77), RMSNorm input ----
-    if (layer == 0)
-      embed_row(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], xres, xhl, red);
-    else
+    const bool early = (kb / KT + wr) * KT < ke;
+    // ---- A: x = x' + sum_k D_k (layer 0: the embedding row, embedding.cpp:51-77, requested before the key tile),
+    //      RMSNorm input ----
+    if (layer == 0) {
+      EmbedFetch ef;
+      embed_fetch(c, wid, a.embed + static_cast<size_t>(c.token) * H, W[0], ef);
+      if (early) load_tile(kb / KT + wr);
+      embed_finish(c, wid, ef, xres, xhl, red);
+    } else {
+      if (early) load_tile(kb / KT + wr);
       cross_reduce2(c, wid, jj, true, a.xd, loc_xg, (tag - 1u) & 3u, loc_xa, W[0], xres, xhl, nullptr, red, 2 * layer + 1,
                     layer == a.L / 2 ? 15 : -1);
+    }
     XTRACE(1);
     XSYNC();  // #1
     // ---- B: q/k/v rows of RMSNorm(x): each wave its K slice of every row, the partial sums added in LDS ----

@@ -128,7 +128,7 @@ struct BatchWs {
 constexpr int kAttnChunk = 256;
 // Decode steps per launch of the XCD-partitioned one-launch kernel (its blocks stay resident from step to step: the
 // next token's first layer streams while the last layer of the current one runs).
-constexpr int kXcdStepsPerLaunch = 64;
+constexpr int kXcdStepsPerLaunch = 128;
 
 // Keys per attention chunk of single-sequence per-op decode for a cache of `cap` positions: the smallest of 64, 128,
 // 256 that keeps a full cache within 160 chunks (the kernel's combine limit). Smaller chunks give a short context
