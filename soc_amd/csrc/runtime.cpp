@@ -729,7 +729,9 @@ int run_decode_steps(soc_model* m, soc_kv* kv, int slot, int32_t last, int steps
                                : trace_roles + static_cast<size_t>(w.nblocks) * 8;
     if (trace_path != nullptr) {
       if ((e = hipMalloc(&p.trace, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMalloc trace");
-      if ((e = hipMemset(p.trace, 0, trace_n * sizeof(uint64_t))) != hipSuccess) return hip_fail(e, "hipMemset");
+      // on the decode stream: a null-stream memset is not ordered with the launches below and could clear the
+      // timestamps after a long launch has written them (diagnostics only; this path is never captured)
+      if ((e = hipMemsetAsync(p.trace, 0, trace_n * sizeof(uint64_t), s)) != hipSuccess) return hip_fail(e, "hipMemset");
     }
     if (xcd) {  // k_decode_xcd runs up to kXcdStepsPerLaunch steps per launch, releasing each token on the device
       for (int i = 0; i < steps; i += kXcdStepsPerLaunch) {
