@@ -542,6 +542,10 @@ hipError_t launch_split_epi(const GemmSplitArgs& g, hipStream_t s) {
     if (g.al != nullptr && mt128 * (g.N / 128) >= 512) return launch_split_cfg<EPI, 128, 128, 3, 2, 32, true, 4, 2>(g, s);
   }
   if constexpr (EPI == EPI_SWIGLU) {
+    // gate/up of a full chip of 256-row tiles: 256 x 192 (96 gate and 96 up rows) on 8 waves of 32 rows, one block
+    // per CU, one tile each (2048 tokens: 39.7 -> 37.9 us; 128 x 128 tiles make 1.5 rounds of two blocks per CU)
+    if (g.al == nullptr && g.K % 64 == 0 && ((g.M + 255) / 256) * ((g.N + 95) / 96) >= 256)
+      return launch_split_cfg<EPI, 256, 192, 2, 1, 64, false, 8, 1>(g, s);
     if (g.al == nullptr && g.K % 64 == 0 && mt128 * ((g.N + 63) / 64) >= 512)
       return launch_split_cfg<EPI, 128, 128, 2, 2, 64, false, 4, 2>(g, s);
   }

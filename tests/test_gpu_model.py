@@ -126,8 +126,8 @@ def test_prefill_split_gemm_matches_staged_kernel(gpu_ctx, monkeypatch, n, hilo)
     that converts the fp32 activations itself, with hi/lo pairs on every projection (SOC_PREFILL_SPLIT=1), on none
     (0), on the QKV projection only (the default) and on another mix: logits are bit-identical, for a single prefill
     (row counts off the 64/128-row tiles) and a chunked one. Qwen3-0.6B-wide layers (hidden 1024, 16 q / 8 kv heads,
-    3072). At 2000 rows the projections take the 128-row, 8-wave tile configurations (the 77-row chunk the small
-    ones)."""
+    3072). At 2000 rows the projections take the 8-wave tile configurations (128-row tiles; 256 x 192 for gate/up),
+    the 77-row chunk the small ones."""
     if hilo == "default":
         monkeypatch.delenv("SOC_PREFILL_SPLIT", raising=False)
     else:
