@@ -857,12 +857,16 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
         f32x16 sh;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sh[r] = 0.0f;
+        // a wave's MFMA runs at raised priority: on a SIMD whose other wave is in its softmax, the matrix core then
+        // takes this wave's MFMAs as they come while the other wave's VALU work fills the issue slots between them
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
           const fa_h8 ka = *reinterpret_cast<const fa_h8*>(&Ks[ql * HD + ((2 * ks + hb) ^ (ql & 15)) * 8]);
           sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[ks], sh, 0, 0, 0);
           if constexpr (LOQ) sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[ks], sh, 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
         // this lane: keys kt*32 + (r/4)*8 + hb*4 + r%4 of query row t
         float sv[16];
         float mt = -INFINITY;
@@ -917,12 +921,14 @@ __global__ __launch_bounds__(512, 1) void k_attention_prefill_pairs(AttnArgs a) 
               ph8[i + 1] = static_cast<_Float16>(p1);
             }
           }
+          __builtin_amdgcn_s_setprio(1);
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
             const fa_h8 va = read_vt(Vt, db, k2);
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph8, o[db], 0, 0, 0);
             if constexpr (LOP) o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl8, o[db], 0, 0, 0);
           }
+          __builtin_amdgcn_s_setprio(0);
         }
       }
       __syncthreads();

@@ -360,9 +360,13 @@ __global__ __launch_bounds__(64 * NWM * NWN, MINB) void k_gemm_split(GemmSplitAr
     const int st = kt % ST;
 #pragma unroll
     for (int ks = 0; ks < KS; ks += 2) {
+      // the first half of each step pair at raised priority: the waves of a SIMD fall into alternating phases, one
+      // issuing its MFMAs while another reads its next operands (2048-token prefill 5.90 -> 5.79 ms)
+      __builtin_amdgcn_s_setprio(1);
       read(a1, b1, st, ks + 1);
       mma(a0, b0);
       interleave();
+      __builtin_amdgcn_s_setprio(0);
       if (ks + 2 < KS) {
         read(a0, b0, st, ks + 2);
         mma(a1, b1);
