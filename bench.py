@@ -512,6 +512,8 @@ def main() -> None:
     ap.add_argument("--no-cpp-api", action="store_true", help="skip the GenerationContext (C++ API) measurement")
     ap.add_argument("--ragged-steps", type=int, default=RAGGED_STEPS, help="steps of the ragged run (profiling)")
     ap.add_argument("--steps-4b", type=int, default=64, help="timed steps of the Qwen3-4B batch-1 decode")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="profiling: only the 2048-token prefill (prints {\"prefill_ms_2048\": ...}, no decode line)")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="only run a plain copy of known size (for scaling rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -524,6 +526,10 @@ def main() -> None:
     cfg = S.QWEN3_0_6B
     ctx = S.Context(0)
     m = S.Model(ctx, cfg).synthesize(1, 0.02)
+    if args.prefill_only:
+        print(json.dumps({"prefill_ms_2048": round(bench_prefill(ctx, m, cfg, 2048), 3)}), flush=True)
+        m.close()
+        return
     path = m.decode_path()
     ms, mean_kv, toks = bench_decode(ctx, m, cfg, args.steps, args.warmup)
     _progress(f"decode: {ms / args.steps:.4f} ms per token ({path})")
