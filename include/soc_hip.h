@@ -142,8 +142,9 @@ int soc_quantize_group(const uint16_t* w, int64_t n, int64_t k, int32_t bits, vo
 int soc_model_quantize(soc_model* model, int32_t bits);
 /* Bytes of weights held on the device. */
 int soc_model_weight_bytes(const soc_model* model, int64_t* bytes);
-/* Which decode implementation soc_decode / soc_decode_steps use on this device: 2 = one kernel launch per token with
- * every layer split over the 8 XCDs (k_decode_xcd; models with 8 KV heads), 1 = one kernel launch per token with
+/* Which decode implementation soc_decode / soc_decode_steps use on this device: 2 = one kernel launch per token
+ * (soc_decode) or per up to 128 tokens (soc_decode_steps) with every layer split over the 8 XCDs (k_decode_xcd;
+ * models with 8 KV heads), 1 = one kernel launch per token with
  * dedicated attention blocks (k_decode_persistent), 0 = the per-operator kernel sequence replayed as a HIP graph.
  * Diagnostics only; the reference has no counterpart (it has one decode implementation per backend). */
 int soc_model_decode_path(soc_model* model, int32_t* path);
