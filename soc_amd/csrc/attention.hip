@@ -65,13 +65,16 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   // trip for each)
   constexpr int T4H = 4 / KH, UH = 16 / KH;
   u32x4 raw[16 / KH];  // keys: [tile t4][dim step t] -> raw[4 (t4 % T4H) + t]; values: the row layout below
+  // the ragged rows' keys and values stream past the caches (each is read once per step: 4.05 -> 4.02 ms per
+  // Qwen3-4B x 16 step); the single-sequence decode keeps cached loads
+  auto kv_load = [](const f16* p) { return KH == 2 ? load_stream16(p) : load16(p); };
   auto load_keys = [&](int h) {
 #pragma unroll
     for (int t4 = h * T4H; t4 < (h + 1) * T4H; ++t4) {
       const int p = min(64 * wid + 16 * t4 + kl, n - 1);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        raw[4 * (t4 - h * T4H) + t] = load16(kb + static_cast<size_t>(c0 + p) * HD + 32 * t + 8 * kg);
+        raw[4 * (t4 - h * T4H) + t] = kv_load(kb + static_cast<size_t>(c0 + p) * HD + 32 * t + 8 * kg);
     }
   };
 
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 #pragma unroll
     for (int u = h * UH; u < (h + 1) * UH; ++u) {
       const int p = min(u * 16 + wid * 4 + r, n - 1);
-      raw[u - h * UH] = load16(vb + static_cast<size_t>(c0 + p) * HD + sub * 8);
+      raw[u - h * UH] = kv_load(vb + static_cast<size_t>(c0 + p) * HD + sub * 8);
     }
   };
   load_values(0);
