@@ -65,9 +65,9 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
   // trip for each)
   constexpr int T4H = 4 / KH, UH = 16 / KH;
   u32x4 raw[16 / KH];  // keys: [tile t4][dim step t] -> raw[4 (t4 % T4H) + t]; values: the row layout below
-  // the ragged rows' keys and values stream past the caches (each is read once per step: 4.05 -> 4.02 ms per
-  // Qwen3-4B x 16 step); the single-sequence decode keeps cached loads
-  auto kv_load = [](const f16* p) { return KH == 2 ? load_stream16(p) : load16(p); };
+  // keys and values stream past the caches (each is read once per step: 4.05 -> 4.02 ms per Qwen3-4B x 16 ragged
+  // step, 1.99 -> 1.98 ms per Qwen3-4B batch-1 token)
+  auto kv_load = [](const f16* p) { return load_stream16(p); };
   auto load_keys = [&](int h) {
 #pragma unroll
     for (int t4 = h * T4H; t4 < (h + 1) * T4H; ++t4) {
